@@ -1,0 +1,123 @@
+/*
+ * theria_sdpa.h - C ABI of the MI355X (gfx950) scaled-dot-product-attention operator family.
+ *
+ * One shared library, libtheria_sdpa.so, exports these entry points. They take caller-owned device
+ * pointers, plain integer shapes and strides, and a hipStream_t passed as void*. The library never
+ * allocates or frees device memory: every output and every workspace is caller-owned. Every entry
+ * point is reentrant; the only mutable state is the thread-local message behind theria_last_error().
+ *
+ * Semantics follow theria's operator contract (docs/phase9.md:12-39 in the reference):
+ *   S = scale * Q K^T (+ causal mask), P = softmax_row(S), O = P V,
+ *   m_i = max_j S_ij, l_i = sum_j exp(S_ij - m_i), lse_i = m_i + log(l_i).
+ *
+ * Tensors are (B, H, rows, D) views with element strides for batch, head and row; the last
+ * dimension must be contiguous (stride 1). Row statistics (lse, m, l, delta, r, t) are contiguous
+ * float32 arrays shaped (B, H, rows). Supported dtypes are float32, float16 and bfloat16 (the
+ * reference's _ALLOWED_DTYPES, theria/attention/triton_sdpa_backward.py:20); head_dim <= 128.
+ *
+ * Return value: THERIA_OK, THERIA_ERR_CONTRACT (a shape, dtype, stride or pointer the contract
+ * rejects: the reference raises AssertionError for these) or THERIA_ERR_HIP (a launch failure).
+ * theria_last_error() returns the message of the last failing call on the calling thread.
+ */
+#ifndef THERIA_SDPA_H
+#define THERIA_SDPA_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define THERIA_SDPA_ABI_VERSION 1
+
+enum theria_dtype { THERIA_DTYPE_F32 = 0, THERIA_DTYPE_F16 = 1, THERIA_DTYPE_BF16 = 2 };
+enum theria_status { THERIA_OK = 0, THERIA_ERR_CONTRACT = 1, THERIA_ERR_HIP = 2 };
+
+/* A (B, H, rows, D) tensor view. data == NULL means "absent" where an entry point allows it. */
+typedef struct {
+  void* data;
+  int64_t stride_b, stride_h, stride_row; /* element strides; the last dimension has stride 1 */
+} theria_tensor_t;
+
+/* Problem description shared by every entry point. tq = query rows (T), tk = key rows (M). */
+typedef struct {
+  int32_t dtype; /* enum theria_dtype of q, k, v and the other (B,H,rows,D) tensors */
+  int32_t batch, heads, tq, tk, head_dim;
+  float scale;    /* softmax scale; theria uses 1/sqrt(head_dim) */
+  int32_t causal; /* 1: key j is visible to query i only when j <= i (top-left aligned) */
+} theria_sdpa_problem_t;
+
+/* ABI version (THERIA_SDPA_ABI_VERSION of the built library). */
+int theria_abi_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* theria_last_error(void);
+
+/*
+ * Fused forward: O = softmax(scale Q K^T) V, saving lse (natural log) per query row.
+ * Replaces triton_sdpa_fused + _fused_sdpa_kernel (theria/attention/triton_qk.py:242-369).
+ * o_is_f32 selects float32 O (the reference kernel's output dtype, triton_qk.py:321) instead of
+ * the input dtype. row_max / row_sum may be NULL; when given they receive the reference's saved
+ * statistics m (row max of scaled scores) and l (sum of exp(S - m)) (triton_qk.py:299-304).
+ * A query row with no visible key gets O = 0, lse = -inf, m = -inf, l = 0.
+ */
+int theria_sdpa_fwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
+                    const theria_tensor_t* v, const theria_tensor_t* o, int32_t o_is_f32, float* lse,
+                    float* row_max, float* row_sum, void* stream);
+
+/*
+ * Explicit backward given the forward output O: dQ, dK, dV.
+ * Replaces sdpa_bwd_dq / sdpa_bwd_dk / sdpa_bwd_dv and their kernels
+ * (theria/attention/triton_sdpa_backward.py:106-266, 269-462, 505-696) and the backward of
+ * TritonFusedSDPAFunction (triton_qk.py:379-387). The row term z_i = sum_j dP_ij P_ij of the
+ * reference (triton_sdpa_backward.py:312-353, 543-585) is computed once as delta_i = dO_i . O_i and
+ * written to delta_out (B,H,tq) float32. dout has the input dtype; o may be float32 (o_is_f32).
+ * dq / dk may have data == NULL to skip that output. dq_accum is a caller-owned float32 workspace
+ * of batch*heads*tq*head_dim elements (contents on entry are ignored).
+ */
+int theria_sdpa_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
+                    const theria_tensor_t* v, const theria_tensor_t* o, int32_t o_is_f32,
+                    const theria_tensor_t* dout, const float* lse, float* delta_out, const theria_tensor_t* dq,
+                    const theria_tensor_t* dk, const theria_tensor_t* dv, float* dq_accum, void* stream);
+
+/*
+ * Explicit backward from saved statistics only (no O), the reference's sdpa_bwd_* signature
+ * (q, k, v, dout, m, l, scale) with lse = m + log(l). The row term is recomputed from P(lse) and V.
+ * v may have data == NULL: then only dV is computed (sdpa_bwd_dv takes no v,
+ * triton_sdpa_backward.py:194), and dq / dk must be absent. Workspaces as in theria_sdpa_bwd.
+ */
+int theria_sdpa_bwd_from_stats(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
+                               const theria_tensor_t* v, const theria_tensor_t* dout, const float* lse,
+                               float* delta_out, const theria_tensor_t* dq, const theria_tensor_t* dk,
+                               const theria_tensor_t* dv, float* dq_accum, void* stream);
+
+/*
+ * Frozen-stats JVP: tangent of O along (tq, tk, tv) with P rebuilt from lse.
+ * Replaces sdpa_jvp (theria/attention/triton_sdpa_backward.py:465-503), which runs eager PyTorch:
+ *   G = scale (tq K^T + Q tk^T), c_i = sum_j P_ij G_ij, tO = (P o G) V - c o O + P tv.
+ * o may have data == NULL: O is then rebuilt from P(lse) and V inside the kernel. Any tangent may
+ * have data == NULL (a zero tangent). tout has the input dtype.
+ */
+int theria_sdpa_jvp(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
+                    const theria_tensor_t* v, const theria_tensor_t* o, const float* lse, const theria_tensor_t* tq,
+                    const theria_tensor_t* tk, const theria_tensor_t* tv, const theria_tensor_t* tout, void* stream);
+
+/*
+ * Double backward: the vector-Jacobian product of the backward map (Q, K, V, dO) -> (dQ, dK, dV)
+ * with cotangents (gq, gk, gv) of (dQ, dK, dV). Outputs out_gq, out_gk, out_gv, out_gdout.
+ * The reference has no kernel for this: its HVP is a finite difference of the VJP
+ * (theria/attention/hvp_utils.py:30-49) or autograd-in-backward (theria/autograd/sdpa_custom_function.py:32-53).
+ * delta is the row term written by theria_sdpa_bwd. Any cotangent may have data == NULL (zero).
+ * row_ws is a caller-owned float32 workspace of 2*batch*heads*tq elements.
+ */
+int theria_sdpa_bwd_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
+                        const theria_tensor_t* v, const theria_tensor_t* o, const theria_tensor_t* dout,
+                        const float* lse, const float* delta, const theria_tensor_t* gq, const theria_tensor_t* gk,
+                        const theria_tensor_t* gv, const theria_tensor_t* out_gq, const theria_tensor_t* out_gk,
+                        const theria_tensor_t* out_gv, const theria_tensor_t* out_gdout, float* row_ws, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* THERIA_SDPA_H */

@@ -1,0 +1,93 @@
+"""The C ABI library loads and exports exactly what include/theria_sdpa.h declares (no GPU needed).
+
+Also checks the host-side contract validation of every entry point (it runs before any HIP call, so
+no device is touched), and that the Python bindings and the header agree on struct layouts.
+"""
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "theria_sdpa.h"
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(theria_[a-z_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    from theria_amd import _lib
+
+    lib = _lib.load()
+    declared = _declared_functions()
+    assert declared, "no declarations parsed from the header"
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in {HEADER.name} but not exported"
+    assert set(declared) == set(_lib.SIGNATURES), "ctypes signature table out of sync with the header"
+    nm = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True, check=True)
+    exported = sorted(set(re.findall(r"\sT\s(theria_\w+)", nm.stdout)))
+    assert exported == declared, f"exported {exported} != declared {declared}"
+
+
+def test_abi_version_matches():
+    from theria_amd import _lib
+
+    assert _lib.load().theria_abi_version() == _lib.ABI_VERSION
+
+
+def test_struct_layouts_match_header():
+    from theria_amd import _lib
+
+    assert ctypes.sizeof(_lib.TensorView) == 32
+    assert ctypes.sizeof(_lib.Problem) == 32
+
+
+def _call_all(prob):
+    """Call every compute entry point with the given problem and NULL tensors; return status codes."""
+    from theria_amd import _lib
+
+    lib = _lib.load()
+    p = ctypes.byref(prob)
+    return {
+        "fwd": lib.theria_sdpa_fwd(p, None, None, None, None, 0, None, None, None, None),
+        "bwd": lib.theria_sdpa_bwd(p, None, None, None, None, 0, None, None, None, None, None, None, None, None),
+        "bwd_from_stats": lib.theria_sdpa_bwd_from_stats(p, None, None, None, None, None, None, None, None, None, None, None),
+        "jvp": lib.theria_sdpa_jvp(p, None, None, None, None, None, None, None, None, None, None),
+        "bwd_bwd": lib.theria_sdpa_bwd_bwd(
+            p, None, None, None, None, None, None, None, None, None, None, None, None, None, None, None, None
+        ),
+    }
+
+
+@pytest.mark.parametrize(
+    "fields,needle",
+    [
+        ((9, 1, 1, 4, 4, 8, 0.5, 0), "dtype"),
+        ((2, 1, 1, 4, 4, 200, 0.5, 0), "head_dim"),
+        ((2, 1, 1, 4, 4, 8, -1.0, 0), "scale"),
+        ((2, -1, 1, 4, 4, 8, 0.5, 0), "negative"),
+        ((2, 1, 1, 4, 4, 8, 0.5, 0), "required"),
+    ],
+)
+def test_contract_violations_are_reported(fields, needle):
+    from theria_amd import _lib
+
+    codes = _call_all(_lib.Problem(*fields))
+    lib = _lib.load()
+    for name, rc in codes.items():
+        assert rc == _lib.ERR_CONTRACT, f"{name} returned {rc}"
+    assert needle in lib.theria_last_error().decode()
+
+
+def test_python_check_maps_contract_errors_to_assertion():
+    from theria_amd import _lib
+
+    codes = _call_all(_lib.Problem(9, 1, 1, 4, 4, 8, 0.5, 0))
+    with pytest.raises(AssertionError):
+        _lib.check(codes["fwd"], "theria_sdpa_fwd")

@@ -1,0 +1,245 @@
+"""The HIP operator through torch.autograd: gradients, forward-mode JVP, HVP by double backward,
+the reference-named entry points, and the second-order boundary (GPU).
+
+Config 4 (BASELINE): B8 H8 S512 D64 in float32 and bfloat16; primals ~ N(0,1), tangents ~ N(0, 0.1^2);
+HVP of 0.5 ||O - T||^2 with T, v ~ N(0,1) via double backward through the explicit kernels.
+Bars: float32 1e-5 abs/rel, bfloat16/float16 2e-2 abs.
+"""
+
+import math
+
+import pytest
+import torch
+
+from oracle import sdpa_oracle as O
+from theria_amd.attention import (
+    TritonFusedSDPAFunction,
+    hip_sdpa,
+    sdpa_bwd_dk,
+    sdpa_bwd_dq,
+    sdpa_bwd_dv,
+    sdpa_jvp,
+    triton_sdpa_fused,
+)
+from theria_amd.attention.custom import sdpa_custom
+from theria_amd.attention.hvp_utils import hvp_fd_vjp
+
+pytestmark = pytest.mark.gpu
+
+
+def tol(dtype):
+    """float32: 1e-5 abs/rel. 16-bit: the reference's GPU-test bound rtol = atol = 2e-2
+    (tests/test_triton_fused_forward.py:27, test_triton_sdpa_dq.py:42): outputs are rounded to the input
+    dtype, and half a bfloat16 ulp already exceeds 2e-2 for |x| >= 8, so a pure absolute bound cannot hold."""
+    return dict(rtol=1e-5, atol=1e-5) if dtype == torch.float32 else dict(rtol=2e-2, atol=2e-2)
+
+
+def close(gpu, ref, dtype, what):
+    a = gpu.detach().double().cpu()
+    assert torch.isfinite(a).all(), f"{what}: non-finite"
+    torch.testing.assert_close(a, ref.double(), **tol(dtype), msg=lambda m: f"{what}: {m}")
+
+
+def make(shape, dtype, dev, seed, std=1.0, grad=False):
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(*shape, generator=g) * std).to(dtype)
+    return x.to(dev).requires_grad_(grad), x.double()
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("causal", [False, True])
+def test_autograd_first_order(dt, causal, hip_device):
+    dev = hip_device
+    q, qc = make((2, 3, 100, 64), dt, dev, 1, grad=True)
+    k, kc = make((2, 3, 100, 64), dt, dev, 2, grad=True)
+    v, vc = make((2, 3, 100, 64), dt, dev, 3, grad=True)
+    do, doc = make((2, 3, 100, 64), dt, dev, 4)
+    o = hip_sdpa(q, k, v, causal=causal)
+    close(o, O.forward(qc, kc, vc, causal=causal)[0], dt, "O")
+    grads = torch.autograd.grad(o, (q, k, v), do)
+    for name, a, b in zip(("dQ", "dK", "dV"), grads, O.backward(qc, kc, vc, doc, causal=causal)):
+        close(a, b, dt, name)
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_config4_jvp_forward_mode(dt, hip_device):
+    dev = hip_device
+    B, H, S, D = 8, 8, 512, 64
+    print(f"[autograd] config4 jvp {dt}", flush=True)
+    q, qc = make((B, H, S, D), dt, dev, 31)
+    k, kc = make((B, H, S, D), dt, dev, 32)
+    v, vc = make((B, H, S, D), dt, dev, 33)
+    tq, tqc = make((B, H, S, D), dt, dev, 34, std=0.1)
+    tk, tkc = make((B, H, S, D), dt, dev, 35, std=0.1)
+    tv, tvc = make((B, H, S, D), dt, dev, 36, std=0.1)
+    o, jv = torch.func.jvp(lambda a, b, c: hip_sdpa(a, b, c), (q, k, v), (tq, tk, tv))
+    ref = O.jvp(qc, kc, vc, tqc, tkc, tvc)
+    close(jv, ref, dt, "JVP")
+    with torch.autograd.forward_ad.dual_level():
+        dual = torch.autograd.forward_ad.make_dual(q, tq)
+        tangent = torch.autograd.forward_ad.unpack_dual(hip_sdpa(dual, k, v)).tangent
+    close(tangent, O.jvp(qc, kc, vc, tqc, None, None), dt, "JVP(forward_ad, q only)")
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_config4_hvp_double_backward(dt, hip_device):
+    dev = hip_device
+    B, H, S, D = 8, 8, 512, 64
+    print(f"[autograd] config4 hvp {dt}", flush=True)
+    q, qc = make((B, H, S, D), dt, dev, 41, grad=True)
+    k, kc = make((B, H, S, D), dt, dev, 42, grad=True)
+    v, vc = make((B, H, S, D), dt, dev, 43, grad=True)
+    T_, Tc = make((B, H, S, D), dt, dev, 44)
+    vq, vqc = make((B, H, S, D), dt, dev, 45)
+    vk, vkc = make((B, H, S, D), dt, dev, 46)
+    vv, vvc = make((B, H, S, D), dt, dev, 47)
+    out = hip_sdpa(q, k, v)
+    loss = 0.5 * ((out.float() - T_.float()) ** 2).sum()
+    g = torch.autograd.grad(loss, (q, k, v), create_graph=True)
+    dot = sum((a.float() * b.float()).sum() for a, b in zip(g, (vq, vk, vv)))
+    hvp = torch.autograd.grad(dot, (q, k, v))
+    ref = O.hvp_quadratic(qc, kc, vc, Tc, vqc, vkc, vvc)
+    for name, a, b in zip(("Hq", "Hk", "Hv"), hvp, ref):
+        close(a, b, dt, name)
+
+
+def test_config1_hvp_weighted_sum_fp32(hip_device):
+    dev = hip_device
+    q, qc = make((2, 2, 16, 8), torch.float32, dev, 51, grad=True)
+    k, kc = make((2, 2, 16, 8), torch.float32, dev, 52, grad=True)
+    v, vc = make((2, 2, 16, 8), torch.float32, dev, 53, grad=True)
+    W, Wc = make((2, 2, 16, 8), torch.float32, dev, 54)
+    u = [make((2, 2, 16, 8), torch.float32, dev, 55 + i) for i in range(3)]
+    g = torch.autograd.grad((hip_sdpa(q, k, v) * W).sum(), (q, k, v), create_graph=True)
+    h = torch.autograd.grad(sum((a * b[0]).sum() for a, b in zip(g, u)), (q, k, v))
+    for name, a, b in zip(("Hq", "Hk", "Hv"), h, O.hvp_weighted_sum(qc, kc, vc, Wc, *(x[1] for x in u))):
+        close(a, b, torch.float32, name)
+
+
+def test_autograd_functional_jvp_uses_double_backward(hip_device):
+    """torch.autograd.functional.jvp runs the double-backward trick: it exercises G_dO."""
+    dev = hip_device
+    q, qc = make((1, 2, 24, 32), torch.float32, dev, 61)
+    k, kc = make((1, 2, 24, 32), torch.float32, dev, 62)
+    v, vc = make((1, 2, 24, 32), torch.float32, dev, 63)
+    t = [make((1, 2, 24, 32), torch.float32, dev, 64 + i) for i in range(3)]
+    _, jv = torch.autograd.functional.jvp(lambda a, b, c: hip_sdpa(a, b, c), (q, k, v), tuple(x[0] for x in t))
+    close(jv, O.jvp(qc, kc, vc, *(x[1] for x in t)), torch.float32, "functional.jvp")
+
+
+def test_third_order_raises_instead_of_dropping_terms(hip_device):
+    dev = hip_device
+    q = torch.randn(1, 1, 8, 16, device=dev, requires_grad=True)
+    k = torch.randn(1, 1, 8, 16, device=dev, requires_grad=True)
+    v = torch.randn(1, 1, 8, 16, device=dev, requires_grad=True)
+    g = torch.autograd.grad(hip_sdpa(q, k, v).pow(2).sum(), (q, k, v), create_graph=True)
+    g2 = torch.autograd.grad(sum(x.pow(2).sum() for x in g), (q, k, v), create_graph=True)
+    with pytest.raises(RuntimeError, match="third-order"):
+        torch.autograd.grad(sum(x.sum() for x in g2), (q, k, v))
+
+
+def test_second_order_probe_sees_attention_curvature(hip_device):
+    """The Phase-11 probe (_attention_second_order_ok): grad of ||grad||^2 through SDPA alone is nonzero."""
+    dev = hip_device
+    torch.manual_seed(0)
+    q = torch.randn(1, 1, 1, 4, device=dev, requires_grad=True)
+    k = torch.randn(1, 1, 2, 4, device=dev, requires_grad=True)
+    v = torch.randn(1, 1, 2, 4, device=dev, requires_grad=True)
+    out = sdpa_custom(q, k, v, backend="triton_full_fused")
+    g1 = torch.autograd.grad(out.sum(), (q, k, v), retain_graph=True, create_graph=True)
+    g2 = torch.autograd.grad(sum(x.pow(2).sum() for x in g1), (q, k, v), allow_unused=True)
+    assert any(x is not None and float(x.abs().sum()) > 1e-12 for x in g2)
+    # and it equals the exact value from the oracle
+    qc, kc, vc = (t.detach().double().cpu() for t in (q, k, v))
+    g1c = O.backward(qc, kc, vc, torch.ones(1, 1, 1, 4, dtype=torch.float64))
+    ref = O.double_backward(qc, kc, vc, torch.ones(1, 1, 1, 4, dtype=torch.float64), *(2 * x for x in g1c))
+    for a, b in zip(g2, ref[:3]):
+        close(a, b, torch.float32, "probe")
+
+
+# ---- reference-named entry points (the drop-in surface) ----------------------------------------
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 32, 32, 32), (4, 8, 128, 128, 64), (1, 1, 1, 1, 32)])
+def test_sdpa_custom_fused_matches_reference_backend(shape, hip_device):
+    B, H, T, M, D = shape
+    torch.manual_seed(0)
+    q = torch.randn(B, H, T, D, device=hip_device, dtype=torch.float16)
+    k = torch.randn(B, H, M, D, device=hip_device, dtype=torch.float16)
+    v = torch.randn(B, H, M, D, device=hip_device, dtype=torch.float16)
+    fused = sdpa_custom(q, k, v, backend="triton_full_fused")
+    assert fused.dtype == q.dtype
+    ref = O.forward(q.double().cpu(), k.double().cpu(), v.double().cpu())[0]
+    close(fused, ref, torch.float16, "sdpa_custom fused")
+
+
+def test_triton_sdpa_fused_returns_fp32_and_stats(hip_device):
+    torch.manual_seed(0)
+    q, k, v = (torch.randn(2, 3, 50, 64, device=hip_device, dtype=torch.bfloat16) for _ in range(3))
+    o, m, l = triton_sdpa_fused(q, k, v, return_stats=True)
+    assert o.dtype == torch.float32 and m.shape == (2, 3, 50) and l.shape == (2, 3, 50)
+    Or, _, mr, lr = O.forward(q.double().cpu(), k.double().cpu(), v.double().cpu())
+    close(o, Or, torch.bfloat16, "O")
+    torch.testing.assert_close(m.double().cpu(), mr, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(l.double().cpu(), lr, rtol=1e-5, atol=1e-5)
+    o2 = TritonFusedSDPAFunction.apply(q, k, v)
+    assert o2.dtype == torch.float32
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 32, 32, 32), (2, 4, 128, 128, 64)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_explicit_backward_with_torch_stats(shape, dtype, hip_device):
+    """The reference's kernel tests: stats (m, l) computed by torch, inputs fed as given."""
+    B, H, T, M, D = shape
+    torch.manual_seed(0)
+    dev = hip_device
+    q = torch.randn(B, H, T, D, device=dev, dtype=torch.float16).to(dtype)
+    k = torch.randn(B, H, M, D, device=dev, dtype=torch.float16).to(dtype)
+    v = torch.randn(B, H, M, D, device=dev, dtype=torch.float16).to(dtype)
+    dout = torch.randn(B, H, T, D, device=dev, dtype=torch.float16).to(dtype)
+    scale = 1.0 / D**0.5
+    scores = torch.matmul(q.float(), k.float().transpose(-2, -1)) * scale
+    m = scores.max(dim=-1).values
+    l = torch.exp(scores - m.unsqueeze(-1)).sum(dim=-1)
+    ref = O.backward(*(t.double().cpu() for t in (q, k, v, dout)), scale)
+    for name, fn, r in (
+        ("dq", lambda: sdpa_bwd_dq(q, k, v, dout, m, l, scale), ref[0]),
+        ("dk", lambda: sdpa_bwd_dk(q, k, v, dout, m, l, scale), ref[1]),
+        ("dv", lambda: sdpa_bwd_dv(q, k, dout, m, l, scale), ref[2]),
+    ):
+        out = fn()
+        assert out.dtype == dtype
+        close(out, r, dtype, name)
+
+
+def test_explicit_jvp_matches_frozen_stats_oracle(hip_device):
+    torch.manual_seed(0)
+    dev = hip_device
+    q, k, v = (torch.randn(2, 2, 64, 64, device=dev, dtype=torch.float16) for _ in range(3))
+    dq, dk, dv = (torch.randn_like(q) for _ in range(3))
+    _, m, l = triton_sdpa_fused(q, k, v, return_stats=True)
+    out = sdpa_jvp(q, k, v, dq, dk, dv, m, l, 1 / 8.0)
+    ref = O.frozen_jvp(*(t.double().cpu() for t in (q, k, v, dq, dk, dv, m, l)), 1 / 8.0)
+    close(out, ref, torch.float16, "sdpa_jvp")
+
+
+def test_explicit_guards_raise_assertion(hip_device):
+    q = torch.randn(1, 1, 4, 8, device=hip_device)
+    m = torch.zeros(1, 1, 4, device=hip_device)
+    with pytest.raises(AssertionError):
+        sdpa_bwd_dq(q, q, q, q, m, m.unsqueeze(-1), 0.3)  # wrong stats shape
+    with pytest.raises(AssertionError):
+        sdpa_jvp(q, q, q, q, q, q, m, m, 0.3)  # l <= 0
+    with pytest.raises(AssertionError):
+        sdpa_bwd_dq(q.double(), q.double(), q.double(), q.double(), m, m + 1, 0.3)  # float64 unsupported
+
+
+def test_hvp_fd_vjp_agrees_with_exact_hvp(hip_device):
+    torch.manual_seed(0)
+    dev = hip_device
+    q, k, v = (torch.randn(1, 1, 8, 8, device=dev) for _ in range(3))
+    d = [torch.randn_like(q) for _ in range(3)]
+    fd = hvp_fd_vjp(q, k, v, *d, eps=1e-2)
+    exact = O.hvp_sum(*(t.double().cpu() for t in (q, k, v, *d)))
+    cos = torch.nn.functional.cosine_similarity(torch.cat([x.double().cpu().flatten() for x in fd]), torch.cat([x.flatten() for x in exact]), dim=0)
+    assert float(cos) > 0.99

@@ -1,0 +1,250 @@
+"""Torch-level wrappers over the C ABI: shape/dtype/device guards, output allocation, stream plumbing.
+
+Each function validates its arguments the way the reference's guards do (AssertionError with a
+message, theria/attention/triton_sdpa_backward.py:23-103), allocates fresh outputs on the inputs'
+device (the reference's ownership rule, triton_qk.py:321-323) and launches on torch's current stream
+of that device. Inputs are never mutated.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import _lib
+
+ALLOWED_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+_DTYPE_CODE = {torch.float32: _lib.DTYPE_F32, torch.float16: _lib.DTYPE_F16, torch.bfloat16: _lib.DTYPE_BF16}
+MAX_HEAD_DIM = 128
+
+
+def default_scale(head_dim: int) -> float:
+    return 1.0 / math.sqrt(head_dim)
+
+
+def _rowmajor(t: torch.Tensor | None) -> torch.Tensor | None:
+    """The kernels need a contiguous last dimension; other strides (incl. broadcast) are fine."""
+    if t is None:
+        return None
+    if t.shape[-1] > 1 and t.stride(-1) != 1:
+        return t.contiguous()
+    return t
+
+
+def _plain(t: torch.Tensor) -> torch.Tensor:
+    """Underlying tensor of a torch.func (functorch) wrapper, whose storage the kernels read.
+
+    torch.func.jvp calls SDPAOp.jvp with its saved tensors wrapped for gradient tracking; the values
+    are those of the wrapped tensor.
+    """
+    from torch._C._functorch import get_unwrapped, is_functorch_wrapped_tensor
+
+    while is_functorch_wrapped_tensor(t):
+        t = get_unwrapped(t)
+    return t
+
+
+def _tv(t: torch.Tensor | None):
+    if t is None:
+        return None
+    t = _plain(t)
+    return ctypes.byref(_lib.TensorView(t.data_ptr(), t.stride(0), t.stride(1), t.stride(2)))
+
+
+def _fp(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(_plain(t).data_ptr())
+
+
+def _stream(dev: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _problem(q: torch.Tensor, k: torch.Tensor, scale: float, causal: bool) -> _lib.Problem:
+    B, H, T, D = q.shape
+    return _lib.Problem(_DTYPE_CODE[q.dtype], B, H, T, k.shape[2], D, float(scale), 1 if causal else 0)
+
+
+def check_inputs(q, k, v, what: str = "theria_amd SDPA", require_v: bool = True) -> None:
+    """Device, dtype and shape contract shared by every HIP entry point."""
+    for name, t in (("q", q), ("k", k), ("v", v) if require_v else (None, None)):
+        if name is None:
+            continue
+        if t is None:
+            raise AssertionError(f"{what}: {name} is required")
+        if not t.is_cuda:
+            raise AssertionError(f"{what} requires GPU (HIP) tensors; {name} is on {t.device}")
+        if t.dtype not in ALLOWED_DTYPES:
+            raise AssertionError(f"Unsupported dtype for {name}: {t.dtype}")
+        if t.dim() != 4:
+            raise AssertionError(f"{what}: {name} must be 4-D (B,H,rows,D), got shape {tuple(t.shape)}")
+    B, H, T, D = q.shape
+    if k.shape[0] != B or k.shape[1] != H or k.shape[3] != D:
+        raise AssertionError("k must have shape (B,H,M,D) with D matching q")
+    if k.dtype != q.dtype:
+        raise AssertionError(f"{what}: k dtype {k.dtype} != q dtype {q.dtype}")
+    if k.device != q.device:
+        raise AssertionError(f"{what}: q and k are on different devices")
+    if require_v:
+        if v.shape[0] != B or v.shape[1] != H or v.shape[2] != k.shape[2]:
+            raise AssertionError("v must have shape (B,H,M,Dv) matching k")
+        if v.shape[3] != D:
+            raise AssertionError("theria_amd SDPA requires Dv == D")
+        if v.dtype != q.dtype or v.device != q.device:
+            raise AssertionError(f"{what}: v must match q in dtype and device")
+    if D > MAX_HEAD_DIM or D < 1:
+        raise AssertionError(f"{what} supports 1 <= D <= {MAX_HEAD_DIM}, got D={D}")
+    if max(q.shape[2], k.shape[2]) >= 2**31 or B * H >= 2**31:
+        raise AssertionError(f"{what}: sizes exceed the 32-bit row index range")
+
+
+def _like_rows(t: torch.Tensor | None, ref: torch.Tensor, rows: int, name: str) -> torch.Tensor | None:
+    """Cast a (B,H,rows,D) operand to the compute dtype and check its shape."""
+    if t is None:
+        return None
+    B, H, _, D = ref.shape
+    if tuple(t.shape) != (B, H, rows, D):
+        raise AssertionError(f"{name} must have shape {(B, H, rows, D)}, got {tuple(t.shape)}")
+    if not t.is_cuda or t.device != ref.device:
+        raise AssertionError(f"{name} must be on {ref.device}")
+    if t.dtype != ref.dtype:
+        t = t.to(ref.dtype)
+    return _rowmajor(t)
+
+
+def fwd(q, k, v, scale: float, causal: bool, out_fp32: bool = False, stats: bool = False):
+    """O, lse (and the reference's m, l when stats=True). O is float32 when out_fp32."""
+    check_inputs(q, k, v)
+    q, k, v = _rowmajor(q), _rowmajor(k), _rowmajor(v)
+    B, H, T, D = q.shape
+    dev = q.device
+    o = torch.empty((B, H, T, D), dtype=torch.float32 if out_fp32 else q.dtype, device=dev)
+    lse = torch.empty((B, H, T), dtype=torch.float32, device=dev)
+    m = torch.empty_like(lse) if stats else None
+    l = torch.empty_like(lse) if stats else None
+    lib = _lib.load()
+    prob = _problem(q, k, scale, causal)
+    with torch.cuda.device(dev):
+        rc = lib.theria_sdpa_fwd(
+            ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(o), 1 if out_fp32 else 0, _fp(lse), _fp(m), _fp(l),
+            _stream(dev),
+        )
+    _lib.check(rc, "theria_sdpa_fwd")
+    return o, lse, m, l
+
+
+def bwd(q, k, v, o, lse, do, scale: float, causal: bool, need_dq: bool = True, need_dk: bool = True):
+    """dQ, dK, dV (input dtype) and the row term delta = rowsum(dO * O) (float32)."""
+    check_inputs(q, k, v)
+    q, k, v = _rowmajor(q), _rowmajor(k), _rowmajor(v)
+    B, H, T, D = q.shape
+    M = k.shape[2]
+    do = _like_rows(do, q, T, "dout")
+    o = _rowmajor(o)
+    if tuple(o.shape) != (B, H, T, D):
+        raise AssertionError("o must have shape (B,H,T,D)")
+    o_f32 = o.dtype == torch.float32 and q.dtype != torch.float32
+    if not o_f32 and o.dtype != q.dtype:
+        o = o.to(q.dtype)
+    lse = lse.contiguous()
+    dev = q.device
+    delta = torch.empty((B, H, T), dtype=torch.float32, device=dev)
+    dq = torch.empty((B, H, T, D), dtype=q.dtype, device=dev) if need_dq else None
+    dk = torch.empty((B, H, M, D), dtype=q.dtype, device=dev) if need_dk else None
+    dv = torch.empty((B, H, M, D), dtype=q.dtype, device=dev)
+    acc = torch.empty((B, H, T, D), dtype=torch.float32, device=dev) if need_dq else None
+    lib = _lib.load()
+    prob = _problem(q, k, scale, causal)
+    with torch.cuda.device(dev):
+        rc = lib.theria_sdpa_bwd(
+            ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(o), 1 if o_f32 else 0, _tv(do), _fp(lse), _fp(delta),
+            _tv(dq), _tv(dk), _tv(dv), _fp(acc), _stream(dev),
+        )
+    _lib.check(rc, "theria_sdpa_bwd")
+    return dq, dk, dv, delta
+
+
+def bwd_from_stats(q, k, v, do, lse, scale: float, causal: bool, need_dq: bool, need_dk: bool, need_dv: bool):
+    """Backward from saved statistics only (no O). v may be None when only dV is requested."""
+    check_inputs(q, k, v, require_v=v is not None)
+    q, k = _rowmajor(q), _rowmajor(k)
+    v = _rowmajor(v)
+    B, H, T, D = q.shape
+    M = k.shape[2]
+    do = _like_rows(do, q, T, "dout")
+    lse = lse.contiguous()
+    dev = q.device
+    delta = torch.empty((B, H, T), dtype=torch.float32, device=dev) if v is not None else None
+    dq = torch.empty((B, H, T, D), dtype=q.dtype, device=dev) if need_dq else None
+    dk = torch.empty((B, H, M, D), dtype=q.dtype, device=dev) if need_dk else None
+    dv = torch.empty((B, H, M, D), dtype=q.dtype, device=dev)
+    acc = torch.empty((B, H, T, D), dtype=torch.float32, device=dev) if need_dq else None
+    lib = _lib.load()
+    prob = _problem(q, k, scale, causal)
+    with torch.cuda.device(dev):
+        rc = lib.theria_sdpa_bwd_from_stats(
+            ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(do), _fp(lse), _fp(delta), _tv(dq), _tv(dk), _tv(dv),
+            _fp(acc), _stream(dev),
+        )
+    _lib.check(rc, "theria_sdpa_bwd_from_stats")
+    return dq, dk, (dv if need_dv else None)
+
+
+def jvp(q, k, v, o, lse, tq, tk, tv, scale: float, causal: bool):
+    """Frozen-stats tangent of O along (tq, tk, tv); o=None rebuilds O from lse inside the kernel."""
+    check_inputs(q, k, v)
+    q, k, v = _rowmajor(q), _rowmajor(k), _rowmajor(v)
+    B, H, T, D = q.shape
+    M = k.shape[2]
+    tq = _like_rows(tq, q, T, "tq")
+    tk = _like_rows(tk, q, M, "tk")
+    tv = _like_rows(tv, q, M, "tv")
+    if o is not None:
+        if o.dtype != q.dtype:
+            o = None  # a float32 O of a low-precision op: rebuild it at full precision instead
+        else:
+            o = _rowmajor(o)
+    lse = lse.contiguous()
+    dev = q.device
+    out = torch.empty((B, H, T, D), dtype=q.dtype, device=dev)
+    lib = _lib.load()
+    prob = _problem(q, k, scale, causal)
+    with torch.cuda.device(dev):
+        rc = lib.theria_sdpa_jvp(
+            ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(o), _fp(lse), _tv(tq), _tv(tk), _tv(tv), _tv(out),
+            _stream(dev),
+        )
+    _lib.check(rc, "theria_sdpa_jvp")
+    return out
+
+
+def bwd_bwd(q, k, v, o, do, lse, delta, gq, gk, gv, scale: float, causal: bool):
+    """(G_Q, G_K, G_V, G_dO): VJP of the backward map with cotangents (gq, gk, gv) (None = zero)."""
+    check_inputs(q, k, v)
+    q, k, v = _rowmajor(q), _rowmajor(k), _rowmajor(v)
+    B, H, T, D = q.shape
+    M = k.shape[2]
+    do = _like_rows(do, q, T, "dout")
+    gq = _like_rows(gq, q, T, "gq")
+    gk = _like_rows(gk, q, M, "gk")
+    gv = _like_rows(gv, q, M, "gv")
+    if o is not None:
+        o = _rowmajor(o) if o.dtype == q.dtype else None
+    lse = lse.contiguous()
+    delta = delta.contiguous()
+    dev = q.device
+    out_q = torch.empty((B, H, T, D), dtype=q.dtype, device=dev)
+    out_k = torch.empty((B, H, M, D), dtype=q.dtype, device=dev)
+    out_v = torch.empty((B, H, M, D), dtype=q.dtype, device=dev)
+    out_do = torch.empty((B, H, T, D), dtype=q.dtype, device=dev)
+    ws = torch.empty((2 * B * H * T,), dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    prob = _problem(q, k, scale, causal)
+    with torch.cuda.device(dev):
+        rc = lib.theria_sdpa_bwd_bwd(
+            ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(o), _tv(do), _fp(lse), _fp(delta), _tv(gq), _tv(gk),
+            _tv(gv), _tv(out_q), _tv(out_k), _tv(out_v), _tv(out_do), _fp(ws), _stream(dev),
+        )
+    _lib.check(rc, "theria_sdpa_bwd_bwd")
+    return out_q, out_k, out_v, out_do

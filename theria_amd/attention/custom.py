@@ -1,0 +1,59 @@
+"""sdpa_custom: theria's backend-string dispatcher (theria/attention/custom.py:15-71), the drop-in boundary.
+
+Backends:
+  "reference"                                  pure-PyTorch softmax attention (any order of derivative)
+  "custom"                                     SDPACustom (autograd-in-backward, any order)
+  "triton_full_fused", "triton_full_fused_phase8"
+                                               the gfx950 HIP operator (names kept for drop-in
+                                               compatibility; no Triton underneath), output in q.dtype
+  "hip", "hip_fused"                           the same HIP operator under its own name
+  "triton_qk", "triton_ref", "triton", "triton_fast", "triton_qk_softmax"
+                                               the reference's partial-fusion QK^T backends: not built
+                                               here yet; they raise NotImplementedError rather than
+                                               silently running something else
+Unknown names raise ValueError (custom.py:57).
+"""
+
+from __future__ import annotations
+
+from ..autograd.hip_sdpa import hip_sdpa
+from ..autograd.sdpa_custom_function import SDPACustom
+from .reference import reference_attention
+
+HIP_BACKENDS = ("triton_full_fused", "triton_full_fused_phase8", "hip", "hip_fused")
+PARTIAL_FUSION_BACKENDS = ("triton_qk", "triton_ref", "triton", "triton_fast", "triton_qk_softmax")
+
+
+def sdpa_custom(q, k, v, *, backend: str = "reference", causal: bool = False):
+    """Attention output (B,H,T,Dv) through the named backend. causal is honoured by the HIP backends."""
+    if backend == "reference":
+        if causal:
+            raise AssertionError("the reference backend has no causal mask; use a HIP backend")
+        return reference_attention(q, k, v)
+    if backend == "custom":
+        if causal:
+            raise AssertionError("the custom backend has no causal mask; use a HIP backend")
+        return SDPACustom.apply(q, k, v)
+    if backend in HIP_BACKENDS:
+        if q.shape[-1] != v.shape[-1]:
+            raise AssertionError(f"{backend} requires Dv == D")
+        return hip_sdpa(q, k, v, causal=causal).to(q.dtype)
+    if backend in PARTIAL_FUSION_BACKENDS:
+        raise NotImplementedError(
+            f"sdpa_custom backend {backend!r} (partial-fusion QK^T kernel) is not implemented in theria_amd; "
+            "use 'triton_full_fused' / 'hip' for the fused HIP operator"
+        )
+    raise ValueError(f"Unsupported sdpa_custom backend: {backend}")
+
+
+def sdpa_custom_hvp(q, k, v, dq, dk, dv):
+    """Explicit HVP of sum(O) for the custom backend (test/debug helper)."""
+    return SDPACustom.hvp(q, k, v, dq, dk, dv)
+
+
+def sdpa_custom_jvp(q, k, v, dq, dk, dv):
+    """Explicit JVP for the custom backend (test/debug helper)."""
+    return SDPACustom.jvp(q, k, v, dq, dk, dv)
+
+
+__all__ = ["sdpa_custom", "sdpa_custom_hvp", "sdpa_custom_jvp", "HIP_BACKENDS"]

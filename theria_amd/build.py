@@ -1,0 +1,85 @@
+"""Build libtheria_sdpa.so (the gfx950 HIP kernels + C ABI) in-tree.
+
+Usage: ``python -m theria_amd.build`` (or ``theria_amd.build.build()``). Every ``csrc/*.hip`` file is
+compiled for gfx950 in parallel into ``_build/`` at the repository root and linked into
+``theria_amd/lib/libtheria_sdpa.so``. The library links against the HIP runtime by its soname
+(libamdhip64.so.7), so inside a process that already imported torch it binds to the runtime torch
+loaded: one HIP runtime per process.
+"""
+
+from __future__ import annotations
+
+import concurrent.futures as _cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+REPO_DIR = PKG_DIR.parent
+CSRC = PKG_DIR / "csrc"
+LIB_DIR = PKG_DIR / "lib"
+LIB_PATH = LIB_DIR / "libtheria_sdpa.so"
+BUILD_DIR = REPO_DIR / "_build"
+
+ARCH = "gfx950"
+COMMON_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-fvisibility=hidden",
+    "-mcode-object-version=5",
+    # Packed float32 VALU ops (v_pk_fma_f32 and friends) are kept out of the generated code.
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+    f"-I{REPO_DIR / 'include'}",
+]
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found: the HIP toolchain is required to build libtheria_sdpa.so")
+
+
+def _compile(hipcc: str, src: Path) -> Path:
+    obj = BUILD_DIR / (src.stem + ".o")
+    cmd = [hipcc, *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}")
+    return obj
+
+
+def build(verbose: bool = True, jobs: int | None = None) -> Path:
+    """Compile every kernel source and link the shared library. Always rebuilds."""
+    hipcc = _hipcc()
+    BUILD_DIR.mkdir(parents=True, exist_ok=True)
+    LIB_DIR.mkdir(parents=True, exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+    if not sources:
+        raise RuntimeError(f"no HIP sources under {CSRC}")
+    jobs = jobs or min(len(sources), max(1, (os.cpu_count() or 4)))
+    if verbose:
+        print(f"[theria_amd.build] compiling {len(sources)} sources for {ARCH} with {jobs} jobs", flush=True)
+    with _cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(lambda s: _compile(hipcc, s), sources))
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed: {' '.join(cmd)}\n{res.stdout}")
+    os.replace(tmp, LIB_PATH)
+    if verbose:
+        print(f"[theria_amd.build] built {LIB_PATH}", flush=True)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    build()
+    sys.exit(0)

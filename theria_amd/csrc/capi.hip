@@ -1,0 +1,341 @@
+// C ABI of libtheria_sdpa.so (declared in include/theria_sdpa.h): argument validation, launch
+// sequencing and error reporting. No device memory is allocated here.
+#include <cmath>
+#include <cstdio>
+#include <string>
+
+#include "../../include/theria_sdpa.h"
+#include "sdpa_params.hpp"
+
+#define THERIA_API extern "C" __attribute__((visibility("default")))
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+struct Checker {
+  std::string err;
+  bool vec = true;
+  int vec_elems = 8;
+  bool q_rows = true;  // the query-side tensors hold at least one element (B*H*T > 0)
+  bool k_rows = true;  // the key-side tensors hold at least one element (B*H*M > 0)
+  explicit Checker(const theria::Shape& s)
+      : vec_elems(s.dtype == THERIA_DTYPE_F32 ? 4 : 8),
+        q_rows((int64_t)s.B * s.H * s.T > 0),
+        k_rows((int64_t)s.B * s.H * s.M > 0) {}
+  void need(bool ok, const char* msg) {
+    if (!ok && err.empty()) err = msg;
+  }
+  // A tensor with no elements needs no storage: it is only required when its rows exist.
+  void qview(const theria_tensor_t* t, const char* name, bool required) { view(t, name, required && q_rows); }
+  void kview(const theria_tensor_t* t, const char* name, bool required) { view(t, name, required && k_rows); }
+  void view(const theria_tensor_t* t, const char* name, bool required) {
+    if (!t || !t->data) {
+      if (required && err.empty()) err = std::string(name) + " is required";
+      return;
+    }
+    if (t->stride_b < 0 || t->stride_h < 0 || t->stride_row < 0) {
+      if (err.empty()) err = std::string(name) + " has a negative stride";
+      return;
+    }
+    if (reinterpret_cast<uintptr_t>(t->data) % 16 != 0) vec = false;
+    if (t->stride_b % vec_elems || t->stride_h % vec_elems || t->stride_row % vec_elems) vec = false;
+  }
+};
+
+bool shape_from(const theria_sdpa_problem_t* p, theria::Shape& s, std::string& err) {
+  if (!p) {
+    err = "problem descriptor is NULL";
+    return false;
+  }
+  if (p->dtype < THERIA_DTYPE_F32 || p->dtype > THERIA_DTYPE_BF16) {
+    err = "Unsupported dtype (expected float32, float16 or bfloat16)";
+    return false;
+  }
+  if (p->batch < 0 || p->heads < 0 || p->tq < 0 || p->tk < 0) {
+    err = "negative batch, heads, tq or tk";
+    return false;
+  }
+  if (p->head_dim < 1 || p->head_dim > 128) {
+    err = "head_dim must be in [1, 128]";
+    return false;
+  }
+  if (!(std::isfinite(p->scale) && p->scale > 0.f)) {
+    err = "scale must be finite and positive";
+    return false;
+  }
+  s.B = p->batch;
+  s.H = p->heads;
+  s.T = p->tq;
+  s.M = p->tk;
+  s.D = p->head_dim;
+  s.scale = p->scale;
+  s.causal = p->causal != 0;
+  s.dtype = p->dtype;
+  s.dp = p->head_dim <= 32 ? 32 : (p->head_dim <= 64 ? 64 : 128);
+  s.vec = true;
+  return true;
+}
+
+theria::View cv(const theria_tensor_t* t) {
+  if (!t || !t->data) return theria::View{nullptr, 0, 0, 0};
+  return theria::View{t->data, t->stride_b, t->stride_h, t->stride_row};
+}
+theria::MutView mv(const theria_tensor_t* t) {
+  if (!t || !t->data) return theria::MutView{nullptr, 0, 0, 0};
+  return theria::MutView{t->data, t->stride_b, t->stride_h, t->stride_row};
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return THERIA_OK;
+  return fail(THERIA_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+bool empty_problem(const theria::Shape& s) { return s.B == 0 || s.H == 0 || s.T == 0; }
+
+}  // namespace
+
+THERIA_API int theria_abi_version(void) { return THERIA_SDPA_ABI_VERSION; }
+
+THERIA_API const char* theria_last_error(void) { return g_last_error.c_str(); }
+
+THERIA_API int theria_sdpa_fwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
+                               const theria_tensor_t* v, const theria_tensor_t* o, int32_t o_is_f32, float* lse,
+                               float* row_max, float* row_sum, void* stream) {
+  theria::Shape s;
+  std::string err;
+  if (!shape_from(p, s, err)) return fail(THERIA_ERR_CONTRACT, err);
+  Checker c(s);
+  c.qview(q, "q", true);
+  c.kview(k, "k", true);
+  c.kview(v, "v", true);
+  c.qview(o, "o", true);
+  c.need(lse != nullptr || !c.q_rows, "lse is required");
+  if (o_is_f32 && o && (o->stride_b % 4 || o->stride_h % 4 || o->stride_row % 4)) c.vec = false;
+  if (!c.err.empty()) return fail(THERIA_ERR_CONTRACT, c.err);
+  s.vec = c.vec;
+  if (empty_problem(s)) return THERIA_OK;
+  theria::FwdParams fp{};
+  fp.s = s;
+  fp.q = cv(q);
+  fp.k = cv(k);
+  fp.v = cv(v);
+  fp.o = mv(o);
+  fp.o_f32 = o_is_f32 != 0;
+  fp.lse = lse;
+  fp.row_max = row_max;
+  fp.row_sum = row_sum;
+  return hip_status(theria::launch_fwd(fp, 0, (hipStream_t)stream), "theria_sdpa_fwd");
+}
+
+static int run_bwd_main(const theria::Shape& s, const theria_tensor_t* q, const theria_tensor_t* k,
+                        const theria_tensor_t* v, const theria_tensor_t* dout, const float* lse, const float* delta,
+                        const theria_tensor_t* dq, const theria_tensor_t* dk, const theria_tensor_t* dv,
+                        float* dq_accum, bool dv_only, hipStream_t st) {
+  theria::BwdParams bp{};
+  bp.s = s;
+  bp.q = cv(q);
+  bp.k = cv(k);
+  bp.v = cv(v);
+  bp.dout = cv(dout);
+  bp.lse = lse;
+  bp.delta = delta;
+  bp.dk = mv(dk);
+  bp.dv = mv(dv);
+  bp.dq_accum = dq_accum;
+  bp.dv_only = dv_only;
+  bp.want_dq = !dv_only && dq && dq->data;
+  bp.want_dk = !dv_only && dk && dk->data;
+  int rc = hip_status(theria::launch_bwd(bp, st), "theria_sdpa_bwd");
+  if (rc != THERIA_OK || !bp.want_dq) return rc;
+  theria::DqParams dp{};
+  dp.s = s;
+  dp.dq_accum = dq_accum;
+  dp.dq = mv(dq);
+  return hip_status(theria::launch_dq_convert(dp, st), "theria_sdpa_bwd (dq)");
+}
+
+THERIA_API int theria_sdpa_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
+                               const theria_tensor_t* v, const theria_tensor_t* o, int32_t o_is_f32,
+                               const theria_tensor_t* dout, const float* lse, float* delta_out,
+                               const theria_tensor_t* dq, const theria_tensor_t* dk, const theria_tensor_t* dv,
+                               float* dq_accum, void* stream) {
+  theria::Shape s;
+  std::string err;
+  if (!shape_from(p, s, err)) return fail(THERIA_ERR_CONTRACT, err);
+  Checker c(s);
+  c.qview(q, "q", true);
+  c.kview(k, "k", true);
+  c.kview(v, "v", true);
+  c.qview(o, "o", true);
+  c.qview(dout, "dout", true);
+  c.qview(dq, "dq", false);
+  c.kview(dk, "dk", false);
+  c.kview(dv, "dv", true);
+  c.need(lse != nullptr || !c.q_rows, "lse is required");
+  c.need(delta_out != nullptr || !c.q_rows, "delta_out is required");
+  c.need(!(dq && dq->data) || dq_accum != nullptr || !c.q_rows, "dq_accum is required when dq is requested");
+  if (!c.err.empty()) return fail(THERIA_ERR_CONTRACT, c.err);
+  s.vec = c.vec;
+  if (s.B == 0 || s.H == 0) return THERIA_OK;
+  const hipStream_t st = (hipStream_t)stream;
+  const bool want_dq = dq && dq->data;
+  if (s.T > 0) {
+    theria::PreParams pp{};
+    pp.s = s;
+    pp.o = cv(o);
+    pp.dout = cv(dout);
+    pp.o_f32 = o_is_f32 != 0;
+    pp.delta = delta_out;
+    pp.dq_accum = want_dq ? dq_accum : nullptr;
+    int rc = hip_status(theria::launch_bwd_pre(pp, st), "theria_sdpa_bwd (delta)");
+    if (rc != THERIA_OK) return rc;
+  }
+  return run_bwd_main(s, q, k, v, dout, lse, delta_out, dq, dk, dv, dq_accum, false, st);
+}
+
+THERIA_API int theria_sdpa_bwd_from_stats(const theria_sdpa_problem_t* p, const theria_tensor_t* q,
+                                          const theria_tensor_t* k, const theria_tensor_t* v,
+                                          const theria_tensor_t* dout, const float* lse, float* delta_out,
+                                          const theria_tensor_t* dq, const theria_tensor_t* dk,
+                                          const theria_tensor_t* dv, float* dq_accum, void* stream) {
+  theria::Shape s;
+  std::string err;
+  if (!shape_from(p, s, err)) return fail(THERIA_ERR_CONTRACT, err);
+  const bool dv_only = !(v && v->data) && (int64_t)s.B * s.H * s.M > 0;
+  Checker c(s);
+  c.qview(q, "q", true);
+  c.kview(k, "k", true);
+  c.kview(v, "v", false);
+  c.qview(dout, "dout", true);
+  c.qview(dq, "dq", false);
+  c.kview(dk, "dk", false);
+  c.kview(dv, "dv", true);
+  c.need(lse != nullptr || !c.q_rows, "lse is required");
+  c.need(dv_only || delta_out != nullptr || !c.q_rows, "delta_out is required");
+  c.need(!dv_only || !((dq && dq->data) || (dk && dk->data)), "dq and dk need v");
+  c.need(!(dq && dq->data) || dq_accum != nullptr || !c.q_rows, "dq_accum is required when dq is requested");
+  if (!c.err.empty()) return fail(THERIA_ERR_CONTRACT, c.err);
+  s.vec = c.vec;
+  if (s.B == 0 || s.H == 0) return THERIA_OK;
+  const hipStream_t st = (hipStream_t)stream;
+  if (!dv_only && s.T > 0) {
+    theria::FwdParams fp{};
+    fp.s = s;
+    fp.q = cv(q);
+    fp.k = cv(k);
+    fp.v = cv(v);
+    fp.dout = cv(dout);
+    fp.lse = const_cast<float*>(lse);
+    fp.delta = delta_out;
+    fp.dq_accum = (dq && dq->data) ? dq_accum : nullptr;
+    int rc = hip_status(theria::launch_fwd(fp, 1, st), "theria_sdpa_bwd_from_stats (delta)");
+    if (rc != THERIA_OK) return rc;
+  }
+  return run_bwd_main(s, q, k, v, dout, lse, delta_out, dq, dk, dv, dq_accum, dv_only, st);
+}
+
+THERIA_API int theria_sdpa_jvp(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
+                               const theria_tensor_t* v, const theria_tensor_t* o, const float* lse,
+                               const theria_tensor_t* tq, const theria_tensor_t* tk, const theria_tensor_t* tv,
+                               const theria_tensor_t* tout, void* stream) {
+  theria::Shape s;
+  std::string err;
+  if (!shape_from(p, s, err)) return fail(THERIA_ERR_CONTRACT, err);
+  Checker c(s);
+  c.qview(q, "q", true);
+  c.kview(k, "k", true);
+  c.kview(v, "v", true);
+  c.qview(o, "o", false);
+  c.qview(tq, "tq", false);
+  c.kview(tk, "tk", false);
+  c.kview(tv, "tv", false);
+  c.qview(tout, "tout", true);
+  c.need(lse != nullptr || !c.q_rows, "lse is required");
+  if (!c.err.empty()) return fail(THERIA_ERR_CONTRACT, c.err);
+  s.vec = c.vec;
+  if (empty_problem(s)) return THERIA_OK;
+  theria::JvpParams jp{};
+  jp.s = s;
+  jp.q = cv(q);
+  jp.k = cv(k);
+  jp.v = cv(v);
+  jp.o = cv(o);
+  jp.tq = cv(tq);
+  jp.tk = cv(tk);
+  jp.tv = cv(tv);
+  jp.lse = lse;
+  jp.tout = mv(tout);
+  return hip_status(theria::launch_jvp(jp, (hipStream_t)stream), "theria_sdpa_jvp");
+}
+
+THERIA_API int theria_sdpa_bwd_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
+                                   const theria_tensor_t* v, const theria_tensor_t* o, const theria_tensor_t* dout,
+                                   const float* lse, const float* delta, const theria_tensor_t* gq,
+                                   const theria_tensor_t* gk, const theria_tensor_t* gv, const theria_tensor_t* out_gq,
+                                   const theria_tensor_t* out_gk, const theria_tensor_t* out_gv,
+                                   const theria_tensor_t* out_gdout, float* row_ws, void* stream) {
+  theria::Shape s;
+  std::string err;
+  if (!shape_from(p, s, err)) return fail(THERIA_ERR_CONTRACT, err);
+  Checker c(s);
+  c.qview(q, "q", true);
+  c.kview(k, "k", true);
+  c.kview(v, "v", true);
+  c.qview(o, "o", false);
+  c.qview(dout, "dout", true);
+  c.qview(gq, "gq", false);
+  c.kview(gk, "gk", false);
+  c.kview(gv, "gv", false);
+  c.qview(out_gq, "out_gq", true);
+  c.kview(out_gk, "out_gk", true);
+  c.kview(out_gv, "out_gv", true);
+  c.qview(out_gdout, "out_gdout", true);
+  c.need(lse != nullptr || !c.q_rows, "lse is required");
+  c.need(delta != nullptr || !c.q_rows, "delta is required");
+  c.need(row_ws != nullptr || !c.q_rows, "row_ws is required");
+  if (!c.err.empty()) return fail(THERIA_ERR_CONTRACT, c.err);
+  s.vec = c.vec;
+  if (s.B == 0 || s.H == 0) return THERIA_OK;
+  const hipStream_t st = (hipStream_t)stream;
+  const int64_t nrows = (int64_t)s.B * s.H * s.T;
+  theria::BwdBwdParams bp{};
+  bp.s = s;
+  bp.q = cv(q);
+  bp.k = cv(k);
+  bp.v = cv(v);
+  bp.dout = cv(dout);
+  bp.gq = cv(gq);
+  bp.gk = cv(gk);
+  bp.gv = cv(gv);
+  bp.lse = lse;
+  bp.delta = delta;
+  bp.r_row = row_ws;
+  bp.t_row = row_ws + nrows;
+  bp.out_gq = mv(out_gq);
+  bp.out_gk = mv(out_gk);
+  bp.out_gv = mv(out_gv);
+  if (s.T > 0) {
+    int rc = hip_status(theria::launch_bwdbwd_rows(bp, st), "theria_sdpa_bwd_bwd (rows)");
+    if (rc != THERIA_OK) return rc;
+  }
+  int rc = hip_status(theria::launch_bwdbwd_cols(bp, st), "theria_sdpa_bwd_bwd (cols)");
+  if (rc != THERIA_OK || s.T == 0) return rc;
+  theria::JvpParams jp{};
+  jp.s = s;
+  jp.q = cv(q);
+  jp.k = cv(k);
+  jp.v = cv(v);
+  jp.o = cv(o);
+  jp.tq = cv(gq);
+  jp.tk = cv(gk);
+  jp.tv = cv(gv);
+  jp.lse = lse;
+  jp.tout = mv(out_gdout);
+  return hip_status(theria::launch_jvp(jp, st), "theria_sdpa_bwd_bwd (dout)");
+}

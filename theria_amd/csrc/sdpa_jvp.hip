@@ -1,0 +1,181 @@
+// Frozen-stats SDPA JVP for gfx950.
+//
+// Replaces the eager sdpa_jvp of the reference (theria/attention/triton_sdpa_backward.py:465-503),
+// which materialises several (B,H,T,M) float32 tensors. Contract (docs/phase9.md:30-39): P is rebuilt
+// from the saved row statistics and held fixed, and with tangents (tq, tk, tv)
+//   G = scale (tq K^T + Q tk^T),  c_i = sum_j P_ij G_ij,
+//   tO = P o (G - c) V + P tv = (P o G) V - c o O + P tv,
+// where O = P V (the saved forward output, or rebuilt in the same pass when it is not supplied).
+// The same kernel yields the G_dO output of the double backward (tangents = cotangents of dQ, dK, dV).
+//
+// Work decomposition as in the forward: one workgroup = 4 waves = 128 query rows, lane per query in
+// the transposed score tiles S^T = K Q^T and G^T = K tq^T + tk Q^T (Q and tq stay in registers as B
+// operands); per 64-key tile, K, tk, V, tv are staged in LDS and the three output products
+// (P o G) V, P tv and (if needed) P V accumulate lane-per-query as V^T (.)^T, with V^T / tv^T
+// fragments from the LDS transpose read. A single pass: c_i is folded in at the end.
+#include "dispatch.hpp"
+#include "sdpa_common.hpp"
+
+namespace theria {
+
+template <typename T, int DP, bool CAUSAL, bool HAS_O>
+__global__ __launch_bounds__(256) void jvp_kernel(const JvpParams p) {
+  using MM = Mfma<T>;
+  using F = typename MM::frag_t;
+  constexpr int KC = MM::KC;
+  constexpr int NW = 4, BM = 32 * NW, NT = 64 * NW;
+  constexpr int BN = (DP == 128 || sizeof(T) == 4) ? 32 : 64;  // keys per tile (register budget)
+  constexpr int PITCH = DP + 16 / (int)sizeof(T);
+  constexpr int NDT = DP / 32, NKC = DP / KC, NPC = 32 / KC, NST = BN / 32;
+  __shared__ __attribute__((aligned(16))) T sK[BN * PITCH];
+  __shared__ __attribute__((aligned(16))) T sV[BN * PITCH];
+  __shared__ __attribute__((aligned(16))) T stK[BN * PITCH];
+  __shared__ __attribute__((aligned(16))) T stV[BN * PITCH];
+
+  const Shape& s = p.s;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, li = lane & 31, g = lane >> 5;
+  const int nqb = (s.T + BM - 1) / BM;
+  const int bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int bh = bid / nqb;
+  int qb = bid - bh * nqb;
+  if (CAUSAL) qb = nqb - 1 - qb;
+  const int b = bh / s.H, h = bh - b * s.H;
+  const T* Q = (const T*)p.q.p + b * p.q.sb + h * p.q.sh;
+  const T* K = (const T*)p.k.p + b * p.k.sb + h * p.k.sh;
+  const T* V = (const T*)p.v.p + b * p.v.sb + h * p.v.sh;
+  const bool has_tq = p.tq.p != nullptr, has_tk = p.tk.p != nullptr, has_tv = p.tv.p != nullptr;
+  const T* TQ = has_tq ? (const T*)p.tq.p + b * p.tq.sb + h * p.tq.sh : nullptr;
+  const T* TK = has_tk ? (const T*)p.tk.p + b * p.tk.sb + h * p.tk.sh : nullptr;
+  const T* TV = has_tv ? (const T*)p.tv.p + b * p.tv.sb + h * p.tv.sh : nullptr;
+  const int q0w = qb * BM + wave * 32;
+  const int myq = q0w + li;
+  const bool qvalid = myq < s.T;
+  const int64_t row_id = (int64_t)bh * s.T + myq;
+
+  F qf[NKC], tqf[NKC];
+#pragma unroll
+  for (int c = 0; c < NKC; ++c) {
+    qf[c] = gload_frag<T>(Q, p.q.sr, myq, s.T, c, s.D, s.vec);
+    tqf[c] = has_tq ? gload_frag<T>(TQ, p.tq.sr, myq, s.T, c, s.D, s.vec) : F{};
+  }
+  f32x16_t accA[NDT], accC[NDT], accO[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) {
+    accA[dt] = zero16();
+    accC[dt] = zero16();
+    accO[dt] = zero16();
+  }
+  const float c2 = s.scale * kLog2e;
+  const float lse2 = qvalid ? p.lse[row_id] * kLog2e : THERIA_INF;
+  const float moff = lse2 == -THERIA_INF ? THERIA_INF : lse2;  // a row without visible keys has P = 0
+  float cpart = 0.f;
+
+  int kend = s.M;
+  if (CAUSAL) kend = min(s.M, qb * BM + BM);
+  const int nkt = (kend + BN - 1) / BN;
+  TileStage<T, BN, DP, NT> gK, gV, gtK, gtV;
+  auto prefetch = [&](int k0) {
+    gK.load(K, p.k.sr, k0, s.M, s.D, s.vec);
+    gV.load(V, p.v.sr, k0, s.M, s.D, s.vec);
+    if (has_tk) gtK.load(TK, p.tk.sr, k0, s.M, s.D, s.vec);
+    if (has_tv) gtV.load(TV, p.tv.sr, k0, s.M, s.D, s.vec);
+  };
+  if (nkt > 0) prefetch(0);
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int k0 = kt * BN;
+    __syncthreads();
+    gK.store(sK, PITCH);
+    gV.store(sV, PITCH);
+    if (has_tk) gtK.store(stK, PITCH);
+    if (has_tv) gtV.store(stV, PITCH);
+    __syncthreads();
+    if (kt + 1 < nkt) prefetch(k0 + BN);
+    if (CAUSAL && k0 > q0w + 31) continue;
+
+    f32x16_t sc[NST], gm[NST];
+#pragma unroll
+    for (int t = 0; t < NST; ++t) {
+      sc[t] = zero16();
+      gm[t] = zero16();
+#pragma unroll
+      for (int c = 0; c < NKC; ++c) {
+        const F kfr = lds_cols<T, KLIN>(sK, PITCH, t * 32 + li, 0, c);
+        sc[t] = MM::mma(kfr, qf[c], sc[t]);
+        if (has_tq) gm[t] = MM::mma(kfr, tqf[c], gm[t]);
+        if (has_tk) gm[t] = MM::mma(lds_cols<T, KLIN>(stK, PITCH, t * 32 + li, 0, c), qf[c], gm[t]);
+      }
+    }
+    const bool need_mask = (k0 + BN > s.M) || (CAUSAL && k0 + BN - 1 > q0w);
+#pragma unroll
+    for (int t = 0; t < NST; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float pv = fast_exp2(fmaf(sc[t][r], c2, -moff));
+        if (need_mask) {
+          const int key = k0 + t * 32 + acc_row(r, g);
+          if (key >= s.M || (CAUSAL && key > myq)) pv = 0.f;
+        }
+        sc[t][r] = pv;
+        const float pg = pv * gm[t][r];
+        gm[t][r] = pg;
+        cpart += pg;
+      }
+#pragma unroll
+    for (int t = 0; t < NST; ++t)
+#pragma unroll
+      for (int cc = 0; cc < NPC; ++cc) {
+        const F pf = acc_frag<T>(sc[t], cc);
+        const F pgf = acc_frag<T>(gm[t], cc);
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+          const F vfr = lds_rows<T, KACC>(sV, PITCH, t * 32, cc, dt * 32);
+          accA[dt] = MM::mma(vfr, pgf, accA[dt]);
+          if (!HAS_O) accO[dt] = MM::mma(vfr, pf, accO[dt]);
+          if (has_tv) accC[dt] = MM::mma(lds_rows<T, KACC>(stV, PITCH, t * 32, cc, dt * 32), pf, accC[dt]);
+        }
+      }
+  }
+
+  const float cval = pair_sum(cpart) * s.scale;
+  if (qvalid) {
+    const T* O = HAS_O ? (const T*)p.o.p + b * p.o.sb + h * p.o.sh : nullptr;
+    T* TO = (T*)p.tout.p + b * p.tout.sb + h * p.tout.sh;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const int d0 = dt * 32 + 8 * qd + 4 * g;
+        if (d0 < s.D) {
+          f32x4_t ov;
+          if (HAS_O) {
+            ov = load4<T>(O, p.o.sr, myq, d0, s.D, s.vec);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) ov[e] = accO[dt][4 * qd + e];
+          }
+          float r4[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) r4[e] = s.scale * accA[dt][4 * qd + e] - cval * ov[e] + accC[dt][4 * qd + e];
+          store4<T>(TO, p.tout.sr, myq, d0, s.D, r4[0], r4[1], r4[2], r4[3], s.vec);
+        }
+      }
+  }
+}
+
+template <bool HAS_O>
+struct JvpLauncher {
+  template <typename T, int DP, bool CAUSAL>
+  static hipError_t run(const JvpParams& p, hipStream_t st) {
+    const int nqb = (p.s.T + 127) / 128;
+    const int64_t nblk = (int64_t)nqb * p.s.B * p.s.H;
+    if (nblk == 0) return hipSuccess;
+    hipLaunchKernelGGL((jvp_kernel<T, DP, CAUSAL, HAS_O>), dim3((unsigned)nblk), dim3(256), 0, st, p);
+    return hipGetLastError();
+  }
+};
+
+hipError_t launch_jvp(const JvpParams& p, hipStream_t st) {
+  return p.o.p ? dispatch_all<JvpLauncher<true>>(p, st) : dispatch_all<JvpLauncher<false>>(p, st);
+}
+
+}  // namespace theria
