@@ -1,0 +1,377 @@
+#!/usr/bin/env python
+"""Benchmark of theria_amd's HIP SDPA operator on one MI355X (BASELINE.json metric).
+
+A "step" is one forward + backward pass of the SDPA operator over BASELINE config 2
+(B4 H16 S2048 D64, bfloat16, non-causal, scale 1/8, Q, K, V, dO ~ N(0,1), synthetic, resident in HBM):
+forward kernel (O, lse), then the backward's two kernels (dQ with the row term, then dK/dV). Throughput counts algorithmic FLOPs, FlashAttention convention: 4*B*H*S^2*D forward,
+10*B*H*S^2*D backward (the recomputed QK^T included), 14*B*H*S^2*D per step.
+
+Printed as ONE JSON line (rank 0): value = TFLOP/s of the whole step, plus
+  roofline     the dominant kernel (the backward's dK/dV kernel), its algorithmic FLOPs per launch over
+               its average HIP-event duration, against the dense bf16 MFMA peak; traffic = HBM bytes
+               per launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE runs (profiles/traffic.json);
+  cpu_baseline the CPU oracle (oracle/sdpa_oracle.py, the reference's pure-PyTorch math, float32)
+               timed on a bounded sample of heads of the same workload on this host's cores;
+  extra        the other BASELINE configs: C3 causal long sequence, C4 JVP / HVP ms, C5 MAML.
+One GPU only: --gpus N with N > 1 exits with a message.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "SDPA fwd+bwd TFLOP/s & % MFMA peak, B4 H16 S2048 D64 bf16; JVP/HVP ms"
+# MI355X dense bf16 MFMA peak: 256 CU x 4096 FLOP/clk/CU x 2.4 GHz (no sparsity).
+PEAK_BF16_TFLOPS = 2516.6
+PEAK_FP32_TFLOPS = 157.3
+TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
+
+
+def _args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU-baseline sample")
+    ap.add_argument("--no-extras", action="store_true", help="only the config-2 line (for profiling runs)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (for profiling runs)")
+    ap.add_argument("--copy-calibration", action="store_true", help="run a plain copy of known size (PMC scaling)")
+    return ap.parse_args()
+
+
+def _rand(shape, dtype, dev, seed, std=1.0):
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * std).to(dtype).to(dev)
+
+
+def bench_config2(steps: int, warmup: int):
+    """Timed fwd+bwd steps at config 2; per-kernel HIP-event durations of the three kernels."""
+    import torch
+
+    from theria_amd import _ops
+
+    dev = torch.device("cuda:0")
+    B, H, S, D = 4, 16, 2048, 64
+    dt = torch.bfloat16
+    q, k, v, do = (_rand((B, H, S, D), dt, dev, 100 + i) for i in range(4))
+    scale = 1.0 / math.sqrt(D)
+    prob = _ops._problem(q, k, scale, False)
+    delta = torch.empty((B, H, S), dtype=torch.float32, device=dev)
+    dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+
+    def step(ev=None):
+        if ev:
+            ev[0].record()
+        o, lse, _, _ = _ops.fwd(q, k, v, scale, False)
+        if ev:
+            ev[1].record()
+        _ops.bwd_dq(prob, q, k, v, o, False, do, lse, delta, dq)
+        if ev:
+            ev[2].record()
+        _ops.bwd_dkdv(prob, q, k, v, do, lse, delta, dk, dv)
+        if ev:
+            ev[3].record()
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    # per-kernel durations, measured on the stream the kernels run on (torch's current stream)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+    for e in evs:
+        step(e)
+    torch.cuda.synchronize()
+    fwd_ms = statistics.mean(e[0].elapsed_time(e[1]) for e in evs)
+    dq_ms = statistics.mean(e[1].elapsed_time(e[2]) for e in evs)
+    dkdv_ms = statistics.mean(e[2].elapsed_time(e[3]) for e in evs)
+    unit = B * H * S * S * D
+    return dict(
+        wall_ms=wall * 1e3, fwd_ms=fwd_ms, dq_ms=dq_ms, dkdv_ms=dkdv_ms,
+        flop_step=14 * unit, flop_fwd=4 * unit, flop_bwd=10 * unit,
+        # algorithmic work of each backward kernel: dq = S, dP, dQ products (6 B H S^2 D);
+        # dkdv = S, dP, dV, dK products (8 B H S^2 D); together 14, of which the FA convention counts 10
+        flop_dq=6 * unit, flop_dkdv=8 * unit,
+        B=B, H=H, S=S, D=D,
+    )
+
+
+def cpu_baseline(budget_s: float):
+    """The CPU oracle (float32 fwd + bwd, torch on the host cores) on a bounded sample of config-2 heads."""
+    import torch
+
+    from oracle import sdpa_oracle as O
+
+    S, D = 2048, 64
+    threads = torch.get_num_threads()
+    heads = 0
+    t_total = 0.0
+    while heads < 64 and (t_total < budget_s or heads == 0):
+        g = torch.Generator().manual_seed(200 + heads)
+        q, k, v, do = (torch.randn(1, 1, S, D, generator=g).to(torch.bfloat16).float() for _ in range(4))
+        t0 = time.perf_counter()
+        O.forward(q, k, v, 1 / 8.0, dtype=torch.float32)
+        O.backward(q, k, v, do, 1 / 8.0, dtype=torch.float32)
+        t_total += time.perf_counter() - t0
+        heads += 1
+    flops = 14 * heads * S * S * D
+    return {
+        "value": round(flops / t_total / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{heads} of the 64 (batch, head) slices of config 2 (S2048 D64), fp32 fwd+bwd via the CPU "
+        f"oracle, {t_total:.1f} s; cpu={_cpu_model()}",
+    }
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _time(fn, reps: int, warm: int = 3) -> float:
+    import torch
+
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / reps * 1e3
+
+
+def extras_c3():
+    """Config 3: B1 H32 S8192 D128 causal bf16 fwd+bwd; FLOPs over the unmasked triangle."""
+    import torch
+
+    from theria_amd import _ops
+
+    dev = torch.device("cuda:0")
+    B, H, S, D = 1, 32, 8192, 128
+    q, k, v = (_rand((B, H, S, D), torch.bfloat16, dev, 300 + i, std=0.5) for i in range(3))
+    do = _rand((B, H, S, D), torch.bfloat16, dev, 303)
+    scale = 1 / math.sqrt(D)
+
+    def run():
+        o, lse, _, _ = _ops.fwd(q, k, v, scale, True)
+        _ops.bwd(q, k, v, o, lse, do, scale, True)
+
+    ms = _time(run, 5, 2)
+    useful = 14 * B * H * (S * (S + 1) / 2) * D  # unmasked elements only
+    # tile accounting of the kernels' schedules (forward: 32-query wave tile x 64-key tile, skipped when
+    # the whole tile is above the diagonal; backward: 32-key wave block x 32-query sub-tile)
+    def count(qt, kt):
+        executed = needed = elems = 0
+        for q0 in range(0, S, qt):
+            for k0 in range(0, S, kt):
+                if k0 <= q0 + qt - 1:
+                    executed += 1
+                    needed += 1
+                    elems += qt * kt
+        return executed, needed, elems
+
+    ef, nf, elf = count(32, 64)
+    eb, nb, elb = count(32, 32)
+    unmasked = S * (S + 1) / 2
+    return {
+        "config": "B1 H32 S8192 D128 causal bf16 fwd+bwd",
+        "ms": round(ms, 3),
+        "tflops": round(useful / (ms * 1e-3) / 1e12, 1),
+        "tile_skip_efficiency_fwd": round(nf / ef, 4),
+        "tile_skip_efficiency_bwd": round(nb / eb, 4),
+        "useful_flop_fraction_fwd": round(unmasked / elf, 4),
+        "useful_flop_fraction_bwd": round(unmasked / elb, 4),
+    }
+
+
+def extras_c4():
+    """Config 4: B8 H8 S512 D64; JVP (saved stats) and HVP of 0.5||O - T||^2 (double backward), ms."""
+    import torch
+
+    from theria_amd import _ops
+    from theria_amd.autograd.hip_sdpa import hip_sdpa
+
+    dev = torch.device("cuda:0")
+    B, H, S, D = 8, 8, 512, 64
+    out = {}
+    for dt, name in ((torch.float32, "fp32"), (torch.bfloat16, "bf16")):
+        q, k, v = (_rand((B, H, S, D), dt, dev, 400 + i) for i in range(3))
+        tq, tk, tv = (_rand((B, H, S, D), dt, dev, 410 + i, std=0.1) for i in range(3))
+        T_ = _rand((B, H, S, D), dt, dev, 420)
+        vq, vk, vv = (_rand((B, H, S, D), dt, dev, 430 + i) for i in range(3))
+        o, lse, _, _ = _ops.fwd(q, k, v, 1 / 8.0, False)
+        out[f"jvp_ms_{name}"] = round(_time(lambda: _ops.jvp(q, k, v, o, lse, tq, tk, tv, 1 / 8.0, False), 20), 4)
+        qg, kg, vg = (t.clone().requires_grad_(True) for t in (q, k, v))
+
+        def hvp():
+            o2 = hip_sdpa(qg, kg, vg)
+            loss = 0.5 * ((o2.float() - T_.float()) ** 2).sum()
+            g = torch.autograd.grad(loss, (qg, kg, vg), create_graph=True)
+            dot = sum((a.float() * b.float()).sum() for a, b in zip(g, (vq, vk, vv)))
+            return torch.autograd.grad(dot, (qg, kg, vg))
+
+        out[f"hvp_ms_{name}"] = round(_time(hvp, 10), 4)
+        bb = lambda: _ops.bwd_bwd(q, k, v, o, T_, lse, torch.zeros_like(lse), vq, vk, vv, 1 / 8.0, False)  # noqa: E731
+        out[f"double_backward_kernels_ms_{name}"] = round(_time(bb, 20), 4)
+    unit = B * H * S * S * D
+    out["jvp_tflops_bf16"] = round(10 * unit / (out["jvp_ms_bf16"] * 1e-3) / 1e12, 1)
+    out["config"] = "B8 H8 S512 D64; JVP with saved stats; HVP of 0.5||O-T||^2 via autograd double backward"
+    return out
+
+
+def extras_c5():
+    """Config 5: full vs first-order MAML on the 2-layer 4-head classifier, 16 tasks, 5 inner steps."""
+    import copy
+
+    import torch
+
+    from theria_amd.maml import meta_loss_on_tasks
+    from theria_amd.models import MHAClassifier, MHAConfig
+    from theria_amd.tasks import sample_token_count_task
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    model = MHAClassifier(MHAConfig(), backend="hip").to(dev)
+    g = torch.Generator().manual_seed(0)
+    tasks = [sample_token_count_task(generator=g, device=dev)[0] for _ in range(16)]
+    opt = torch.optim.Adam(model.parameters(), lr=1e-3)
+
+    def meta_step(fo: bool):
+        opt.zero_grad(set_to_none=True)
+        loss = meta_loss_on_tasks(model, tasks, inner_lr=0.4, inner_steps=5, fo=fo)
+        loss.backward()
+        opt.step()
+
+    res = {"config": "MHA 2 layers d64 4 heads, token-count task, 16 tasks 5-shot/15-query, 5 inner SGD @0.4, Adam 1e-3"}
+    for fo in (False, True):
+        ms = _time(lambda: meta_step(fo), 3, 1)
+        res[f"meta_steps_per_s_{'fo' if fo else 'full'}"] = round(1e3 / ms, 3)
+    # meta-gradient agreement with the same weights on the pure-PyTorch reference backend
+    ref = copy.deepcopy(model)
+    ref.set_attention_backend("reference")
+    params_h = list(model.parameters())
+    params_r = list(ref.parameters())
+    gh = torch.autograd.grad(meta_loss_on_tasks(model, tasks[:4], inner_lr=0.4, inner_steps=5), params_h)
+    gr = torch.autograd.grad(meta_loss_on_tasks(ref, tasks[:4], inner_lr=0.4, inner_steps=5), params_r)
+    fh = torch.cat([x.flatten() for x in gh]).double()
+    fr = torch.cat([x.flatten() for x in gr]).double()
+    res["metagrad_rel_l2_vs_reference"] = float((fh - fr).norm() / fr.norm())
+    res["metagrad_cosine_vs_reference"] = float(torch.nn.functional.cosine_similarity(fh, fr, dim=0))
+    return res
+
+
+def copy_calibration():
+    """A plain device copy of 256 MiB (FETCH_SIZE / WRITE_SIZE calibration for rocprofv3 --pmc)."""
+    import torch
+
+    src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_each_way": src.numel() * 4, "launches": 5}), flush=True)
+
+
+def main() -> int:
+    args = _args()
+    if args.gpus != 1:
+        print(
+            f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (SDPA shards over "
+            "batch x heads with no exchange, so the per-GPU figure is the one-GPU run).",
+            file=sys.stderr,
+        )
+        return 2
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        return 1
+    from theria_amd import _lib
+
+    _lib.load()
+    if args.copy_calibration:
+        copy_calibration()
+        return 0
+    r = bench_config2(args.steps, args.warmup)
+    value = r["flop_step"] / (r["wall_ms"] * 1e-3) / 1e12
+    achieved = r["flop_dkdv"] / (r["dkdv_ms"] * 1e-3) / 1e12
+    traffic = None
+    if TRAFFIC_FILE.exists():
+        try:
+            traffic = json.loads(TRAFFIC_FILE.read_text()).get("dkdv_kernel_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["wall_ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "sdpa_fwd_bwd", "batch": 4, "heads": 16, "seq_len": 2048, "head_dim": 64, "causal": False},
+        "mfma_peak_frac": round(value / PEAK_BF16_TFLOPS, 4),
+        "roofline": {
+            "kernel": "dkdv_kernel<bf16,64> (theria_sdpa_bwd_dkdv)",
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": traffic,
+            "flop_per_launch": r["flop_dkdv"],
+            "avg_launch_ms": round(r["dkdv_ms"], 4),
+        },
+        "kernels_ms": {
+            "fwd": round(r["fwd_ms"], 4),
+            "bwd_dq": round(r["dq_ms"], 4),
+            "bwd_dkdv": round(r["dkdv_ms"], 4),
+        },
+        "fwd_tflops": round(r["flop_fwd"] / (r["fwd_ms"] * 1e-3) / 1e12, 1),
+        "bwd_tflops": round(r["flop_bwd"] / ((r["dq_ms"] + r["dkdv_ms"]) * 1e-3) / 1e12, 1),
+        "dq_kernel_tflops": round(r["flop_dq"] / (r["dq_ms"] * 1e-3) / 1e12, 1),
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    if not args.no_extras:
+        extra = {}
+        for name, fn in (("c3", extras_c3), ("c4", extras_c4), ("c5", extras_c5)):
+            try:
+                extra[name] = fn()
+            except Exception as exc:  # an extra must not hide the headline line
+                extra[name] = {"error": f"{type(exc).__name__}: {exc}"}
+        line["extra"] = extra
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define THERIA_SDPA_ABI_VERSION 1
+#define THERIA_SDPA_ABI_VERSION 2
 
 enum theria_dtype { THERIA_DTYPE_F32 = 0, THERIA_DTYPE_F16 = 1, THERIA_DTYPE_BF16 = 2 };
 enum theria_status { THERIA_OK = 0, THERIA_ERR_CONTRACT = 1, THERIA_ERR_HIP = 2 };
@@ -72,24 +72,39 @@ int theria_sdpa_fwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q, co
  * TritonFusedSDPAFunction (triton_qk.py:379-387). The row term z_i = sum_j dP_ij P_ij of the
  * reference (triton_sdpa_backward.py:312-353, 543-585) is computed once as delta_i = dO_i . O_i and
  * written to delta_out (B,H,tq) float32. dout has the input dtype; o may be float32 (o_is_f32).
- * dq / dk may have data == NULL to skip that output. dq_accum is a caller-owned float32 workspace
- * of batch*heads*tq*head_dim elements (contents on entry are ignored).
+ * dq / dk may have data == NULL to skip that output. Deterministic (no atomics, no workspace).
+ * theria_sdpa_bwd = theria_sdpa_bwd_dq followed by theria_sdpa_bwd_dkdv on the same stream.
  */
 int theria_sdpa_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
                     const theria_tensor_t* v, const theria_tensor_t* o, int32_t o_is_f32,
                     const theria_tensor_t* dout, const float* lse, float* delta_out, const theria_tensor_t* dq,
-                    const theria_tensor_t* dk, const theria_tensor_t* dv, float* dq_accum, void* stream);
+                    const theria_tensor_t* dk, const theria_tensor_t* dv, void* stream);
+
+/*
+ * The two kernels of theria_sdpa_bwd, for callers that schedule or time them separately.
+ *  bwd_dq:   dQ. When o has data, delta = rowsum(dO * O) is computed and written to delta;
+ *            when o is absent, delta is read (the row term computed by an earlier call).
+ *            dq may be absent: then only delta is produced.
+ *  bwd_dkdv: dK and dV from delta (dk may be absent).
+ */
+int theria_sdpa_bwd_dq(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
+                       const theria_tensor_t* v, const theria_tensor_t* o, int32_t o_is_f32,
+                       const theria_tensor_t* dout, const float* lse, float* delta, const theria_tensor_t* dq,
+                       void* stream);
+int theria_sdpa_bwd_dkdv(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
+                         const theria_tensor_t* v, const theria_tensor_t* dout, const float* lse,
+                         const float* delta, const theria_tensor_t* dk, const theria_tensor_t* dv, void* stream);
 
 /*
  * Explicit backward from saved statistics only (no O), the reference's sdpa_bwd_* signature
  * (q, k, v, dout, m, l, scale) with lse = m + log(l). The row term is recomputed from P(lse) and V.
  * v may have data == NULL: then only dV is computed (sdpa_bwd_dv takes no v,
- * triton_sdpa_backward.py:194), and dq / dk must be absent. Workspaces as in theria_sdpa_bwd.
+ * triton_sdpa_backward.py:194), and dq / dk must be absent. delta_out receives the row term.
  */
 int theria_sdpa_bwd_from_stats(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
                                const theria_tensor_t* v, const theria_tensor_t* dout, const float* lse,
                                float* delta_out, const theria_tensor_t* dq, const theria_tensor_t* dk,
-                               const theria_tensor_t* dv, float* dq_accum, void* stream);
+                               const theria_tensor_t* dv, void* stream);
 
 /*
  * Frozen-stats JVP: tangent of O along (tq, tk, tv) with P rebuilt from lse.

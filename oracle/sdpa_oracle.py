@@ -34,8 +34,8 @@ import math
 import torch
 
 
-def _f64(*ts):
-    return tuple(None if t is None else t.detach().to("cpu", torch.float64) for t in ts)
+def _f64(*ts, dtype=torch.float64):
+    return tuple(None if t is None else t.detach().to("cpu", dtype) for t in ts)
 
 
 def _scale(q, scale):
@@ -59,9 +59,9 @@ def probs(q, k, scale=None, causal=False):
     return torch.nan_to_num(P, nan=0.0)
 
 
-def forward(q, k, v, scale=None, causal=False):
-    """(O, lse, m, l) in float64. m = row max of scaled scores, l = sum exp(S - m), lse = m + log l."""
-    q, k, v = _f64(q, k, v)
+def forward(q, k, v, scale=None, causal=False, dtype=torch.float64):
+    """(O, lse, m, l) in float64 (or `dtype`). m = row max of scaled scores, l = sum exp(S - m), lse = m + log l."""
+    q, k, v = _f64(q, k, v, dtype=dtype)
     s = _scale(q, scale)
     S = (q @ k.transpose(-2, -1)) * s
     msk = _mask(q.shape[-2], k.shape[-2], causal)
@@ -75,9 +75,9 @@ def forward(q, k, v, scale=None, causal=False):
     return O, lse, m, l
 
 
-def backward(q, k, v, dout, scale=None, causal=False):
+def backward(q, k, v, dout, scale=None, causal=False, dtype=torch.float64):
     """(dQ, dK, dV): dV = P^T dO, dP = dO V^T, z = rowsum(dP P), dS = P (dP - z), dQ = s dS K, dK = s dS^T Q."""
-    q, k, v, dout = _f64(q, k, v, dout)
+    q, k, v, dout = _f64(q, k, v, dout, dtype=dtype)
     s = _scale(q, scale)
     P = probs(q, k, s, causal)
     dv = P.transpose(-2, -1) @ dout

@@ -153,16 +153,29 @@ def bwd(q, k, v, o, lse, do, scale: float, causal: bool, need_dq: bool = True, n
     dq = torch.empty((B, H, T, D), dtype=q.dtype, device=dev) if need_dq else None
     dk = torch.empty((B, H, M, D), dtype=q.dtype, device=dev) if need_dk else None
     dv = torch.empty((B, H, M, D), dtype=q.dtype, device=dev)
-    acc = torch.empty((B, H, T, D), dtype=torch.float32, device=dev) if need_dq else None
-    lib = _lib.load()
     prob = _problem(q, k, scale, causal)
     with torch.cuda.device(dev):
-        rc = lib.theria_sdpa_bwd(
-            ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(o), 1 if o_f32 else 0, _tv(do), _fp(lse), _fp(delta),
-            _tv(dq), _tv(dk), _tv(dv), _fp(acc), _stream(dev),
-        )
-    _lib.check(rc, "theria_sdpa_bwd")
+        bwd_dq(prob, q, k, v, o, o_f32, do, lse, delta, dq)
+        bwd_dkdv(prob, q, k, v, do, lse, delta, dk, dv)
     return dq, dk, dv, delta
+
+
+# The two backward kernels (theria_sdpa_bwd = bwd_dq then bwd_dkdv), on the current stream of the
+# current device. Arguments are already validated and laid out by bwd().
+def bwd_dq(prob, q, k, v, o, o_f32, do, lse, delta, dq) -> None:
+    """dQ; with o given, delta = rowsum(dO * O) is computed and written, else it is read."""
+    rc = _lib.load().theria_sdpa_bwd_dq(
+        ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(o), 1 if o_f32 else 0, _tv(do), _fp(lse), _fp(delta),
+        _tv(dq), _stream(q.device),
+    )
+    _lib.check(rc, "theria_sdpa_bwd_dq")
+
+
+def bwd_dkdv(prob, q, k, v, do, lse, delta, dk, dv) -> None:
+    rc = _lib.load().theria_sdpa_bwd_dkdv(
+        ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(do), _fp(lse), _fp(delta), _tv(dk), _tv(dv), _stream(q.device)
+    )
+    _lib.check(rc, "theria_sdpa_bwd_dkdv")
 
 
 def bwd_from_stats(q, k, v, do, lse, scale: float, causal: bool, need_dq: bool, need_dk: bool, need_dv: bool):
@@ -179,13 +192,12 @@ def bwd_from_stats(q, k, v, do, lse, scale: float, causal: bool, need_dq: bool, 
     dq = torch.empty((B, H, T, D), dtype=q.dtype, device=dev) if need_dq else None
     dk = torch.empty((B, H, M, D), dtype=q.dtype, device=dev) if need_dk else None
     dv = torch.empty((B, H, M, D), dtype=q.dtype, device=dev)
-    acc = torch.empty((B, H, T, D), dtype=torch.float32, device=dev) if need_dq else None
     lib = _lib.load()
     prob = _problem(q, k, scale, causal)
     with torch.cuda.device(dev):
         rc = lib.theria_sdpa_bwd_from_stats(
             ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(do), _fp(lse), _fp(delta), _tv(dq), _tv(dk), _tv(dv),
-            _fp(acc), _stream(dev),
+            _stream(dev),
         )
     _lib.check(rc, "theria_sdpa_bwd_from_stats")
     return dq, dk, (dv if need_dv else None)

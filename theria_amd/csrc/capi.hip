@@ -133,38 +133,90 @@ THERIA_API int theria_sdpa_fwd(const theria_sdpa_problem_t* p, const theria_tens
   return hip_status(theria::launch_fwd(fp, 0, (hipStream_t)stream), "theria_sdpa_fwd");
 }
 
-static int run_bwd_main(const theria::Shape& s, const theria_tensor_t* q, const theria_tensor_t* k,
-                        const theria_tensor_t* v, const theria_tensor_t* dout, const float* lse, const float* delta,
-                        const theria_tensor_t* dq, const theria_tensor_t* dk, const theria_tensor_t* dv,
-                        float* dq_accum, bool dv_only, hipStream_t st) {
-  theria::BwdParams bp{};
-  bp.s = s;
-  bp.q = cv(q);
-  bp.k = cv(k);
-  bp.v = cv(v);
-  bp.dout = cv(dout);
-  bp.lse = lse;
-  bp.delta = delta;
-  bp.dk = mv(dk);
-  bp.dv = mv(dv);
-  bp.dq_accum = dq_accum;
-  bp.dv_only = dv_only;
-  bp.want_dq = !dv_only && dq && dq->data;
-  bp.want_dk = !dv_only && dk && dk->data;
-  int rc = hip_status(theria::launch_bwd(bp, st), "theria_sdpa_bwd");
-  if (rc != THERIA_OK || !bp.want_dq) return rc;
+static int run_dq(const theria::Shape& s, const theria_tensor_t* q, const theria_tensor_t* k,
+                  const theria_tensor_t* v, const theria_tensor_t* o, bool o_f32, const theria_tensor_t* dout,
+                  const float* lse, float* delta, const theria_tensor_t* dq, hipStream_t st) {
   theria::DqParams dp{};
   dp.s = s;
-  dp.dq_accum = dq_accum;
+  dp.q = cv(q);
+  dp.k = cv(k);
+  dp.v = cv(v);
+  dp.dout = cv(dout);
+  dp.o = cv(o);
+  dp.o_f32 = o_f32;
+  dp.lse = lse;
+  dp.delta = delta;
   dp.dq = mv(dq);
-  return hip_status(theria::launch_dq_convert(dp, st), "theria_sdpa_bwd (dq)");
+  return hip_status(theria::launch_bwd_dq(dp, st), "theria_sdpa_bwd_dq");
+}
+
+static int run_dkdv(const theria::Shape& s, const theria_tensor_t* q, const theria_tensor_t* k,
+                    const theria_tensor_t* v, const theria_tensor_t* dout, const float* lse, const float* delta,
+                    const theria_tensor_t* dk, const theria_tensor_t* dv, bool dv_only, hipStream_t st) {
+  theria::DkdvParams kp{};
+  kp.s = s;
+  kp.q = cv(q);
+  kp.k = cv(k);
+  kp.v = cv(v);
+  kp.dout = cv(dout);
+  kp.lse = lse;
+  kp.delta = delta;
+  kp.dk = mv(dk);
+  kp.dv = mv(dv);
+  kp.dv_only = dv_only;
+  return hip_status(theria::launch_bwd_dkdv(kp, st), "theria_sdpa_bwd_dkdv");
+}
+
+THERIA_API int theria_sdpa_bwd_dq(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
+                                  const theria_tensor_t* v, const theria_tensor_t* o, int32_t o_is_f32,
+                                  const theria_tensor_t* dout, const float* lse, float* delta,
+                                  const theria_tensor_t* dq, void* stream) {
+  theria::Shape s;
+  std::string err;
+  if (!shape_from(p, s, err)) return fail(THERIA_ERR_CONTRACT, err);
+  Checker c(s);
+  c.qview(q, "q", true);
+  c.kview(k, "k", true);
+  c.kview(v, "v", true);
+  c.qview(o, "o", false);
+  c.qview(dout, "dout", true);
+  c.qview(dq, "dq", false);
+  c.need(lse != nullptr || !c.q_rows, "lse is required");
+  c.need(delta != nullptr || !c.q_rows, "delta is required");
+  if (o_is_f32 && o && (o->stride_b % 4 || o->stride_h % 4 || o->stride_row % 4)) c.vec = false;
+  if (!c.err.empty()) return fail(THERIA_ERR_CONTRACT, c.err);
+  s.vec = c.vec;
+  if (!c.q_rows) return THERIA_OK;
+  return run_dq(s, q, k, v, o, o_is_f32 != 0, dout, lse, delta, dq, (hipStream_t)stream);
+}
+
+THERIA_API int theria_sdpa_bwd_dkdv(const theria_sdpa_problem_t* p, const theria_tensor_t* q,
+                                    const theria_tensor_t* k, const theria_tensor_t* v,
+                                    const theria_tensor_t* dout, const float* lse, const float* delta,
+                                    const theria_tensor_t* dk, const theria_tensor_t* dv, void* stream) {
+  theria::Shape s;
+  std::string err;
+  if (!shape_from(p, s, err)) return fail(THERIA_ERR_CONTRACT, err);
+  Checker c(s);
+  c.qview(q, "q", true);
+  c.kview(k, "k", true);
+  c.kview(v, "v", true);
+  c.qview(dout, "dout", true);
+  c.kview(dk, "dk", false);
+  c.kview(dv, "dv", true);
+  c.need(lse != nullptr || !c.q_rows, "lse is required");
+  c.need(delta != nullptr || !c.q_rows, "delta is required");
+  if (!c.err.empty()) return fail(THERIA_ERR_CONTRACT, c.err);
+  s.vec = c.vec;
+  if (!c.k_rows) return THERIA_OK;
+  return run_dkdv(s, q, k, v, dout, lse, delta, dk, dv, false, (hipStream_t)stream);
 }
 
 THERIA_API int theria_sdpa_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
                                const theria_tensor_t* v, const theria_tensor_t* o, int32_t o_is_f32,
                                const theria_tensor_t* dout, const float* lse, float* delta_out,
                                const theria_tensor_t* dq, const theria_tensor_t* dk, const theria_tensor_t* dv,
-                               float* dq_accum, void* stream) {
+                               void* stream) {
   theria::Shape s;
   std::string err;
   if (!shape_from(p, s, err)) return fail(THERIA_ERR_CONTRACT, err);
@@ -179,31 +231,23 @@ THERIA_API int theria_sdpa_bwd(const theria_sdpa_problem_t* p, const theria_tens
   c.kview(dv, "dv", true);
   c.need(lse != nullptr || !c.q_rows, "lse is required");
   c.need(delta_out != nullptr || !c.q_rows, "delta_out is required");
-  c.need(!(dq && dq->data) || dq_accum != nullptr || !c.q_rows, "dq_accum is required when dq is requested");
+  if (o_is_f32 && o && (o->stride_b % 4 || o->stride_h % 4 || o->stride_row % 4)) c.vec = false;
   if (!c.err.empty()) return fail(THERIA_ERR_CONTRACT, c.err);
   s.vec = c.vec;
-  if (s.B == 0 || s.H == 0) return THERIA_OK;
   const hipStream_t st = (hipStream_t)stream;
-  const bool want_dq = dq && dq->data;
-  if (s.T > 0) {
-    theria::PreParams pp{};
-    pp.s = s;
-    pp.o = cv(o);
-    pp.dout = cv(dout);
-    pp.o_f32 = o_is_f32 != 0;
-    pp.delta = delta_out;
-    pp.dq_accum = want_dq ? dq_accum : nullptr;
-    int rc = hip_status(theria::launch_bwd_pre(pp, st), "theria_sdpa_bwd (delta)");
+  if (c.q_rows) {
+    int rc = run_dq(s, q, k, v, o, o_is_f32 != 0, dout, lse, delta_out, dq, st);
     if (rc != THERIA_OK) return rc;
   }
-  return run_bwd_main(s, q, k, v, dout, lse, delta_out, dq, dk, dv, dq_accum, false, st);
+  if (!c.k_rows) return THERIA_OK;
+  return run_dkdv(s, q, k, v, dout, lse, delta_out, dk, dv, false, st);
 }
 
 THERIA_API int theria_sdpa_bwd_from_stats(const theria_sdpa_problem_t* p, const theria_tensor_t* q,
                                           const theria_tensor_t* k, const theria_tensor_t* v,
                                           const theria_tensor_t* dout, const float* lse, float* delta_out,
                                           const theria_tensor_t* dq, const theria_tensor_t* dk,
-                                          const theria_tensor_t* dv, float* dq_accum, void* stream) {
+                                          const theria_tensor_t* dv, void* stream) {
   theria::Shape s;
   std::string err;
   if (!shape_from(p, s, err)) return fail(THERIA_ERR_CONTRACT, err);
@@ -219,12 +263,11 @@ THERIA_API int theria_sdpa_bwd_from_stats(const theria_sdpa_problem_t* p, const 
   c.need(lse != nullptr || !c.q_rows, "lse is required");
   c.need(dv_only || delta_out != nullptr || !c.q_rows, "delta_out is required");
   c.need(!dv_only || !((dq && dq->data) || (dk && dk->data)), "dq and dk need v");
-  c.need(!(dq && dq->data) || dq_accum != nullptr || !c.q_rows, "dq_accum is required when dq is requested");
   if (!c.err.empty()) return fail(THERIA_ERR_CONTRACT, c.err);
   s.vec = c.vec;
-  if (s.B == 0 || s.H == 0) return THERIA_OK;
   const hipStream_t st = (hipStream_t)stream;
-  if (!dv_only && s.T > 0) {
+  if (!dv_only && c.q_rows) {
+    // row term from P(lse) and V (mode 1 of the forward kernel), then dQ with that delta
     theria::FwdParams fp{};
     fp.s = s;
     fp.q = cv(q);
@@ -233,11 +276,15 @@ THERIA_API int theria_sdpa_bwd_from_stats(const theria_sdpa_problem_t* p, const 
     fp.dout = cv(dout);
     fp.lse = const_cast<float*>(lse);
     fp.delta = delta_out;
-    fp.dq_accum = (dq && dq->data) ? dq_accum : nullptr;
     int rc = hip_status(theria::launch_fwd(fp, 1, st), "theria_sdpa_bwd_from_stats (delta)");
     if (rc != THERIA_OK) return rc;
+    if (dq && dq->data) {
+      rc = run_dq(s, q, k, v, nullptr, false, dout, lse, delta_out, dq, st);
+      if (rc != THERIA_OK) return rc;
+    }
   }
-  return run_bwd_main(s, q, k, v, dout, lse, delta_out, dq, dk, dv, dq_accum, dv_only, st);
+  if (!c.k_rows) return THERIA_OK;
+  return run_dkdv(s, q, k, v, dout, lse, delta_out, dk, dv, dv_only, st);
 }
 
 THERIA_API int theria_sdpa_jvp(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,

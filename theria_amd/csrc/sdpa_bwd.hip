@@ -1,42 +1,203 @@
-// Explicit SDPA backward (dQ, dK, dV) for gfx950.
+// Explicit SDPA backward (dQ, dK, dV) for gfx950: two deterministic kernels.
 //
 // Replaces the reference's three kernels _sdpa_bwd_dv_kernel, _sdpa_bwd_dk_kernel and
-// _sdpa_bwd_dq_kernel (theria/attention/triton_sdpa_backward.py:106-191, 269-398, 505-632) with one
-// pass. Math (docs/phase9.md:19-26 of the reference): P from the saved lse, dV = P^T dO,
-// dP = dO V^T, dS = P o (dP - delta), dQ = scale dS K, dK = scale dS^T Q, where delta_i = dO_i . O_i
-// equals the reference's z_i = sum_j dP_ij P_ij and is computed once per row beforehand.
+// _sdpa_bwd_dq_kernel (theria/attention/triton_sdpa_backward.py:106-191, 269-398, 505-632). Math
+// (docs/phase9.md:19-26 of the reference): P from the saved lse, dV = P^T dO, dP = dO V^T,
+// dS = P o (dP - delta), dQ = scale dS K, dK = scale dS^T Q, where delta_i = dO_i . O_i equals the
+// reference's z_i = sum_j dP_ij P_ij and is computed once per row (the reference recomputes it per
+// key tile inside its dK kernel, an O(S^3) pass).
 //
-// Work decomposition: one workgroup = 4 waves owns 128 keys of one (batch, head) for the whole
-// kernel (32 per wave) and walks over the query rows in tiles of 64 (32 for float32). Score tiles
-// are computed as S = Q K^T so that, in the accumulator layout, each lane owns one key: the P and dS
-// tiles are then directly the A operands of dV += P^T dO and dK += dS^T Q, whose B operands
-// (dO^T, Q^T) come from the LDS transpose read, and dV/dK live in registers until the end. K and V
-// fragments stay in registers as the B operands of S and dP. dP is seeded with -delta so the MFMA
-// produces dP - delta directly. dQ needs the other orientation: each wave writes its scale*dS block
-// to LDS, and after one barrier every wave computes one 32x32 dQ tile over all 128 keys of the
-// workgroup (A = dS rows, B = K^T by transpose read of the LDS copy of K) and adds it into a float32
-// accumulator with global float atomics; a final pass converts that accumulator to the input dtype.
-// Causal: query tiles entirely above the block's first key are never visited, fully masked
-// (wave, tile) pairs skip their MFMAs, and only diagonal tiles are masked element-wise.
+// dq_kernel (first): lane per query, like the forward. Per 32-key tile it forms S^T = K Q^T and
+// dP^T = V dO^T with Q and dO in registers as B operands and K / V rows from LDS, seeds dP with
+// -delta so the MFMA yields dP - delta directly, rebuilds P = exp2(S scale log2e - lse log2e), and
+// accumulates dQ^T += K^T dS^T with K^T from the LDS transpose read and dS^T straight from the
+// accumulator tile. It also computes delta from O and dO at the start and writes it for dkdv_kernel.
+// dkdv_kernel (second): lane per key. Each wave owns KT tiles of 32 keys (K and V fragments in
+// registers as B operands) and walks the query rows in tiles of 64 staged in LDS; S = Q K^T and
+// dP = dO V^T land with one key per lane, so P and dS are directly the A operands of
+// dV += P^T dO and dK += dS^T Q (dO^T / Q^T by LDS transpose read), accumulated in registers.
+// Every LDS fragment feeds QT (dq) or KT (dkdv) MFMAs. No atomics, no float32 dQ workspace: the
+// result is deterministic. The split costs two extra score products (S and dP are formed in both
+// kernels) but removes the LDS round trip of dS, the atomics and the accumulator conversion.
+// Causal: key tiles above a query block (dq) and query tiles before a key block (dkdv) are never
+// visited, fully masked wave tiles skip their MFMAs, and only diagonal tiles are masked element-wise.
 #include "dispatch.hpp"
 #include "sdpa_common.hpp"
 
 namespace theria {
 
-template <typename T, int DP, bool CAUSAL>
-__global__ __launch_bounds__(256) void bwd_kernel(const BwdParams p) {
+template <typename T, int DP, bool CAUSAL, int QT>
+__global__ __launch_bounds__(256) void dq_kernel(const DqParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
   constexpr int KC = MM::KC;
-  constexpr int NW = 4, BN = 32 * NW, NT = 64 * NW;
+  constexpr int NW = 4, BM = 32 * NW * QT, BN = 32, NT = 64 * NW;
+  constexpr int PITCH = DP + 16 / (int)sizeof(T);
+  constexpr int NDT = DP / 32, NKC = DP / KC, NPC = 32 / KC;
+  __shared__ __attribute__((aligned(16))) T sK[BN * PITCH];
+  __shared__ __attribute__((aligned(16))) T sV[BN * PITCH];
+
+  const Shape& s = p.s;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, li = lane & 31, g = lane >> 5;
+  const int nqb = (s.T + BM - 1) / BM;
+  const int bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int bh = bid / nqb;
+  int qb = bid - bh * nqb;
+  if (CAUSAL) qb = nqb - 1 - qb;
+  const int b = bh / s.H, h = bh - b * s.H;
+  const T* Q = (const T*)p.q.p + b * p.q.sb + h * p.q.sh;
+  const T* K = (const T*)p.k.p + b * p.k.sb + h * p.k.sh;
+  const T* V = (const T*)p.v.p + b * p.v.sb + h * p.v.sh;
+  const T* dO = (const T*)p.dout.p + b * p.dout.sb + h * p.dout.sh;
+  const int q0w = qb * BM + wave * 32 * QT;
+  const int64_t rowbase = (int64_t)bh * s.T;
+
+  F qf[QT][NKC], of[QT][NKC];
+  float lse2[QT], del[QT];
+#pragma unroll
+  for (int j = 0; j < QT; ++j) {
+    const int myq = q0w + 32 * j + li;
+    const bool qvalid = myq < s.T;
+#pragma unroll
+    for (int c = 0; c < NKC; ++c) {
+      qf[j][c] = gload_frag<T>(Q, p.q.sr, myq, s.T, c, s.D, s.vec);
+      of[j][c] = gload_frag<T>(dO, p.dout.sr, myq, s.T, c, s.D, s.vec);
+    }
+    const float l2 = qvalid ? p.lse[rowbase + myq] * kLog2e : THERIA_INF;
+    lse2[j] = l2 == -THERIA_INF ? THERIA_INF : l2;  // a row without visible keys has P = 0
+    if (p.o.p) {
+      // delta = dO . O over this lane's half of the head dim (the dO fragment's columns), then the pair
+      float part = 0.f;
+      if (qvalid) {
+#pragma unroll
+        for (int c = 0; c < NKC; ++c) {
+          const F od = of[j][c];
+          if constexpr (sizeof(T) == 2) {
+            const int col = c * 16 + 8 * g;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              if (col + e < s.D) {
+                const int64_t off = (int64_t)myq * p.o.sr + col + e;
+                const float ov = p.o_f32 ? ((const float*)p.o.p + b * p.o.sb + h * p.o.sh)[off]
+                                         : (float)((const T*)p.o.p + b * p.o.sb + h * p.o.sh)[off];
+                part += ov * (float)od[e];
+              }
+            }
+          } else {
+            const int col = 2 * c + g;
+            if (col < s.D) part += ((const float*)p.o.p + b * p.o.sb + h * p.o.sh)[(int64_t)myq * p.o.sr + col] * od;
+          }
+        }
+      }
+      del[j] = pair_sum(part);
+      if (qvalid && g == 0) p.delta[rowbase + myq] = del[j];
+    } else {
+      del[j] = qvalid ? p.delta[rowbase + myq] : 0.f;
+    }
+  }
+  if (!p.dq.p) return;  // only the row term was requested (uniform over the grid)
+  f32x16_t acc[QT][NDT];
+#pragma unroll
+  for (int j = 0; j < QT; ++j)
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) acc[j][dt] = zero16();
+  const float c2 = s.scale * kLog2e;
+
+  int kend = s.M;
+  if (CAUSAL) kend = min(s.M, qb * BM + BM);
+  const int nkt = (kend + BN - 1) / BN;
+  TileStage<T, BN, DP, NT> stK, stV;
+  if (nkt > 0) {
+    stK.load(K, p.k.sr, 0, s.M, s.D, s.vec);
+    stV.load(V, p.v.sr, 0, s.M, s.D, s.vec);
+  }
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int k0 = kt * BN;
+    __syncthreads();
+    stK.store(sK, PITCH);
+    stV.store(sV, PITCH);
+    __syncthreads();
+    if (kt + 1 < nkt) {
+      stK.load(K, p.k.sr, k0 + BN, s.M, s.D, s.vec);
+      stV.load(V, p.v.sr, k0 + BN, s.M, s.D, s.vec);
+    }
+    if (CAUSAL && k0 > q0w + 32 * QT - 1) continue;
+
+    f32x16_t sc[QT], dp[QT];
+#pragma unroll
+    for (int j = 0; j < QT; ++j) {
+      sc[j] = zero16();
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dp[j][r] = -del[j];
+    }
+#pragma unroll
+    for (int c = 0; c < NKC; ++c) {
+      const F kfr = lds_cols<T, KLIN>(sK, PITCH, li, 0, c);
+      const F vfr = lds_cols<T, KLIN>(sV, PITCH, li, 0, c);
+#pragma unroll
+      for (int j = 0; j < QT; ++j) {
+        sc[j] = MM::mma(kfr, qf[j][c], sc[j]);
+        dp[j] = MM::mma(vfr, of[j][c], dp[j]);
+      }
+    }
+    const bool need_mask = (k0 + BN > s.M) || (CAUSAL && k0 + BN - 1 > q0w);
+#pragma unroll
+    for (int j = 0; j < QT; ++j) {
+      const int myq = q0w + 32 * j + li;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float pv = fast_exp2(fmaf(sc[j][r], c2, -lse2[j]));
+        if (need_mask) {
+          const int key = k0 + acc_row(r, g);
+          if (key >= s.M || (CAUSAL && key > myq)) pv = 0.f;
+        }
+        sc[j][r] = pv * dp[j][r];  // dS^T
+      }
+    }
+#pragma unroll
+    for (int cc = 0; cc < NPC; ++cc) {
+      F dsf[QT];
+#pragma unroll
+      for (int j = 0; j < QT; ++j) dsf[j] = acc_frag<T>(sc[j], cc);
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const F ktf = lds_rows<T, KACC>(sK, PITCH, 0, cc, dt * 32);
+#pragma unroll
+        for (int j = 0; j < QT; ++j) acc[j][dt] = MM::mma(ktf, dsf[j], acc[j][dt]);
+      }
+    }
+  }
+
+  T* DQ = (T*)p.dq.p + b * p.dq.sb + h * p.dq.sh;
+#pragma unroll
+  for (int j = 0; j < QT; ++j) {
+    const int myq = q0w + 32 * j + li;
+    if (myq >= s.T) continue;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const int d0 = dt * 32 + 8 * qd + 4 * g;
+        if (d0 < s.D) {
+          const f32x16_t& a = acc[j][dt];
+          store4<T>(DQ, p.dq.sr, myq, d0, s.D, a[4 * qd] * s.scale, a[4 * qd + 1] * s.scale, a[4 * qd + 2] * s.scale,
+                    a[4 * qd + 3] * s.scale, s.vec);
+        }
+      }
+  }
+}
+
+template <typename T, int DP, bool CAUSAL, int KT, bool DV_ONLY>
+__global__ __launch_bounds__(256) void dkdv_kernel(const DkdvParams p) {
+  using MM = Mfma<T>;
+  using F = typename MM::frag_t;
+  constexpr int KC = MM::KC;
+  constexpr int NW = 4, BN = 32 * NW * KT, NT = 64 * NW;
   constexpr int BM = sizeof(T) == 2 ? 64 : 32;
   constexpr int PITCH = DP + 16 / (int)sizeof(T);
-  constexpr int SPITCH = BN + 16 / (int)sizeof(T);
   constexpr int NDT = DP / 32, NKC = DP / KC, NPC = 32 / KC, NQT = BM / 32;
   __shared__ __attribute__((aligned(16))) T sQ[BM * PITCH];
   __shared__ __attribute__((aligned(16))) T sdO[BM * PITCH];
-  __shared__ __attribute__((aligned(16))) T sK[BN * PITCH];
-  __shared__ __attribute__((aligned(16))) T sdS[BM * SPITCH];
   __shared__ __attribute__((aligned(16))) float sLse[BM];
   __shared__ __attribute__((aligned(16))) float sDel[BM];
 
@@ -51,38 +212,33 @@ __global__ __launch_bounds__(256) void bwd_kernel(const BwdParams p) {
   const T* Q = (const T*)p.q.p + b * p.q.sb + h * p.q.sh;
   const T* K = (const T*)p.k.p + b * p.k.sb + h * p.k.sh;
   const T* dO = (const T*)p.dout.p + b * p.dout.sb + h * p.dout.sh;
-  const bool dv_only = p.dv_only;
-  const bool want_dq = p.want_dq && !dv_only;
-  const bool want_dk = p.want_dk && !dv_only;
-
+  constexpr bool dv_only = DV_ONLY;
   const int key0 = kb * BN;
-  const int kw0 = key0 + wave * 32;
-  const int mykey = kw0 + li;
-  const bool kvalid = mykey < s.M;
+  const int kw0 = key0 + wave * 32 * KT;  // key tile t of this wave starts at kw0 + 32 t
 
-  F kf[NKC], vf[NKC];
+  F kf[KT][NKC], vf[KT][NKC];
 #pragma unroll
-  for (int c = 0; c < NKC; ++c) kf[c] = gload_frag<T>(K, p.k.sr, mykey, s.M, c, s.D, s.vec);
-  if (!dv_only) {
+  for (int t = 0; t < KT; ++t)
+#pragma unroll
+    for (int c = 0; c < NKC; ++c) {
+      kf[t][c] = gload_frag<T>(K, p.k.sr, kw0 + 32 * t + li, s.M, c, s.D, s.vec);
+      vf[t][c] = F{};
+    }
+  if constexpr (!DV_ONLY) {
     const T* V = (const T*)p.v.p + b * p.v.sb + h * p.v.sh;
 #pragma unroll
-    for (int c = 0; c < NKC; ++c) vf[c] = gload_frag<T>(V, p.v.sr, mykey, s.M, c, s.D, s.vec);
-  } else {
+    for (int t = 0; t < KT; ++t)
 #pragma unroll
-    for (int c = 0; c < NKC; ++c) vf[c] = F{};
+      for (int c = 0; c < NKC; ++c) vf[t][c] = gload_frag<T>(V, p.v.sr, kw0 + 32 * t + li, s.M, c, s.D, s.vec);
   }
-  if (want_dq) {
-    TileStage<T, BN, DP, NT> stK;
-    stK.load(K, p.k.sr, key0, s.M, s.D, s.vec);
-    stK.store(sK, PITCH);  // published by the first barrier of the query loop
-  }
-
-  f32x16_t dv[NDT], dk[NDT];
+  f32x16_t dv[KT][NDT], dk[KT][NDT];
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) {
-    dv[dt] = zero16();
-    dk[dt] = zero16();
-  }
+  for (int t = 0; t < KT; ++t)
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      dv[t][dt] = zero16();
+      dk[t][dt] = zero16();
+    }
   const float c2 = s.scale * kLog2e;
   const int qbeg = CAUSAL ? (key0 / BM) * BM : 0;
   const int nqt = s.T > qbeg ? (s.T - qbeg + BM - 1) / BM : 0;
@@ -95,7 +251,8 @@ __global__ __launch_bounds__(256) void bwd_kernel(const BwdParams p) {
     stO.load(dO, p.dout.sr, q0, s.T, s.D, s.vec);
     if (tid < BM) {
       const int qq = q0 + tid;
-      pre_lse = qq < s.T ? p.lse[rowbase + qq] * kLog2e : THERIA_INF;
+      const float l2 = qq < s.T ? p.lse[rowbase + qq] * kLog2e : THERIA_INF;
+      pre_lse = l2 == -THERIA_INF ? THERIA_INF : l2;
       pre_del = (qq < s.T && !dv_only) ? p.delta[rowbase + qq] : 0.f;
     }
   };
@@ -117,129 +274,134 @@ __global__ __launch_bounds__(256) void bwd_kernel(const BwdParams p) {
     for (int qt = 0; qt < NQT; ++qt) {
       const int qr0 = qt * 32;
       const int q0t = q0 + qr0;
-      const bool active = q0t < s.T && (!CAUSAL || kw0 <= q0t + 31);
-      if (!active) {
-        if (want_dq) {
+      if (q0t >= s.T || (CAUSAL && kw0 > q0t + 31)) continue;  // wave-uniform
+      f32x4_t lse4[4], del4[4];
 #pragma unroll
-          for (int r = 0; r < 16; ++r) sdS[(qr0 + acc_row(r, g)) * SPITCH + wave * 32 + li] = (T)0.f;
-        }
-        continue;
+      for (int qd = 0; qd < 4; ++qd) {
+        lse4[qd] = *reinterpret_cast<const f32x4_t*>(sLse + qr0 + 8 * qd + 4 * g);
+        del4[qd] = *reinterpret_cast<const f32x4_t*>(sDel + qr0 + 8 * qd + 4 * g);
       }
-      f32x16_t sc = zero16();
+      f32x16_t sc[KT], dp[KT];
 #pragma unroll
-      for (int c = 0; c < NKC; ++c) sc = MM::mma(lds_cols<T, KLIN>(sQ, PITCH, qr0 + li, 0, c), kf[c], sc);
-      f32x4_t lse4[4];
+      for (int t = 0; t < KT; ++t) {
+        sc[t] = zero16();
 #pragma unroll
-      for (int qd = 0; qd < 4; ++qd) lse4[qd] = *reinterpret_cast<const f32x4_t*>(sLse + qr0 + 8 * qd + 4 * g);
-      f32x16_t dp;
-      if (!dv_only) {
-#pragma unroll
-        for (int qd = 0; qd < 4; ++qd) {
-          const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(sDel + qr0 + 8 * qd + 4 * g);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) dp[4 * qd + e] = -d4[e];
-        }
-#pragma unroll
-        for (int c = 0; c < NKC; ++c) dp = MM::mma(lds_cols<T, KLIN>(sdO, PITCH, qr0 + li, 0, c), vf[c], dp);
+        for (int r = 0; r < 16; ++r) dp[t][r] = -del4[r >> 2][r & 3];
       }
-      const bool diag = CAUSAL && (kw0 + 31 > q0t);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float pv = fast_exp2(fmaf(sc[r], c2, -lse4[r >> 2][r & 3]));
-        if (!kvalid) pv = 0.f;
-        if (diag && mykey > q0t + acc_row(r, g)) pv = 0.f;
-        sc[r] = pv;
+      for (int c = 0; c < NKC; ++c) {
+        const F qfr = lds_cols<T, KLIN>(sQ, PITCH, qr0 + li, 0, c);
+#pragma unroll
+        for (int t = 0; t < KT; ++t) sc[t] = MM::mma(qfr, kf[t][c], sc[t]);
+        if constexpr (!DV_ONLY) {
+          const F ofr = lds_cols<T, KLIN>(sdO, PITCH, qr0 + li, 0, c);
+#pragma unroll
+          for (int t = 0; t < KT; ++t) dp[t] = MM::mma(ofr, vf[t][c], dp[t]);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < KT; ++t) {
+        const int mykey = kw0 + 32 * t + li;
+        const bool kvalid = mykey < s.M;
+        const bool diag = CAUSAL && (kw0 + 32 * t + 31 > q0t);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float pv = fast_exp2(fmaf(sc[t][r], c2, -lse4[r >> 2][r & 3]));
+          if (!kvalid || (diag && mykey > q0t + acc_row(r, g))) pv = 0.f;
+          sc[t][r] = pv;
+          if constexpr (!DV_ONLY) dp[t][r] *= pv;  // dS
+        }
       }
 #pragma unroll
       for (int cc = 0; cc < NPC; ++cc) {
-        const F pa = acc_frag<T>(sc, cc);
+        F ot[NDT], qtr[NDT];
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) dv[dt] = MM::mma(pa, lds_rows<T, KACC>(sdO, PITCH, qr0, cc, dt * 32), dv[dt]);
-      }
-      if (!dv_only) {
+        for (int dt = 0; dt < NDT; ++dt) ot[dt] = lds_rows<T, KACC>(sdO, PITCH, qr0, cc, dt * 32);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) dp[r] *= sc[r];  // dS
-        if (want_dk) {
+        for (int t = 0; t < KT; ++t) {
+          const F pa = acc_frag<T>(sc[t], cc);
 #pragma unroll
-          for (int cc = 0; cc < NPC; ++cc) {
-            const F da = acc_frag<T>(dp, cc);
-#pragma unroll
-            for (int dt = 0; dt < NDT; ++dt)
-              dk[dt] = MM::mma(da, lds_rows<T, KACC>(sQ, PITCH, qr0, cc, dt * 32), dk[dt]);
-          }
+          for (int dt = 0; dt < NDT; ++dt) dv[t][dt] = MM::mma(pa, ot[dt], dv[t][dt]);
         }
-        if (want_dq) {
+        if constexpr (!DV_ONLY) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) sdS[(qr0 + acc_row(r, g)) * SPITCH + wave * 32 + li] = (T)(dp[r] * s.scale);
-        }
-      }
-    }
-
-    if (want_dq) {
-      __syncthreads();
+          for (int dt = 0; dt < NDT; ++dt) qtr[dt] = lds_rows<T, KACC>(sQ, PITCH, qr0, cc, dt * 32);
 #pragma unroll
-      for (int tile = wave; tile < NQT * NDT; tile += NW) {
-        const int qt = tile / NDT, dt = tile - (tile / NDT) * NDT;
-        const int qr0 = qt * 32;
-        if (q0 + qr0 >= s.T) continue;
-        f32x16_t acc = zero16();
+          for (int t = 0; t < KT; ++t) {
+            const F da = acc_frag<T>(dp[t], cc);
 #pragma unroll
-        for (int kc = 0; kc < BN / KC; ++kc)
-          acc = MM::mma(lds_cols<T, KLIN>(sdS, SPITCH, qr0 + li, 0, kc), lds_rows<T, KLIN>(sK, PITCH, 0, kc, dt * 32), acc);
-        const int d = dt * 32 + li;
-        if (d < s.D) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int q = q0 + qr0 + acc_row(r, g);
-            if (q < s.T) unsafeAtomicAdd(p.dq_accum + (rowbase + q) * s.D + d, acc[r]);
+            for (int dt = 0; dt < NDT; ++dt) dk[t][dt] = MM::mma(da, qtr[dt], dk[t][dt]);
           }
         }
       }
     }
   }
 
-  // Epilogue: lane holds column d = dt*32 + li of rows (keys) kw0 + acc_row(r, g).
-  {
-    T* DV = (T*)p.dv.p + b * p.dv.sb + h * p.dv.sh;
+  // Epilogue: lane holds column d = dt*32 + li of rows (keys) kw0 + 32 t + acc_row(r, g).
+  T* DV = (T*)p.dv.p + b * p.dv.sb + h * p.dv.sh;
+  T* DK = p.dk.p ? (T*)p.dk.p + b * p.dk.sb + h * p.dk.sh : nullptr;
+#pragma unroll
+  for (int t = 0; t < KT; ++t)
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
       const int d = dt * 32 + li;
       if (d < s.D) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int key = kw0 + acc_row(r, g);
-          if (key < s.M) DV[(int64_t)key * p.dv.sr + d] = (T)dv[dt][r];
+          const int key = kw0 + 32 * t + acc_row(r, g);
+          if (key < s.M) {
+            DV[(int64_t)key * p.dv.sr + d] = (T)dv[t][dt][r];
+            if (!DV_ONLY && DK) DK[(int64_t)key * p.dk.sr + d] = (T)(dk[t][dt][r] * s.scale);
+          }
         }
       }
     }
-  }
-  if (want_dk) {
-    T* DK = (T*)p.dk.p + b * p.dk.sb + h * p.dk.sh;
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      const int d = dt * 32 + li;
-      if (d < s.D) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kw0 + acc_row(r, g);
-          if (key < s.M) DK[(int64_t)key * p.dk.sr + d] = (T)(dk[dt][r] * s.scale);
-        }
-      }
-    }
-  }
 }
 
-struct BwdLauncher {
+struct DqLauncher {
   template <typename T, int DP, bool CAUSAL>
-  static hipError_t run(const BwdParams& p, hipStream_t st) {
-    const int nkb = (p.s.M + 127) / 128;
-    const int64_t nblk = (int64_t)nkb * p.s.B * p.s.H;
+  static hipError_t run(const DqParams& p, hipStream_t st) {
+    const int qt = (DP <= 64 && p.s.T > 128) ? 2 : 1;
+    const int bm = 128 * qt;
+    const int64_t nblk = (int64_t)((p.s.T + bm - 1) / bm) * p.s.B * p.s.H;
     if (nblk == 0) return hipSuccess;
-    hipLaunchKernelGGL((bwd_kernel<T, DP, CAUSAL>), dim3((unsigned)nblk), dim3(256), 0, st, p);
+    if constexpr (DP <= 64) {
+      if (qt == 2) {
+        hipLaunchKernelGGL((dq_kernel<T, DP, CAUSAL, 2>), dim3((unsigned)nblk), dim3(256), 0, st, p);
+        return hipGetLastError();
+      }
+    }
+    hipLaunchKernelGGL((dq_kernel<T, DP, CAUSAL, 1>), dim3((unsigned)nblk), dim3(256), 0, st, p);
     return hipGetLastError();
   }
 };
 
-hipError_t launch_bwd(const BwdParams& p, hipStream_t st) { return dispatch_all<BwdLauncher>(p, st); }
+struct DkdvLauncher {
+  template <typename T, int DP, bool CAUSAL, int KT>
+  static void go(const DkdvParams& p, unsigned nblk, hipStream_t st) {
+    if (p.dv_only)
+      hipLaunchKernelGGL((dkdv_kernel<T, DP, CAUSAL, KT, true>), dim3(nblk), dim3(256), 0, st, p);
+    else
+      hipLaunchKernelGGL((dkdv_kernel<T, DP, CAUSAL, KT, false>), dim3(nblk), dim3(256), 0, st, p);
+  }
+  template <typename T, int DP, bool CAUSAL>
+  static hipError_t run(const DkdvParams& p, hipStream_t st) {
+    const int kt = (DP <= 64 && p.s.M > 128) ? 2 : 1;
+    const int bn = 128 * kt;
+    const int64_t nblk = (int64_t)((p.s.M + bn - 1) / bn) * p.s.B * p.s.H;
+    if (nblk == 0) return hipSuccess;
+    if constexpr (DP <= 64) {
+      if (kt == 2) {
+        go<T, DP, CAUSAL, 2>(p, (unsigned)nblk, st);
+        return hipGetLastError();
+      }
+    }
+    go<T, DP, CAUSAL, 1>(p, (unsigned)nblk, st);
+    return hipGetLastError();
+  }
+};
+
+hipError_t launch_bwd_dq(const DqParams& p, hipStream_t st) { return dispatch_all<DqLauncher>(p, st); }
+hipError_t launch_bwd_dkdv(const DkdvParams& p, hipStream_t st) { return dispatch_all<DkdvLauncher>(p, st); }
 
 }  // namespace theria

@@ -35,31 +35,27 @@ struct FwdParams {
   float* row_max;   // optional (mode 0)
   float* row_sum;   // optional (mode 0)
   float* delta;     // mode 1: out
-  float* dq_accum;  // mode 1: zeroed when non-null
 };
 
-struct PreParams {
+// dQ pass of the backward. When o.p is set, delta = rowsum(dO * O) is computed and written to
+// delta; otherwise delta is read.
+struct DqParams {
   Shape s;
-  View o, dout;
+  View q, k, v, dout, o;
   bool o_f32;
+  const float* lse;
   float* delta;
-  float* dq_accum;  // zeroed when non-null
+  MutView dq;
 };
 
-struct BwdParams {
+// dK / dV pass of the backward (dv_only: no V, dK not computed).
+struct DkdvParams {
   Shape s;
   View q, k, v, dout;
   const float* lse;
   const float* delta;
   MutView dk, dv;
-  float* dq_accum;
-  bool want_dq, want_dk, dv_only;
-};
-
-struct DqParams {
-  Shape s;
-  const float* dq_accum;
-  MutView dq;
+  bool dv_only;
 };
 
 struct JvpParams {
@@ -80,9 +76,8 @@ struct BwdBwdParams {
 };
 
 hipError_t launch_fwd(const FwdParams& p, int mode, hipStream_t st);
-hipError_t launch_bwd_pre(const PreParams& p, hipStream_t st);
-hipError_t launch_bwd(const BwdParams& p, hipStream_t st);
-hipError_t launch_dq_convert(const DqParams& p, hipStream_t st);
+hipError_t launch_bwd_dq(const DqParams& p, hipStream_t st);
+hipError_t launch_bwd_dkdv(const DkdvParams& p, hipStream_t st);
 hipError_t launch_jvp(const JvpParams& p, hipStream_t st);
 hipError_t launch_bwdbwd_rows(const BwdBwdParams& p, hipStream_t st);
 hipError_t launch_bwdbwd_cols(const BwdBwdParams& p, hipStream_t st);
