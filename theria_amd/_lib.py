@@ -14,7 +14,8 @@ from pathlib import Path
 
 import torch  # noqa: F401  (must be imported first: it loads the HIP runtime the library binds to)
 
-LIB_PATH = Path(__file__).resolve().parent / "lib" / "libtheria_sdpa.so"
+# THERIA_SDPA_LIB overrides the in-tree build (e.g. a library installed elsewhere).
+LIB_PATH = Path(os.environ.get("THERIA_SDPA_LIB") or Path(__file__).resolve().parent / "lib" / "libtheria_sdpa.so")
 ABI_VERSION = 2
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2

@@ -24,10 +24,24 @@
 #include "dispatch.hpp"
 #include "sdpa_common.hpp"
 
+// Tile choices (compile-time knobs; the defaults are the measured best on MI355X).
+#ifndef DKDV_MINW
+#define DKDV_MINW 1
+#endif
+#ifndef DQ_MINW
+#define DQ_MINW 2
+#endif
+#ifndef DQ_QT_MAX
+#define DQ_QT_MAX 2
+#endif
+#ifndef DKDV_KT_MAX
+#define DKDV_KT_MAX 2
+#endif
+
 namespace theria {
 
 template <typename T, int DP, bool CAUSAL, int QT>
-__global__ __launch_bounds__(256) void dq_kernel(const DqParams p) {
+__global__ __launch_bounds__(256, (DP <= 64 ? DQ_MINW : 1)) void dq_kernel(const DqParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
   constexpr int KC = MM::KC;
@@ -188,7 +202,7 @@ __global__ __launch_bounds__(256) void dq_kernel(const DqParams p) {
 }
 
 template <typename T, int DP, bool CAUSAL, int KT, bool DV_ONLY>
-__global__ __launch_bounds__(256) void dkdv_kernel(const DkdvParams p) {
+__global__ __launch_bounds__(256, DKDV_MINW) void dkdv_kernel(const DkdvParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
   constexpr int KC = MM::KC;
@@ -361,7 +375,7 @@ __global__ __launch_bounds__(256) void dkdv_kernel(const DkdvParams p) {
 struct DqLauncher {
   template <typename T, int DP, bool CAUSAL>
   static hipError_t run(const DqParams& p, hipStream_t st) {
-    const int qt = (DP <= 64 && p.s.T > 128) ? 2 : 1;
+    const int qt = (DQ_QT_MAX >= 2 && DP <= 64 && p.s.T > 128) ? 2 : 1;
     const int bm = 128 * qt;
     const int64_t nblk = (int64_t)((p.s.T + bm - 1) / bm) * p.s.B * p.s.H;
     if (nblk == 0) return hipSuccess;
@@ -386,7 +400,7 @@ struct DkdvLauncher {
   }
   template <typename T, int DP, bool CAUSAL>
   static hipError_t run(const DkdvParams& p, hipStream_t st) {
-    const int kt = (DP <= 64 && p.s.M > 128) ? 2 : 1;
+    const int kt = (DKDV_KT_MAX >= 2 && DP <= 64 && p.s.M > 128) ? 2 : 1;
     const int bn = 128 * kt;
     const int64_t nblk = (int64_t)((p.s.M + bn - 1) / bn) * p.s.B * p.s.H;
     if (nblk == 0) return hipSuccess;

@@ -216,6 +216,27 @@ struct TileStage {
   static constexpr int PER = (NCH + NT - 1) / NT;
   i16x8_t r[PER];
 
+  // Straight-line 16-byte loads; only for tiles whose rows and columns are all in range with
+  // vector-legal alignment (callers check `row0 + ROWS <= nrows && D == DP && vec` first).
+  __device__ __forceinline__ void load_fast(const T* base, int64_t rs, int row0) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int ch = (int)threadIdx.x + i * NT;
+      if (NCH % NT == 0 || ch < NCH) {
+        const int row = ch / CPR, col = (ch % CPR) * VEC;
+        r[i] = *reinterpret_cast<const i16x8_t*>(base + (int64_t)(row0 + row) * rs + col);
+      }
+    }
+  }
+
+  // Picks the fast path when the whole tile is in range (a uniform branch).
+  __device__ __forceinline__ void load_any(const T* base, int64_t rs, int row0, int nrows, int D, bool vec) {
+    if (vec && D == DP && row0 + ROWS <= nrows)
+      load_fast(base, rs, row0);
+    else
+      load(base, rs, row0, nrows, D, vec);
+  }
+
   __device__ __forceinline__ void load(const T* base, int64_t rs, int row0, int nrows, int D, bool vec) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {

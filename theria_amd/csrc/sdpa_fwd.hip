@@ -17,17 +17,23 @@
 // LDS traffic per FLOP. exp is evaluated as exp2 with scale*log2(e) folded into one FMA. The running
 // max used for P is only moved when a row's max grows by more than 2^8 (P <= 256 stays exact in
 // float32 and representable in bf16/fp16), so the O rescale is skipped on almost every tile.
+#include <type_traits>
+
 #include "dispatch.hpp"
 #include "sdpa_common.hpp"
 
+#ifndef FWD_MINW
+#define FWD_MINW 2
+#endif
+
 namespace theria {
 
-template <typename T, int DP, bool CAUSAL, int MODE, int QT>
-__global__ __launch_bounds__(256) void fwd_kernel(const FwdParams p) {
+template <typename T, int DP, bool CAUSAL, int MODE, int QT, int BN>
+__global__ __launch_bounds__(256, (DP <= 64 ? FWD_MINW : 1)) void fwd_kernel(const FwdParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
   constexpr int KC = MM::KC;
-  constexpr int NW = 4, BM = 32 * NW * QT, BN = 64, NT = 64 * NW;
+  constexpr int NW = 4, BM = 32 * NW * QT, NT = 64 * NW;
   constexpr int PITCH = DP + 16 / (int)sizeof(T);
   constexpr int NDT = DP / 32, NKC = DP / KC, NPC = 32 / KC, NST = BN / 32;
   __shared__ __attribute__((aligned(16))) T sK[BN * PITCH];
@@ -64,26 +70,10 @@ __global__ __launch_bounds__(256) void fwd_kernel(const FwdParams p) {
   }
   const float c2 = s.scale * kLog2e;
 
-  int kend = s.M;
-  if (CAUSAL) kend = min(s.M, qb * BM + BM);
-  const int nkt = (kend + BN - 1) / BN;
-  TileStage<T, BN, DP, NT> stK, stV;
-  if (nkt > 0) {
-    stK.load(K, p.k.sr, 0, s.M, s.D, s.vec);
-    stV.load(V, p.v.sr, 0, s.M, s.D, s.vec);
-  }
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int k0 = kt * BN;
-    __syncthreads();
-    stK.store(sK, PITCH);
-    stV.store(sV, PITCH);
-    __syncthreads();
-    if (kt + 1 < nkt) {
-      stK.load(K, p.k.sr, k0 + BN, s.M, s.D, s.vec);
-      stV.load(V, p.v.sr, k0 + BN, s.M, s.D, s.vec);
-    }
-    if (CAUSAL && k0 > q0w + 32 * QT - 1) continue;  // tile entirely above this wave's diagonal
-
+  // One staged key tile: scores, (masking,) online softmax, PV. MASK is a compile-time tag so that
+  // interior tiles run without any per-element mask test.
+  auto tile = [&](const int k0, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
     f32x16_t sc[QT][NST];
 #pragma unroll
     for (int t = 0; t < NST; ++t) {
@@ -96,11 +86,10 @@ __global__ __launch_bounds__(256) void fwd_kernel(const FwdParams p) {
         for (int j = 0; j < QT; ++j) sc[j][t] = MM::mma(kfr, qf[j][c], sc[j][t]);
       }
     }
-    const bool need_mask = (k0 + BN > s.M) || (CAUSAL && k0 + BN - 1 > q0w);
 #pragma unroll
     for (int j = 0; j < QT; ++j) {
-      const int myq = q0w + 32 * j + li;
-      if (need_mask) {
+      if constexpr (MASK) {
+        const int myq = q0w + 32 * j + li;
 #pragma unroll
         for (int t = 0; t < NST; ++t)
 #pragma unroll
@@ -128,9 +117,11 @@ __global__ __launch_bounds__(256) void fwd_kernel(const FwdParams p) {
             for (int r = 0; r < 16; ++r) o[j][dt][r] *= alpha;
         }
       }
-      // m_use is -inf only while every key seen so far is masked (then every score is -inf and P = 0);
-      // in mode 1 a row without visible keys has lse = -inf and P must be 0 as well.
-      const float moff = (m_use[j] == -THERIA_INF) ? (MODE == 0 ? 0.f : THERIA_INF) : m_use[j];
+      // Unmasked tiles have finite scores, so after the rescale check m_use is finite. In masked
+      // tiles m_use stays -inf while every key seen so far is masked (then every score is -inf and
+      // P = 0); in mode 1 a row without visible keys has lse = -inf and P must be 0 as well.
+      float moff = m_use[j];
+      if (MASK || MODE == 1) moff = (m_use[j] == -THERIA_INF) ? (MODE == 0 ? 0.f : THERIA_INF) : m_use[j];
       float ls = 0.f;
 #pragma unroll
       for (int t = 0; t < NST; ++t)
@@ -156,6 +147,32 @@ __global__ __launch_bounds__(256) void fwd_kernel(const FwdParams p) {
           for (int j = 0; j < QT; ++j) o[j][dt] = MM::mma(vfr, pf[j], o[j][dt]);
         }
       }
+  };
+
+  int kend = s.M;
+  if (CAUSAL) kend = min(s.M, qb * BM + BM);
+  const int nkt = (kend + BN - 1) / BN;
+  TileStage<T, BN, DP, NT> stK, stV;
+  if (nkt > 0) {
+    stK.load_any(K, p.k.sr, 0, s.M, s.D, s.vec);
+    stV.load_any(V, p.v.sr, 0, s.M, s.D, s.vec);
+  }
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int k0 = kt * BN;
+    __syncthreads();
+    stK.store(sK, PITCH);
+    stV.store(sV, PITCH);
+    __syncthreads();
+    if (kt + 1 < nkt) {
+      stK.load_any(K, p.k.sr, k0 + BN, s.M, s.D, s.vec);
+      stV.load_any(V, p.v.sr, k0 + BN, s.M, s.D, s.vec);
+    }
+    if (CAUSAL && k0 > q0w + 32 * QT - 1) continue;  // tile entirely above this wave's diagonal
+    const bool need_mask = (k0 + BN > s.M) || (CAUSAL && k0 + BN - 1 > q0w);
+    if (need_mask)
+      tile(k0, std::true_type{});
+    else
+      tile(k0, std::false_type{});
   }
 
 #pragma unroll
@@ -210,8 +227,15 @@ __global__ __launch_bounds__(256) void fwd_kernel(const FwdParams p) {
   }
 }
 
+// Tile choices (compile-time knobs; the defaults are the measured best on MI355X).
+#ifndef FWD_BN_QT2
+#define FWD_BN_QT2 32
+#endif
+#ifndef FWD_QT_MAX
+#define FWD_QT_MAX 2
+#endif
 // Query tiles per wave: 2 where the registers allow it and the sequence fills the block.
-template <int DP> constexpr int fwd_qt(int T) { return (DP <= 64 && T > 128) ? 2 : 1; }
+template <int DP> constexpr int fwd_qt(int T) { return (FWD_QT_MAX >= 2 && DP <= 64 && T > 128) ? 2 : 1; }
 
 template <int MODE>
 struct FwdLauncher {
@@ -223,11 +247,11 @@ struct FwdLauncher {
     if (nblk == 0) return hipSuccess;
     if constexpr (DP <= 64) {
       if (qt == 2) {
-        hipLaunchKernelGGL((fwd_kernel<T, DP, CAUSAL, MODE, 2>), dim3((unsigned)nblk), dim3(256), 0, st, p);
+        hipLaunchKernelGGL((fwd_kernel<T, DP, CAUSAL, MODE, 2, FWD_BN_QT2>), dim3((unsigned)nblk), dim3(256), 0, st, p);
         return hipGetLastError();
       }
     }
-    hipLaunchKernelGGL((fwd_kernel<T, DP, CAUSAL, MODE, 1>), dim3((unsigned)nblk), dim3(256), 0, st, p);
+    hipLaunchKernelGGL((fwd_kernel<T, DP, CAUSAL, MODE, 1, 64>), dim3((unsigned)nblk), dim3(256), 0, st, p);
     return hipGetLastError();
   }
 };
