@@ -154,20 +154,20 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DQ_MINW : 1)) void dq_kernel(const
         dp[j] = MM::mma(vfr, of[j][c], dp[j]);
       }
     }
-    const bool need_mask = (k0 + BN > s.M) || (CAUSAL && k0 + BN - 1 > q0w);
+    // Boundary tiles only (a uniform branch): masked scores become -inf, so P = 0 there.
+    if ((k0 + BN > s.M) || (CAUSAL && k0 + BN - 1 > q0w)) {
 #pragma unroll
-    for (int j = 0; j < QT; ++j) {
-      const int myq = q0w + 32 * j + li;
+      for (int j = 0; j < QT; ++j) {
+        const int lim = CAUSAL ? min(s.M, q0w + 32 * j + li + 1) : s.M;  // first key this query cannot see
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float pv = fast_exp2(fmaf(sc[j][r], c2, -lse2[j]));
-        if (need_mask) {
-          const int key = k0 + acc_row(r, g);
-          if (key >= s.M || (CAUSAL && key > myq)) pv = 0.f;
-        }
-        sc[j][r] = pv * dp[j][r];  // dS^T
+        for (int r = 0; r < 16; ++r)
+          if (k0 + acc_row(r, g) >= lim) sc[j][r] = -THERIA_INF;
       }
     }
+#pragma unroll
+    for (int j = 0; j < QT; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sc[j][r] = fast_exp2(fmaf(sc[j][r], c2, -lse2[j])) * dp[j][r];  // dS^T
 #pragma unroll
     for (int cc = 0; cc < NPC; ++cc) {
       F dsf[QT];
@@ -313,19 +313,24 @@ __global__ __launch_bounds__(256, DKDV_MINW) void dkdv_kernel(const DkdvParams p
           for (int t = 0; t < KT; ++t) dp[t] = MM::mma(ofr, vf[t][c], dp[t]);
         }
       }
+      // Boundary sub-tiles only (a uniform branch): masked scores become -inf, so P = 0 there.
+      if ((kw0 + 32 * KT > s.M) || (CAUSAL && kw0 + 32 * KT - 1 > q0t)) {
 #pragma unroll
-      for (int t = 0; t < KT; ++t) {
-        const int mykey = kw0 + 32 * t + li;
-        const bool kvalid = mykey < s.M;
-        const bool diag = CAUSAL && (kw0 + 32 * t + 31 > q0t);
+        for (int t = 0; t < KT; ++t) {
+          const int mykey = kw0 + 32 * t + li;
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (mykey >= s.M || (CAUSAL && mykey > q0t + acc_row(r, g))) sc[t][r] = -THERIA_INF;
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < KT; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          float pv = fast_exp2(fmaf(sc[t][r], c2, -lse4[r >> 2][r & 3]));
-          if (!kvalid || (diag && mykey > q0t + acc_row(r, g))) pv = 0.f;
+          const float pv = fast_exp2(fmaf(sc[t][r], c2, -lse4[r >> 2][r & 3]));
           sc[t][r] = pv;
           if constexpr (!DV_ONLY) dp[t][r] *= pv;  // dS
         }
-      }
 #pragma unroll
       for (int cc = 0; cc < NPC; ++cc) {
         F ot[NDT], qtr[NDT];

@@ -17,8 +17,6 @@
 // LDS traffic per FLOP. exp is evaluated as exp2 with scale*log2(e) folded into one FMA. The running
 // max used for P is only moved when a row's max grows by more than 2^8 (P <= 256 stays exact in
 // float32 and representable in bf16/fp16), so the O rescale is skipped on almost every tile.
-#include <type_traits>
-
 #include "dispatch.hpp"
 #include "sdpa_common.hpp"
 
@@ -70,10 +68,26 @@ __global__ __launch_bounds__(256, (DP <= 64 ? FWD_MINW : 1)) void fwd_kernel(con
   }
   const float c2 = s.scale * kLog2e;
 
-  // One staged key tile: scores, (masking,) online softmax, PV. MASK is a compile-time tag so that
-  // interior tiles run without any per-element mask test.
-  auto tile = [&](const int k0, auto mask_tag) {
-    constexpr bool MASK = decltype(mask_tag)::value;
+  int kend = s.M;
+  if (CAUSAL) kend = min(s.M, qb * BM + BM);
+  const int nkt = (kend + BN - 1) / BN;
+  TileStage<T, BN, DP, NT> stK, stV;
+  if (nkt > 0) {
+    stK.load_any(K, p.k.sr, 0, s.M, s.D, s.vec);
+    stV.load_any(V, p.v.sr, 0, s.M, s.D, s.vec);
+  }
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int k0 = kt * BN;
+    __syncthreads();
+    stK.store(sK, PITCH);
+    stV.store(sV, PITCH);
+    __syncthreads();
+    if (kt + 1 < nkt) {
+      stK.load_any(K, p.k.sr, k0 + BN, s.M, s.D, s.vec);
+      stV.load_any(V, p.v.sr, k0 + BN, s.M, s.D, s.vec);
+    }
+    if (CAUSAL && k0 > q0w + 32 * QT - 1) continue;  // tile entirely above this wave's diagonal
+
     f32x16_t sc[QT][NST];
 #pragma unroll
     for (int t = 0; t < NST; ++t) {
@@ -86,18 +100,21 @@ __global__ __launch_bounds__(256, (DP <= 64 ? FWD_MINW : 1)) void fwd_kernel(con
         for (int j = 0; j < QT; ++j) sc[j][t] = MM::mma(kfr, qf[j][c], sc[j][t]);
       }
     }
+    // Boundary tiles only (a uniform branch): masked scores become -inf, so P = 0 there. Interior
+    // tiles run the same code below with no per-element test.
+    if ((k0 + BN > s.M) || (CAUSAL && k0 + BN - 1 > q0w)) {
 #pragma unroll
-    for (int j = 0; j < QT; ++j) {
-      if constexpr (MASK) {
-        const int myq = q0w + 32 * j + li;
+      for (int j = 0; j < QT; ++j) {
+        const int lim = CAUSAL ? min(s.M, q0w + 32 * j + li + 1) : s.M;  // first key this query cannot see
 #pragma unroll
         for (int t = 0; t < NST; ++t)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = k0 + t * 32 + acc_row(r, g);
-            if (key >= s.M || (CAUSAL && key > myq)) sc[j][t][r] = -THERIA_INF;
-          }
+          for (int r = 0; r < 16; ++r)
+            if (k0 + t * 32 + acc_row(r, g) >= lim) sc[j][t][r] = -THERIA_INF;
       }
+    }
+#pragma unroll
+    for (int j = 0; j < QT; ++j) {
       if (MODE == 0) {
         float mx = -THERIA_INF;
 #pragma unroll
@@ -117,11 +134,9 @@ __global__ __launch_bounds__(256, (DP <= 64 ? FWD_MINW : 1)) void fwd_kernel(con
             for (int r = 0; r < 16; ++r) o[j][dt][r] *= alpha;
         }
       }
-      // Unmasked tiles have finite scores, so after the rescale check m_use is finite. In masked
-      // tiles m_use stays -inf while every key seen so far is masked (then every score is -inf and
+      // m_use is -inf only while every key seen so far is masked (then every score is -inf and
       // P = 0); in mode 1 a row without visible keys has lse = -inf and P must be 0 as well.
-      float moff = m_use[j];
-      if (MASK || MODE == 1) moff = (m_use[j] == -THERIA_INF) ? (MODE == 0 ? 0.f : THERIA_INF) : m_use[j];
+      const float moff = (m_use[j] == -THERIA_INF) ? (MODE == 0 ? 0.f : THERIA_INF) : m_use[j];
       float ls = 0.f;
 #pragma unroll
       for (int t = 0; t < NST; ++t)
@@ -147,32 +162,6 @@ __global__ __launch_bounds__(256, (DP <= 64 ? FWD_MINW : 1)) void fwd_kernel(con
           for (int j = 0; j < QT; ++j) o[j][dt] = MM::mma(vfr, pf[j], o[j][dt]);
         }
       }
-  };
-
-  int kend = s.M;
-  if (CAUSAL) kend = min(s.M, qb * BM + BM);
-  const int nkt = (kend + BN - 1) / BN;
-  TileStage<T, BN, DP, NT> stK, stV;
-  if (nkt > 0) {
-    stK.load_any(K, p.k.sr, 0, s.M, s.D, s.vec);
-    stV.load_any(V, p.v.sr, 0, s.M, s.D, s.vec);
-  }
-  for (int kt = 0; kt < nkt; ++kt) {
-    const int k0 = kt * BN;
-    __syncthreads();
-    stK.store(sK, PITCH);
-    stV.store(sV, PITCH);
-    __syncthreads();
-    if (kt + 1 < nkt) {
-      stK.load_any(K, p.k.sr, k0 + BN, s.M, s.D, s.vec);
-      stV.load_any(V, p.v.sr, k0 + BN, s.M, s.D, s.vec);
-    }
-    if (CAUSAL && k0 > q0w + 32 * QT - 1) continue;  // tile entirely above this wave's diagonal
-    const bool need_mask = (k0 + BN > s.M) || (CAUSAL && k0 + BN - 1 > q0w);
-    if (need_mask)
-      tile(k0, std::true_type{});
-    else
-      tile(k0, std::false_type{});
   }
 
 #pragma unroll
@@ -229,7 +218,7 @@ __global__ __launch_bounds__(256, (DP <= 64 ? FWD_MINW : 1)) void fwd_kernel(con
 
 // Tile choices (compile-time knobs; the defaults are the measured best on MI355X).
 #ifndef FWD_BN_QT2
-#define FWD_BN_QT2 32
+#define FWD_BN_QT2 64
 #endif
 #ifndef FWD_QT_MAX
 #define FWD_QT_MAX 2
