@@ -4,7 +4,8 @@
  * One shared library, libtheria_sdpa.so, exports these entry points. They take caller-owned device
  * pointers, plain integer shapes and strides, and a hipStream_t passed as void*. The library never
  * allocates or frees device memory: every output and every workspace is caller-owned. Every entry
- * point is reentrant; the only mutable state is the thread-local message behind theria_last_error().
+ * point is reentrant; the only mutable state is the thread-local message behind theria_last_error()
+ * and a per-device cache of the compute-unit count (used to pick launch shapes).
  *
  * Semantics follow theria's operator contract (docs/phase9.md:12-39 in the reference):
  *   S = scale * Q K^T (+ causal mask), P = softmax_row(S), O = P V,

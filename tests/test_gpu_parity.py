@@ -30,6 +30,14 @@ def tol(dtype):
     return dict(rtol=1e-5, atol=1e-5) if dtype == torch.float32 else dict(rtol=2e-2, atol=2e-2)
 
 
+def stat_tol(dtype):
+    """Row statistics (lse, l). float32: 1e-5. 16-bit inputs: the row sum is accumulated from the
+    16-bit-rounded probabilities that also feed the PV product (so the weights of O sum to one exactly);
+    each carries a relative rounding error below 2^-8 (bfloat16; 2^-11 for float16), so l is within a
+    relative 2^-8 of the float32 sum and lse within 2^-8 absolute: 4e-3."""
+    return dict(rtol=1e-5, atol=1e-5) if dtype == torch.float32 else dict(rtol=4e-3, atol=4e-3)
+
+
 def close(gpu, ref, dtype, what):
     a = gpu.detach().double().cpu()
     b = ref.double()
@@ -86,9 +94,9 @@ def test_kernels_match_oracle(case, hip_device):
     Or, lser, mr, lr = O.forward(qc, kc, vc, s, causal)
     close(o, Or, dt, "O")
     close(o32, Or, dt, "O(fp32 out)")
-    torch.testing.assert_close(lse.double().cpu(), lser, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(lse.double().cpu(), lser, **stat_tol(dt))
     torch.testing.assert_close(m.double().cpu(), mr, rtol=1e-5, atol=1e-5)
-    torch.testing.assert_close(l.double().cpu(), lr, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(l.double().cpu(), lr, **stat_tol(dt))
 
     dq, dk, dv, delta = _ops.bwd(q, k, v, o, lse, do, s, causal)
     ref = O.backward(qc, kc, vc, doc, s, causal)
@@ -191,7 +199,7 @@ def test_config2_full_size(dt, hip_device):
         sl = (slice(b, b + 1), slice(h, h + 1))
         Or, lser, _, _ = O.forward(qc[sl], kc[sl], vc[sl], s)
         close(o[sl], Or, dt, f"O[{b},{h}]")
-        torch.testing.assert_close(lse[sl].double().cpu(), lser, rtol=1e-5, atol=1e-5)
+        torch.testing.assert_close(lse[sl].double().cpu(), lser, **stat_tol(dt))
         for name, a, r in zip(("dQ", "dK", "dV"), (dq[sl], dk[sl], dv[sl]), O.backward(qc[sl], kc[sl], vc[sl], doc[sl], s)):
             close(a, r, dt, f"{name}[{b},{h}]")
     # invariants over every head

@@ -1,5 +1,6 @@
 // C ABI of libtheria_sdpa.so (declared in include/theria_sdpa.h): argument validation, launch
 // sequencing and error reporting. No device memory is allocated here.
+#include <atomic>
 #include <cmath>
 #include <cstdio>
 #include <string>
@@ -99,6 +100,26 @@ int hip_status(hipError_t e, const char* what) {
 bool empty_problem(const theria::Shape& s) { return s.B == 0 || s.H == 0 || s.T == 0; }
 
 }  // namespace
+
+namespace theria {
+
+// Compute units of the current device. The per-device cache is written with the same value by any
+// thread that fills it, so concurrent first calls are harmless.
+int device_cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+  if (dev < 64) {
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+  if (dev < 64) cache[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+}  // namespace theria
 
 THERIA_API int theria_abi_version(void) { return THERIA_SDPA_ABI_VERSION; }
 

@@ -26,7 +26,7 @@
 
 // Tile choices (compile-time knobs; the defaults are the measured best on MI355X).
 #ifndef DKDV_MINW
-#define DKDV_MINW 1
+#define DKDV_MINW 2
 #endif
 #ifndef DQ_MINW
 #define DQ_MINW 2
@@ -35,7 +35,7 @@
 #define DQ_QT_MAX 2
 #endif
 #ifndef DKDV_KT_MAX
-#define DKDV_KT_MAX 2
+#define DKDV_KT_MAX 1
 #endif
 
 namespace theria {
@@ -202,7 +202,7 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DQ_MINW : 1)) void dq_kernel(const
 }
 
 template <typename T, int DP, bool CAUSAL, int KT, bool DV_ONLY>
-__global__ __launch_bounds__(256, DKDV_MINW) void dkdv_kernel(const DkdvParams p) {
+__global__ __launch_bounds__(256, (DP <= 64 ? DKDV_MINW : 1)) void dkdv_kernel(const DkdvParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
   constexpr int KC = MM::KC;
@@ -267,7 +267,7 @@ __global__ __launch_bounds__(256, DKDV_MINW) void dkdv_kernel(const DkdvParams p
       const int qq = q0 + tid;
       const float l2 = qq < s.T ? p.lse[rowbase + qq] * kLog2e : THERIA_INF;
       pre_lse = l2 == -THERIA_INF ? THERIA_INF : l2;
-      pre_del = (qq < s.T && !dv_only) ? p.delta[rowbase + qq] : 0.f;
+      pre_del = (qq < s.T && !dv_only) ? -p.delta[rowbase + qq] : 0.f;  // staged negated: dP starts at -delta
     }
   };
   if (nqt > 0) prefetch(qbeg);
@@ -300,7 +300,7 @@ __global__ __launch_bounds__(256, DKDV_MINW) void dkdv_kernel(const DkdvParams p
       for (int t = 0; t < KT; ++t) {
         sc[t] = zero16();
 #pragma unroll
-        for (int r = 0; r < 16; ++r) dp[t][r] = -del4[r >> 2][r & 3];
+        for (int r = 0; r < 16; ++r) dp[t][r] = del4[r >> 2][r & 3];
       }
 #pragma unroll
       for (int c = 0; c < NKC; ++c) {
@@ -409,7 +409,7 @@ struct DkdvLauncher {
     const int bn = 128 * kt;
     const int64_t nblk = (int64_t)((p.s.M + bn - 1) / bn) * p.s.B * p.s.H;
     if (nblk == 0) return hipSuccess;
-    if constexpr (DP <= 64) {
+    if constexpr (DP <= 64 && DKDV_KT_MAX >= 2) {
       if (kt == 2) {
         go<T, DP, CAUSAL, 2>(p, (unsigned)nblk, st);
         return hipGetLastError();

@@ -226,10 +226,18 @@ __global__ __launch_bounds__(256, (DP <= 64 ? FWD_MINW : 1)) void fwd_kernel(con
 // Query tiles per wave: 2 where the registers allow it and the sequence fills the block.
 template <int DP> constexpr int fwd_qt(int T) { return (FWD_QT_MAX >= 2 && DP <= 64 && T > 128) ? 2 : 1; }
 
+// Pipelined 16-bit head-dim-64 forward (sdpa_fwd_pipe.hip); false when it does not cover the problem.
+template <typename T, bool CAUSAL>
+bool launch_fwd_pipe(const FwdParams& p, hipStream_t st, hipError_t* err);
+
 template <int MODE>
 struct FwdLauncher {
   template <typename T, int DP, bool CAUSAL>
   static hipError_t run(const FwdParams& p, hipStream_t st) {
+    if constexpr (MODE == 0 && sizeof(T) == 2 && DP == 64) {
+      hipError_t err;
+      if (launch_fwd_pipe<T, CAUSAL>(p, st, &err)) return err;
+    }
     const int qt = fwd_qt<DP>(p.s.T);
     const int bm = 128 * qt;
     const int64_t nblk = (int64_t)((p.s.T + bm - 1) / bm) * p.s.B * p.s.H;

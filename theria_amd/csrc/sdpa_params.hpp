@@ -75,6 +75,9 @@ struct BwdBwdParams {
   MutView out_gq, out_gk, out_gv;
 };
 
+// Compute units of the current device (cached per device).
+int device_cu_count();
+
 hipError_t launch_fwd(const FwdParams& p, int mode, hipStream_t st);
 hipError_t launch_bwd_dq(const DqParams& p, hipStream_t st);
 hipError_t launch_bwd_dkdv(const DkdvParams& p, hipStream_t st);
