@@ -395,6 +395,10 @@ struct DqLauncher {
   }
 };
 
+// Pipelined 16-bit head-dim-64 dK/dV (sdpa_bwd_pipe.hip); false when it does not cover the problem.
+template <typename T, bool CAUSAL>
+bool launch_dkdv_pipe(const DkdvParams& p, hipStream_t st, hipError_t* err);
+
 struct DkdvLauncher {
   template <typename T, int DP, bool CAUSAL, int KT>
   static void go(const DkdvParams& p, unsigned nblk, hipStream_t st) {
@@ -405,6 +409,10 @@ struct DkdvLauncher {
   }
   template <typename T, int DP, bool CAUSAL>
   static hipError_t run(const DkdvParams& p, hipStream_t st) {
+    if constexpr (sizeof(T) == 2 && DP == 64) {
+      hipError_t err;
+      if (launch_dkdv_pipe<T, CAUSAL>(p, st, &err)) return err;
+    }
     const int kt = (DKDV_KT_MAX >= 2 && DP <= 64 && p.s.M > 128) ? 2 : 1;
     const int bn = 128 * kt;
     const int64_t nblk = (int64_t)((p.s.M + bn - 1) / bn) * p.s.B * p.s.H;

@@ -1,0 +1,264 @@
+// Pipelined dK/dV pass of the SDPA backward for 16-bit inputs with head_dim 64 on gfx950.
+//
+// Same contract as dkdv_kernel (sdpa_bwd.hip): dV = P^T dO and dK = scale dS^T Q with
+// P = exp(scale Q K^T - lse) rebuilt from the saved row statistic and dS = P o (dO V^T - delta)
+// (reference theria/attention/triton_sdpa_backward.py:106-266 and 269-462). It is used when the head
+// dim is exactly 64 and every view allows 16-byte access; the general kernel covers the rest.
+//
+// Work decomposition: one workgroup = NW waves, each owning 32 keys (K and V fragments in registers,
+// dK and dV accumulated in registers); the workgroup streams the query tiles (64 rows) of its head.
+//  * Q and dO tiles reach LDS by DMA (sdpa_lds.hpp) into double buffers with one barrier per tile;
+//    the row terms lse * log2(e) and -delta of the next tile are loaded by the first 64 threads during
+//    the current tile and written beside them.
+//  * Scores are S = Q K^T with this lane's key in the column, so dV += P^T dO and dK += dS^T Q take
+//    P and dS straight from the accumulators (KACC order) and dO^T / Q^T from LDS transpose reads.
+//  * Phase order per tile of two 32-query subtiles (scheduling barriers keep it):
+//      S, dP of subtile 0 | S, dP of subtile 1 with exp / dS of subtile 0
+//      | dV, dK of subtile 0 with exp / dS of subtile 1 | dV, dK of subtile 1.
+//  * dP starts from -delta as the MFMA accumulator input, so dS = P o dP is one multiply.
+#include <type_traits>
+
+#include "sdpa_common.hpp"
+#include "sdpa_lds.hpp"
+#include "sdpa_params.hpp"
+
+namespace theria {
+
+template <typename T, bool CAUSAL, int NW>
+__global__ __launch_bounds__(64 * NW, 2) void dkdv_pipe_kernel(const DkdvParams p) {
+  using MM = Mfma<T>;
+  using F = typename MM::frag_t;
+  constexpr int BN = 32 * NW, BM = 64, TILE = BM * SWZ_ROW_BYTES, NSLAB = BM / (8 * NW);
+  __shared__ __attribute__((aligned(1024))) char sQ0[TILE];
+  __shared__ __attribute__((aligned(1024))) char sQ1[TILE];
+  __shared__ __attribute__((aligned(1024))) char sO0[TILE];
+  __shared__ __attribute__((aligned(1024))) char sO1[TILE];
+  __shared__ __attribute__((aligned(16))) float sR0[2 * BM];  // [lse * log2(e) | -delta] of a tile
+  __shared__ __attribute__((aligned(16))) float sR1[2 * BM];
+
+  const Shape& s = p.s;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, li = lane & 31, g = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nkb = (s.M + BN - 1) / BN;
+  const int bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int bh = bid / nkb;
+  const int kb = bid - bh * nkb;  // causal: ascending key blocks = longest query ranges first
+  const int b = bh / s.H, h = bh - b * s.H;
+  const T* Q = (const T*)p.q.p + b * p.q.sb + h * p.q.sh;
+  const T* K = (const T*)p.k.p + b * p.k.sb + h * p.k.sh;
+  const T* V = (const T*)p.v.p + b * p.v.sb + h * p.v.sh;
+  const T* dO = (const T*)p.dout.p + b * p.dout.sb + h * p.dout.sh;
+  const int key0 = kb * BN;
+  const int kw0 = key0 + wave * 32;  // this wave's keys: kw0 + li
+  const int64_t rowbase = (int64_t)bh * s.T;
+  const float c2 = s.scale * kLog2e;
+
+  F kf[4], vf[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    kf[c] = gload_frag<T>(K, p.k.sr, kw0 + li, s.M, c, 64, true);
+    vf[c] = gload_frag<T>(V, p.v.sr, kw0 + li, s.M, c, 64, true);
+  }
+  f32x16_t dv[2], dk[2];
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt) {
+    dv[dt] = zero16();
+    dk[dt] = zero16();
+  }
+
+  const int qbeg = CAUSAL ? (key0 / BM) * BM : 0;
+  const int nqt = s.T > qbeg ? (s.T - qbeg + BM - 1) / BM : 0;
+  // Tiles with every query in range and (causal) every key of the block visible to every query,
+  // in a key block whose keys are all in range, take the unmasked path.
+  // Causal: tiles before ifull straddle the diagonal (q0 < last key of the block). Full tiles end at fend.
+  const int ifull = CAUSAL ? min(nqt, (key0 + BN - 1 - qbeg + BM - 1) / BM) : 0;
+  const int fend = (key0 + BN <= s.M) ? max(ifull, min(nqt, (s.T - qbeg) / BM)) : ifull;
+
+  const SwzDma<NW> dma(wave, lane);
+  const uint32_t qrs = (uint32_t)p.q.sr * 2, ors = (uint32_t)p.dout.sr * 2;
+  const rsrc_t qrsrc = make_rsrc(Q, (uint32_t)s.T * qrs);
+  const rsrc_t orsrc = make_rsrc(dO, (uint32_t)s.T * ors);
+
+  // Row terms of tile `it` for thread tid < BM: lse * log2(e) (rows past the end or without visible
+  // keys: +inf, so P = 0) and -delta.
+  float r_lse = THERIA_INF, r_del = 0.f;
+  auto load_rows = [&](int it) {
+    if (tid < BM && it < nqt) {
+      const int qq = qbeg + it * BM + tid;
+      const float l2 = qq < s.T ? p.lse[rowbase + qq] * kLog2e : THERIA_INF;
+      r_lse = l2 == -THERIA_INF ? THERIA_INF : l2;
+      r_del = qq < s.T ? -p.delta[rowbase + qq] : 0.f;
+    }
+  };
+  auto store_rows = [&](float* sr) {
+    if (tid < BM) {
+      sr[tid] = r_lse;
+      sr[BM + tid] = r_del;
+    }
+  };
+
+  // S = Q K^T and dP = dO V^T - delta for subtile qs (32 queries) of the tile in (tq, to, tr).
+  auto sdp = [&](const char* tq, const char* to, const float* tr, int qs, f32x16_t& sc, f32x16_t& dp) {
+    sc = zero16();
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(tr + BM + 32 * qs + 8 * qd + 4 * g);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dp[4 * qd + e] = d4[e];
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      sc = MM::mma(swz_cols<T>(tq, 32 * qs + li, c), kf[c], sc);
+      dp = MM::mma(swz_cols<T>(to, 32 * qs + li, c), vf[c], dp);
+    }
+  };
+  // Masks of a general tile: keys out of range and (causal) keys after the query get S = -inf.
+  auto mask = [&](f32x16_t& sc, int q0s) {
+    const int mykey = kw0 + li;
+    if (kw0 + 31 >= s.M || (CAUSAL && kw0 + 31 > q0s)) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (mykey >= s.M || (CAUSAL && mykey > q0s + acc_row(r, g))) sc[r] = -THERIA_INF;
+    }
+  };
+  // P = exp2(S c2 - lse2) and dS = P o dP as 16-bit fragments (KACC chunks 0, 1).
+  auto pds = [&](const float* tr, int qs, const f32x16_t& sc, const f32x16_t& dp, F (&pf)[2], F (&df)[2]) {
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(tr + 32 * qs + 8 * qd + 4 * g);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = 4 * qd + e;
+        const float pv = fast_exp2(fmaf(sc[r], c2, -l4[e]));
+        pf[r >> 3][r & 7] = (T)pv;
+        df[r >> 3][r & 7] = (T)(pv * dp[r]);
+      }
+    }
+  };
+  // dV += P^T dO and dK += dS^T Q for subtile qs.
+  auto dvdk = [&](const char* tq, const char* to, int qs, const F (&pf)[2], const F (&df)[2]) {
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) {
+        dv[dt] = MM::mma(pf[cc], swz_rows<T>(to, 32 * qs, cc, 32 * dt), dv[dt]);
+        dk[dt] = MM::mma(df[cc], swz_rows<T>(tq, 32 * qs, cc, 32 * dt), dk[dt]);
+      }
+  };
+
+  // One query tile `it` from buffers (tq, to, tr); the next tile goes to (nq, no, nr).
+  auto step = [&](auto fast_tag, int it, const char* tq, const char* to, const float* tr, char* nq, char* no,
+                  float* nr) {
+    constexpr bool FAST = decltype(fast_tag)::value;
+    const int q0 = qbeg + it * BM;
+    wait_vm_all();
+    __syncthreads();  // tile it visible to all waves; the other buffers (tile it-1) are free
+    if (it + 1 < nqt) {
+      dma.template issue_clamped<NSLAB>(qrsrc, qrs, q0 + BM, s.T, nq);
+      dma.template issue_clamped<NSLAB>(orsrc, ors, q0 + BM, s.T, no);
+      store_rows(nr);
+      load_rows(it + 2);
+    }
+    if constexpr (FAST) {
+      f32x16_t s0, p0, s1, p1;
+      F pf0[2], df0[2], pf1[2], df1[2];
+      sdp(tq, to, tr, 0, s0, p0);
+      __builtin_amdgcn_sched_barrier(0);
+      sdp(tq, to, tr, 1, s1, p1);
+      pds(tr, 0, s0, p0, pf0, df0);
+      __builtin_amdgcn_sched_barrier(0);
+      dvdk(tq, to, 0, pf0, df0);
+      pds(tr, 1, s1, p1, pf1, df1);
+      __builtin_amdgcn_sched_barrier(0);
+      dvdk(tq, to, 1, pf1, df1);
+    } else {
+#pragma unroll
+      for (int qs = 0; qs < 2; ++qs) {
+        const int q0s = q0 + 32 * qs;
+        if (q0s >= s.T || (CAUSAL && kw0 > q0s + 31)) continue;  // wave-uniform
+        f32x16_t sc, dp;
+        F pf[2], df[2];
+        sdp(tq, to, tr, qs, sc, dp);
+        mask(sc, q0s);
+        pds(tr, qs, sc, dp, pf, df);
+        dvdk(tq, to, qs, pf, df);
+      }
+    }
+  };
+  const std::integral_constant<bool, true> fast;
+  const std::integral_constant<bool, false> general;
+
+  if (nqt > 0) {
+    dma.template issue_clamped<NSLAB>(qrsrc, qrs, qbeg, s.T, sQ0);
+    dma.template issue_clamped<NSLAB>(orsrc, ors, qbeg, s.T, sO0);
+    load_rows(0);
+    wait_vm_all();
+    store_rows(sR0);
+    load_rows(1);
+    int it = 0;
+    // causal diagonal tiles first (general), then the full tiles two at a time (fixed buffers), then the rest
+    for (; it < ifull; ++it) {
+      if (it & 1)
+        step(general, it, sQ1, sO1, sR1, sQ0, sO0, sR0);
+      else
+        step(general, it, sQ0, sO0, sR0, sQ1, sO1, sR1);
+    }
+    if (it < fend && (it & 1)) {
+      step(fast, it, sQ1, sO1, sR1, sQ0, sO0, sR0);
+      ++it;
+    }
+    for (; it + 1 < fend; it += 2) {
+      step(fast, it, sQ0, sO0, sR0, sQ1, sO1, sR1);
+      step(fast, it + 1, sQ1, sO1, sR1, sQ0, sO0, sR0);
+    }
+    for (; it < nqt; ++it) {
+      if (it & 1)
+        step(general, it, sQ1, sO1, sR1, sQ0, sO0, sR0);
+      else
+        step(general, it, sQ0, sO0, sR0, sQ1, sO1, sR1);
+    }
+  }
+
+  // Epilogue: lane holds column d = dt*32 + li of keys kw0 + acc_row(r, g).
+  T* DV = (T*)p.dv.p + b * p.dv.sb + h * p.dv.sh;
+  T* DK = p.dk.p ? (T*)p.dk.p + b * p.dk.sb + h * p.dk.sh : nullptr;
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt) {
+    const int d = dt * 32 + li;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = kw0 + acc_row(r, g);
+      if (key < s.M) {
+        DV[(int64_t)key * p.dv.sr + d] = (T)dv[dt][r];
+        if (DK) DK[(int64_t)key * p.dk.sr + d] = (T)(dk[dt][r] * s.scale);
+      }
+    }
+  }
+}
+
+// Launch if the pipelined kernel covers this problem (16-bit, head dim 64, vector access, dK and dV
+// both wanted); returns false otherwise.
+template <typename T, bool CAUSAL>
+bool launch_dkdv_pipe(const DkdvParams& p, hipStream_t st, hipError_t* err) {
+  if (!(p.s.D == 64 && p.s.vec && !p.dv_only)) return false;
+  // 32-bit byte offsets inside each (batch, head) slab of Q and dO
+  if ((int64_t)p.s.T * p.q.sr * 2 >= (int64_t(1) << 31) || (int64_t)p.s.T * p.dout.sr * 2 >= (int64_t(1) << 31))
+    return false;
+  const int64_t bh = (int64_t)p.s.B * p.s.H;
+  const int64_t nblk = (int64_t)((p.s.M + 127) / 128) * bh;
+  if (nblk == 0) {
+    *err = hipSuccess;
+    return true;
+  }
+  hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, 4>), dim3((unsigned)nblk), dim3(256), 0, st, p);
+  *err = hipGetLastError();
+  return true;
+}
+
+template bool launch_dkdv_pipe<__bf16, false>(const DkdvParams&, hipStream_t, hipError_t*);
+template bool launch_dkdv_pipe<__bf16, true>(const DkdvParams&, hipStream_t, hipError_t*);
+template bool launch_dkdv_pipe<_Float16, false>(const DkdvParams&, hipStream_t, hipError_t*);
+template bool launch_dkdv_pipe<_Float16, true>(const DkdvParams&, hipStream_t, hipError_t*);
+
+}  // namespace theria
