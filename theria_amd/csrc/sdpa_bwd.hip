@@ -377,9 +377,17 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DKDV_MINW : 1)) void dkdv_kernel(c
     }
 }
 
+// Pipelined 16-bit head-dim-64 dQ (sdpa_bwd_pipe.hip); false when it does not cover the problem.
+template <typename T, bool CAUSAL>
+bool launch_dq_pipe(const DqParams& p, hipStream_t st, hipError_t* err);
+
 struct DqLauncher {
   template <typename T, int DP, bool CAUSAL>
   static hipError_t run(const DqParams& p, hipStream_t st) {
+    if constexpr (sizeof(T) == 2 && DP == 64) {
+      hipError_t err;
+      if (launch_dq_pipe<T, CAUSAL>(p, st, &err)) return err;
+    }
     const int qt = (DQ_QT_MAX >= 2 && DP <= 64 && p.s.T > 128) ? 2 : 1;
     const int bm = 128 * qt;
     const int64_t nblk = (int64_t)((p.s.T + bm - 1) / bm) * p.s.B * p.s.H;

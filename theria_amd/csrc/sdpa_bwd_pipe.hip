@@ -1,6 +1,6 @@
-// Pipelined dK/dV pass of the SDPA backward for 16-bit inputs with head_dim 64 on gfx950.
+// Pipelined dQ and dK/dV passes of the SDPA backward for 16-bit inputs with head_dim 64 on gfx950.
 //
-// Same contract as dkdv_kernel (sdpa_bwd.hip): dV = P^T dO and dK = scale dS^T Q with
+// dkdv_pipe_kernel has the contract of dkdv_kernel (sdpa_bwd.hip): dV = P^T dO and dK = scale dS^T Q with
 // P = exp(scale Q K^T - lse) rebuilt from the saved row statistic and dS = P o (dO V^T - delta)
 // (reference theria/attention/triton_sdpa_backward.py:106-266 and 269-462). It is used when the head
 // dim is exactly 64 and every view allows 16-byte access; the general kernel covers the rest.
@@ -236,6 +236,216 @@ __global__ __launch_bounds__(64 * NW, 2) void dkdv_pipe_kernel(const DkdvParams 
     }
   }
 }
+
+// dQ pass with the contract of dq_kernel (sdpa_bwd.hip): dQ = scale dS K with dS = P o (dO V^T - delta)
+// (reference triton_sdpa_backward.py:505-696), and delta = rowsum(dO o O) computed here when O is given.
+// One workgroup = NW waves of 32 queries each (Q and dO fragments, dQ accumulated in registers); K and V
+// tiles of 64 keys stream through DMA-filled swizzled double buffers, one barrier per tile. Scores are
+// transposed (S^T = K Q^T, this lane's query in the column), so lse and delta are per-lane scalars and
+// dQ^T += K^T dS^T takes dS^T from the accumulators. Phase order per key tile of two 32-key subtiles:
+//   S, dP of subtile 0 | S, dP of subtile 1 with exp / dS of subtile 0
+//   | dQ of subtile 0 with exp / dS of subtile 1 | dQ of subtile 1.
+template <typename T, bool CAUSAL, int NW>
+__global__ __launch_bounds__(64 * NW, 2) void dq_pipe_kernel(const DqParams p) {
+  using MM = Mfma<T>;
+  using F = typename MM::frag_t;
+  constexpr int BM = 32 * NW, BN = 64, TILE = BN * SWZ_ROW_BYTES, NSLAB = BN / (8 * NW);
+  __shared__ __attribute__((aligned(1024))) char sK0[TILE];
+  __shared__ __attribute__((aligned(1024))) char sK1[TILE];
+  __shared__ __attribute__((aligned(1024))) char sV0[TILE];
+  __shared__ __attribute__((aligned(1024))) char sV1[TILE];
+
+  const Shape& s = p.s;
+  const int lane = threadIdx.x & 63, li = lane & 31, g = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nqb = (s.T + BM - 1) / BM;
+  const int bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int bh = bid / nqb;
+  int qb = bid - bh * nqb;
+  if (CAUSAL) qb = nqb - 1 - qb;  // longest rows first
+  const int b = bh / s.H, h = bh - b * s.H;
+  const T* Q = (const T*)p.q.p + b * p.q.sb + h * p.q.sh;
+  const T* K = (const T*)p.k.p + b * p.k.sb + h * p.k.sh;
+  const T* V = (const T*)p.v.p + b * p.v.sb + h * p.v.sh;
+  const T* dO = (const T*)p.dout.p + b * p.dout.sb + h * p.dout.sh;
+  const int q0w = qb * BM + wave * 32;
+  const int myq = q0w + li;
+  const bool qvalid = myq < s.T;
+  const int64_t rowbase = (int64_t)bh * s.T;
+
+  F qf[4], of[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    qf[c] = gload_frag<T>(Q, p.q.sr, myq, s.T, c, 64, true);
+    of[c] = gload_frag<T>(dO, p.dout.sr, myq, s.T, c, 64, true);
+  }
+  const float l2 = qvalid ? p.lse[rowbase + myq] * kLog2e : THERIA_INF;
+  const float lse2 = l2 == -THERIA_INF ? THERIA_INF : l2;  // a row without visible keys has P = 0
+  float del;
+  if (p.o.p) {
+    // delta = dO . O over this lane's half of the head dim (the dO fragment's columns), then the pair
+    float part = 0.f;
+    if (qvalid) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int col = c * 16 + 8 * g;
+        const int64_t off = (int64_t)myq * p.o.sr + col;
+        if (p.o_f32) {
+          const float* Op = (const float*)p.o.p + b * p.o.sb + h * p.o.sh + off;
+          const f32x4_t a0 = *reinterpret_cast<const f32x4_t*>(Op);
+          const f32x4_t a1 = *reinterpret_cast<const f32x4_t*>(Op + 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) part += a0[e] * (float)of[c][e] + a1[e] * (float)of[c][4 + e];
+        } else {
+          const F ov = __builtin_bit_cast(F, *reinterpret_cast<const i16x8_t*>((const T*)p.o.p + b * p.o.sb +
+                                                                             h * p.o.sh + off));
+#pragma unroll
+          for (int e = 0; e < 8; ++e) part += (float)ov[e] * (float)of[c][e];
+        }
+      }
+    }
+    del = pair_sum(part);
+    if (qvalid && g == 0) p.delta[rowbase + myq] = del;
+  } else {
+    del = qvalid ? p.delta[rowbase + myq] : 0.f;
+  }
+  if (!p.dq.p) return;  // only the row term was requested (uniform over the grid)
+
+  f32x16_t acc[2];
+  acc[0] = zero16();
+  acc[1] = zero16();
+  const float c2 = s.scale * kLog2e;
+
+  int kend = s.M;
+  if (CAUSAL) kend = min(s.M, qb * BM + BM);
+  const int nkt = (kend + BN - 1) / BN;
+  // Tiles [0, nfull) have every key in range and visible to every query of the block.
+  int nfull = s.M / BN;
+  if (CAUSAL) nfull = min(nfull, qb * BM / BN);
+
+  const SwzDma<NW> dma(wave, lane);
+  const uint32_t krs = (uint32_t)p.k.sr * 2, vrs = (uint32_t)p.v.sr * 2;
+  const rsrc_t krsrc = make_rsrc(K, (uint32_t)s.M * krs);
+  const rsrc_t vrsrc = make_rsrc(V, (uint32_t)s.M * vrs);
+
+  // S^T = K Q^T and dP^T = V dO^T - delta for key subtile t of the tile in (tk, tv).
+  auto sdp = [&](const char* tk, const char* tv, int t, f32x16_t& sc, f32x16_t& dp) {
+    sc = zero16();
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dp[r] = -del;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      sc = MM::mma(swz_cols<T>(tk, 32 * t + li, c), qf[c], sc);
+      dp = MM::mma(swz_cols<T>(tv, 32 * t + li, c), of[c], dp);
+    }
+  };
+  auto mask = [&](f32x16_t& sc, int k0t) {
+    if ((k0t + 32 > s.M) || (CAUSAL && k0t + 31 > q0w)) {
+      const int lim = CAUSAL ? min(s.M, myq + 1) : s.M;  // first key this query cannot see
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (k0t + acc_row(r, g) >= lim) sc[r] = -THERIA_INF;
+    }
+  };
+  // dS^T = P^T o dP^T as 16-bit fragments (KACC chunks 0, 1)
+  auto pds = [&](const f32x16_t& sc, const f32x16_t& dp, F (&df)[2]) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) df[r >> 3][r & 7] = (T)(fast_exp2(fmaf(sc[r], c2, -lse2)) * dp[r]);
+  };
+  auto dqm = [&](const char* tk, int t, const F (&df)[2]) {
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) acc[dt] = MM::mma(swz_rows<T>(tk, 32 * t, cc, 32 * dt), df[cc], acc[dt]);
+  };
+
+  auto step = [&](auto fast_tag, int k, const char* tk, const char* tv, char* nk, char* nv) {
+    constexpr bool FAST = decltype(fast_tag)::value;
+    const int k0 = k * BN;
+    wait_vm_all();
+    __syncthreads();  // tile k visible to all waves; the other buffers (tile k-1) are free
+    if (k + 1 < nkt) {
+      dma.template issue_clamped<NSLAB>(krsrc, krs, k0 + BN, s.M, nk);
+      dma.template issue_clamped<NSLAB>(vrsrc, vrs, k0 + BN, s.M, nv);
+    }
+    if constexpr (FAST) {
+      f32x16_t s0, p0, s1, p1;
+      F d0[2], d1[2];
+      sdp(tk, tv, 0, s0, p0);
+      __builtin_amdgcn_sched_barrier(0);
+      sdp(tk, tv, 1, s1, p1);
+      pds(s0, p0, d0);
+      __builtin_amdgcn_sched_barrier(0);
+      dqm(tk, 0, d0);
+      pds(s1, p1, d1);
+      __builtin_amdgcn_sched_barrier(0);
+      dqm(tk, 1, d1);
+    } else {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int k0t = k0 + 32 * t;
+        if (CAUSAL && k0t > q0w + 31) continue;  // every key after every query of the wave (uniform)
+        f32x16_t sc, dp;
+        F df[2];
+        sdp(tk, tv, t, sc, dp);
+        mask(sc, k0t);
+        pds(sc, dp, df);
+        dqm(tk, t, df);
+      }
+    }
+  };
+  const std::integral_constant<bool, true> fast;
+  const std::integral_constant<bool, false> general;
+
+  if (nkt > 0) {
+    dma.template issue_clamped<NSLAB>(krsrc, krs, 0, s.M, sK0);
+    dma.template issue_clamped<NSLAB>(vrsrc, vrs, 0, s.M, sV0);
+    int k = 0;
+    for (; k + 1 < nfull; k += 2) {
+      step(fast, k, sK0, sV0, sK1, sV1);
+      step(fast, k + 1, sK1, sV1, sK0, sV0);
+    }
+    for (; k < nkt; ++k) {
+      if (k & 1)
+        step(general, k, sK1, sV1, sK0, sV0);
+      else
+        step(general, k, sK0, sV0, sK1, sV1);
+    }
+  }
+
+  if (qvalid) {
+    T* DQ = (T*)p.dq.p + b * p.dq.sb + h * p.dq.sh;
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const int d0 = dt * 32 + 8 * qd + 4 * g;
+        const f32x16_t& a = acc[dt];
+        store4<T>(DQ, p.dq.sr, myq, d0, 64, a[4 * qd] * s.scale, a[4 * qd + 1] * s.scale, a[4 * qd + 2] * s.scale,
+                  a[4 * qd + 3] * s.scale, true);
+      }
+  }
+}
+
+template <typename T, bool CAUSAL>
+bool launch_dq_pipe(const DqParams& p, hipStream_t st, hipError_t* err) {
+  if (!(p.s.D == 64 && p.s.vec)) return false;
+  // 32-bit byte offsets inside each (batch, head) slab of K and V
+  if ((int64_t)p.s.M * p.k.sr * 2 >= (int64_t(1) << 31) || (int64_t)p.s.M * p.v.sr * 2 >= (int64_t(1) << 31)) return false;
+  const int64_t nblk = (int64_t)((p.s.T + 127) / 128) * p.s.B * p.s.H;
+  if (nblk == 0) {
+    *err = hipSuccess;
+    return true;
+  }
+  hipLaunchKernelGGL((dq_pipe_kernel<T, CAUSAL, 4>), dim3((unsigned)nblk), dim3(256), 0, st, p);
+  *err = hipGetLastError();
+  return true;
+}
+
+template bool launch_dq_pipe<__bf16, false>(const DqParams&, hipStream_t, hipError_t*);
+template bool launch_dq_pipe<__bf16, true>(const DqParams&, hipStream_t, hipError_t*);
+template bool launch_dq_pipe<_Float16, false>(const DqParams&, hipStream_t, hipError_t*);
+template bool launch_dq_pipe<_Float16, true>(const DqParams&, hipStream_t, hipError_t*);
 
 // Launch if the pipelined kernel covers this problem (16-bit, head dim 64, vector access, dK and dV
 // both wanted); returns false otherwise.
