@@ -33,32 +33,62 @@ def _rowmajor(t: torch.Tensor | None) -> torch.Tensor | None:
     return t
 
 
+_functorch = None
+
+
 def _plain(t: torch.Tensor) -> torch.Tensor:
     """Underlying tensor of a torch.func (functorch) wrapper, whose storage the kernels read.
 
     torch.func.jvp calls SDPAOp.jvp with its saved tensors wrapped for gradient tracking; the values
     are those of the wrapped tensor.
     """
-    from torch._C._functorch import get_unwrapped, is_functorch_wrapped_tensor
+    global _functorch
+    if _functorch is None:
+        from torch._C import _functorch as ft
 
-    while is_functorch_wrapped_tensor(t):
-        t = get_unwrapped(t)
+        _functorch = (ft.is_functorch_wrapped_tensor, ft.get_unwrapped)
+    is_wrapped, unwrap = _functorch
+    while is_wrapped(t):
+        t = unwrap(t)
     return t
 
 
 def _tv(t: torch.Tensor | None):
+    """theria_tensor_t of a (B,H,rows,D) tensor (ctypes passes it by reference), or NULL."""
     if t is None:
         return None
     t = _plain(t)
-    return ctypes.byref(_lib.TensorView(t.data_ptr(), t.stride(0), t.stride(1), t.stride(2)))
+    return _lib.TensorView(t.data_ptr(), t.stride(0), t.stride(1), t.stride(2))
 
 
 def _fp(t: torch.Tensor | None):
-    return None if t is None else ctypes.c_void_p(_plain(t).data_ptr())
+    return None if t is None else _plain(t).data_ptr()
 
 
 def _stream(dev: torch.device):
-    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    """Raw hipStream_t of torch's current stream on `dev`."""
+    return torch._C._cuda_getCurrentRawStream(dev.index if dev.index is not None else torch.cuda.current_device())
+
+
+class _OnDevice:
+    """Make `dev` the current device for the duration of a launch (a no-op when it already is)."""
+
+    __slots__ = ("idx", "prev")
+
+    def __init__(self, dev: torch.device):
+        self.idx = dev.index if dev.index is not None else torch.cuda.current_device()
+        self.prev = None
+
+    def __enter__(self):
+        cur = torch.cuda.current_device()
+        if cur != self.idx:
+            self.prev = cur
+            torch.cuda.set_device(self.idx)
+
+    def __exit__(self, *exc):
+        if self.prev is not None:
+            torch.cuda.set_device(self.prev)
+        return False
 
 
 def _problem(q: torch.Tensor, k: torch.Tensor, scale: float, causal: bool) -> _lib.Problem:
@@ -125,7 +155,7 @@ def fwd(q, k, v, scale: float, causal: bool, out_fp32: bool = False, stats: bool
     l = torch.empty_like(lse) if stats else None
     lib = _lib.load()
     prob = _problem(q, k, scale, causal)
-    with torch.cuda.device(dev):
+    with _OnDevice(dev):
         rc = lib.theria_sdpa_fwd(
             ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(o), 1 if out_fp32 else 0, _fp(lse), _fp(m), _fp(l),
             _stream(dev),
@@ -154,7 +184,7 @@ def bwd(q, k, v, o, lse, do, scale: float, causal: bool, need_dq: bool = True, n
     dk = torch.empty((B, H, M, D), dtype=q.dtype, device=dev) if need_dk else None
     dv = torch.empty((B, H, M, D), dtype=q.dtype, device=dev)
     prob = _problem(q, k, scale, causal)
-    with torch.cuda.device(dev):
+    with _OnDevice(dev):
         bwd_dq(prob, q, k, v, o, o_f32, do, lse, delta, dq)
         bwd_dkdv(prob, q, k, v, do, lse, delta, dk, dv)
     return dq, dk, dv, delta
@@ -194,7 +224,7 @@ def bwd_from_stats(q, k, v, do, lse, scale: float, causal: bool, need_dq: bool, 
     dv = torch.empty((B, H, M, D), dtype=q.dtype, device=dev)
     lib = _lib.load()
     prob = _problem(q, k, scale, causal)
-    with torch.cuda.device(dev):
+    with _OnDevice(dev):
         rc = lib.theria_sdpa_bwd_from_stats(
             ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(do), _fp(lse), _fp(delta), _tv(dq), _tv(dk), _tv(dv),
             _stream(dev),
@@ -222,7 +252,7 @@ def jvp(q, k, v, o, lse, tq, tk, tv, scale: float, causal: bool):
     out = torch.empty((B, H, T, D), dtype=q.dtype, device=dev)
     lib = _lib.load()
     prob = _problem(q, k, scale, causal)
-    with torch.cuda.device(dev):
+    with _OnDevice(dev):
         rc = lib.theria_sdpa_jvp(
             ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(o), _fp(lse), _tv(tq), _tv(tk), _tv(tv), _tv(out),
             _stream(dev),
@@ -253,7 +283,7 @@ def bwd_bwd(q, k, v, o, do, lse, delta, gq, gk, gv, scale: float, causal: bool):
     ws = torch.empty((2 * B * H * T,), dtype=torch.float32, device=dev)
     lib = _lib.load()
     prob = _problem(q, k, scale, causal)
-    with torch.cuda.device(dev):
+    with _OnDevice(dev):
         rc = lib.theria_sdpa_bwd_bwd(
             ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(o), _tv(do), _fp(lse), _fp(delta), _tv(gq), _tv(gk),
             _tv(gv), _tv(out_q), _tv(out_k), _tv(out_v), _tv(out_do), _fp(ws), _stream(dev),

@@ -22,6 +22,14 @@
 #include "sdpa_lds.hpp"
 #include "sdpa_params.hpp"
 
+// Waves per workgroup (compile-time knobs; the defaults are the measured best on MI355X).
+#ifndef DQ_PIPE_NW
+#define DQ_PIPE_NW 4
+#endif
+#ifndef DKDV_PIPE_NW
+#define DKDV_PIPE_NW 4
+#endif
+
 namespace theria {
 
 template <typename T, bool CAUSAL, int NW>
@@ -432,12 +440,13 @@ bool launch_dq_pipe(const DqParams& p, hipStream_t st, hipError_t* err) {
   if (!(p.s.D == 64 && p.s.vec)) return false;
   // 32-bit byte offsets inside each (batch, head) slab of K and V
   if ((int64_t)p.s.M * p.k.sr * 2 >= (int64_t(1) << 31) || (int64_t)p.s.M * p.v.sr * 2 >= (int64_t(1) << 31)) return false;
-  const int64_t nblk = (int64_t)((p.s.T + 127) / 128) * p.s.B * p.s.H;
+  constexpr int NW = DQ_PIPE_NW;
+  const int64_t nblk = (int64_t)((p.s.T + 32 * NW - 1) / (32 * NW)) * p.s.B * p.s.H;
   if (nblk == 0) {
     *err = hipSuccess;
     return true;
   }
-  hipLaunchKernelGGL((dq_pipe_kernel<T, CAUSAL, 4>), dim3((unsigned)nblk), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((dq_pipe_kernel<T, CAUSAL, NW>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p);
   *err = hipGetLastError();
   return true;
 }
@@ -455,13 +464,13 @@ bool launch_dkdv_pipe(const DkdvParams& p, hipStream_t st, hipError_t* err) {
   // 32-bit byte offsets inside each (batch, head) slab of Q and dO
   if ((int64_t)p.s.T * p.q.sr * 2 >= (int64_t(1) << 31) || (int64_t)p.s.T * p.dout.sr * 2 >= (int64_t(1) << 31))
     return false;
-  const int64_t bh = (int64_t)p.s.B * p.s.H;
-  const int64_t nblk = (int64_t)((p.s.M + 127) / 128) * bh;
+  constexpr int NW = DKDV_PIPE_NW;
+  const int64_t nblk = (int64_t)((p.s.M + 32 * NW - 1) / (32 * NW)) * p.s.B * p.s.H;
   if (nblk == 0) {
     *err = hipSuccess;
     return true;
   }
-  hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, 4>), dim3((unsigned)nblk), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, NW>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p);
   *err = hipGetLastError();
   return true;
 }
