@@ -384,7 +384,7 @@ bool launch_dq_pipe(const DqParams& p, hipStream_t st, hipError_t* err);
 struct DqLauncher {
   template <typename T, int DP, bool CAUSAL>
   static hipError_t run(const DqParams& p, hipStream_t st) {
-    if constexpr (sizeof(T) == 2 && DP == 64) {
+    if constexpr (sizeof(T) == 2 && DP >= 64) {
       hipError_t err;
       if (launch_dq_pipe<T, CAUSAL>(p, st, &err)) return err;
     }
@@ -417,7 +417,7 @@ struct DkdvLauncher {
   }
   template <typename T, int DP, bool CAUSAL>
   static hipError_t run(const DkdvParams& p, hipStream_t st) {
-    if constexpr (sizeof(T) == 2 && DP == 64) {
+    if constexpr (sizeof(T) == 2 && DP >= 64) {
       hipError_t err;
       if (launch_dkdv_pipe<T, CAUSAL>(p, st, &err)) return err;
     }

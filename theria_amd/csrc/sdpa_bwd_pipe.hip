@@ -1,9 +1,9 @@
-// Pipelined dQ and dK/dV passes of the SDPA backward for 16-bit inputs with head_dim 64 on gfx950.
+// Pipelined dQ and dK/dV passes of the SDPA backward for 16-bit inputs with head_dim 64 or 128 on gfx950.
 //
 // dkdv_pipe_kernel has the contract of dkdv_kernel (sdpa_bwd.hip): dV = P^T dO and dK = scale dS^T Q with
 // P = exp(scale Q K^T - lse) rebuilt from the saved row statistic and dS = P o (dO V^T - delta)
 // (reference theria/attention/triton_sdpa_backward.py:106-266 and 269-462). It is used when the head
-// dim is exactly 64 and every view allows 16-byte access; the general kernel covers the rest.
+// dim is 64 or 128 and every view allows 16-byte access; the general kernel covers the rest.
 //
 // Work decomposition: one workgroup = NW waves, each owning 32 keys (K and V fragments in registers,
 // dK and dV accumulated in registers); the workgroup streams the query tiles (64 rows) of its head.
@@ -29,14 +29,31 @@
 #ifndef DKDV_PIPE_NW
 #define DKDV_PIPE_NW 4
 #endif
+// Head dim 128: subtile overlap and waves per SIMD
+#ifndef DQ128_OVERLAP
+#define DQ128_OVERLAP true
+#endif
+#ifndef DQ128_WPS
+#define DQ128_WPS 1
+#endif
+#ifndef DKDV128_OVERLAP
+#define DKDV128_OVERLAP true
+#endif
+#ifndef DKDV128_WPS
+#define DKDV128_WPS 1
+#endif
 
 namespace theria {
 
-template <typename T, bool CAUSAL, int NW>
-__global__ __launch_bounds__(64 * NW, 2) void dkdv_pipe_kernel(const DkdvParams p) {
+template <typename T, bool CAUSAL, int NW, int DP, bool OVERLAP, int WPS>
+__global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
-  constexpr int BN = 32 * NW, BM = 64, TILE = BM * SWZ_ROW_BYTES, NSLAB = BM / (8 * NW);
+  using Dma = SwzDma<NW, DP>;
+  constexpr int NKC = DP / 16, NDT = DP / 32;
+  constexpr int BN = 32 * NW, BM = 64, TILE = BM * 2 * DP, NSLAB = BM / Dma::SLAB_ROWS;
+  // OVERLAP: the exp / dS work of one subtile overlaps the products of the next (more live registers);
+  // otherwise subtiles run one after the other. WPS: waves per SIMD the register budget is sized for.
   __shared__ __attribute__((aligned(1024))) char sQ0[TILE];
   __shared__ __attribute__((aligned(1024))) char sQ1[TILE];
   __shared__ __attribute__((aligned(1024))) char sO0[TILE];
@@ -62,15 +79,15 @@ __global__ __launch_bounds__(64 * NW, 2) void dkdv_pipe_kernel(const DkdvParams 
   const int64_t rowbase = (int64_t)bh * s.T;
   const float c2 = s.scale * kLog2e;
 
-  F kf[4], vf[4];
+  F kf[NKC], vf[NKC];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    kf[c] = gload_frag<T>(K, p.k.sr, kw0 + li, s.M, c, 64, true);
-    vf[c] = gload_frag<T>(V, p.v.sr, kw0 + li, s.M, c, 64, true);
+  for (int c = 0; c < NKC; ++c) {
+    kf[c] = gload_frag<T>(K, p.k.sr, kw0 + li, s.M, c, DP, true);
+    vf[c] = gload_frag<T>(V, p.v.sr, kw0 + li, s.M, c, DP, true);
   }
-  f32x16_t dv[2], dk[2];
+  f32x16_t dv[NDT], dk[NDT];
 #pragma unroll
-  for (int dt = 0; dt < 2; ++dt) {
+  for (int dt = 0; dt < NDT; ++dt) {
     dv[dt] = zero16();
     dk[dt] = zero16();
   }
@@ -83,7 +100,7 @@ __global__ __launch_bounds__(64 * NW, 2) void dkdv_pipe_kernel(const DkdvParams 
   const int ifull = CAUSAL ? min(nqt, (key0 + BN - 1 - qbeg + BM - 1) / BM) : 0;
   const int fend = (key0 + BN <= s.M) ? max(ifull, min(nqt, (s.T - qbeg) / BM)) : ifull;
 
-  const SwzDma<NW> dma(wave, lane);
+  const Dma dma(wave, lane);
   const uint32_t qrs = (uint32_t)p.q.sr * 2, ors = (uint32_t)p.dout.sr * 2;
   const rsrc_t qrsrc = make_rsrc(Q, (uint32_t)s.T * qrs);
   const rsrc_t orsrc = make_rsrc(dO, (uint32_t)s.T * ors);
@@ -116,9 +133,9 @@ __global__ __launch_bounds__(64 * NW, 2) void dkdv_pipe_kernel(const DkdvParams 
       for (int e = 0; e < 4; ++e) dp[4 * qd + e] = d4[e];
     }
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      sc = MM::mma(swz_cols<T>(tq, 32 * qs + li, c), kf[c], sc);
-      dp = MM::mma(swz_cols<T>(to, 32 * qs + li, c), vf[c], dp);
+    for (int c = 0; c < NKC; ++c) {
+      sc = MM::mma(swz_cols<T, DP>(tq, 32 * qs + li, c), kf[c], sc);
+      dp = MM::mma(swz_cols<T, DP>(to, 32 * qs + li, c), vf[c], dp);
     }
   };
   // Masks of a general tile: keys out of range and (causal) keys after the query get S = -inf.
@@ -149,9 +166,9 @@ __global__ __launch_bounds__(64 * NW, 2) void dkdv_pipe_kernel(const DkdvParams 
 #pragma unroll
     for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
-      for (int dt = 0; dt < 2; ++dt) {
-        dv[dt] = MM::mma(pf[cc], swz_rows<T>(to, 32 * qs, cc, 32 * dt), dv[dt]);
-        dk[dt] = MM::mma(df[cc], swz_rows<T>(tq, 32 * qs, cc, 32 * dt), dk[dt]);
+      for (int dt = 0; dt < NDT; ++dt) {
+        dv[dt] = MM::mma(pf[cc], swz_rows<T, DP>(to, 32 * qs, cc, 32 * dt), dv[dt]);
+        dk[dt] = MM::mma(df[cc], swz_rows<T, DP>(tq, 32 * qs, cc, 32 * dt), dk[dt]);
       }
   };
 
@@ -168,7 +185,7 @@ __global__ __launch_bounds__(64 * NW, 2) void dkdv_pipe_kernel(const DkdvParams 
       store_rows(nr);
       load_rows(it + 2);
     }
-    if constexpr (FAST) {
+    if constexpr (FAST && OVERLAP) {
       f32x16_t s0, p0, s1, p1;
       F pf0[2], df0[2], pf1[2], df1[2];
       sdp(tq, to, tr, 0, s0, p0);
@@ -180,6 +197,15 @@ __global__ __launch_bounds__(64 * NW, 2) void dkdv_pipe_kernel(const DkdvParams 
       pds(tr, 1, s1, p1, pf1, df1);
       __builtin_amdgcn_sched_barrier(0);
       dvdk(tq, to, 1, pf1, df1);
+    } else if constexpr (FAST) {
+#pragma unroll
+      for (int qs = 0; qs < 2; ++qs) {
+        f32x16_t sc, dp;
+        F pf[2], df[2];
+        sdp(tq, to, tr, qs, sc, dp);
+        pds(tr, qs, sc, dp, pf, df);
+        dvdk(tq, to, qs, pf, df);
+      }
     } else {
 #pragma unroll
       for (int qs = 0; qs < 2; ++qs) {
@@ -232,7 +258,7 @@ __global__ __launch_bounds__(64 * NW, 2) void dkdv_pipe_kernel(const DkdvParams 
   T* DV = (T*)p.dv.p + b * p.dv.sb + h * p.dv.sh;
   T* DK = p.dk.p ? (T*)p.dk.p + b * p.dk.sb + h * p.dk.sh : nullptr;
 #pragma unroll
-  for (int dt = 0; dt < 2; ++dt) {
+  for (int dt = 0; dt < NDT; ++dt) {
     const int d = dt * 32 + li;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -253,11 +279,13 @@ __global__ __launch_bounds__(64 * NW, 2) void dkdv_pipe_kernel(const DkdvParams 
 // dQ^T += K^T dS^T takes dS^T from the accumulators. Phase order per key tile of two 32-key subtiles:
 //   S, dP of subtile 0 | S, dP of subtile 1 with exp / dS of subtile 0
 //   | dQ of subtile 0 with exp / dS of subtile 1 | dQ of subtile 1.
-template <typename T, bool CAUSAL, int NW>
-__global__ __launch_bounds__(64 * NW, 2) void dq_pipe_kernel(const DqParams p) {
+template <typename T, bool CAUSAL, int NW, int DP, bool OVERLAP, int WPS>
+__global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
-  constexpr int BM = 32 * NW, BN = 64, TILE = BN * SWZ_ROW_BYTES, NSLAB = BN / (8 * NW);
+  using Dma = SwzDma<NW, DP>;
+  constexpr int NKC = DP / 16, NDT = DP / 32;
+  constexpr int BM = 32 * NW, BN = 64, TILE = BN * 2 * DP, NSLAB = BN / Dma::SLAB_ROWS;
   __shared__ __attribute__((aligned(1024))) char sK0[TILE];
   __shared__ __attribute__((aligned(1024))) char sK1[TILE];
   __shared__ __attribute__((aligned(1024))) char sV0[TILE];
@@ -281,11 +309,11 @@ __global__ __launch_bounds__(64 * NW, 2) void dq_pipe_kernel(const DqParams p) {
   const bool qvalid = myq < s.T;
   const int64_t rowbase = (int64_t)bh * s.T;
 
-  F qf[4], of[4];
+  F qf[NKC], of[NKC];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    qf[c] = gload_frag<T>(Q, p.q.sr, myq, s.T, c, 64, true);
-    of[c] = gload_frag<T>(dO, p.dout.sr, myq, s.T, c, 64, true);
+  for (int c = 0; c < NKC; ++c) {
+    qf[c] = gload_frag<T>(Q, p.q.sr, myq, s.T, c, DP, true);
+    of[c] = gload_frag<T>(dO, p.dout.sr, myq, s.T, c, DP, true);
   }
   const float l2 = qvalid ? p.lse[rowbase + myq] * kLog2e : THERIA_INF;
   const float lse2 = l2 == -THERIA_INF ? THERIA_INF : l2;  // a row without visible keys has P = 0
@@ -295,7 +323,7 @@ __global__ __launch_bounds__(64 * NW, 2) void dq_pipe_kernel(const DqParams p) {
     float part = 0.f;
     if (qvalid) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
+      for (int c = 0; c < NKC; ++c) {
         const int col = c * 16 + 8 * g;
         const int64_t off = (int64_t)myq * p.o.sr + col;
         if (p.o_f32) {
@@ -319,9 +347,9 @@ __global__ __launch_bounds__(64 * NW, 2) void dq_pipe_kernel(const DqParams p) {
   }
   if (!p.dq.p) return;  // only the row term was requested (uniform over the grid)
 
-  f32x16_t acc[2];
-  acc[0] = zero16();
-  acc[1] = zero16();
+  f32x16_t acc[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) acc[dt] = zero16();
   const float c2 = s.scale * kLog2e;
 
   int kend = s.M;
@@ -331,7 +359,7 @@ __global__ __launch_bounds__(64 * NW, 2) void dq_pipe_kernel(const DqParams p) {
   int nfull = s.M / BN;
   if (CAUSAL) nfull = min(nfull, qb * BM / BN);
 
-  const SwzDma<NW> dma(wave, lane);
+  const Dma dma(wave, lane);
   const uint32_t krs = (uint32_t)p.k.sr * 2, vrs = (uint32_t)p.v.sr * 2;
   const rsrc_t krsrc = make_rsrc(K, (uint32_t)s.M * krs);
   const rsrc_t vrsrc = make_rsrc(V, (uint32_t)s.M * vrs);
@@ -342,9 +370,9 @@ __global__ __launch_bounds__(64 * NW, 2) void dq_pipe_kernel(const DqParams p) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) dp[r] = -del;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      sc = MM::mma(swz_cols<T>(tk, 32 * t + li, c), qf[c], sc);
-      dp = MM::mma(swz_cols<T>(tv, 32 * t + li, c), of[c], dp);
+    for (int c = 0; c < NKC; ++c) {
+      sc = MM::mma(swz_cols<T, DP>(tk, 32 * t + li, c), qf[c], sc);
+      dp = MM::mma(swz_cols<T, DP>(tv, 32 * t + li, c), of[c], dp);
     }
   };
   auto mask = [&](f32x16_t& sc, int k0t) {
@@ -364,7 +392,7 @@ __global__ __launch_bounds__(64 * NW, 2) void dq_pipe_kernel(const DqParams p) {
 #pragma unroll
     for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
-      for (int dt = 0; dt < 2; ++dt) acc[dt] = MM::mma(swz_rows<T>(tk, 32 * t, cc, 32 * dt), df[cc], acc[dt]);
+      for (int dt = 0; dt < NDT; ++dt) acc[dt] = MM::mma(swz_rows<T, DP>(tk, 32 * t, cc, 32 * dt), df[cc], acc[dt]);
   };
 
   auto step = [&](auto fast_tag, int k, const char* tk, const char* tv, char* nk, char* nv) {
@@ -376,7 +404,16 @@ __global__ __launch_bounds__(64 * NW, 2) void dq_pipe_kernel(const DqParams p) {
       dma.template issue_clamped<NSLAB>(krsrc, krs, k0 + BN, s.M, nk);
       dma.template issue_clamped<NSLAB>(vrsrc, vrs, k0 + BN, s.M, nv);
     }
-    if constexpr (FAST) {
+    if constexpr (FAST && !OVERLAP) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        f32x16_t sc, dp;
+        F df[2];
+        sdp(tk, tv, t, sc, dp);
+        pds(sc, dp, df);
+        dqm(tk, t, df);
+      }
+    } else if constexpr (FAST) {
       f32x16_t s0, p0, s1, p1;
       F d0[2], d1[2];
       sdp(tk, tv, 0, s0, p0);
@@ -424,12 +461,12 @@ __global__ __launch_bounds__(64 * NW, 2) void dq_pipe_kernel(const DqParams p) {
   if (qvalid) {
     T* DQ = (T*)p.dq.p + b * p.dq.sb + h * p.dq.sh;
 #pragma unroll
-    for (int dt = 0; dt < 2; ++dt)
+    for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
       for (int qd = 0; qd < 4; ++qd) {
         const int d0 = dt * 32 + 8 * qd + 4 * g;
         const f32x16_t& a = acc[dt];
-        store4<T>(DQ, p.dq.sr, myq, d0, 64, a[4 * qd] * s.scale, a[4 * qd + 1] * s.scale, a[4 * qd + 2] * s.scale,
+        store4<T>(DQ, p.dq.sr, myq, d0, DP, a[4 * qd] * s.scale, a[4 * qd + 1] * s.scale, a[4 * qd + 2] * s.scale,
                   a[4 * qd + 3] * s.scale, true);
       }
   }
@@ -437,7 +474,7 @@ __global__ __launch_bounds__(64 * NW, 2) void dq_pipe_kernel(const DqParams p) {
 
 template <typename T, bool CAUSAL>
 bool launch_dq_pipe(const DqParams& p, hipStream_t st, hipError_t* err) {
-  if (!(p.s.D == 64 && p.s.vec)) return false;
+  if (!((p.s.D == 64 || p.s.D == 128) && p.s.vec)) return false;
   // 32-bit byte offsets inside each (batch, head) slab of K and V
   if ((int64_t)p.s.M * p.k.sr * 2 >= (int64_t(1) << 31) || (int64_t)p.s.M * p.v.sr * 2 >= (int64_t(1) << 31)) return false;
   constexpr int NW = DQ_PIPE_NW;
@@ -446,7 +483,11 @@ bool launch_dq_pipe(const DqParams& p, hipStream_t st, hipError_t* err) {
     *err = hipSuccess;
     return true;
   }
-  hipLaunchKernelGGL((dq_pipe_kernel<T, CAUSAL, NW>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p);
+  if (p.s.D == 64)
+    hipLaunchKernelGGL((dq_pipe_kernel<T, CAUSAL, NW, 64, true, 2>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p);
+  else
+    hipLaunchKernelGGL((dq_pipe_kernel<T, CAUSAL, NW, 128, DQ128_OVERLAP, DQ128_WPS>), dim3((unsigned)nblk),
+                       dim3(64 * NW), 0, st, p);
   *err = hipGetLastError();
   return true;
 }
@@ -460,7 +501,7 @@ template bool launch_dq_pipe<_Float16, true>(const DqParams&, hipStream_t, hipEr
 // both wanted); returns false otherwise.
 template <typename T, bool CAUSAL>
 bool launch_dkdv_pipe(const DkdvParams& p, hipStream_t st, hipError_t* err) {
-  if (!(p.s.D == 64 && p.s.vec && !p.dv_only)) return false;
+  if (!((p.s.D == 64 || p.s.D == 128) && p.s.vec && !p.dv_only)) return false;
   // 32-bit byte offsets inside each (batch, head) slab of Q and dO
   if ((int64_t)p.s.T * p.q.sr * 2 >= (int64_t(1) << 31) || (int64_t)p.s.T * p.dout.sr * 2 >= (int64_t(1) << 31))
     return false;
@@ -470,7 +511,11 @@ bool launch_dkdv_pipe(const DkdvParams& p, hipStream_t st, hipError_t* err) {
     *err = hipSuccess;
     return true;
   }
-  hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, NW>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p);
+  if (p.s.D == 64)
+    hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, NW, 64, true, 2>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p);
+  else
+    hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, NW, 128, DKDV128_OVERLAP, DKDV128_WPS>), dim3((unsigned)nblk),
+                       dim3(64 * NW), 0, st, p);
   *err = hipGetLastError();
   return true;
 }

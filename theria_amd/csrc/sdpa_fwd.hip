@@ -234,7 +234,7 @@ template <int MODE>
 struct FwdLauncher {
   template <typename T, int DP, bool CAUSAL>
   static hipError_t run(const FwdParams& p, hipStream_t st) {
-    if constexpr (MODE == 0 && sizeof(T) == 2 && DP == 64) {
+    if constexpr (MODE == 0 && sizeof(T) == 2 && DP >= 64) {
       hipError_t err;
       if (launch_fwd_pipe<T, CAUSAL>(p, st, &err)) return err;
     }

@@ -1,10 +1,11 @@
-// Pipelined SDPA forward for 16-bit inputs with head_dim 64 on gfx950.
+// Pipelined SDPA forward for 16-bit inputs with head_dim 64 or 128 on gfx950.
 //
 // Same contract as fwd_kernel mode 0 (sdpa_fwd.hip): O = softmax(scale Q K^T) V with lse and the
 // optional reference statistics (m, l) (reference theria/attention/triton_qk.py:242-304). It is used when
-// the head dim is exactly 64, every view allows 16-byte access and the sequence fills a 256-query block.
+// the head dim is exactly 64 or 128, every view allows 16-byte access and there are more than 128 queries.
 //
-// Work decomposition: one workgroup = NW waves x 2 tiles of 32 queries; keys in tiles of 64. Scores are
+// Work decomposition: one workgroup = NW waves x QT tiles of 32 queries (QT = 2 at head dim 64, 1 at
+// 128); keys in tiles of 64. Scores are
 // transposed (S^T = K Q^T), so each lane owns one query and the row sums are per-lane. Every SIMD runs two
 // waves. With NW = 8 both are waves of one workgroup, kept in step by the per-tile barrier; two
 // independent 4-wave workgroups on one CU do not share the SIMDs evenly (the older one is issued
@@ -29,11 +30,15 @@
 
 namespace theria {
 
-template <typename T, bool CAUSAL, bool STATS, int NW>
+template <typename T, bool CAUSAL, bool STATS, int NW, int DP>
 __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
-  constexpr int QT = 2, BM = 32 * NW * QT, BN = 64, TILE = BN * SWZ_ROW_BYTES;
+  // QT query tiles of 32 per wave (two at DP = 64, where each K / V^T fragment then feeds two MFMAs;
+  // one at DP = 128, where the registers would not allow two); NKC k-chunks of 16 and NDT output tiles
+  // of 32 across the head dim.
+  constexpr int QT = DP == 64 ? 2 : 1, NKC = DP / 16, NDT = DP / 32;
+  constexpr int BM = 32 * NW * QT, BN = 64, TILE = BN * 2 * DP;
   // Separate arrays (not one [2][TILE] array) so that the compiler can tell the tile being read from the
   // tile being filled and does not wait for the DMA in flight before every LDS read.
   __shared__ __attribute__((aligned(1024))) char sK0[TILE];
@@ -64,8 +69,9 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
   int nfull = s.M / BN;
   if (CAUSAL) nfull = min(nfull, qb * BM / BN);
 
-  const SwzDma<NW> dma(wave, lane);
-  constexpr int NSLAB = BN / (8 * NW);
+  using Dma = SwzDma<NW, DP>;
+  const Dma dma(wave, lane);
+  constexpr int NSLAB = BN / Dma::SLAB_ROWS;
   // Byte offsets fit in 32 bits: the host only selects this kernel when every (batch, head) slab of K
   // and V spans less than 2^31 bytes.
   const uint32_t krs = (uint32_t)p.k.sr * 2, vrs = (uint32_t)p.v.sr * 2;
@@ -79,18 +85,18 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
   }
   if (nkt > 0) dma.template issue_clamped<NSLAB>(krsrc, krs, 0, s.M, sK0);
 
-  F qf[QT][4];
+  F qf[QT][NKC];
 #pragma unroll
   for (int j = 0; j < QT; ++j)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) qf[j][c] = gload_frag<T>(Q, p.q.sr, q0w + 32 * j + li, s.T, c, 64, true);
+    for (int c = 0; c < NKC; ++c) qf[j][c] = gload_frag<T>(Q, p.q.sr, q0w + 32 * j + li, s.T, c, DP, true);
 
-  f32x16_t o[QT][2];
+  f32x16_t o[QT][NDT];
   float m_use[QT], l_part[QT], m_max[QT];
 #pragma unroll
   for (int j = 0; j < QT; ++j) {
-    o[j][0] = zero16();
-    o[j][1] = zero16();
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) o[j][dt] = zero16();
     m_use[j] = -THERIA_INF;
     l_part[j] = 0.f;
     m_max[j] = -THERIA_INF;
@@ -103,8 +109,8 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
 #pragma unroll
     for (int j = 0; j < QT; ++j) st[j] = zero16();
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const F kf = swz_cols<T>(kt, 32 * t + li, c);
+    for (int c = 0; c < NKC; ++c) {
+      const F kf = swz_cols<T, DP>(kt, 32 * t + li, c);
 #pragma unroll
       for (int j = 0; j < QT; ++j) st[j] = MM::mma(kf, qf[j][c], st[j]);
     }
@@ -126,8 +132,8 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
 #pragma unroll
       for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
-        for (int dt = 0; dt < 2; ++dt) {
-          const F vf = swz_rows<T>(vt, 32 * t, cc, 32 * dt);
+        for (int dt = 0; dt < NDT; ++dt) {
+          const F vf = swz_rows<T, DP>(vt, 32 * t, cc, 32 * dt);
 #pragma unroll
           for (int j = 0; j < QT; ++j) o[j][dt] = MM::mma(vf, pf[j][t][cc], o[j][dt]);
         }
@@ -197,7 +203,7 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
       m_use[j] = mnew;
       l_part[j] *= alpha;
 #pragma unroll
-      for (int dt = 0; dt < 2; ++dt)
+      for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[j][dt][r] *= alpha;
       off[j] = mnew == -THERIA_INF ? 0.f : mnew;  // all keys so far masked: P = exp2(-inf) = 0
@@ -226,7 +232,9 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
       // Phase order (kept by scheduling barriers, which also bound the live registers):
       //   S(k) subtile 0 | S(k) subtile 1 with exp of subtile 0 | O += V(k-1)^T P(k-1)^T with exp of subtile 1.
       f32x16_t s0[QT], s1[QT];
-      float ps[QT] = {0.f, 0.f};
+      float ps[QT];
+#pragma unroll
+      for (int j = 0; j < QT; ++j) ps[j] = 0.f;
       scores_t(kc, 0, s0);
       __builtin_amdgcn_sched_barrier(0);
       scores_t(kc, 1, s1);
@@ -341,7 +349,7 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
     const float inv = l > 0.f ? 1.f / l : 0.f;
     if (myq < s.T) {
 #pragma unroll
-      for (int dt = 0; dt < 2; ++dt)
+      for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
         for (int qd = 0; qd < 4; ++qd) {
           const int d0 = dt * 32 + 8 * qd + 4 * g;
@@ -349,10 +357,10 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
           const float a2 = o[j][dt][4 * qd + 2] * inv, a3 = o[j][dt][4 * qd + 3] * inv;
           if (p.o_f32) {
             float* O = (float*)p.o.p + b * p.o.sb + h * p.o.sh;
-            store4<float>(O, p.o.sr, myq, d0, 64, a0, a1, a2, a3, true);
+            store4<float>(O, p.o.sr, myq, d0, DP, a0, a1, a2, a3, true);
           } else {
             T* O = (T*)p.o.p + b * p.o.sb + h * p.o.sh;
-            store4<T>(O, p.o.sr, myq, d0, 64, a0, a1, a2, a3, true);
+            store4<T>(O, p.o.sr, myq, d0, DP, a0, a1, a2, a3, true);
           }
         }
       if (g == 0) {
@@ -367,31 +375,41 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
   }
 }
 
-// Launch if the pipelined kernel covers this problem (16-bit, head dim 64, vector access, >= 256
-// queries); returns false otherwise.
+template <typename T, bool CAUSAL, int NW, int DP>
+static void fwd_pipe_go(const FwdParams& p, int64_t nblk, hipStream_t st) {
+  if (p.row_max || p.row_sum)
+    hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, true, NW, DP>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p);
+  else
+    hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, false, NW, DP>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p);
+}
+
+template <typename T, bool CAUSAL, int DP>
+static void fwd_pipe_launch(const FwdParams& p, hipStream_t st) {
+  constexpr int QT = DP == 64 ? 2 : 1;
+  const int64_t bh = (int64_t)p.s.B * p.s.H;
+  const int64_t nblk8 = (int64_t)((p.s.T + 256 * QT - 1) / (256 * QT)) * bh;
+  const int64_t nblk4 = (int64_t)((p.s.T + 128 * QT - 1) / (128 * QT)) * bh;
+  if (nblk8 >= device_cu_count())
+    fwd_pipe_go<T, CAUSAL, 8, DP>(p, nblk8, st);
+  else
+    fwd_pipe_go<T, CAUSAL, 4, DP>(p, nblk4, st);
+}
+
+// Launch if the pipelined kernel covers this problem (16-bit, head dim 64 or 128, vector access, more
+// than 128 queries); returns false otherwise.
 template <typename T, bool CAUSAL>
 bool launch_fwd_pipe(const FwdParams& p, hipStream_t st, hipError_t* err) {
-  if (!(p.s.D == 64 && p.s.vec && p.s.T > 128)) return false;
+  if (!((p.s.D == 64 || p.s.D == 128) && p.s.vec && p.s.T > 128)) return false;
   // 32-bit byte offsets inside each (batch, head) slab of K and V
   if ((int64_t)p.s.M * p.k.sr * 2 >= (int64_t(1) << 31) || (int64_t)p.s.M * p.v.sr * 2 >= (int64_t(1) << 31)) return false;
-  const int64_t bh = (int64_t)p.s.B * p.s.H;
-  const int64_t nblk8 = (int64_t)((p.s.T + 511) / 512) * bh, nblk4 = (int64_t)((p.s.T + 255) / 256) * bh;
-  if (nblk4 == 0) {
+  if ((int64_t)p.s.B * p.s.H == 0) {
     *err = hipSuccess;
     return true;
   }
-  const bool stats = p.row_max || p.row_sum;
-  if (nblk8 >= device_cu_count()) {
-    if (stats)
-      hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, true, 8>), dim3((unsigned)nblk8), dim3(512), 0, st, p);
-    else
-      hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, false, 8>), dim3((unsigned)nblk8), dim3(512), 0, st, p);
-  } else {
-    if (stats)
-      hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, true, 4>), dim3((unsigned)nblk4), dim3(256), 0, st, p);
-    else
-      hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, false, 4>), dim3((unsigned)nblk4), dim3(256), 0, st, p);
-  }
+  if (p.s.D == 64)
+    fwd_pipe_launch<T, CAUSAL, 64>(p, st);
+  else
+    fwd_pipe_launch<T, CAUSAL, 128>(p, st);
   *err = hipGetLastError();
   return true;
 }

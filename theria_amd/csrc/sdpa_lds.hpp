@@ -1,27 +1,33 @@
-// LDS tiles filled by DMA for 16-bit inputs with a 64-wide head dimension (gfx950).
+// LDS tiles filled by DMA for 16-bit inputs with a head dimension DP of 64 or 128 (gfx950).
 //
-// A tile holds R rows x 64 columns of a 16-bit type, 128 bytes per row, with no padding. Its global
-// rows are copied by LDS DMA (buffer_load_dwordx4 ... lds), which writes the 16 bytes of lane l of a
-// wave to LDS address M0 + 16 * l (checked on the device), so one wave instruction fills 8 consecutive
-// rows and the data never passes through VGPRs.
+// A tile holds R rows x DP columns of a 16-bit type, RB = 2 DP bytes per row (128 or 256), with no
+// padding. Its global rows are copied by LDS DMA (buffer_load_dwordx4 ... lds), which writes the 16
+// bytes of lane l of a wave to LDS address M0 + 16 * l (checked on the device), so one wave instruction
+// fills 1024 / RB consecutive rows and the data never passes through VGPRs.
 //
-// The eight 16-byte chunks of row r are stored XOR-swizzled: logical chunk c sits at slot c ^ swz(r),
-// where swz(r) is bits 1..3 of r, bit-reversed. The DMA lane that fills slot s of row r therefore fetches
-// logical chunk s ^ swz(r). The swizzle spreads the two read patterns over the LDS banks:
-//  * "cols" fragments (ds_read_b128, one lane-fixed row, k along the row): 16 lanes read the same
-//    logical chunk of 16 consecutive rows; rows of one parity differ in bits 1..3, so their slots differ;
-//  * "rows" fragments (ds_read_b64_tr_b16, k down a column): 32 lanes read 4 consecutive rows x 4
-//    consecutive chunks; the two rows of one parity differ in bit 1 of the row, which flips slot bit 2,
-//    so they read disjoint halves of the row.
+// The RB/16 chunks (16 bytes) of row r are stored XOR-swizzled: logical chunk c sits at slot
+// c ^ swz<DP>(r), and the DMA lane that fills slot s of row r fetches logical chunk s ^ swz<DP>(r). The
+// swizzle makes both read patterns bank-conflict free:
+//  * "cols" fragments (ds_read_b128, one lane-fixed row, k along the row): 16 lanes read the same logical
+//    chunk of 16 consecutive rows (16-aligned). DP = 64: rows of one parity share a 32-bank half and
+//    swz = bits 1..3 of r (bit-reversed) gives them distinct slots. DP = 128: every row spans all 64
+//    banks and swz = ((r & 3) << 2) | ((r >> 2) & 3) is a bijection of r & 15.
+//  * "rows" (transpose) fragments (ds_read_b64_tr_b16, k down a column): 32 lanes read 4 consecutive rows
+//    (4-aligned) x 4 consecutive chunks (4-aligned). DP = 64: the two rows of one parity differ in bit 1,
+//    which flips slot bit 2. DP = 128: the 4 rows XOR by 0, 4, 8, 12, i.e. land in 4 different chunk quads.
 #pragma once
 
 #include "sdpa_common.hpp"
 
 namespace theria {
 
-constexpr int SWZ_ROW_BYTES = 128;
-
-__device__ __forceinline__ int swz(int r) { return (((r >> 1) & 1) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1); }
+template <int DP>
+__device__ __forceinline__ int swz(int r) {
+  if constexpr (DP == 64)
+    return (((r >> 1) & 1) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1);
+  else
+    return ((r & 3) << 2) | ((r >> 2) & 3);
+}
 
 // Wait until every global load (and LDS DMA) this wave issued has completed (s_waitcnt vmcnt(0)).
 __device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
@@ -55,20 +61,24 @@ __device__ __forceinline__ void dma16(rsrc_t rsrc, char* lds, uint32_t voffset, 
 #endif
 }
 
-// Per-lane constants of the cooperative DMA of slabs of 8 * NW rows by a workgroup of NW waves: wave w
-// fills rows 8w..8w+7 of every slab (bytes [1024 w, 1024 w + 1024) of it). `wave` must be wave-uniform
-// (an SGPR value), since it selects the LDS destination. The copies are buffer_load_dwordx4 ... lds with
-// a per-lane 32-bit offset and a wave-uniform offset for the tile, so no 64-bit address math is needed.
-template <int NW>
+// Per-lane constants of the cooperative DMA of slabs by a workgroup of NW waves. One wave instruction
+// fills RPW = 1024 / RB rows; wave w fills rows RPW w .. RPW w + RPW - 1 of every slab of RPW * NW rows
+// (bytes [1024 w, 1024 w + 1024) of it). `wave` must be wave-uniform (an SGPR value), since it selects
+// the LDS destination. The copies are buffer_load_dwordx4 ... lds with a per-lane 32-bit offset and a
+// wave-uniform offset for the tile, so no 64-bit address math is needed.
+template <int NW, int DP>
 struct SwzDma {
-  static constexpr int SLAB_ROWS = 8 * NW;
-  static constexpr int SLAB_BYTES = SLAB_ROWS * SWZ_ROW_BYTES;
+  static constexpr int RB = 2 * DP;            // bytes per row
+  static constexpr int CPR = RB / 16;          // chunks per row
+  static constexpr int RPW = 1024 / RB;        // rows per wave instruction
+  static constexpr int SLAB_ROWS = RPW * NW;
+  static constexpr int SLAB_BYTES = SLAB_ROWS * RB;
   int row;    // row of the slab filled by this lane
   int chunk;  // logical 16-byte chunk this lane fetches
   int dst;    // byte offset of this wave's piece in a slab
 
   __device__ __forceinline__ SwzDma(int wave, int lane)
-      : row(8 * wave + (lane >> 3)), chunk((lane & 7) ^ swz(8 * wave + (lane >> 3))), dst(1024 * wave) {}
+      : row(RPW * wave + lane / CPR), chunk((lane % CPR) ^ swz<DP>(RPW * wave + lane / CPR)), dst(1024 * wave) {}
 
   // Byte offset, from the tile's first row, of what this lane fetches for slab i.
   __device__ __forceinline__ uint32_t lane_offset(uint32_t rs_bytes, int i) const {
@@ -97,25 +107,24 @@ struct SwzDma {
 };
 
 // "cols" fragment (KLIN order): lane row `row` of the tile, k = columns 16c + 8g .. 16c + 8g + 7.
-template <typename T>
+template <typename T, int DP>
 __device__ __forceinline__ typename Mfma<T>::frag_t swz_cols(const char* tile, int row, int c) {
   const int g = (threadIdx.x >> 5) & 1;
-  const int slot = (2 * c + g) ^ swz(row);
-  return __builtin_bit_cast(typename Mfma<T>::frag_t,
-                            *reinterpret_cast<const i16x8_t*>(tile + row * SWZ_ROW_BYTES + slot * 16));
+  const int slot = (2 * c + g) ^ swz<DP>(row);
+  return __builtin_bit_cast(typename Mfma<T>::frag_t, *reinterpret_cast<const i16x8_t*>(tile + row * (2 * DP) + slot * 16));
 }
 
 // "rows" fragment (KACC order): lane-fixed column col0 + li, k = tile rows kbase + acc_row(8c + e, g)
-// (the same rows as lds_rows<T, KACC> in sdpa_common.hpp, on the swizzled layout).
-template <typename T>
+// (the same rows as lds_rows<T, KACC> in sdpa_common.hpp, on the swizzled layout). kbase is a multiple of 16.
+template <typename T, int DP>
 __device__ __forceinline__ typename Mfma<T>::frag_t swz_rows(const char* tile, int kbase, int c, int col0) {
   const int lane = threadIdx.x & 63;
   const int s = lane & 15, hh = (lane >> 4) & 1, g = lane >> 5;
   const int col = col0 + 16 * hh + 4 * (s & 3);
   const int r0 = kbase + 16 * c + 4 * g + (s >> 2);
   const int r1 = r0 + 8;
-  const i16x4_t a = ds_read_tr16(tile + r0 * SWZ_ROW_BYTES + (((col >> 3) ^ swz(r0)) << 4) + (col & 7) * 2);
-  const i16x4_t b = ds_read_tr16(tile + r1 * SWZ_ROW_BYTES + (((col >> 3) ^ swz(r1)) << 4) + (col & 7) * 2);
+  const i16x4_t a = ds_read_tr16(tile + r0 * (2 * DP) + (((col >> 3) ^ swz<DP>(r0)) << 4) + (col & 7) * 2);
+  const i16x4_t b = ds_read_tr16(tile + r1 * (2 * DP) + (((col >> 3) ^ swz<DP>(r1)) << 4) + (col & 7) * 2);
   const i16x8_t v = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
   return __builtin_bit_cast(typename Mfma<T>::frag_t, v);
 }
