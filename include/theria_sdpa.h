@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define THERIA_SDPA_ABI_VERSION 2
+#define THERIA_SDPA_ABI_VERSION 3
 
 enum theria_dtype { THERIA_DTYPE_F32 = 0, THERIA_DTYPE_F16 = 1, THERIA_DTYPE_BF16 = 2 };
 enum theria_status { THERIA_OK = 0, THERIA_ERR_CONTRACT = 1, THERIA_ERR_HIP = 2 };
@@ -131,6 +131,20 @@ int theria_sdpa_bwd_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q
                         const float* lse, const float* delta, const theria_tensor_t* gq, const theria_tensor_t* gk,
                         const theria_tensor_t* gv, const theria_tensor_t* out_gq, const theria_tensor_t* out_gk,
                         const theria_tensor_t* out_gv, const theria_tensor_t* out_gdout, float* row_ws, void* stream);
+
+/*
+ * Materialised scores for the partial-fusion sdpa_custom backends (theria/attention/custom.py:30-49).
+ * theria_qk_scores: unscaled S = Q K^T as a contiguous (B, H, tq, tk) tensor at `out`, float32 when
+ *   out_f32 (or when the inputs are float32), else the input dtype. Replaces _qk_kernel and
+ *   _qk_kernel_fast behind triton_qk / triton_qk_fast (theria/attention/triton_qk.py:24-125, 402-522).
+ * theria_qk_softmax: P = softmax(scale Q K^T) over the keys as a contiguous float32 (B, H, tq, tk)
+ *   tensor. Replaces _qk_softmax_kernel / triton_qk_softmax (triton_qk.py:128-240).
+ * p->causal must be 0 (the reference's score backends have no mask); v-related fields are unused.
+ */
+int theria_qk_scores(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k, void* out,
+                     int32_t out_f32, void* stream);
+int theria_qk_softmax(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k, float* probs,
+                      void* stream);
 
 #ifdef __cplusplus
 }

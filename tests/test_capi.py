@@ -64,6 +64,8 @@ def _call_all(prob):
         "bwd_bwd": lib.theria_sdpa_bwd_bwd(
             p, None, None, None, None, None, None, None, None, None, None, None, None, None, None, None, None
         ),
+        "qk_scores": lib.theria_qk_scores(p, None, None, None, 1, None),
+        "qk_softmax": lib.theria_qk_softmax(p, None, None, None, None),
     }
 
 
@@ -93,3 +95,13 @@ def test_python_check_maps_contract_errors_to_assertion():
     codes = _call_all(_lib.Problem(9, 1, 1, 4, 4, 8, 0.5, 0))
     with pytest.raises(AssertionError):
         _lib.check(codes["fwd"], "theria_sdpa_fwd")
+
+
+def test_score_kernels_reject_causal():
+    from theria_amd import _lib
+
+    lib = _lib.load()
+    prob = _lib.Problem(2, 1, 1, 4, 4, 8, 0.5, 1)
+    assert lib.theria_qk_scores(ctypes.byref(prob), None, None, None, 1, None) == _lib.ERR_CONTRACT
+    assert "causal" in lib.theria_last_error().decode()
+    assert lib.theria_qk_softmax(ctypes.byref(prob), None, None, None, None) == _lib.ERR_CONTRACT

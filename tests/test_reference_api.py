@@ -123,7 +123,8 @@ def test_dispatcher_errors():
     q, k, v = _qkv(1, 1, 2, 2, 4)
     with pytest.raises(ValueError):
         sdpa_custom(q, k, v, backend="no_such_backend")
-    with pytest.raises(NotImplementedError):
-        sdpa_custom(q, k, v, backend="triton_qk")
+    for backend in ("triton_full_fused", "triton_qk", "triton_fast", "triton_qk_softmax"):
+        with pytest.raises(AssertionError):
+            sdpa_custom(q, k, v, backend=backend)  # CPU tensors: the HIP guards reject them
     with pytest.raises(AssertionError):
-        sdpa_custom(q, k, v, backend="triton_full_fused")  # CPU tensors: the HIP guard rejects them
+        sdpa_custom(q, k, v, backend="triton_qk", causal=True)

@@ -290,3 +290,34 @@ def bwd_bwd(q, k, v, o, do, lse, delta, gq, gk, gv, scale: float, causal: bool):
         )
     _lib.check(rc, "theria_sdpa_bwd_bwd")
     return out_q, out_k, out_v, out_do
+
+
+def qk_scores(q, k, out_f32: bool = True):
+    """Unscaled scores Q K^T (B,H,T,M): float32, or the input dtype when out_f32 is False."""
+    check_inputs(q, k, None, require_v=False)
+    q, k = _rowmajor(q), _rowmajor(k)
+    B, H, T, _ = q.shape
+    M = k.shape[2]
+    f32 = out_f32 or q.dtype == torch.float32
+    dev = q.device
+    out = torch.empty((B, H, T, M), dtype=torch.float32 if f32 else q.dtype, device=dev)
+    prob = _problem(q, k, 1.0, False)
+    with _OnDevice(dev):
+        rc = _lib.load().theria_qk_scores(ctypes.byref(prob), _tv(q), _tv(k), out.data_ptr(), 1 if f32 else 0, _stream(dev))
+    _lib.check(rc, "theria_qk_scores")
+    return out
+
+
+def qk_softmax(q, k, scale: float):
+    """Probabilities softmax(scale Q K^T) over the keys, float32 (B,H,T,M)."""
+    check_inputs(q, k, None, require_v=False)
+    q, k = _rowmajor(q), _rowmajor(k)
+    B, H, T, _ = q.shape
+    M = k.shape[2]
+    dev = q.device
+    out = torch.empty((B, H, T, M), dtype=torch.float32, device=dev)
+    prob = _problem(q, k, scale, False)
+    with _OnDevice(dev):
+        rc = _lib.load().theria_qk_softmax(ctypes.byref(prob), _tv(q), _tv(k), out.data_ptr(), _stream(dev))
+    _lib.check(rc, "theria_qk_softmax")
+    return out

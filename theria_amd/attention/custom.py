@@ -7,18 +7,23 @@ Backends:
                                                the gfx950 HIP operator (names kept for drop-in
                                                compatibility; no Triton underneath), output in q.dtype
   "hip", "hip_fused"                           the same HIP operator under its own name
-  "triton_qk", "triton_ref", "triton", "triton_fast", "triton_qk_softmax"
-                                               the reference's partial-fusion QK^T backends: not built
-                                               here yet; they raise NotImplementedError rather than
-                                               silently running something else
+  "triton_qk", "triton_ref", "triton"          HIP Q K^T scores (float32), softmax and PV in PyTorch
+                                               (custom.py:30-36)
+  "triton_fast"                                HIP Q K^T scores in the input dtype, then the same
+                                               (custom.py:37-43)
+  "triton_qk_softmax"                          HIP fused Q K^T + scale + softmax, PV in PyTorch; as in
+                                               the reference no gradient reaches q or k (custom.py:44-49)
 Unknown names raise ValueError (custom.py:57).
 """
 
 from __future__ import annotations
 
+import torch
+
 from ..autograd.hip_sdpa import hip_sdpa
 from ..autograd.sdpa_custom_function import SDPACustom
 from .reference import reference_attention
+from .scores import triton_qk, triton_qk_fast, triton_qk_softmax
 
 HIP_BACKENDS = ("triton_full_fused", "triton_full_fused_phase8", "hip", "hip_fused")
 PARTIAL_FUSION_BACKENDS = ("triton_qk", "triton_ref", "triton", "triton_fast", "triton_qk_softmax")
@@ -38,11 +43,19 @@ def sdpa_custom(q, k, v, *, backend: str = "reference", causal: bool = False):
         if q.shape[-1] != v.shape[-1]:
             raise AssertionError(f"{backend} requires Dv == D")
         return hip_sdpa(q, k, v, causal=causal).to(q.dtype)
-    if backend in PARTIAL_FUSION_BACKENDS:
-        raise NotImplementedError(
-            f"sdpa_custom backend {backend!r} (partial-fusion QK^T kernel) is not implemented in theria_amd; "
-            "use 'triton_full_fused' / 'hip' for the fused HIP operator"
-        )
+    if backend in PARTIAL_FUSION_BACKENDS and causal:
+        raise AssertionError(f"the {backend} backend has no causal mask; use a HIP fused backend")
+    if backend in ("triton_qk", "triton_ref", "triton"):
+        scores = triton_qk(q, k).to(torch.float32) / (q.shape[-1] ** 0.5)
+        probs = torch.softmax(scores, dim=-1)
+        return torch.matmul(probs, v.to(probs.dtype)).to(q.dtype)
+    if backend == "triton_fast":
+        scores = triton_qk_fast(q, k).to(torch.float32) / (q.shape[-1] ** 0.5)
+        probs = torch.softmax(scores, dim=-1)
+        return torch.matmul(probs, v.to(probs.dtype)).to(q.dtype)
+    if backend == "triton_qk_softmax":
+        probs = triton_qk_softmax(q, k).to(torch.float32)
+        return torch.matmul(probs, v.to(probs.dtype)).to(q.dtype)
     raise ValueError(f"Unsupported sdpa_custom backend: {backend}")
 
 
@@ -56,4 +69,4 @@ def sdpa_custom_jvp(q, k, v, dq, dk, dv):
     return SDPACustom.jvp(q, k, v, dq, dk, dv)
 
 
-__all__ = ["sdpa_custom", "sdpa_custom_hvp", "sdpa_custom_jvp", "HIP_BACKENDS"]
+__all__ = ["sdpa_custom", "sdpa_custom_hvp", "sdpa_custom_jvp", "HIP_BACKENDS", "PARTIAL_FUSION_BACKENDS"]

@@ -407,3 +407,37 @@ THERIA_API int theria_sdpa_bwd_bwd(const theria_sdpa_problem_t* p, const theria_
   jp.tout = mv(out_gdout);
   return hip_status(theria::launch_jvp(jp, st), "theria_sdpa_bwd_bwd (dout)");
 }
+
+// Partial-fusion score kernels: the problem's v-related fields are unused; causal must be 0.
+static int run_scores(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k, void* out,
+                      bool out_f32, bool softmax, void* stream, const char* what) {
+  theria::Shape s;
+  std::string err;
+  if (!shape_from(p, s, err)) return fail(THERIA_ERR_CONTRACT, err);
+  if (s.causal) return fail(THERIA_ERR_CONTRACT, std::string(what) + ": the score kernels have no causal mask");
+  Checker c(s);
+  c.qview(q, "q", true);
+  c.kview(k, "k", true);
+  c.need(out != nullptr || !c.q_rows || !c.k_rows, "out is required");
+  if (!c.err.empty()) return fail(THERIA_ERR_CONTRACT, c.err);
+  s.vec = c.vec;
+  if (empty_problem(s) || s.M == 0) return THERIA_OK;
+  theria::ScoresParams sp{};
+  sp.s = s;
+  sp.q = cv(q);
+  sp.k = cv(k);
+  sp.out = out;
+  sp.out_f32 = out_f32;
+  sp.softmax = softmax;
+  return hip_status(theria::launch_scores(sp, (hipStream_t)stream), what);
+}
+
+THERIA_API int theria_qk_scores(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
+                                void* out, int32_t out_f32, void* stream) {
+  return run_scores(p, q, k, out, out_f32 != 0 || (p && p->dtype == THERIA_DTYPE_F32), false, stream, "theria_qk_scores");
+}
+
+THERIA_API int theria_qk_softmax(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
+                                 float* probs, void* stream) {
+  return run_scores(p, q, k, probs, true, true, stream, "theria_qk_softmax");
+}

@@ -75,6 +75,16 @@ struct BwdBwdParams {
   MutView out_gq, out_gk, out_gv;
 };
 
+// Materialised scores (partial-fusion backends): S = Q K^T or P = softmax(scale Q K^T), contiguous
+// (B, H, T, M) output.
+struct ScoresParams {
+  Shape s;
+  View q, k;
+  void* out;
+  bool out_f32;  // scores in float32 (else the input dtype); P is always float32
+  bool softmax;
+};
+
 // Compute units of the current device (cached per device).
 int device_cu_count();
 
@@ -84,5 +94,6 @@ hipError_t launch_bwd_dkdv(const DkdvParams& p, hipStream_t st);
 hipError_t launch_jvp(const JvpParams& p, hipStream_t st);
 hipError_t launch_bwdbwd_rows(const BwdBwdParams& p, hipStream_t st);
 hipError_t launch_bwdbwd_cols(const BwdBwdParams& p, hipStream_t st);
+hipError_t launch_scores(const ScoresParams& p, hipStream_t st);
 
 }  // namespace theria
