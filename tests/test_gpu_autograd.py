@@ -127,15 +127,39 @@ def test_autograd_functional_jvp_uses_double_backward(hip_device):
     close(jv, O.jvp(qc, kc, vc, *(x[1] for x in t)), torch.float32, "functional.jvp")
 
 
-def test_third_order_raises_instead_of_dropping_terms(hip_device):
-    dev = hip_device
-    q = torch.randn(1, 1, 8, 16, device=dev, requires_grad=True)
-    k = torch.randn(1, 1, 8, 16, device=dev, requires_grad=True)
-    v = torch.randn(1, 1, 8, 16, device=dev, requires_grad=True)
-    g = torch.autograd.grad(hip_sdpa(q, k, v).pow(2).sum(), (q, k, v), create_graph=True)
+def _third_order(fn, q, k, v):
+    """grad of sum(g2) where g2 = grad ||grad ||O||^2||^2: a third derivative of O through attention."""
+    g = torch.autograd.grad(fn(q, k, v).pow(2).sum(), (q, k, v), create_graph=True)
     g2 = torch.autograd.grad(sum(x.pow(2).sum() for x in g), (q, k, v), create_graph=True)
-    with pytest.raises(RuntimeError, match="third-order"):
-        torch.autograd.grad(sum(x.sum() for x in g2), (q, k, v))
+    return torch.autograd.grad(sum(x.sum() for x in g2), (q, k, v))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_third_order_matches_oracle(causal, hip_device):
+    """Differentiating a create_graph'ed double backward (orders >= 3) is exact, not a dropped term."""
+    dev = hip_device
+    q, qc = make((1, 2, 9, 16), torch.float32, dev, 71, grad=True)
+    k, kc = make((1, 2, 12, 16), torch.float32, dev, 72, grad=True)
+    v, vc = make((1, 2, 12, 16), torch.float32, dev, 73, grad=True)
+    got = _third_order(lambda a, b, c: hip_sdpa(a, b, c, causal=causal), q, k, v)
+    ref = _third_order(lambda a, b, c: O.autograd_attention(a, b, c, causal=causal),
+                       *(t.clone().requires_grad_(True) for t in (qc, kc, vc)))
+    for name, a, b in zip(("q", "k", "v"), got, ref):
+        torch.testing.assert_close(a.double().cpu(), b, rtol=1e-4, atol=1e-4, msg=lambda m: f"d3/d{name}: {m}")
+
+
+def test_autograd_functional_hvp(hip_device):
+    """torch.autograd.functional.hvp differentiates the double backward with respect to its cotangent."""
+    dev = hip_device
+    q, qc = make((1, 2, 24, 32), torch.float32, dev, 81)
+    k, kc = make((1, 2, 24, 32), torch.float32, dev, 82)
+    v, vc = make((1, 2, 24, 32), torch.float32, dev, 83)
+    w, wc = make((1, 2, 24, 32), torch.float32, dev, 84)
+    u = [make((1, 2, 24, 32), torch.float32, dev, 85 + i) for i in range(3)]
+    _, h = torch.autograd.functional.hvp(lambda a, b, c: (hip_sdpa(a, b, c) * w).sum(), (q, k, v),
+                                         tuple(x[0] for x in u))
+    for name, a, b in zip(("q", "k", "v"), h, O.hvp_weighted_sum(qc, kc, vc, wc, *(x[1] for x in u))):
+        torch.testing.assert_close(a.double().cpu(), b, rtol=1e-4, atol=1e-4, msg=lambda m: f"hvp {name}: {m}")
 
 
 def test_second_order_probe_sees_attention_curvature(hip_device):

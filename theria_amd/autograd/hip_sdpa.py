@@ -1,4 +1,4 @@
-"""autograd wiring of the HIP SDPA operator: exact first and second order, forward-mode JVP.
+"""autograd wiring of the HIP SDPA operator: exact derivatives of every order, forward-mode JVP.
 
 SDPAOp            O = softmax(scale Q K^T) V (optional causal mask); forward kernel, saves (O, lse).
   .backward       -> SDPABackwardOp.apply(...), itself an autograd.Function, so gradients computed
@@ -9,9 +9,12 @@ SDPABackwardOp    (dQ, dK, dV) from the backward kernel; its backward is the exp
 
 The reference's Triton path returns backward outputs with no graph (theria/attention/triton_qk.py:
 379-387), which silently drops attention's second-order terms under MAML create_graph=True. Here the
-second-order terms are explicit kernels. Third-order derivatives are not implemented: if a graph built
-with create_graph=True through the double backward is differentiated again, a RuntimeError is raised
-instead of silently returning graph-less tensors.
+second-order terms are explicit kernels. When the double backward itself must stay differentiable
+(create_graph=True while differentiating a create_graph'ed gradient: third order, as in the
+meta-gradient probe of experiments/phase10/scripts/run_maml_backend_compare.py:169-199), the double
+backward is instead taken by autograd through a float32 PyTorch restatement of the backward map on
+the same device (materialised T x M scores), which is exact to any order. Everything up to second
+order, including every MAML outer backward, runs on the kernels.
 """
 
 from __future__ import annotations
@@ -21,20 +24,46 @@ import torch
 from .. import _ops
 
 
-class _ThirdOrderBarrier(torch.autograd.Function):
-    """Identity on the double-backward outputs whose own backward refuses to run."""
+def _backward_map(q, k, v, dout, scale: float, causal: bool):
+    """(dQ, dK, dV) of O = softmax(scale Q K^T) V given dO, as differentiable PyTorch ops (float32 or wider).
 
-    @staticmethod
-    def forward(ctx, n_out: int, *tensors):
-        ctx.n_out = n_out
-        return tuple(t.clone() for t in tensors[:n_out])
+    dV = P^T dO, dP = dO V^T, dS = P * (dP - rowsum(dP * P)), dQ = scale dS K, dK = scale dS^T Q
+    (reference theria/attention/reference_backward_sdpa.py:31-51). Only used for derivatives of order
+    three and higher, which no kernel covers.
+    """
+    ct = torch.promote_types(q.dtype, torch.float32)
+    qf, kf, vf, df = (t.to(ct) for t in (q, k, v, dout))
+    s = torch.matmul(qf, kf.transpose(-2, -1)) * scale
+    if causal:
+        keep = torch.ones(s.shape[-2], s.shape[-1], dtype=torch.bool, device=s.device).tril()
+        s = s.masked_fill(~keep, float("-inf"))
+    p = torch.softmax(s, dim=-1)
+    dp = torch.matmul(df, vf.transpose(-2, -1))
+    ds = p * (dp - (dp * p).sum(dim=-1, keepdim=True))
+    dq = torch.matmul(ds, kf) * scale
+    dk = torch.matmul(ds.transpose(-2, -1), qf) * scale
+    dv = torch.matmul(p.transpose(-2, -1), df)
+    return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype)
 
-    @staticmethod
-    def backward(ctx, *grads):
-        raise RuntimeError(
-            "theria_amd HIP SDPA: third-order derivatives through attention are not implemented "
-            "(the double-backward kernels are not themselves differentiable)"
-        )
+
+def _differentiable_double_backward(q, k, v, dout, gq, gk, gv, scale: float, causal: bool):
+    """(G_Q, G_K, G_V, G_dO) with a graph: the VJP of _backward_map taken with create_graph=True.
+
+    The map is differentiated through aliases (view_as) of its inputs, so each result is the partial
+    derivative with respect to that argument: dO usually depends on q, k, v itself (dO = dL/dO of a
+    loss of O), and that path is already carried by G_dO. The aliases keep the results connected to
+    the original tensors for the next order.
+    """
+    prim = tuple(t.view_as(t) if t.requires_grad else t for t in (q, k, v, dout))
+    wrt = [t for t in prim if t.requires_grad]
+    if not wrt:
+        return None, None, None, None
+    q, k, v, dout = prim
+    outs = _backward_map(q, k, v, dout, scale, causal)
+    pairs = [(o, g) for o, g in zip(outs, (gq, gk, gv)) if g is not None]
+    grads = iter(torch.autograd.grad([o for o, _ in pairs], wrt, [g for _, g in pairs], create_graph=True,
+                                     allow_unused=True))
+    return tuple(next(grads) if t.requires_grad else None for t in prim)
 
 
 class SDPABackwardOp(torch.autograd.Function):
@@ -53,13 +82,11 @@ class SDPABackwardOp(torch.autograd.Function):
         q, k, v, o, lse, dout, delta = ctx.saved_tensors
         if gq is None and gk is None and gv is None:
             return None, None, None, None, None, None, None, None
+        if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (q, k, v, dout, gq, gk, gv)):
+            g_q, g_k, g_v, g_do = _differentiable_double_backward(q, k, v, dout, gq, gk, gv, ctx.scale, ctx.causal)
+            return g_q, g_k, g_v, None, None, g_do, None, None
         g_q, g_k, g_v, g_do = _ops.bwd_bwd(q, k, v, o, dout, lse, delta, gq, gk, gv, ctx.scale, ctx.causal)
-        g_do = g_do.to(dout.dtype)
-        if torch.is_grad_enabled():
-            anchors = [t for t in (q, k, v, dout, gq, gk, gv) if t is not None and t.requires_grad]
-            if anchors:
-                g_q, g_k, g_v, g_do = _ThirdOrderBarrier.apply(4, g_q, g_k, g_v, g_do, *anchors)
-        return g_q, g_k, g_v, None, None, g_do, None, None
+        return g_q, g_k, g_v, None, None, g_do.to(dout.dtype), None, None
 
 
 class SDPAOp(torch.autograd.Function):
@@ -98,7 +125,7 @@ class SDPAOp(torch.autograd.Function):
 
 
 def hip_sdpa(q, k, v, *, causal: bool = False, scale: float | None = None, out_fp32: bool = False):
-    """Differentiable (to second order) SDPA through the HIP kernels. Returns O only."""
+    """Differentiable SDPA through the HIP kernels (any order; see the module docstring). Returns O only."""
     if scale is None:
         scale = _ops.default_scale(q.shape[-1])
     o, _ = SDPAOp.apply(q, k, v, float(scale), bool(causal), bool(out_fp32))

@@ -1,3 +1,7 @@
+from .diagnostics import attention_second_order_ok, meta_gradient_probe
 from .loops import inner_adapt, loss_fn, meta_loss_on_tasks, named_buffers, named_params, outer_loss
 
-__all__ = ["inner_adapt", "loss_fn", "meta_loss_on_tasks", "named_buffers", "named_params", "outer_loss"]
+__all__ = [
+    "attention_second_order_ok",
+    "meta_gradient_probe",
+    "inner_adapt", "loss_fn", "meta_loss_on_tasks", "named_buffers", "named_params", "outer_loss"]
