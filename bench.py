@@ -248,7 +248,7 @@ def extras_c5():
 
     import torch
 
-    from theria_amd.maml import meta_loss_on_tasks
+    from theria_amd.maml import meta_loss_on_tasks, meta_loss_on_tasks_batched
     from theria_amd.models import MHAClassifier, MHAConfig
     from theria_amd.tasks import sample_token_count_task
 
@@ -259,9 +259,10 @@ def extras_c5():
     tasks = [sample_token_count_task(generator=g, device=dev)[0] for _ in range(16)]
     opt = torch.optim.Adam(model.parameters(), lr=1e-3)
 
-    def meta_step(fo: bool):
+    def meta_step(fo: bool, batched: bool = False):
         opt.zero_grad(set_to_none=True)
-        loss = meta_loss_on_tasks(model, tasks, inner_lr=0.4, inner_steps=5, fo=fo)
+        fn = meta_loss_on_tasks_batched if batched else meta_loss_on_tasks
+        loss = fn(model, tasks, inner_lr=0.4, inner_steps=5, fo=fo)
         loss.backward()
         opt.step()
 
@@ -269,6 +270,10 @@ def extras_c5():
     for fo in (False, True):
         ms = _time(lambda: meta_step(fo), 3, 1)
         res[f"meta_steps_per_s_{'fo' if fo else 'full'}"] = round(1e3 / ms, 3)
+    # the same meta-step with all 16 tasks adapted in one batched forward/backward per inner step
+    for fo in (False, True):
+        ms = _time(lambda: meta_step(fo, batched=True), 10, 2)
+        res[f"meta_steps_per_s_{'fo' if fo else 'full'}_task_batched"] = round(1e3 / ms, 3)
     # meta-gradient agreement with the same weights on the pure-PyTorch reference backend
     ref = copy.deepcopy(model)
     ref.set_attention_backend("reference")
@@ -280,6 +285,9 @@ def extras_c5():
     fr = torch.cat([x.flatten() for x in gr]).double()
     res["metagrad_rel_l2_vs_reference"] = float((fh - fr).norm() / fr.norm())
     res["metagrad_cosine_vs_reference"] = float(torch.nn.functional.cosine_similarity(fh, fr, dim=0))
+    gb = torch.autograd.grad(meta_loss_on_tasks_batched(model, tasks[:4], inner_lr=0.4, inner_steps=5), params_h)
+    fb = torch.cat([x.flatten() for x in gb]).double()
+    res["metagrad_rel_l2_task_batched_vs_reference"] = float((fb - fr).norm() / fr.norm())
     return res
 
 

@@ -109,3 +109,32 @@ def test_mha_classifier_full_maml_on_reference_backend():
     loss = meta_loss_on_tasks(model, tasks, inner_lr=0.4, inner_steps=2)
     loss.backward()
     assert all(torch.isfinite(p.grad).all() for p in model.parameters() if p.grad is not None)
+
+
+def test_task_batched_maml_equals_sequential_loop():
+    """meta_loss_on_tasks_batched is the same function of theta as the per-task loop (float64)."""
+    from theria_amd.maml import meta_loss_on_tasks, meta_loss_on_tasks_batched
+    from theria_amd.models import MHAClassifier, MHAConfig
+    from theria_amd.tasks import sample_token_count_task
+
+    torch.manual_seed(0)
+    model = MHAClassifier(MHAConfig(), backend="reference").double()
+    g = torch.Generator().manual_seed(3)
+    tasks = [sample_token_count_task(generator=g)[0] for _ in range(3)]
+    params = list(model.parameters())
+    one = {k: v.unsqueeze(0) for k, v in model.named_parameters()}
+    torch.testing.assert_close(model.forward_batched(one, tasks[0].x_q.unsqueeze(0))[0], model(tasks[0].x_q))
+    for kw in (dict(fo=False), dict(fo=True), dict(fo=True, fo_strict=True)):
+        a = meta_loss_on_tasks(model, tasks, inner_lr=0.4, inner_steps=2, **kw)
+        b = meta_loss_on_tasks_batched(model, tasks, inner_lr=0.4, inner_steps=2, **kw)
+        torch.testing.assert_close(b, a, rtol=1e-12, atol=1e-12)
+        assert a.requires_grad == b.requires_grad
+        if not a.requires_grad:  # fo_strict: the adapted weights are cut from theta in both
+            continue
+        ga = torch.autograd.grad(a, params, allow_unused=True)
+        gb = torch.autograd.grad(b, params, allow_unused=True)
+        for x, y in zip(ga, gb):
+            if x is None or y is None:
+                assert x is None and y is None
+            else:
+                torch.testing.assert_close(y, x, rtol=1e-10, atol=1e-12)

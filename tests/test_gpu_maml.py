@@ -9,7 +9,7 @@ import copy
 import pytest
 import torch
 
-from theria_amd.maml import meta_loss_on_tasks
+from theria_amd.maml import meta_loss_on_tasks, meta_loss_on_tasks_batched
 from theria_amd.models import BackendAttentionModel, MHAClassifier, MHAConfig, TinyAttentionConfig
 from theria_amd.tasks import sample_token_count_task, task_sampler
 
@@ -59,3 +59,24 @@ def test_phase10_model_full_vs_reference(hip_device):
     rel = float((g_hip - g_ref).norm() / g_ref.norm())
     print(f"[maml] phase10 rel_l2={rel:.3e}", flush=True)
     assert rel < 1e-3
+
+
+def test_config5_task_batched_full_maml_matches_reference_loop(hip_device):
+    """All tasks adapted at once (one SDPA call over tasks x sequences) through the HIP operator, against
+    the per-task loop on the pure-PyTorch backend: the same meta-loss and meta-gradient."""
+    dev = hip_device
+    torch.manual_seed(0)
+    ref_model = MHAClassifier(MHAConfig(), backend="reference").to(dev)
+    hip_model = copy.deepcopy(ref_model)
+    hip_model.set_attention_backend("hip")
+    g = torch.Generator().manual_seed(0)
+    tasks = [sample_token_count_task(generator=g, device=dev)[0] for _ in range(4)]
+    params = list(hip_model.parameters())
+    for fo in (False, True):
+        l_ref, g_ref = _metagrad(ref_model, tasks, fo=fo)
+        loss = meta_loss_on_tasks_batched(hip_model, tasks, inner_lr=0.4, inner_steps=5, fo=fo)
+        g_hip = _flat(torch.autograd.grad(loss, params, allow_unused=True))
+        torch.testing.assert_close(loss.detach().double(), l_ref.double(), rtol=1e-4, atol=1e-5)
+        rel = float((g_hip - g_ref).norm() / g_ref.norm())
+        print(f"[maml] task-batched fo={fo} rel_l2={rel:.3e}", flush=True)
+        assert rel < 1e-3

@@ -70,5 +70,37 @@ class MHAClassifier(nn.Module):
             x = blk(x, self.backend)
         return self.head(self.ln_f(x).mean(dim=1))
 
+    def forward_batched(self, params: dict, tokens: torch.Tensor) -> torch.Tensor:
+        """Many parameter sets at once: params[name] is (n, *shape), tokens (n, N, T) -> logits (n, N, C).
+
+        The same computation as forward() for each of the n parameter sets, with every layer batched
+        over n: per-set linear layers are batched matmuls, the embedding is a one-hot matmul (its
+        backward is a matmul too, so every order of derivative stays deterministic) and attention is
+        one sdpa_custom call over n * N sequences.
+        """
+        cfg = self.cfg
+        n, N, T = tokens.shape
+        d, H = cfg.d_model, cfg.heads
+
+        def lin(x, name):
+            w, b = params[name + ".weight"], params[name + ".bias"]
+            y = torch.matmul(x.reshape(n, -1, x.shape[-1]), w.transpose(1, 2)) + b.unsqueeze(1)
+            return y.reshape(*x.shape[:-1], w.shape[1])
+
+        def norm(x, name):
+            shape = (n,) + (1,) * (x.dim() - 2) + (x.shape[-1],)
+            y = F.layer_norm(x, (x.shape[-1],))
+            return y * params[name + ".weight"].reshape(shape) + params[name + ".bias"].reshape(shape)
+
+        onehot = F.one_hot(tokens.reshape(n, N * T), cfg.vocab).to(params["embed.weight"].dtype)
+        x = torch.matmul(onehot, params["embed.weight"]).reshape(n, N, T, d)
+        for i in range(cfg.layers):
+            pre = f"blocks.{i}."
+            qkv = lin(norm(x, pre + "ln1"), pre + "qkv").reshape(n * N, T, 3, H, d // H).permute(2, 0, 3, 1, 4)
+            att = sdpa_custom(qkv[0], qkv[1], qkv[2], backend=self.backend)  # (n*N, H, T, d/H)
+            x = x + lin(att.transpose(1, 2).reshape(n, N, T, d), pre + "proj")
+            x = x + lin(F.gelu(lin(norm(x, pre + "ln2"), pre + "fc1")), pre + "fc2")
+        return lin(norm(x, "ln_f").mean(dim=2), "head")
+
 
 __all__ = ["MHAConfig", "MHAClassifier"]
