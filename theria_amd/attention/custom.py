@@ -6,7 +6,7 @@ Backends:
   "triton_full_fused", "triton_full_fused_phase8"
                                                the gfx950 HIP operator (names kept for drop-in
                                                compatibility; no Triton underneath), output in q.dtype
-  "hip", "hip_fused"                           the same HIP operator under its own name
+  "hip", "hip_fused"                           the same HIP operator under its own name; also Dv != D
   "triton_qk", "triton_ref", "triton"          HIP Q K^T scores (float32), softmax and PV in PyTorch
                                                (custom.py:30-36)
   "triton_fast"                                HIP Q K^T scores in the input dtype, then the same
@@ -40,8 +40,8 @@ def sdpa_custom(q, k, v, *, backend: str = "reference", causal: bool = False):
             raise AssertionError("the custom backend has no causal mask; use a HIP backend")
         return SDPACustom.apply(q, k, v)
     if backend in HIP_BACKENDS:
-        if q.shape[-1] != v.shape[-1]:
-            raise AssertionError(f"{backend} requires Dv == D")
+        if backend.startswith("triton") and q.shape[-1] != v.shape[-1]:
+            raise AssertionError(f"{backend} requires Dv == D")  # the reference's guard, custom.py:52
         return hip_sdpa(q, k, v, causal=causal).to(q.dtype)
     if backend in PARTIAL_FUSION_BACKENDS and causal:
         raise AssertionError(f"the {backend} backend has no causal mask; use a HIP fused backend")

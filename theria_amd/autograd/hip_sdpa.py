@@ -124,19 +124,44 @@ class SDPAOp(torch.autograd.Function):
         return to, None
 
 
+def _common_head_dim(q, k, v):
+    """q, k, v zero-padded along the head dim to max(D, Dv) when Dv != D, and Dv.
+
+    Zero columns add nothing to Q K^T and the padded columns of O = P V are sliced off, so the result
+    and every derivative (padding and slicing are linear) equal the unpadded operator's; the kernels
+    themselves take one head dim for Q, K and V.
+    """
+    D, Dv = q.shape[-1], v.shape[-1]
+    if D == Dv:
+        return q, k, v, Dv
+    Dp = max(D, Dv)
+    if D < Dp:
+        q = torch.nn.functional.pad(q, (0, Dp - D))
+        k = torch.nn.functional.pad(k, (0, Dp - D))
+    else:
+        v = torch.nn.functional.pad(v, (0, Dp - Dv))
+    return q, k, v, Dv
+
+
 def hip_sdpa(q, k, v, *, causal: bool = False, scale: float | None = None, out_fp32: bool = False):
-    """Differentiable SDPA through the HIP kernels (any order; see the module docstring). Returns O only."""
+    """Differentiable SDPA through the HIP kernels (any order; see the module docstring). Returns O only.
+
+    v may have its own head dim Dv (B, H, M, Dv); scale defaults to 1/sqrt(D) of q and k.
+    """
     if scale is None:
         scale = _ops.default_scale(q.shape[-1])
+    q, k, v, dv = _common_head_dim(q, k, v)
     o, _ = SDPAOp.apply(q, k, v, float(scale), bool(causal), bool(out_fp32))
-    return o
+    return o if o.shape[-1] == dv else o[..., :dv]
 
 
 def hip_sdpa_with_lse(q, k, v, *, causal: bool = False, scale: float | None = None):
     """(O, lse) with lse = log-sum-exp of the scaled scores per query row (not differentiable)."""
     if scale is None:
         scale = _ops.default_scale(q.shape[-1])
-    return SDPAOp.apply(q, k, v, float(scale), bool(causal), False)
+    q, k, v, dv = _common_head_dim(q, k, v)
+    o, lse = SDPAOp.apply(q, k, v, float(scale), bool(causal), False)
+    return (o if o.shape[-1] == dv else o[..., :dv]), lse
 
 
 __all__ = ["SDPAOp", "SDPABackwardOp", "hip_sdpa", "hip_sdpa_with_lse"]
