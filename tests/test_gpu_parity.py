@@ -67,6 +67,9 @@ CASES = [
     (torch.bfloat16, 1, 2, 96, 80, 128, False),
     (torch.bfloat16, 1, 1, 1, 17, 16, False),
     (torch.float16, 1, 2, 200, 200, 128, True),
+    # several full 128-row tiles plus ragged ends (head dim 128 runs the backward on 128-row tiles)
+    (torch.bfloat16, 1, 2, 600, 600, 128, True),
+    (torch.float16, 1, 1, 520, 777, 128, False),
 ]
 
 

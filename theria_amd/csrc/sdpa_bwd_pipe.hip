@@ -6,13 +6,13 @@
 // dim is 64 or 128 and every view allows 16-byte access; the general kernel covers the rest.
 //
 // Work decomposition: one workgroup = NW waves, each owning 32 keys (K and V fragments in registers,
-// dK and dV accumulated in registers); the workgroup streams the query tiles (64 rows) of its head.
+// dK and dV accumulated in registers); the workgroup streams the query tiles (64 or 128 rows) of its head.
 //  * Q and dO tiles reach LDS by DMA (sdpa_lds.hpp) into double buffers with one barrier per tile;
 //    the row terms lse * log2(e) and -delta of the next tile are loaded by the first 64 threads during
 //    the current tile and written beside them.
 //  * Scores are S = Q K^T with this lane's key in the column, so dV += P^T dO and dK += dS^T Q take
 //    P and dS straight from the accumulators (KACC order) and dO^T / Q^T from LDS transpose reads.
-//  * Phase order per tile of two 32-query subtiles (scheduling barriers keep it):
+//  * Phase order per 64-row half of a tile, i.e. two 32-query subtiles (scheduling barriers keep it):
 //      S, dP of subtile 0 | S, dP of subtile 1 with exp / dS of subtile 0
 //      | dV, dK of subtile 0 with exp / dS of subtile 1 | dV, dK of subtile 1.
 //  * dP starts from -delta as the MFMA accumulator input, so dS = P o dP is one multiply.
@@ -28,6 +28,21 @@
 #endif
 #ifndef DKDV_PIPE_NW
 #define DKDV_PIPE_NW 4
+#endif
+// 64-row halves per tile (one barrier per tile): the query tile of dK/dV and the key tile of dQ. At head
+// dim 128 (one wave per SIMD) 128-row tiles halve the barriers, which shortens dK/dV by a quarter; at 64
+// (two waves per SIMD) the tile height makes no measurable difference.
+#ifndef DQ64_HALVES
+#define DQ64_HALVES 1
+#endif
+#ifndef DKDV64_HALVES
+#define DKDV64_HALVES 1
+#endif
+#ifndef DQ128_HALVES
+#define DQ128_HALVES 2
+#endif
+#ifndef DKDV128_HALVES
+#define DKDV128_HALVES 2
 #endif
 // Head dim 128: subtile overlap and waves per SIMD
 #ifndef DQ128_OVERLAP
@@ -45,13 +60,14 @@
 
 namespace theria {
 
-template <typename T, bool CAUSAL, int NW, int DP, bool OVERLAP, int WPS>
+template <typename T, bool CAUSAL, int NW, int DP, bool OVERLAP, int WPS, int HALVES>
 __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
   using Dma = SwzDma<NW, DP>;
   constexpr int NKC = DP / 16, NDT = DP / 32;
-  constexpr int BN = 32 * NW, BM = 64, TILE = BM * 2 * DP, NSLAB = BM / Dma::SLAB_ROWS;
+  constexpr int BN = 32 * NW, BM = 64 * HALVES, TILE = BM * 2 * DP, NSLAB = BM / Dma::SLAB_ROWS;
+  static_assert(64 * NW >= BM, "the row terms of a tile are loaded one per thread");
   // OVERLAP: the exp / dS work of one subtile overlaps the products of the next (more live registers);
   // otherwise subtiles run one after the other. WPS: waves per SIMD the register budget is sized for.
   __shared__ __attribute__((aligned(1024))) char sQ0[TILE];
@@ -186,20 +202,24 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
       load_rows(it + 2);
     }
     if constexpr (FAST && OVERLAP) {
-      f32x16_t s0, p0, s1, p1;
-      F pf0[2], df0[2], pf1[2], df1[2];
-      sdp(tq, to, tr, 0, s0, p0);
-      __builtin_amdgcn_sched_barrier(0);
-      sdp(tq, to, tr, 1, s1, p1);
-      pds(tr, 0, s0, p0, pf0, df0);
-      __builtin_amdgcn_sched_barrier(0);
-      dvdk(tq, to, 0, pf0, df0);
-      pds(tr, 1, s1, p1, pf1, df1);
-      __builtin_amdgcn_sched_barrier(0);
-      dvdk(tq, to, 1, pf1, df1);
+#pragma unroll
+      for (int hf = 0; hf < HALVES; ++hf) {
+        f32x16_t s0, p0, s1, p1;
+        F pf0[2], df0[2], pf1[2], df1[2];
+        sdp(tq, to, tr, 2 * hf, s0, p0);
+        __builtin_amdgcn_sched_barrier(0);
+        sdp(tq, to, tr, 2 * hf + 1, s1, p1);
+        pds(tr, 2 * hf, s0, p0, pf0, df0);
+        __builtin_amdgcn_sched_barrier(0);
+        dvdk(tq, to, 2 * hf, pf0, df0);
+        pds(tr, 2 * hf + 1, s1, p1, pf1, df1);
+        __builtin_amdgcn_sched_barrier(0);
+        dvdk(tq, to, 2 * hf + 1, pf1, df1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     } else if constexpr (FAST) {
 #pragma unroll
-      for (int qs = 0; qs < 2; ++qs) {
+      for (int qs = 0; qs < 2 * HALVES; ++qs) {
         f32x16_t sc, dp;
         F pf[2], df[2];
         sdp(tq, to, tr, qs, sc, dp);
@@ -208,7 +228,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
       }
     } else {
 #pragma unroll
-      for (int qs = 0; qs < 2; ++qs) {
+      for (int qs = 0; qs < 2 * HALVES; ++qs) {
         const int q0s = q0 + 32 * qs;
         if (q0s >= s.T || (CAUSAL && kw0 > q0s + 31)) continue;  // wave-uniform
         f32x16_t sc, dp;
@@ -274,18 +294,19 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
 // dQ pass with the contract of dq_kernel (sdpa_bwd.hip): dQ = scale dS K with dS = P o (dO V^T - delta)
 // (reference triton_sdpa_backward.py:505-696), and delta = rowsum(dO o O) computed here when O is given.
 // One workgroup = NW waves of 32 queries each (Q and dO fragments, dQ accumulated in registers); K and V
-// tiles of 64 keys stream through DMA-filled swizzled double buffers, one barrier per tile. Scores are
-// transposed (S^T = K Q^T, this lane's query in the column), so lse and delta are per-lane scalars and
-// dQ^T += K^T dS^T takes dS^T from the accumulators. Phase order per key tile of two 32-key subtiles:
+// tiles of 64 or 128 keys stream through DMA-filled swizzled double buffers, one barrier per tile. Scores
+// are transposed (S^T = K Q^T, this lane's query in the column), so lse and delta are per-lane scalars and
+// dQ^T += K^T dS^T takes dS^T from the accumulators. Phase order per 64-key half of a tile, i.e. two
+// 32-key subtiles:
 //   S, dP of subtile 0 | S, dP of subtile 1 with exp / dS of subtile 0
 //   | dQ of subtile 0 with exp / dS of subtile 1 | dQ of subtile 1.
-template <typename T, bool CAUSAL, int NW, int DP, bool OVERLAP, int WPS>
+template <typename T, bool CAUSAL, int NW, int DP, bool OVERLAP, int WPS, int HALVES>
 __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
   using Dma = SwzDma<NW, DP>;
   constexpr int NKC = DP / 16, NDT = DP / 32;
-  constexpr int BM = 32 * NW, BN = 64, TILE = BN * 2 * DP, NSLAB = BN / Dma::SLAB_ROWS;
+  constexpr int BM = 32 * NW, BN = 64 * HALVES, TILE = BN * 2 * DP, NSLAB = BN / Dma::SLAB_ROWS;
   __shared__ __attribute__((aligned(1024))) char sK0[TILE];
   __shared__ __attribute__((aligned(1024))) char sK1[TILE];
   __shared__ __attribute__((aligned(1024))) char sV0[TILE];
@@ -406,7 +427,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
     }
     if constexpr (FAST && !OVERLAP) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
+      for (int t = 0; t < 2 * HALVES; ++t) {
         f32x16_t sc, dp;
         F df[2];
         sdp(tk, tv, t, sc, dp);
@@ -414,20 +435,24 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
         dqm(tk, t, df);
       }
     } else if constexpr (FAST) {
-      f32x16_t s0, p0, s1, p1;
-      F d0[2], d1[2];
-      sdp(tk, tv, 0, s0, p0);
-      __builtin_amdgcn_sched_barrier(0);
-      sdp(tk, tv, 1, s1, p1);
-      pds(s0, p0, d0);
-      __builtin_amdgcn_sched_barrier(0);
-      dqm(tk, 0, d0);
-      pds(s1, p1, d1);
-      __builtin_amdgcn_sched_barrier(0);
-      dqm(tk, 1, d1);
+#pragma unroll
+      for (int hf = 0; hf < HALVES; ++hf) {
+        f32x16_t s0, p0, s1, p1;
+        F d0[2], d1[2];
+        sdp(tk, tv, 2 * hf, s0, p0);
+        __builtin_amdgcn_sched_barrier(0);
+        sdp(tk, tv, 2 * hf + 1, s1, p1);
+        pds(s0, p0, d0);
+        __builtin_amdgcn_sched_barrier(0);
+        dqm(tk, 2 * hf, d0);
+        pds(s1, p1, d1);
+        __builtin_amdgcn_sched_barrier(0);
+        dqm(tk, 2 * hf + 1, d1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     } else {
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
+      for (int t = 0; t < 2 * HALVES; ++t) {
         const int k0t = k0 + 32 * t;
         if (CAUSAL && k0t > q0w + 31) continue;  // every key after every query of the wave (uniform)
         f32x16_t sc, dp;
@@ -484,9 +509,10 @@ bool launch_dq_pipe(const DqParams& p, hipStream_t st, hipError_t* err) {
     return true;
   }
   if (p.s.D == 64)
-    hipLaunchKernelGGL((dq_pipe_kernel<T, CAUSAL, NW, 64, true, 2>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p);
+    hipLaunchKernelGGL((dq_pipe_kernel<T, CAUSAL, NW, 64, true, 2, DQ64_HALVES>), dim3((unsigned)nblk), dim3(64 * NW), 0, st,
+                       p);
   else
-    hipLaunchKernelGGL((dq_pipe_kernel<T, CAUSAL, NW, 128, DQ128_OVERLAP, DQ128_WPS>), dim3((unsigned)nblk),
+    hipLaunchKernelGGL((dq_pipe_kernel<T, CAUSAL, NW, 128, DQ128_OVERLAP, DQ128_WPS, DQ128_HALVES>), dim3((unsigned)nblk),
                        dim3(64 * NW), 0, st, p);
   *err = hipGetLastError();
   return true;
@@ -512,9 +538,10 @@ bool launch_dkdv_pipe(const DkdvParams& p, hipStream_t st, hipError_t* err) {
     return true;
   }
   if (p.s.D == 64)
-    hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, NW, 64, true, 2>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p);
+    hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, NW, 64, true, 2, DKDV64_HALVES>), dim3((unsigned)nblk), dim3(64 * NW), 0,
+                       st, p);
   else
-    hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, NW, 128, DKDV128_OVERLAP, DKDV128_WPS>), dim3((unsigned)nblk),
+    hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, NW, 128, DKDV128_OVERLAP, DKDV128_WPS, DKDV128_HALVES>), dim3((unsigned)nblk),
                        dim3(64 * NW), 0, st, p);
   *err = hipGetLastError();
   return true;
