@@ -248,6 +248,18 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
         }
       }
       exps_t(s0, 0, pn, ps);
+      if constexpr (DP == 64) {
+        // Issue order inside the phase: the four K fragment reads first, then each of the 8 MFMAs
+        // followed by 12 VALU instructions of the exponentials (measured ~5% faster than the
+        // compiler's own order at head dim 64).
+#pragma unroll
+        for (int i = 0; i < 4; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);  // VALU
+        }
+      }
       __builtin_amdgcn_sched_barrier(0);
       pv_mma(vp);
       if (STATS) {
@@ -260,6 +272,16 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
         }
       }
       exps_t(s1, 1, pn, ps);
+      if constexpr (DP == 64) {
+        // V fragment reads first, then each of the 16 PV MFMAs followed by 6 VALU instructions.
+#pragma unroll
+        for (int i = 0; i < 8; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+          __builtin_amdgcn_sched_group_barrier(0x002, 6, 1);
+        }
+      }
       bool bad = false;
 #pragma unroll
       for (int j = 0; j < QT; ++j) bad |= !(ps[j] <= 0x1p20f);
