@@ -274,6 +274,16 @@ def extras_c5():
     for fo in (False, True):
         ms = _time(lambda: meta_step(fo, batched=True), 10, 2)
         res[f"meta_steps_per_s_{'fo' if fo else 'full'}_task_batched"] = round(1e3 / ms, 3)
+    # ... and that step captured once in a HIP graph and replayed (Adam with its state on the device)
+    from theria_amd.maml import GraphedMetaStep
+
+    for fo in (False, True):
+        gm = copy.deepcopy(model)
+        gopt = torch.optim.Adam(gm.parameters(), lr=1e-3, capturable=True)
+        graphed = GraphedMetaStep(gm, gopt, tasks, inner_lr=0.4, inner_steps=5, fo=fo)
+        ms = _time(lambda: graphed.step(), 20, 3)
+        res[f"meta_steps_per_s_{'fo' if fo else 'full'}_task_batched_graph"] = round(1e3 / ms, 3)
+        del graphed, gopt, gm
     # meta-gradient agreement with the same weights on the pure-PyTorch reference backend
     ref = copy.deepcopy(model)
     ref.set_attention_backend("reference")

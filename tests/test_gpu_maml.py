@@ -80,3 +80,30 @@ def test_config5_task_batched_full_maml_matches_reference_loop(hip_device):
         rel = float((g_hip - g_ref).norm() / g_ref.norm())
         print(f"[maml] task-batched fo={fo} rel_l2={rel:.3e}", flush=True)
         assert rel < 1e-3
+
+
+def test_graphed_task_batched_meta_step_matches_eager(hip_device):
+    """GraphedMetaStep replays equal eager task-batched meta-steps (parameters after every step), with
+    new tasks copied in before each replay and eager work between the replays."""
+    from theria_amd.maml import GraphedMetaStep
+
+    dev = hip_device
+    torch.manual_seed(0)
+    eager = MHAClassifier(MHAConfig(), backend="hip").to(dev)
+    graphed = copy.deepcopy(eager)
+    g = torch.Generator().manual_seed(5)
+    batches = [[sample_token_count_task(generator=g, device=dev)[0] for _ in range(4)] for _ in range(4)]
+    opt_e = torch.optim.Adam(eager.parameters(), lr=1e-3, capturable=True)
+    opt_g = torch.optim.Adam(graphed.parameters(), lr=1e-3, capturable=True)
+    step = GraphedMetaStep(graphed, opt_g, batches[0], inner_lr=0.4, inner_steps=2)
+    for i, tasks in enumerate(batches):
+        print(f"[graphed meta-step] step {i}", flush=True)
+        opt_e.zero_grad(set_to_none=True)
+        loss_e = meta_loss_on_tasks_batched(eager, tasks, inner_lr=0.4, inner_steps=2)
+        loss_e.backward()
+        opt_e.step()
+        loss_g = step.step(tasks)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(loss_g, loss_e.detach(), rtol=1e-5, atol=1e-6)
+        for (name, a), b in zip(eager.named_parameters(), graphed.parameters()):
+            torch.testing.assert_close(b, a, rtol=1e-5, atol=1e-6, msg=lambda m: f"step {i} {name}: {m}")

@@ -92,7 +92,9 @@ class MHAClassifier(nn.Module):
             y = F.layer_norm(x, (x.shape[-1],))
             return y * params[name + ".weight"].reshape(shape) + params[name + ".bias"].reshape(shape)
 
-        onehot = F.one_hot(tokens.reshape(n, N * T), cfg.vocab).to(params["embed.weight"].dtype)
+        # one-hot by comparison: elementwise, so the pass has no host synchronisation (graph capture)
+        ids = torch.arange(cfg.vocab, device=tokens.device)
+        onehot = (tokens.reshape(n, N * T, 1) == ids).to(params["embed.weight"].dtype)
         x = torch.matmul(onehot, params["embed.weight"]).reshape(n, N, T, d)
         for i in range(cfg.layers):
             pre = f"blocks.{i}."
