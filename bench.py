@@ -163,6 +163,30 @@ def _time(fn, reps: int, warm: int = 3) -> float:
     return (time.perf_counter() - t0) / reps * 1e3
 
 
+def extras_c2_fp16():
+    """Config 2 in float16: the same fwd + dQ + dK/dV step as the headline (which is bfloat16)."""
+    import torch
+
+    from theria_amd import _ops
+
+    dev = torch.device("cuda:0")
+    B, H, S, D = 4, 16, 2048, 64
+    q, k, v, do = (_rand((B, H, S, D), torch.float16, dev, 500 + i) for i in range(4))
+    scale = 1.0 / math.sqrt(D)
+    prob = _ops._problem(q, k, scale, False)
+    delta = torch.empty((B, H, S), dtype=torch.float32, device=dev)
+    dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+
+    def step():
+        o, lse, _, _ = _ops.fwd(q, k, v, scale, False)
+        _ops.bwd_dq(prob, q, k, v, o, False, do, lse, delta, dq)
+        _ops.bwd_dkdv(prob, q, k, v, do, lse, delta, dk, dv)
+
+    ms = _time(step, 30, 5)
+    return {"config": "B4 H16 S2048 D64 fp16 fwd+bwd", "ms": round(ms, 4),
+            "tflops": round(14 * B * H * S * S * D / (ms * 1e-3) / 1e12, 1)}
+
+
 def extras_c3():
     """Config 3: B1 H32 S8192 D128 causal bf16 fwd+bwd; FLOPs over the unmasked triangle."""
     import torch
@@ -381,7 +405,7 @@ def main() -> int:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     if not args.no_extras:
         extra = {}
-        for name, fn in (("c3", extras_c3), ("c4", extras_c4), ("c5", extras_c5)):
+        for name, fn in (("c2_fp16", extras_c2_fp16), ("c3", extras_c3), ("c4", extras_c4), ("c5", extras_c5)):
             try:
                 extra[name] = fn()
             except Exception as exc:  # an extra must not hide the headline line
