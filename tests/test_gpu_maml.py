@@ -107,3 +107,29 @@ def test_graphed_task_batched_meta_step_matches_eager(hip_device):
         torch.testing.assert_close(loss_g, loss_e.detach(), rtol=1e-5, atol=1e-6)
         for (name, a), b in zip(eager.named_parameters(), graphed.parameters()):
             torch.testing.assert_close(b, a, rtol=1e-5, atol=1e-6, msg=lambda m: f"step {i} {name}: {m}")
+
+
+def test_task_batched_meta_step_issues_no_memset(hip_device):
+    """The step GraphedMetaStep captures must contain no device memset (memset nodes in a replayed graph
+    are not trusted): profile one eager step at config 5's meta-batch and count memset activities."""
+    from torch.profiler import ProfilerActivity, profile
+
+    dev = hip_device
+    torch.manual_seed(0)
+    model = MHAClassifier(MHAConfig(), backend="hip").to(dev)
+    g = torch.Generator().manual_seed(9)
+    tasks = [sample_token_count_task(generator=g, device=dev)[0] for _ in range(16)]
+    opt = torch.optim.Adam(model.parameters(), lr=1e-3, capturable=True)
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        meta_loss_on_tasks_batched(model, tasks, inner_lr=0.4, inner_steps=5).backward()
+        opt.step()
+
+    step()
+    torch.cuda.synchronize()
+    with profile(activities=[ProfilerActivity.CPU, ProfilerActivity.CUDA]) as prof:
+        step()
+        torch.cuda.synchronize()
+    memsets = [e.name for e in prof.events() if "memset" in e.name.lower() or "fillbuffer" in e.name.lower()]
+    assert not memsets, f"{len(memsets)} memset activities, e.g. {memsets[:3]}"

@@ -37,7 +37,10 @@ def inner_adapt_batched(model: nn.Module, params, x_s, y_s, *, inner_lr: float =
                         fo: bool = False):
     """Per-task adapted parameters (n, *shape) after `inner_steps` SGD steps; create_graph unless fo."""
     n = x_s.shape[0]
-    phi = OrderedDict((name, w.unsqueeze(0).expand(n, *w.shape)) for name, w in params.items())
+    # theta repeated n times as ones(n, 1) @ theta: the meta-gradient's sum over tasks is then a GEMM
+    # (an expand's backward would be a multi-block sum, which issues a device memset)
+    ones = next(iter(params.values())).new_ones(n, 1)
+    phi = OrderedDict((name, torch.matmul(ones, w.reshape(1, -1)).reshape(n, *w.shape)) for name, w in params.items())
     for _ in range(inner_steps):
         support = _task_losses(model.forward_batched(phi, x_s), y_s).sum()
         grads = torch.autograd.grad(support, tuple(phi.values()), create_graph=not fo, retain_graph=True)

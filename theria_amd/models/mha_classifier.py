@@ -74,23 +74,30 @@ class MHAClassifier(nn.Module):
         """Many parameter sets at once: params[name] is (n, *shape), tokens (n, N, T) -> logits (n, N, C).
 
         The same computation as forward() for each of the n parameter sets, with every layer batched
-        over n: per-set linear layers are batched matmuls, the embedding is a one-hot matmul (its
-        backward is a matmul too, so every order of derivative stays deterministic) and attention is
-        one sdpa_custom call over n * N sequences.
+        over n: per-set linear layers and layer-norm affines are batched matmuls (bias folded in as a
+        ones column), the embedding is a one-hot matmul and attention is one sdpa_custom call over
+        n * N sequences. Every gradient of these is a matmul or elementwise, so no derivative order
+        needs a device memset or atomics: the pass is deterministic and can be captured in a graph.
         """
         cfg = self.cfg
         n, N, T = tokens.shape
         d, H = cfg.d_model, cfg.heads
 
+        def affine(x, wt, b):
+            # x @ wt + b as one batched matmul of [x, 1] with [wt; b]: its gradients are GEMMs, not
+            # multi-block sums over the broadcast rows (those issue device memsets, which a captured
+            # graph must not contain)
+            x2 = x.reshape(n, -1, x.shape[-1])
+            xa = torch.cat([x2, x2.new_ones(n, x2.shape[1], 1)], dim=2)
+            y = torch.matmul(xa, torch.cat([wt, b.unsqueeze(1)], dim=1))
+            return y.reshape(*x.shape[:-1], wt.shape[-1])
+
         def lin(x, name):
-            w, b = params[name + ".weight"], params[name + ".bias"]
-            y = torch.matmul(x.reshape(n, -1, x.shape[-1]), w.transpose(1, 2)) + b.unsqueeze(1)
-            return y.reshape(*x.shape[:-1], w.shape[1])
+            return affine(x, params[name + ".weight"].transpose(1, 2), params[name + ".bias"])
 
         def norm(x, name):
-            shape = (n,) + (1,) * (x.dim() - 2) + (x.shape[-1],)
             y = F.layer_norm(x, (x.shape[-1],))
-            return y * params[name + ".weight"].reshape(shape) + params[name + ".bias"].reshape(shape)
+            return affine(y, torch.diag_embed(params[name + ".weight"]), params[name + ".bias"])
 
         # one-hot by comparison: elementwise, so the pass has no host synchronisation (graph capture)
         ids = torch.arange(cfg.vocab, device=tokens.device)
