@@ -73,6 +73,9 @@ struct SwzDma {
   static constexpr int RPW = 1024 / RB;        // rows per wave instruction
   static constexpr int SLAB_ROWS = RPW * NW;
   static constexpr int SLAB_BYTES = SLAB_ROWS * RB;
+  // A lane derives its swizzle from its row inside the slab; that equals the swizzle of the tile row
+  // only if slabs start on multiples of the swizzle's period (16 rows).
+  static_assert(SLAB_ROWS % 16 == 0, "LDS DMA slabs must span a multiple of 16 rows (more waves per workgroup)");
   int row;    // row of the slab filled by this lane
   int chunk;  // logical 16-byte chunk this lane fetches
   int dst;    // byte offset of this wave's piece in a slab
