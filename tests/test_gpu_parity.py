@@ -70,6 +70,11 @@ CASES = [
     # several full 128-row tiles plus ragged ends (head dim 128 runs the backward on 128-row tiles)
     (torch.bfloat16, 1, 2, 600, 600, 128, True),
     (torch.float16, 1, 1, 520, 777, 128, False),
+    # causal blocks run in mirrored pairs: odd block counts (a middle block that runs alone) and T != M
+    (torch.bfloat16, 1, 2, 300, 300, 64, True),
+    (torch.float16, 2, 1, 390, 390, 128, True),
+    (torch.bfloat16, 1, 2, 200, 330, 64, True),
+    (torch.bfloat16, 1, 1, 330, 200, 64, True),
 ]
 
 

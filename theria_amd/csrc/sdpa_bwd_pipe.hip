@@ -82,213 +82,226 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
   const int lane = tid & 63, li = lane & 31, g = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nkb = (s.M + BN - 1) / BN;
+  // Causal at head dim 64: workgroup `unit` runs key block `unit` (the longest query range) and then its
+  // mirror block nkb - 1 - unit, so every workgroup gets the same number of query tiles; an odd middle
+  // block runs once. At head dim 128 (one workgroup per CU) the plain longest-first order measured faster.
+  constexpr bool PAIR = CAUSAL && DP == 64;
+  const int nunit = PAIR ? (nkb + 1) / 2 : nkb;
   const int bid = xcd_remap(blockIdx.x, gridDim.x);
-  const int bh = bid / nkb;
-  const int kb = bid - bh * nkb;  // causal: ascending key blocks = longest query ranges first
+  const int bh = bid / nunit;
+  const int unit = bid - bh * nunit;
   const int b = bh / s.H, h = bh - b * s.H;
   const T* Q = (const T*)p.q.p + b * p.q.sb + h * p.q.sh;
   const T* K = (const T*)p.k.p + b * p.k.sb + h * p.k.sh;
   const T* V = (const T*)p.v.p + b * p.v.sb + h * p.v.sh;
   const T* dO = (const T*)p.dout.p + b * p.dout.sb + h * p.dout.sh;
-  const int key0 = kb * BN;
-  const int kw0 = key0 + wave * 32;  // this wave's keys: kw0 + li
   const int64_t rowbase = (int64_t)bh * s.T;
   const float c2 = s.scale * kLog2e;
 
-  F kf[NKC], vf[NKC];
-#pragma unroll
-  for (int c = 0; c < NKC; ++c) {
-    kf[c] = gload_frag<T>(K, p.k.sr, kw0 + li, s.M, c, DP, true);
-    vf[c] = gload_frag<T>(V, p.v.sr, kw0 + li, s.M, c, DP, true);
+  for (int pass = 0; pass < (PAIR ? 2 : 1); ++pass) {
+  const int kb = pass == 0 ? unit : nkb - 1 - unit;
+  if (pass == 1) {
+    if (kb == unit) break;  // odd number of blocks: the middle one ran in pass 0
+    __syncthreads();        // every wave is done with the LDS tiles of the first block
   }
-  f32x16_t dv[NDT], dk[NDT];
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) {
-    dv[dt] = zero16();
-    dk[dt] = zero16();
-  }
+  const int key0 = kb * BN;
+  const int kw0 = key0 + wave * 32;  // this wave's keys: kw0 + li
 
-  const int qbeg = CAUSAL ? (key0 / BM) * BM : 0;
-  const int nqt = s.T > qbeg ? (s.T - qbeg + BM - 1) / BM : 0;
-  // Tiles with every query in range and (causal) every key of the block visible to every query,
-  // in a key block whose keys are all in range, take the unmasked path.
-  // Causal: tiles before ifull straddle the diagonal (q0 < last key of the block). Full tiles end at fend.
-  const int ifull = CAUSAL ? min(nqt, (key0 + BN - 1 - qbeg + BM - 1) / BM) : 0;
-  const int fend = (key0 + BN <= s.M) ? max(ifull, min(nqt, (s.T - qbeg) / BM)) : ifull;
-
-  const Dma dma(wave, lane);
-  const uint32_t qrs = (uint32_t)p.q.sr * 2, ors = (uint32_t)p.dout.sr * 2;
-  const rsrc_t qrsrc = make_rsrc(Q, (uint32_t)s.T * qrs);
-  const rsrc_t orsrc = make_rsrc(dO, (uint32_t)s.T * ors);
-
-  // Row terms of tile `it` for thread tid < BM: lse * log2(e) (rows past the end or without visible
-  // keys: +inf, so P = 0) and -delta.
-  float r_lse = THERIA_INF, r_del = 0.f;
-  auto load_rows = [&](int it) {
-    if (tid < BM && it < nqt) {
-      const int qq = qbeg + it * BM + tid;
-      const float l2 = qq < s.T ? p.lse[rowbase + qq] * kLog2e : THERIA_INF;
-      r_lse = l2 == -THERIA_INF ? THERIA_INF : l2;
-      r_del = qq < s.T ? -p.delta[rowbase + qq] : 0.f;
-    }
-  };
-  auto store_rows = [&](float* sr) {
-    if (tid < BM) {
-      sr[tid] = r_lse;
-      sr[BM + tid] = r_del;
-    }
-  };
-
-  // S = Q K^T and dP = dO V^T - delta for subtile qs (32 queries) of the tile in (tq, to, tr).
-  auto sdp = [&](const char* tq, const char* to, const float* tr, int qs, f32x16_t& sc, f32x16_t& dp) {
-    sc = zero16();
-#pragma unroll
-    for (int qd = 0; qd < 4; ++qd) {
-      const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(tr + BM + 32 * qs + 8 * qd + 4 * g);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) dp[4 * qd + e] = d4[e];
-    }
-#pragma unroll
+    F kf[NKC], vf[NKC];
+  #pragma unroll
     for (int c = 0; c < NKC; ++c) {
-      sc = MM::mma(swz_cols<T, DP>(tq, 32 * qs + li, c), kf[c], sc);
-      dp = MM::mma(swz_cols<T, DP>(to, 32 * qs + li, c), vf[c], dp);
+      kf[c] = gload_frag<T>(K, p.k.sr, kw0 + li, s.M, c, DP, true);
+      vf[c] = gload_frag<T>(V, p.v.sr, kw0 + li, s.M, c, DP, true);
     }
-  };
-  // Masks of a general tile: keys out of range and (causal) keys after the query get S = -inf.
-  auto mask = [&](f32x16_t& sc, int q0s) {
-    const int mykey = kw0 + li;
-    if (kw0 + 31 >= s.M || (CAUSAL && kw0 + 31 > q0s)) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-        if (mykey >= s.M || (CAUSAL && mykey > q0s + acc_row(r, g))) sc[r] = -THERIA_INF;
+    f32x16_t dv[NDT], dk[NDT];
+  #pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      dv[dt] = zero16();
+      dk[dt] = zero16();
     }
-  };
-  // P = exp2(S c2 - lse2) and dS = P o dP as 16-bit fragments (KACC chunks 0, 1).
-  auto pds = [&](const float* tr, int qs, const f32x16_t& sc, const f32x16_t& dp, F (&pf)[2], F (&df)[2]) {
-#pragma unroll
-    for (int qd = 0; qd < 4; ++qd) {
-      const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(tr + 32 * qs + 8 * qd + 4 * g);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int r = 4 * qd + e;
-        const float pv = fast_exp2(fmaf(sc[r], c2, -l4[e]));
-        pf[r >> 3][r & 7] = (T)pv;
-        df[r >> 3][r & 7] = (T)(pv * dp[r]);
-      }
-    }
-  };
-  // dV += P^T dO and dK += dS^T Q for subtile qs.
-  auto dvdk = [&](const char* tq, const char* to, int qs, const F (&pf)[2], const F (&df)[2]) {
-#pragma unroll
-    for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-        dv[dt] = MM::mma(pf[cc], swz_rows<T, DP>(to, 32 * qs, cc, 32 * dt), dv[dt]);
-        dk[dt] = MM::mma(df[cc], swz_rows<T, DP>(tq, 32 * qs, cc, 32 * dt), dk[dt]);
-      }
-  };
 
-  // One query tile `it` from buffers (tq, to, tr); the next tile goes to (nq, no, nr).
-  auto step = [&](auto fast_tag, int it, const char* tq, const char* to, const float* tr, char* nq, char* no,
-                  float* nr) {
-    constexpr bool FAST = decltype(fast_tag)::value;
-    const int q0 = qbeg + it * BM;
-    wait_vm_all();
-    __syncthreads();  // tile it visible to all waves; the other buffers (tile it-1) are free
-    if (it + 1 < nqt) {
-      dma.template issue_clamped<NSLAB>(qrsrc, qrs, q0 + BM, s.T, nq);
-      dma.template issue_clamped<NSLAB>(orsrc, ors, q0 + BM, s.T, no);
-      store_rows(nr);
-      load_rows(it + 2);
-    }
-    if constexpr (FAST && OVERLAP) {
-#pragma unroll
-      for (int hf = 0; hf < HALVES; ++hf) {
-        f32x16_t s0, p0, s1, p1;
-        F pf0[2], df0[2], pf1[2], df1[2];
-        sdp(tq, to, tr, 2 * hf, s0, p0);
-        __builtin_amdgcn_sched_barrier(0);
-        sdp(tq, to, tr, 2 * hf + 1, s1, p1);
-        pds(tr, 2 * hf, s0, p0, pf0, df0);
-        __builtin_amdgcn_sched_barrier(0);
-        dvdk(tq, to, 2 * hf, pf0, df0);
-        pds(tr, 2 * hf + 1, s1, p1, pf1, df1);
-        __builtin_amdgcn_sched_barrier(0);
-        dvdk(tq, to, 2 * hf + 1, pf1, df1);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    } else if constexpr (FAST) {
-#pragma unroll
-      for (int qs = 0; qs < 2 * HALVES; ++qs) {
-        f32x16_t sc, dp;
-        F pf[2], df[2];
-        sdp(tq, to, tr, qs, sc, dp);
-        pds(tr, qs, sc, dp, pf, df);
-        dvdk(tq, to, qs, pf, df);
-      }
-    } else {
-#pragma unroll
-      for (int qs = 0; qs < 2 * HALVES; ++qs) {
-        const int q0s = q0 + 32 * qs;
-        if (q0s >= s.T || (CAUSAL && kw0 > q0s + 31)) continue;  // wave-uniform
-        f32x16_t sc, dp;
-        F pf[2], df[2];
-        sdp(tq, to, tr, qs, sc, dp);
-        mask(sc, q0s);
-        pds(tr, qs, sc, dp, pf, df);
-        dvdk(tq, to, qs, pf, df);
-      }
-    }
-  };
-  const std::integral_constant<bool, true> fast;
-  const std::integral_constant<bool, false> general;
+    const int qbeg = CAUSAL ? (key0 / BM) * BM : 0;
+    const int nqt = s.T > qbeg ? (s.T - qbeg + BM - 1) / BM : 0;
+    // Tiles with every query in range and (causal) every key of the block visible to every query,
+    // in a key block whose keys are all in range, take the unmasked path.
+    // Causal: tiles before ifull straddle the diagonal (q0 < last key of the block). Full tiles end at fend.
+    const int ifull = CAUSAL ? min(nqt, (key0 + BN - 1 - qbeg + BM - 1) / BM) : 0;
+    const int fend = (key0 + BN <= s.M) ? max(ifull, min(nqt, (s.T - qbeg) / BM)) : ifull;
 
-  if (nqt > 0) {
-    dma.template issue_clamped<NSLAB>(qrsrc, qrs, qbeg, s.T, sQ0);
-    dma.template issue_clamped<NSLAB>(orsrc, ors, qbeg, s.T, sO0);
-    load_rows(0);
-    wait_vm_all();
-    store_rows(sR0);
-    load_rows(1);
-    int it = 0;
-    // causal diagonal tiles first (general), then the full tiles two at a time (fixed buffers), then the rest
-    for (; it < ifull; ++it) {
-      if (it & 1)
-        step(general, it, sQ1, sO1, sR1, sQ0, sO0, sR0);
-      else
-        step(general, it, sQ0, sO0, sR0, sQ1, sO1, sR1);
-    }
-    if (it < fend && (it & 1)) {
-      step(fast, it, sQ1, sO1, sR1, sQ0, sO0, sR0);
-      ++it;
-    }
-    for (; it + 1 < fend; it += 2) {
-      step(fast, it, sQ0, sO0, sR0, sQ1, sO1, sR1);
-      step(fast, it + 1, sQ1, sO1, sR1, sQ0, sO0, sR0);
-    }
-    for (; it < nqt; ++it) {
-      if (it & 1)
-        step(general, it, sQ1, sO1, sR1, sQ0, sO0, sR0);
-      else
-        step(general, it, sQ0, sO0, sR0, sQ1, sO1, sR1);
-    }
-  }
+    const Dma dma(wave, lane);
+    const uint32_t qrs = (uint32_t)p.q.sr * 2, ors = (uint32_t)p.dout.sr * 2;
+    const rsrc_t qrsrc = make_rsrc(Q, (uint32_t)s.T * qrs);
+    const rsrc_t orsrc = make_rsrc(dO, (uint32_t)s.T * ors);
 
-  // Epilogue: lane holds column d = dt*32 + li of keys kw0 + acc_row(r, g).
-  T* DV = (T*)p.dv.p + b * p.dv.sb + h * p.dv.sh;
-  T* DK = p.dk.p ? (T*)p.dk.p + b * p.dk.sb + h * p.dk.sh : nullptr;
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) {
-    const int d = dt * 32 + li;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = kw0 + acc_row(r, g);
-      if (key < s.M) {
-        DV[(int64_t)key * p.dv.sr + d] = (T)dv[dt][r];
-        if (DK) DK[(int64_t)key * p.dk.sr + d] = (T)(dk[dt][r] * s.scale);
+    // Row terms of tile `it` for thread tid < BM: lse * log2(e) (rows past the end or without visible
+    // keys: +inf, so P = 0) and -delta.
+    float r_lse = THERIA_INF, r_del = 0.f;
+    auto load_rows = [&](int it) {
+      if (tid < BM && it < nqt) {
+        const int qq = qbeg + it * BM + tid;
+        const float l2 = qq < s.T ? p.lse[rowbase + qq] * kLog2e : THERIA_INF;
+        r_lse = l2 == -THERIA_INF ? THERIA_INF : l2;
+        r_del = qq < s.T ? -p.delta[rowbase + qq] : 0.f;
+      }
+    };
+    auto store_rows = [&](float* sr) {
+      if (tid < BM) {
+        sr[tid] = r_lse;
+        sr[BM + tid] = r_del;
+      }
+    };
+
+    // S = Q K^T and dP = dO V^T - delta for subtile qs (32 queries) of the tile in (tq, to, tr).
+    auto sdp = [&](const char* tq, const char* to, const float* tr, int qs, f32x16_t& sc, f32x16_t& dp) {
+      sc = zero16();
+  #pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(tr + BM + 32 * qs + 8 * qd + 4 * g);
+  #pragma unroll
+        for (int e = 0; e < 4; ++e) dp[4 * qd + e] = d4[e];
+      }
+  #pragma unroll
+      for (int c = 0; c < NKC; ++c) {
+        sc = MM::mma(swz_cols<T, DP>(tq, 32 * qs + li, c), kf[c], sc);
+        dp = MM::mma(swz_cols<T, DP>(to, 32 * qs + li, c), vf[c], dp);
+      }
+    };
+    // Masks of a general tile: keys out of range and (causal) keys after the query get S = -inf.
+    auto mask = [&](f32x16_t& sc, int q0s) {
+      const int mykey = kw0 + li;
+      if (kw0 + 31 >= s.M || (CAUSAL && kw0 + 31 > q0s)) {
+  #pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (mykey >= s.M || (CAUSAL && mykey > q0s + acc_row(r, g))) sc[r] = -THERIA_INF;
+      }
+    };
+    // P = exp2(S c2 - lse2) and dS = P o dP as 16-bit fragments (KACC chunks 0, 1).
+    auto pds = [&](const float* tr, int qs, const f32x16_t& sc, const f32x16_t& dp, F (&pf)[2], F (&df)[2]) {
+  #pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(tr + 32 * qs + 8 * qd + 4 * g);
+  #pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * qd + e;
+          const float pv = fast_exp2(fmaf(sc[r], c2, -l4[e]));
+          pf[r >> 3][r & 7] = (T)pv;
+          df[r >> 3][r & 7] = (T)(pv * dp[r]);
+        }
+      }
+    };
+    // dV += P^T dO and dK += dS^T Q for subtile qs.
+    auto dvdk = [&](const char* tq, const char* to, int qs, const F (&pf)[2], const F (&df)[2]) {
+  #pragma unroll
+      for (int cc = 0; cc < 2; ++cc)
+  #pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+          dv[dt] = MM::mma(pf[cc], swz_rows<T, DP>(to, 32 * qs, cc, 32 * dt), dv[dt]);
+          dk[dt] = MM::mma(df[cc], swz_rows<T, DP>(tq, 32 * qs, cc, 32 * dt), dk[dt]);
+        }
+    };
+
+    // One query tile `it` from buffers (tq, to, tr); the next tile goes to (nq, no, nr).
+    auto step = [&](auto fast_tag, int it, const char* tq, const char* to, const float* tr, char* nq, char* no,
+                    float* nr) {
+      constexpr bool FAST = decltype(fast_tag)::value;
+      const int q0 = qbeg + it * BM;
+      wait_vm_all();
+      __syncthreads();  // tile it visible to all waves; the other buffers (tile it-1) are free
+      if (it + 1 < nqt) {
+        dma.template issue_clamped<NSLAB>(qrsrc, qrs, q0 + BM, s.T, nq);
+        dma.template issue_clamped<NSLAB>(orsrc, ors, q0 + BM, s.T, no);
+        store_rows(nr);
+        load_rows(it + 2);
+      }
+      if constexpr (FAST && OVERLAP) {
+  #pragma unroll
+        for (int hf = 0; hf < HALVES; ++hf) {
+          f32x16_t s0, p0, s1, p1;
+          F pf0[2], df0[2], pf1[2], df1[2];
+          sdp(tq, to, tr, 2 * hf, s0, p0);
+          __builtin_amdgcn_sched_barrier(0);
+          sdp(tq, to, tr, 2 * hf + 1, s1, p1);
+          pds(tr, 2 * hf, s0, p0, pf0, df0);
+          __builtin_amdgcn_sched_barrier(0);
+          dvdk(tq, to, 2 * hf, pf0, df0);
+          pds(tr, 2 * hf + 1, s1, p1, pf1, df1);
+          __builtin_amdgcn_sched_barrier(0);
+          dvdk(tq, to, 2 * hf + 1, pf1, df1);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else if constexpr (FAST) {
+  #pragma unroll
+        for (int qs = 0; qs < 2 * HALVES; ++qs) {
+          f32x16_t sc, dp;
+          F pf[2], df[2];
+          sdp(tq, to, tr, qs, sc, dp);
+          pds(tr, qs, sc, dp, pf, df);
+          dvdk(tq, to, qs, pf, df);
+        }
+      } else {
+  #pragma unroll
+        for (int qs = 0; qs < 2 * HALVES; ++qs) {
+          const int q0s = q0 + 32 * qs;
+          if (q0s >= s.T || (CAUSAL && kw0 > q0s + 31)) continue;  // wave-uniform
+          f32x16_t sc, dp;
+          F pf[2], df[2];
+          sdp(tq, to, tr, qs, sc, dp);
+          mask(sc, q0s);
+          pds(tr, qs, sc, dp, pf, df);
+          dvdk(tq, to, qs, pf, df);
+        }
+      }
+    };
+    const std::integral_constant<bool, true> fast;
+    const std::integral_constant<bool, false> general;
+
+    if (nqt > 0) {
+      dma.template issue_clamped<NSLAB>(qrsrc, qrs, qbeg, s.T, sQ0);
+      dma.template issue_clamped<NSLAB>(orsrc, ors, qbeg, s.T, sO0);
+      load_rows(0);
+      wait_vm_all();
+      store_rows(sR0);
+      load_rows(1);
+      int it = 0;
+      // causal diagonal tiles first (general), then the full tiles two at a time (fixed buffers), then the rest
+      for (; it < ifull; ++it) {
+        if (it & 1)
+          step(general, it, sQ1, sO1, sR1, sQ0, sO0, sR0);
+        else
+          step(general, it, sQ0, sO0, sR0, sQ1, sO1, sR1);
+      }
+      if (it < fend && (it & 1)) {
+        step(fast, it, sQ1, sO1, sR1, sQ0, sO0, sR0);
+        ++it;
+      }
+      for (; it + 1 < fend; it += 2) {
+        step(fast, it, sQ0, sO0, sR0, sQ1, sO1, sR1);
+        step(fast, it + 1, sQ1, sO1, sR1, sQ0, sO0, sR0);
+      }
+      for (; it < nqt; ++it) {
+        if (it & 1)
+          step(general, it, sQ1, sO1, sR1, sQ0, sO0, sR0);
+        else
+          step(general, it, sQ0, sO0, sR0, sQ1, sO1, sR1);
       }
     }
-  }
+
+    // Epilogue: lane holds column d = dt*32 + li of keys kw0 + acc_row(r, g).
+    T* DV = (T*)p.dv.p + b * p.dv.sb + h * p.dv.sh;
+    T* DK = p.dk.p ? (T*)p.dk.p + b * p.dk.sb + h * p.dk.sh : nullptr;
+  #pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      const int d = dt * 32 + li;
+  #pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kw0 + acc_row(r, g);
+        if (key < s.M) {
+          DV[(int64_t)key * p.dv.sr + d] = (T)dv[dt][r];
+          if (DK) DK[(int64_t)key * p.dk.sr + d] = (T)(dk[dt][r] * s.scale);
+        }
+      }
+    }
+  }  // pass
 }
 
 // dQ pass with the contract of dq_kernel (sdpa_bwd.hip): dQ = scale dS K with dS = P o (dO V^T - delta)
@@ -316,185 +329,195 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
   const int lane = threadIdx.x & 63, li = lane & 31, g = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nqb = (s.T + BM - 1) / BM;
+  // Causal: workgroup `unit` runs query block nqb - 1 - unit (the longest rows) and then its mirror
+  // block `unit`, so every workgroup gets the same number of key tiles; an odd middle block runs once.
+  const int nunit = CAUSAL ? (nqb + 1) / 2 : nqb;
   const int bid = xcd_remap(blockIdx.x, gridDim.x);
-  const int bh = bid / nqb;
-  int qb = bid - bh * nqb;
-  if (CAUSAL) qb = nqb - 1 - qb;  // longest rows first
+  const int bh = bid / nunit;
+  const int unit = bid - bh * nunit;
   const int b = bh / s.H, h = bh - b * s.H;
   const T* Q = (const T*)p.q.p + b * p.q.sb + h * p.q.sh;
   const T* K = (const T*)p.k.p + b * p.k.sb + h * p.k.sh;
   const T* V = (const T*)p.v.p + b * p.v.sb + h * p.v.sh;
   const T* dO = (const T*)p.dout.p + b * p.dout.sb + h * p.dout.sh;
-  const int q0w = qb * BM + wave * 32;
-  const int myq = q0w + li;
-  const bool qvalid = myq < s.T;
-  const int64_t rowbase = (int64_t)bh * s.T;
 
-  F qf[NKC], of[NKC];
-#pragma unroll
-  for (int c = 0; c < NKC; ++c) {
-    qf[c] = gload_frag<T>(Q, p.q.sr, myq, s.T, c, DP, true);
-    of[c] = gload_frag<T>(dO, p.dout.sr, myq, s.T, c, DP, true);
+  for (int pass = 0; pass < (CAUSAL ? 2 : 1); ++pass) {
+  const int qb = CAUSAL ? (pass == 0 ? nqb - 1 - unit : unit) : unit;
+  if (pass == 1) {
+    if (qb == nqb - 1 - unit) break;  // odd number of blocks: the middle one ran in pass 0
+    __syncthreads();                  // every wave is done with the LDS tiles of the first block
   }
-  const float l2 = qvalid ? p.lse[rowbase + myq] * kLog2e : THERIA_INF;
-  const float lse2 = l2 == -THERIA_INF ? THERIA_INF : l2;  // a row without visible keys has P = 0
-  float del;
-  if (p.o.p) {
-    // delta = dO . O over this lane's half of the head dim (the dO fragment's columns), then the pair
-    float part = 0.f;
-    if (qvalid) {
-#pragma unroll
-      for (int c = 0; c < NKC; ++c) {
-        const int col = c * 16 + 8 * g;
-        const int64_t off = (int64_t)myq * p.o.sr + col;
-        if (p.o_f32) {
-          const float* Op = (const float*)p.o.p + b * p.o.sb + h * p.o.sh + off;
-          const f32x4_t a0 = *reinterpret_cast<const f32x4_t*>(Op);
-          const f32x4_t a1 = *reinterpret_cast<const f32x4_t*>(Op + 4);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) part += a0[e] * (float)of[c][e] + a1[e] * (float)of[c][4 + e];
-        } else {
-          const F ov = __builtin_bit_cast(F, *reinterpret_cast<const i16x8_t*>((const T*)p.o.p + b * p.o.sb +
-                                                                             h * p.o.sh + off));
-#pragma unroll
-          for (int e = 0; e < 8; ++e) part += (float)ov[e] * (float)of[c][e];
+  const int q0w = qb * BM + wave * 32;
+    const int myq = q0w + li;
+    const bool qvalid = myq < s.T;
+    const int64_t rowbase = (int64_t)bh * s.T;
+
+    F qf[NKC], of[NKC];
+  #pragma unroll
+    for (int c = 0; c < NKC; ++c) {
+      qf[c] = gload_frag<T>(Q, p.q.sr, myq, s.T, c, DP, true);
+      of[c] = gload_frag<T>(dO, p.dout.sr, myq, s.T, c, DP, true);
+    }
+    const float l2 = qvalid ? p.lse[rowbase + myq] * kLog2e : THERIA_INF;
+    const float lse2 = l2 == -THERIA_INF ? THERIA_INF : l2;  // a row without visible keys has P = 0
+    float del;
+    if (p.o.p) {
+      // delta = dO . O over this lane's half of the head dim (the dO fragment's columns), then the pair
+      float part = 0.f;
+      if (qvalid) {
+  #pragma unroll
+        for (int c = 0; c < NKC; ++c) {
+          const int col = c * 16 + 8 * g;
+          const int64_t off = (int64_t)myq * p.o.sr + col;
+          if (p.o_f32) {
+            const float* Op = (const float*)p.o.p + b * p.o.sb + h * p.o.sh + off;
+            const f32x4_t a0 = *reinterpret_cast<const f32x4_t*>(Op);
+            const f32x4_t a1 = *reinterpret_cast<const f32x4_t*>(Op + 4);
+  #pragma unroll
+            for (int e = 0; e < 4; ++e) part += a0[e] * (float)of[c][e] + a1[e] * (float)of[c][4 + e];
+          } else {
+            const F ov = __builtin_bit_cast(F, *reinterpret_cast<const i16x8_t*>((const T*)p.o.p + b * p.o.sb +
+                                                                               h * p.o.sh + off));
+  #pragma unroll
+            for (int e = 0; e < 8; ++e) part += (float)ov[e] * (float)of[c][e];
+          }
         }
       }
-    }
-    del = pair_sum(part);
-    if (qvalid && g == 0) p.delta[rowbase + myq] = del;
-  } else {
-    del = qvalid ? p.delta[rowbase + myq] : 0.f;
-  }
-  if (!p.dq.p) return;  // only the row term was requested (uniform over the grid)
-
-  f32x16_t acc[NDT];
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) acc[dt] = zero16();
-  const float c2 = s.scale * kLog2e;
-
-  int kend = s.M;
-  if (CAUSAL) kend = min(s.M, qb * BM + BM);
-  const int nkt = (kend + BN - 1) / BN;
-  // Tiles [0, nfull) have every key in range and visible to every query of the block.
-  int nfull = s.M / BN;
-  if (CAUSAL) nfull = min(nfull, qb * BM / BN);
-
-  const Dma dma(wave, lane);
-  const uint32_t krs = (uint32_t)p.k.sr * 2, vrs = (uint32_t)p.v.sr * 2;
-  const rsrc_t krsrc = make_rsrc(K, (uint32_t)s.M * krs);
-  const rsrc_t vrsrc = make_rsrc(V, (uint32_t)s.M * vrs);
-
-  // S^T = K Q^T and dP^T = V dO^T - delta for key subtile t of the tile in (tk, tv).
-  auto sdp = [&](const char* tk, const char* tv, int t, f32x16_t& sc, f32x16_t& dp) {
-    sc = zero16();
-#pragma unroll
-    for (int r = 0; r < 16; ++r) dp[r] = -del;
-#pragma unroll
-    for (int c = 0; c < NKC; ++c) {
-      sc = MM::mma(swz_cols<T, DP>(tk, 32 * t + li, c), qf[c], sc);
-      dp = MM::mma(swz_cols<T, DP>(tv, 32 * t + li, c), of[c], dp);
-    }
-  };
-  auto mask = [&](f32x16_t& sc, int k0t) {
-    if ((k0t + 32 > s.M) || (CAUSAL && k0t + 31 > q0w)) {
-      const int lim = CAUSAL ? min(s.M, myq + 1) : s.M;  // first key this query cannot see
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-        if (k0t + acc_row(r, g) >= lim) sc[r] = -THERIA_INF;
-    }
-  };
-  // dS^T = P^T o dP^T as 16-bit fragments (KACC chunks 0, 1)
-  auto pds = [&](const f32x16_t& sc, const f32x16_t& dp, F (&df)[2]) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) df[r >> 3][r & 7] = (T)(fast_exp2(fmaf(sc[r], c2, -lse2)) * dp[r]);
-  };
-  auto dqm = [&](const char* tk, int t, const F (&df)[2]) {
-#pragma unroll
-    for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) acc[dt] = MM::mma(swz_rows<T, DP>(tk, 32 * t, cc, 32 * dt), df[cc], acc[dt]);
-  };
-
-  auto step = [&](auto fast_tag, int k, const char* tk, const char* tv, char* nk, char* nv) {
-    constexpr bool FAST = decltype(fast_tag)::value;
-    const int k0 = k * BN;
-    wait_vm_all();
-    __syncthreads();  // tile k visible to all waves; the other buffers (tile k-1) are free
-    if (k + 1 < nkt) {
-      dma.template issue_clamped<NSLAB>(krsrc, krs, k0 + BN, s.M, nk);
-      dma.template issue_clamped<NSLAB>(vrsrc, vrs, k0 + BN, s.M, nv);
-    }
-    if constexpr (FAST && !OVERLAP) {
-#pragma unroll
-      for (int t = 0; t < 2 * HALVES; ++t) {
-        f32x16_t sc, dp;
-        F df[2];
-        sdp(tk, tv, t, sc, dp);
-        pds(sc, dp, df);
-        dqm(tk, t, df);
-      }
-    } else if constexpr (FAST) {
-#pragma unroll
-      for (int hf = 0; hf < HALVES; ++hf) {
-        f32x16_t s0, p0, s1, p1;
-        F d0[2], d1[2];
-        sdp(tk, tv, 2 * hf, s0, p0);
-        __builtin_amdgcn_sched_barrier(0);
-        sdp(tk, tv, 2 * hf + 1, s1, p1);
-        pds(s0, p0, d0);
-        __builtin_amdgcn_sched_barrier(0);
-        dqm(tk, 2 * hf, d0);
-        pds(s1, p1, d1);
-        __builtin_amdgcn_sched_barrier(0);
-        dqm(tk, 2 * hf + 1, d1);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+      del = pair_sum(part);
+      if (qvalid && g == 0) p.delta[rowbase + myq] = del;
     } else {
-#pragma unroll
-      for (int t = 0; t < 2 * HALVES; ++t) {
-        const int k0t = k0 + 32 * t;
-        if (CAUSAL && k0t > q0w + 31) continue;  // every key after every query of the wave (uniform)
-        f32x16_t sc, dp;
-        F df[2];
-        sdp(tk, tv, t, sc, dp);
-        mask(sc, k0t);
-        pds(sc, dp, df);
-        dqm(tk, t, df);
+      del = qvalid ? p.delta[rowbase + myq] : 0.f;
+    }
+    if (!p.dq.p) continue;  // only the row term was requested (uniform over the grid)
+
+    f32x16_t acc[NDT];
+  #pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) acc[dt] = zero16();
+    const float c2 = s.scale * kLog2e;
+
+    int kend = s.M;
+    if (CAUSAL) kend = min(s.M, qb * BM + BM);
+    const int nkt = (kend + BN - 1) / BN;
+    // Tiles [0, nfull) have every key in range and visible to every query of the block.
+    int nfull = s.M / BN;
+    if (CAUSAL) nfull = min(nfull, qb * BM / BN);
+
+    const Dma dma(wave, lane);
+    const uint32_t krs = (uint32_t)p.k.sr * 2, vrs = (uint32_t)p.v.sr * 2;
+    const rsrc_t krsrc = make_rsrc(K, (uint32_t)s.M * krs);
+    const rsrc_t vrsrc = make_rsrc(V, (uint32_t)s.M * vrs);
+
+    // S^T = K Q^T and dP^T = V dO^T - delta for key subtile t of the tile in (tk, tv).
+    auto sdp = [&](const char* tk, const char* tv, int t, f32x16_t& sc, f32x16_t& dp) {
+      sc = zero16();
+  #pragma unroll
+      for (int r = 0; r < 16; ++r) dp[r] = -del;
+  #pragma unroll
+      for (int c = 0; c < NKC; ++c) {
+        sc = MM::mma(swz_cols<T, DP>(tk, 32 * t + li, c), qf[c], sc);
+        dp = MM::mma(swz_cols<T, DP>(tv, 32 * t + li, c), of[c], dp);
+      }
+    };
+    auto mask = [&](f32x16_t& sc, int k0t) {
+      if ((k0t + 32 > s.M) || (CAUSAL && k0t + 31 > q0w)) {
+        const int lim = CAUSAL ? min(s.M, myq + 1) : s.M;  // first key this query cannot see
+  #pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (k0t + acc_row(r, g) >= lim) sc[r] = -THERIA_INF;
+      }
+    };
+    // dS^T = P^T o dP^T as 16-bit fragments (KACC chunks 0, 1)
+    auto pds = [&](const f32x16_t& sc, const f32x16_t& dp, F (&df)[2]) {
+  #pragma unroll
+      for (int r = 0; r < 16; ++r) df[r >> 3][r & 7] = (T)(fast_exp2(fmaf(sc[r], c2, -lse2)) * dp[r]);
+    };
+    auto dqm = [&](const char* tk, int t, const F (&df)[2]) {
+  #pragma unroll
+      for (int cc = 0; cc < 2; ++cc)
+  #pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) acc[dt] = MM::mma(swz_rows<T, DP>(tk, 32 * t, cc, 32 * dt), df[cc], acc[dt]);
+    };
+
+    auto step = [&](auto fast_tag, int k, const char* tk, const char* tv, char* nk, char* nv) {
+      constexpr bool FAST = decltype(fast_tag)::value;
+      const int k0 = k * BN;
+      wait_vm_all();
+      __syncthreads();  // tile k visible to all waves; the other buffers (tile k-1) are free
+      if (k + 1 < nkt) {
+        dma.template issue_clamped<NSLAB>(krsrc, krs, k0 + BN, s.M, nk);
+        dma.template issue_clamped<NSLAB>(vrsrc, vrs, k0 + BN, s.M, nv);
+      }
+      if constexpr (FAST && !OVERLAP) {
+  #pragma unroll
+        for (int t = 0; t < 2 * HALVES; ++t) {
+          f32x16_t sc, dp;
+          F df[2];
+          sdp(tk, tv, t, sc, dp);
+          pds(sc, dp, df);
+          dqm(tk, t, df);
+        }
+      } else if constexpr (FAST) {
+  #pragma unroll
+        for (int hf = 0; hf < HALVES; ++hf) {
+          f32x16_t s0, p0, s1, p1;
+          F d0[2], d1[2];
+          sdp(tk, tv, 2 * hf, s0, p0);
+          __builtin_amdgcn_sched_barrier(0);
+          sdp(tk, tv, 2 * hf + 1, s1, p1);
+          pds(s0, p0, d0);
+          __builtin_amdgcn_sched_barrier(0);
+          dqm(tk, 2 * hf, d0);
+          pds(s1, p1, d1);
+          __builtin_amdgcn_sched_barrier(0);
+          dqm(tk, 2 * hf + 1, d1);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
+  #pragma unroll
+        for (int t = 0; t < 2 * HALVES; ++t) {
+          const int k0t = k0 + 32 * t;
+          if (CAUSAL && k0t > q0w + 31) continue;  // every key after every query of the wave (uniform)
+          f32x16_t sc, dp;
+          F df[2];
+          sdp(tk, tv, t, sc, dp);
+          mask(sc, k0t);
+          pds(sc, dp, df);
+          dqm(tk, t, df);
+        }
+      }
+    };
+    const std::integral_constant<bool, true> fast;
+    const std::integral_constant<bool, false> general;
+
+    if (nkt > 0) {
+      dma.template issue_clamped<NSLAB>(krsrc, krs, 0, s.M, sK0);
+      dma.template issue_clamped<NSLAB>(vrsrc, vrs, 0, s.M, sV0);
+      int k = 0;
+      for (; k + 1 < nfull; k += 2) {
+        step(fast, k, sK0, sV0, sK1, sV1);
+        step(fast, k + 1, sK1, sV1, sK0, sV0);
+      }
+      for (; k < nkt; ++k) {
+        if (k & 1)
+          step(general, k, sK1, sV1, sK0, sV0);
+        else
+          step(general, k, sK0, sV0, sK1, sV1);
       }
     }
-  };
-  const std::integral_constant<bool, true> fast;
-  const std::integral_constant<bool, false> general;
 
-  if (nkt > 0) {
-    dma.template issue_clamped<NSLAB>(krsrc, krs, 0, s.M, sK0);
-    dma.template issue_clamped<NSLAB>(vrsrc, vrs, 0, s.M, sV0);
-    int k = 0;
-    for (; k + 1 < nfull; k += 2) {
-      step(fast, k, sK0, sV0, sK1, sV1);
-      step(fast, k + 1, sK1, sV1, sK0, sV0);
+    if (qvalid) {
+      T* DQ = (T*)p.dq.p + b * p.dq.sb + h * p.dq.sh;
+  #pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+  #pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+          const int d0 = dt * 32 + 8 * qd + 4 * g;
+          const f32x16_t& a = acc[dt];
+          store4<T>(DQ, p.dq.sr, myq, d0, DP, a[4 * qd] * s.scale, a[4 * qd + 1] * s.scale, a[4 * qd + 2] * s.scale,
+                    a[4 * qd + 3] * s.scale, true);
+        }
     }
-    for (; k < nkt; ++k) {
-      if (k & 1)
-        step(general, k, sK1, sV1, sK0, sV0);
-      else
-        step(general, k, sK0, sV0, sK1, sV1);
-    }
-  }
-
-  if (qvalid) {
-    T* DQ = (T*)p.dq.p + b * p.dq.sb + h * p.dq.sh;
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        const int d0 = dt * 32 + 8 * qd + 4 * g;
-        const f32x16_t& a = acc[dt];
-        store4<T>(DQ, p.dq.sr, myq, d0, DP, a[4 * qd] * s.scale, a[4 * qd + 1] * s.scale, a[4 * qd + 2] * s.scale,
-                  a[4 * qd + 3] * s.scale, true);
-      }
-  }
+  }  // pass
 }
 
 template <typename T, bool CAUSAL>
@@ -503,7 +526,8 @@ bool launch_dq_pipe(const DqParams& p, hipStream_t st, hipError_t* err) {
   // 32-bit byte offsets inside each (batch, head) slab of K and V
   if ((int64_t)p.s.M * p.k.sr * 2 >= (int64_t(1) << 31) || (int64_t)p.s.M * p.v.sr * 2 >= (int64_t(1) << 31)) return false;
   constexpr int NW = DQ_PIPE_NW;
-  const int64_t nblk = (int64_t)((p.s.T + 32 * NW - 1) / (32 * NW)) * p.s.B * p.s.H;
+  const int64_t nqb = (p.s.T + 32 * NW - 1) / (32 * NW);
+  const int64_t nblk = (CAUSAL ? (nqb + 1) / 2 : nqb) * p.s.B * p.s.H;  // causal: mirrored pairs
   if (nblk == 0) {
     *err = hipSuccess;
     return true;
@@ -532,7 +556,9 @@ bool launch_dkdv_pipe(const DkdvParams& p, hipStream_t st, hipError_t* err) {
   if ((int64_t)p.s.T * p.q.sr * 2 >= (int64_t(1) << 31) || (int64_t)p.s.T * p.dout.sr * 2 >= (int64_t(1) << 31))
     return false;
   constexpr int NW = DKDV_PIPE_NW;
-  const int64_t nblk = (int64_t)((p.s.M + 32 * NW - 1) / (32 * NW)) * p.s.B * p.s.H;
+  const int64_t nkb = (p.s.M + 32 * NW - 1) / (32 * NW);
+  const int64_t units = (CAUSAL && p.s.D == 64) ? (nkb + 1) / 2 : nkb;  // causal head dim 64: mirrored pairs
+  const int64_t nblk = units * p.s.B * p.s.H;
   if (nblk == 0) {
     *err = hipSuccess;
     return true;

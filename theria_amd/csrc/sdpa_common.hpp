@@ -175,6 +175,21 @@ __device__ __forceinline__ typename Mfma<T>::frag_t acc_frag(const f32x16_t& a, 
   }
 }
 
+// Two-term 16-bit split of accumulator chunk c (16-bit T only): hi = round(x), lo = round(x - hi), so
+// hi + lo carries x to ~2^-16 relative and an MFMA pair over (hi, lo) sums x-weighted products with no
+// operand rounding of consequence.
+template <typename T>
+__device__ __forceinline__ void split_frag(const f32x16_t& a, int c, typename Mfma<T>::frag_t& hi,
+                                           typename Mfma<T>::frag_t& lo) {
+  static_assert(sizeof(T) == 2, "split_frag is for 16-bit operands");
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const T h = (T)a[c * 8 + e];
+    hi[e] = h;
+    lo[e] = (T)(a[c * 8 + e] - (float)h);
+  }
+}
+
 // ----------------------------------------------------------------------------------------------
 // Global memory access
 // ----------------------------------------------------------------------------------------------

@@ -35,9 +35,10 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
   // QT query tiles of 32 per wave (two at DP = 64, where each K / V^T fragment then feeds two MFMAs;
-  // one at DP = 128, where the registers would not allow two); NKC k-chunks of 16 and NDT output tiles
-  // of 32 across the head dim.
-  constexpr int QT = DP == 64 ? 2 : 1, NKC = DP / 16, NDT = DP / 32;
+  // one at DP = 128, where the registers would not allow two, and one with the causal mask, whose paired
+  // blocks need the smaller block to fill the GPU); NKC k-chunks of 16 and NDT output tiles of 32
+  // across the head dim.
+  constexpr int QT = (DP == 64 && !CAUSAL) ? 2 : 1, NKC = DP / 16, NDT = DP / 32;
   constexpr int BM = 32 * NW * QT, BN = 64, TILE = BN * 2 * DP;
   // Separate arrays (not one [2][TILE] array) so that the compiler can tell the tile being read from the
   // tile being filled and does not wait for the DMA in flight before every LDS read.
@@ -50,351 +51,361 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
   const int lane = threadIdx.x & 63, li = lane & 31, g = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nqb = (s.T + BM - 1) / BM;
+  // Causal: workgroup `unit` runs query block nqb - 1 - unit (the longest rows) and then its mirror
+  // block `unit`, so every workgroup gets the same number of key tiles; an odd middle block runs once.
+  const int nunit = CAUSAL ? (nqb + 1) / 2 : nqb;
   const int bid = xcd_remap(blockIdx.x, gridDim.x);
-  const int bh = bid / nqb;
-  int qb = bid - bh * nqb;
-  if (CAUSAL) qb = nqb - 1 - qb;  // longest rows first
+  const int bh = bid / nunit;
+  const int unit = bid - bh * nunit;
   const int b = bh / s.H, h = bh - b * s.H;
   const T* Q = (const T*)p.q.p + b * p.q.sb + h * p.q.sh;
   const T* K = (const T*)p.k.p + b * p.k.sb + h * p.k.sh;
   const T* V = (const T*)p.v.p + b * p.v.sb + h * p.v.sh;
-  const int q0w = qb * BM + wave * 32 * QT;  // query tile j of this wave starts at q0w + 32 j
   const int64_t rowbase = (int64_t)bh * s.T;
   const float c2 = s.scale * kLog2e;
 
-  int kend = s.M;
-  if (CAUSAL) kend = min(s.M, qb * BM + BM);
-  const int nkt = (kend + BN - 1) / BN;
-  // Tiles [0, nfull) have every key in range and visible to every query of the block.
-  int nfull = s.M / BN;
-  if (CAUSAL) nfull = min(nfull, qb * BM / BN);
-
-  using Dma = SwzDma<NW, DP>;
-  const Dma dma(wave, lane);
-  constexpr int NSLAB = BN / Dma::SLAB_ROWS;
-  // Byte offsets fit in 32 bits: the host only selects this kernel when every (batch, head) slab of K
-  // and V spans less than 2^31 bytes.
-  const uint32_t krs = (uint32_t)p.k.sr * 2, vrs = (uint32_t)p.v.sr * 2;
-  const rsrc_t krsrc = make_rsrc(K, (uint32_t)s.M * krs);
-  const rsrc_t vrsrc = make_rsrc(V, (uint32_t)s.M * vrs);
-  uint32_t koff[NSLAB], voff[NSLAB];
-#pragma unroll
-  for (int i = 0; i < NSLAB; ++i) {
-    koff[i] = dma.lane_offset(krs, i);
-    voff[i] = dma.lane_offset(vrs, i);
+  for (int pass = 0; pass < (CAUSAL ? 2 : 1); ++pass) {
+  const int qb = CAUSAL ? (pass == 0 ? nqb - 1 - unit : unit) : unit;
+  if (pass == 1) {
+    if (qb == nqb - 1 - unit) break;  // odd number of blocks: the middle one ran in pass 0
+    __syncthreads();                  // every wave is done with the LDS tiles of the first block
   }
-  if (nkt > 0) dma.template issue_clamped<NSLAB>(krsrc, krs, 0, s.M, sK0);
+  const int q0w = qb * BM + wave * 32 * QT;  // query tile j of this wave starts at q0w + 32 j
 
-  F qf[QT][NKC];
-#pragma unroll
-  for (int j = 0; j < QT; ++j)
-#pragma unroll
-    for (int c = 0; c < NKC; ++c) qf[j][c] = gload_frag<T>(Q, p.q.sr, q0w + 32 * j + li, s.T, c, DP, true);
+    int kend = s.M;
+    if (CAUSAL) kend = min(s.M, qb * BM + BM);
+    const int nkt = (kend + BN - 1) / BN;
+    // Tiles [0, nfull) have every key in range and visible to every query of the block.
+    int nfull = s.M / BN;
+    if (CAUSAL) nfull = min(nfull, qb * BM / BN);
 
-  f32x16_t o[QT][NDT];
-  float m_use[QT], l_part[QT], m_max[QT];
-#pragma unroll
-  for (int j = 0; j < QT; ++j) {
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) o[j][dt] = zero16();
-    m_use[j] = -THERIA_INF;
-    l_part[j] = 0.f;
-    m_max[j] = -THERIA_INF;
-  }
-  F pf[QT][2][2];  // P of the previous tile as MFMA B fragments: [query tile][32-key subtile][16-key chunk]
-  bool pf_skip = false;
-
-  // S^T = K Q^T for both query tiles, key subtile t (32 keys) of the K tile in `kt`.
-  auto scores_t = [&](const char* kt, int t, f32x16_t (&st)[QT]) {
-#pragma unroll
-    for (int j = 0; j < QT; ++j) st[j] = zero16();
-#pragma unroll
-    for (int c = 0; c < NKC; ++c) {
-      const F kf = swz_cols<T, DP>(kt, 32 * t + li, c);
-#pragma unroll
-      for (int j = 0; j < QT; ++j) st[j] = MM::mma(kf, qf[j][c], st[j]);
+    using Dma = SwzDma<NW, DP>;
+    const Dma dma(wave, lane);
+    constexpr int NSLAB = BN / Dma::SLAB_ROWS;
+    // Byte offsets fit in 32 bits: the host only selects this kernel when every (batch, head) slab of K
+    // and V spans less than 2^31 bytes.
+    const uint32_t krs = (uint32_t)p.k.sr * 2, vrs = (uint32_t)p.v.sr * 2;
+    const rsrc_t krsrc = make_rsrc(K, (uint32_t)s.M * krs);
+    const rsrc_t vrsrc = make_rsrc(V, (uint32_t)s.M * vrs);
+    uint32_t koff[NSLAB], voff[NSLAB];
+  #pragma unroll
+    for (int i = 0; i < NSLAB; ++i) {
+      koff[i] = dma.lane_offset(krs, i);
+      voff[i] = dma.lane_offset(vrs, i);
     }
-  };
-  auto scores = [&](const char* kt, f32x16_t (&sc)[QT][2]) {
-    f32x16_t s0[QT], s1[QT];
-    scores_t(kt, 0, s0);
-    scores_t(kt, 1, s1);
-#pragma unroll
+    if (nkt > 0) dma.template issue_clamped<NSLAB>(krsrc, krs, 0, s.M, sK0);
+
+    F qf[QT][NKC];
+  #pragma unroll
+    for (int j = 0; j < QT; ++j)
+  #pragma unroll
+      for (int c = 0; c < NKC; ++c) qf[j][c] = gload_frag<T>(Q, p.q.sr, q0w + 32 * j + li, s.T, c, DP, true);
+
+    f32x16_t o[QT][NDT];
+    float m_use[QT], l_part[QT], m_max[QT];
+  #pragma unroll
     for (int j = 0; j < QT; ++j) {
-      sc[j][0] = s0[j];
-      sc[j][1] = s1[j];
+  #pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) o[j][dt] = zero16();
+      m_use[j] = -THERIA_INF;
+      l_part[j] = 0.f;
+      m_max[j] = -THERIA_INF;
     }
-  };
-  // O^T += V^T P^T with the previous tile's P and the V tile in `vt`.
-  auto pv_mma = [&](const char* vt) __attribute__((always_inline)) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-          const F vf = swz_rows<T, DP>(vt, 32 * t, cc, 32 * dt);
-#pragma unroll
-          for (int j = 0; j < QT; ++j) o[j][dt] = MM::mma(vf, pf[j][t][cc], o[j][dt]);
-        }
-  };
-  // Keys out of range, or (causal) after the query, get -inf. Only boundary tiles pay for the test.
-  auto mask = [&](f32x16_t (&sc)[QT][2], int k0) {
-    if ((k0 + BN > s.M) || (CAUSAL && k0 + BN - 1 > q0w)) {
-#pragma unroll
-      for (int j = 0; j < QT; ++j) {
-        const int lim = CAUSAL ? min(s.M, q0w + 32 * j + li + 1) : s.M;  // first key this query cannot see
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int r = 0; r < 16; ++r)
-            if (k0 + 32 * t + acc_row(r, g) >= lim) sc[j][t][r] = -THERIA_INF;
+    F pf[QT][2][2];  // P of the previous tile as MFMA B fragments: [query tile][32-key subtile][16-key chunk]
+    bool pf_skip = false;
+
+    // S^T = K Q^T for both query tiles, key subtile t (32 keys) of the K tile in `kt`.
+    auto scores_t = [&](const char* kt, int t, f32x16_t (&st)[QT]) {
+  #pragma unroll
+      for (int j = 0; j < QT; ++j) st[j] = zero16();
+  #pragma unroll
+      for (int c = 0; c < NKC; ++c) {
+        const F kf = swz_cols<T, DP>(kt, 32 * t + li, c);
+  #pragma unroll
+        for (int j = 0; j < QT; ++j) st[j] = MM::mma(kf, qf[j][c], st[j]);
       }
-    }
-  };
-  // P = exp2(S c2 - off) as 16-bit fragments into pn, and this tile's lane partial row sums into ps.
-  auto exps = [&](const f32x16_t (&sc)[QT][2], const float (&off)[QT], F (&pn)[QT][2][2], float (&ps)[QT]) {
-#pragma unroll
-    for (int j = 0; j < QT; ++j) {
-      float acc = 0.f;
-#pragma unroll
+    };
+    auto scores = [&](const char* kt, f32x16_t (&sc)[QT][2]) {
+      f32x16_t s0[QT], s1[QT];
+      scores_t(kt, 0, s0);
+      scores_t(kt, 1, s1);
+  #pragma unroll
+      for (int j = 0; j < QT; ++j) {
+        sc[j][0] = s0[j];
+        sc[j][1] = s1[j];
+      }
+    };
+    // O^T += V^T P^T with the previous tile's P and the V tile in `vt`.
+    auto pv_mma = [&](const char* vt) __attribute__((always_inline)) {
+  #pragma unroll
       for (int t = 0; t < 2; ++t)
-#pragma unroll
+  #pragma unroll
+        for (int cc = 0; cc < 2; ++cc)
+  #pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) {
+            const F vf = swz_rows<T, DP>(vt, 32 * t, cc, 32 * dt);
+  #pragma unroll
+            for (int j = 0; j < QT; ++j) o[j][dt] = MM::mma(vf, pf[j][t][cc], o[j][dt]);
+          }
+    };
+    // Keys out of range, or (causal) after the query, get -inf. Only boundary tiles pay for the test.
+    auto mask = [&](f32x16_t (&sc)[QT][2], int k0) {
+      if ((k0 + BN > s.M) || (CAUSAL && k0 + BN - 1 > q0w)) {
+  #pragma unroll
+        for (int j = 0; j < QT; ++j) {
+          const int lim = CAUSAL ? min(s.M, q0w + 32 * j + li + 1) : s.M;  // first key this query cannot see
+  #pragma unroll
+          for (int t = 0; t < 2; ++t)
+  #pragma unroll
+            for (int r = 0; r < 16; ++r)
+              if (k0 + 32 * t + acc_row(r, g) >= lim) sc[j][t][r] = -THERIA_INF;
+        }
+      }
+    };
+    // P = exp2(S c2 - off) as 16-bit fragments into pn, and this tile's lane partial row sums into ps.
+    auto exps = [&](const f32x16_t (&sc)[QT][2], const float (&off)[QT], F (&pn)[QT][2][2], float (&ps)[QT]) {
+  #pragma unroll
+      for (int j = 0; j < QT; ++j) {
+        float acc = 0.f;
+  #pragma unroll
+        for (int t = 0; t < 2; ++t)
+  #pragma unroll
+          for (int cc = 0; cc < 2; ++cc) {
+            F f;
+  #pragma unroll
+            for (int e = 0; e < 8; ++e) f[e] = (T)fast_exp2(fmaf(sc[j][t][8 * cc + e], c2, -off[j]));
+            pn[j][t][cc] = f;
+            acc = frag_sum<T>(f, acc);
+          }
+        ps[j] = acc;
+      }
+    };
+    // The same for key subtile t only, accumulating the lane partial row sums into ps.
+    auto exps_t = [&](const f32x16_t (&st)[QT], int t, F (&pn)[QT][2][2], float (&ps)[QT]) {
+  #pragma unroll
+      for (int j = 0; j < QT; ++j)
+  #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
           F f;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) f[e] = (T)fast_exp2(fmaf(sc[j][t][8 * cc + e], c2, -off[j]));
+  #pragma unroll
+          for (int e = 0; e < 8; ++e) f[e] = (T)fast_exp2(fmaf(st[j][8 * cc + e], c2, -m_use[j]));
           pn[j][t][cc] = f;
-          acc = frag_sum<T>(f, acc);
+          ps[j] = frag_sum<T>(f, ps[j]);
         }
-      ps[j] = acc;
-    }
-  };
-  // The same for key subtile t only, accumulating the lane partial row sums into ps.
-  auto exps_t = [&](const f32x16_t (&st)[QT], int t, F (&pn)[QT][2][2], float (&ps)[QT]) {
-#pragma unroll
-    for (int j = 0; j < QT; ++j)
-#pragma unroll
-      for (int cc = 0; cc < 2; ++cc) {
-        F f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) f[e] = (T)fast_exp2(fmaf(st[j][8 * cc + e], c2, -m_use[j]));
-        pn[j][t][cc] = f;
-        ps[j] = frag_sum<T>(f, ps[j]);
+    };
+    auto tile_max = [&](const f32x16_t (&sc)[QT][2], int j) {
+      float mx = -THERIA_INF;
+  #pragma unroll
+      for (int t = 0; t < 2; ++t)
+  #pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[j][t][r]);
+      return pair_max(mx) * c2;
+    };
+    // Exact path: the running max becomes the offset; O and the row sums are rescaled to it.
+    auto exact = [&](const f32x16_t (&sc)[QT][2], F (&pn)[QT][2][2], float (&ps)[QT]) {
+      float off[QT];
+  #pragma unroll
+      for (int j = 0; j < QT; ++j) {
+        const float mx = tile_max(sc, j);
+        m_max[j] = fmaxf(m_max[j], mx);
+        const float mnew = fmaxf(m_use[j], mx);
+        const float alpha = mnew == -THERIA_INF ? 1.f : fast_exp2(m_use[j] - mnew);
+        m_use[j] = mnew;
+        l_part[j] *= alpha;
+  #pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+  #pragma unroll
+          for (int r = 0; r < 16; ++r) o[j][dt][r] *= alpha;
+        off[j] = mnew == -THERIA_INF ? 0.f : mnew;  // all keys so far masked: P = exp2(-inf) = 0
       }
-  };
-  auto tile_max = [&](const f32x16_t (&sc)[QT][2], int j) {
-    float mx = -THERIA_INF;
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[j][t][r]);
-    return pair_max(mx) * c2;
-  };
-  // Exact path: the running max becomes the offset; O and the row sums are rescaled to it.
-  auto exact = [&](const f32x16_t (&sc)[QT][2], F (&pn)[QT][2][2], float (&ps)[QT]) {
-    float off[QT];
-#pragma unroll
-    for (int j = 0; j < QT; ++j) {
-      const float mx = tile_max(sc, j);
-      m_max[j] = fmaxf(m_max[j], mx);
-      const float mnew = fmaxf(m_use[j], mx);
-      const float alpha = mnew == -THERIA_INF ? 1.f : fast_exp2(m_use[j] - mnew);
-      m_use[j] = mnew;
-      l_part[j] *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[j][dt][r] *= alpha;
-      off[j] = mnew == -THERIA_INF ? 0.f : mnew;  // all keys so far masked: P = exp2(-inf) = 0
-    }
-    exps(sc, off, pn, ps);
-  };
+      exps(sc, off, pn, ps);
+    };
 
-  // One key tile. On entry K(k) and V(k-1) have been requested (one iteration earlier); this step
-  // requests K(k+1) and V(k), issues O += V(k-1)^T P(k-1)^T, S(k) and P(k). kc/vp are the buffers holding
-  // K(k)/V(k-1), kn/vn the buffers for K(k+1)/V(k). FAST: tile k is full (every key in range and visible
-  // to every query of the block), tile k+1 is in range, and the buffers are compile-time distinct arrays.
-  auto step = [&](auto fast_tag, int k, const char* kc, const char* vp, char* kn, char* vn) {
-    constexpr bool FAST = decltype(fast_tag)::value;
-    const int k0 = k * BN;
-    wait_vm_all();
-    __syncthreads();  // K(k), V(k-1) visible to all waves; the buffers of K(k-1), V(k-2) are free
-    if (FAST) {
-      dma.template issue<NSLAB>(krsrc, koff, (uint32_t)(k0 + BN) * krs, kn);
-      dma.template issue<NSLAB>(vrsrc, voff, (uint32_t)k0 * vrs, vn);
-    } else {
-      if (k + 1 < nkt) dma.template issue_clamped<NSLAB>(krsrc, krs, k0 + BN, s.M, kn);
-      dma.template issue_clamped<NSLAB>(vrsrc, vrs, k0, s.M, vn);
-    }
-    F pn[QT][2][2];
-    if constexpr (FAST) {
-      // Phase order (kept by scheduling barriers, which also bound the live registers):
-      //   S(k) subtile 0 | S(k) subtile 1 with exp of subtile 0 | O += V(k-1)^T P(k-1)^T with exp of subtile 1.
-      f32x16_t s0[QT], s1[QT];
-      float ps[QT];
-#pragma unroll
-      for (int j = 0; j < QT; ++j) ps[j] = 0.f;
-      scores_t(kc, 0, s0);
-      __builtin_amdgcn_sched_barrier(0);
-      scores_t(kc, 1, s1);
-      if (STATS) {
-#pragma unroll
-        for (int j = 0; j < QT; ++j) {
-          float mx = -THERIA_INF;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s0[j][r]);
-          m_max[j] = fmaxf(m_max[j], pair_max(mx) * c2);
-        }
+    // One key tile. On entry K(k) and V(k-1) have been requested (one iteration earlier); this step
+    // requests K(k+1) and V(k), issues O += V(k-1)^T P(k-1)^T, S(k) and P(k). kc/vp are the buffers holding
+    // K(k)/V(k-1), kn/vn the buffers for K(k+1)/V(k). FAST: tile k is full (every key in range and visible
+    // to every query of the block), tile k+1 is in range, and the buffers are compile-time distinct arrays.
+    auto step = [&](auto fast_tag, int k, const char* kc, const char* vp, char* kn, char* vn) {
+      constexpr bool FAST = decltype(fast_tag)::value;
+      const int k0 = k * BN;
+      wait_vm_all();
+      __syncthreads();  // K(k), V(k-1) visible to all waves; the buffers of K(k-1), V(k-2) are free
+      if (FAST) {
+        dma.template issue<NSLAB>(krsrc, koff, (uint32_t)(k0 + BN) * krs, kn);
+        dma.template issue<NSLAB>(vrsrc, voff, (uint32_t)k0 * vrs, vn);
+      } else {
+        if (k + 1 < nkt) dma.template issue_clamped<NSLAB>(krsrc, krs, k0 + BN, s.M, kn);
+        dma.template issue_clamped<NSLAB>(vrsrc, vrs, k0, s.M, vn);
       }
-      exps_t(s0, 0, pn, ps);
-      if constexpr (DP == 64) {
-        // Issue order inside the phase: the four K fragment reads first, then each of the 8 MFMAs
-        // followed by 12 VALU instructions of the exponentials (measured ~5% faster than the
-        // compiler's own order at head dim 64).
-#pragma unroll
-        for (int i = 0; i < 4; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-          __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);  // VALU
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      pv_mma(vp);
-      if (STATS) {
-#pragma unroll
-        for (int j = 0; j < QT; ++j) {
-          float mx = -THERIA_INF;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s1[j][r]);
-          m_max[j] = fmaxf(m_max[j], pair_max(mx) * c2);
-        }
-      }
-      exps_t(s1, 1, pn, ps);
-      if constexpr (DP == 64) {
-        // V fragment reads first, then each of the 16 PV MFMAs followed by 6 VALU instructions.
-#pragma unroll
-        for (int i = 0; i < 8; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-          __builtin_amdgcn_sched_group_barrier(0x002, 6, 1);
-        }
-      }
-      bool bad = false;
-#pragma unroll
-      for (int j = 0; j < QT; ++j) bad |= !(ps[j] <= 0x1p20f);
-      if (__any(bad)) {
-        f32x16_t sc2[QT][2];
-        scores(kc, sc2);
-        exact(sc2, pn, ps);
-      }
-#pragma unroll
-      for (int j = 0; j < QT; ++j) l_part[j] += ps[j];
-#pragma unroll
-      for (int j = 0; j < QT; ++j)
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int cc = 0; cc < 2; ++cc) pf[j][t][cc] = pn[j][t][cc];
-      pf_skip = false;
-    } else {
-      const bool skip = CAUSAL && (k0 > q0w + 32 * QT - 1);  // every key after every query of the wave
-      f32x16_t sc[QT][2];
-      if (!skip) scores(kc, sc);
-      if (k > 0 && !pf_skip) pv_mma(vp);
-      if (!skip) {
+      F pn[QT][2][2];
+      if constexpr (FAST) {
+        // Phase order (kept by scheduling barriers, which also bound the live registers):
+        //   S(k) subtile 0 | S(k) subtile 1 with exp of subtile 0 | O += V(k-1)^T P(k-1)^T with exp of subtile 1.
+        f32x16_t s0[QT], s1[QT];
         float ps[QT];
-        mask(sc, k0);
-        if (k == 0) {
-          exact(sc, pn, ps);
-        } else {
-          if (STATS) {
-#pragma unroll
-            for (int j = 0; j < QT; ++j) m_max[j] = fmaxf(m_max[j], tile_max(sc, j));
-          }
-          exps(sc, m_use, pn, ps);
-          bool bad = false;
-#pragma unroll
-          for (int j = 0; j < QT; ++j) bad |= !(ps[j] <= 0x1p20f);
-          if (__any(bad)) {
-            f32x16_t sc2[QT][2];
-            scores(kc, sc2);
-            mask(sc2, k0);
-            exact(sc2, pn, ps);
-          }
-        }
-#pragma unroll
-        for (int j = 0; j < QT; ++j) l_part[j] += ps[j];
-#pragma unroll
-        for (int j = 0; j < QT; ++j)
-#pragma unroll
-          for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int cc = 0; cc < 2; ++cc) pf[j][t][cc] = pn[j][t][cc];
-      }
-      pf_skip = skip;
-    }
-  };
-  const std::integral_constant<bool, true> fast;
-  const std::integral_constant<bool, false> general;
-  if (nkt > 0) {
-    // Tile 0 always takes the exact path (m_use = -inf); then the full tiles two at a time, so that
-    // every buffer is a fixed array; then the boundary tiles.
-    step(general, 0, sK0, sV1, sK1, sV0);
-    // fast steps: k < nfull and K(k+1) in range
-    const int nfast = min(nfull, s.M / BN - 1);
-    int k = 1;
-    for (; k + 1 < nfast; k += 2) {
-      step(fast, k, sK1, sV0, sK0, sV1);      // k odd
-      step(fast, k + 1, sK0, sV1, sK1, sV0);  // k + 1 even
-    }
-    if (k < nfast) {
-      step(fast, k, sK1, sV0, sK0, sV1);
-      ++k;
-    }
-    for (; k < nkt; ++k) {
-      const bool odd = k & 1;
-      step(general, k, odd ? sK1 : sK0, odd ? sV0 : sV1, odd ? sK0 : sK1, odd ? sV1 : sV0);
-    }
-    // drain: the last tile's PV
-    wait_vm_all();
-    __syncthreads();
-    if (!pf_skip) pv_mma(((nkt - 1) & 1) ? sV1 : sV0);
-  }
-
-#pragma unroll
-  for (int j = 0; j < QT; ++j) {
-    const int myq = q0w + 32 * j + li;
-    const float l = pair_sum(l_part[j]);
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    if (myq < s.T) {
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-        for (int qd = 0; qd < 4; ++qd) {
-          const int d0 = dt * 32 + 8 * qd + 4 * g;
-          const float a0 = o[j][dt][4 * qd] * inv, a1 = o[j][dt][4 * qd + 1] * inv;
-          const float a2 = o[j][dt][4 * qd + 2] * inv, a3 = o[j][dt][4 * qd + 3] * inv;
-          if (p.o_f32) {
-            float* O = (float*)p.o.p + b * p.o.sb + h * p.o.sh;
-            store4<float>(O, p.o.sr, myq, d0, DP, a0, a1, a2, a3, true);
-          } else {
-            T* O = (T*)p.o.p + b * p.o.sb + h * p.o.sh;
-            store4<T>(O, p.o.sr, myq, d0, DP, a0, a1, a2, a3, true);
-          }
-        }
-      if (g == 0) {
-        const int64_t row_id = rowbase + myq;
-        p.lse[row_id] = l > 0.f ? (m_use[j] + __builtin_log2f(l)) * kLn2 : -THERIA_INF;
+  #pragma unroll
+        for (int j = 0; j < QT; ++j) ps[j] = 0.f;
+        scores_t(kc, 0, s0);
+        __builtin_amdgcn_sched_barrier(0);
+        scores_t(kc, 1, s1);
         if (STATS) {
-          if (p.row_max) p.row_max[row_id] = m_max[j] * kLn2;
-          if (p.row_sum) p.row_sum[row_id] = l > 0.f ? l * fast_exp2(m_use[j] - m_max[j]) : 0.f;
+  #pragma unroll
+          for (int j = 0; j < QT; ++j) {
+            float mx = -THERIA_INF;
+  #pragma unroll
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s0[j][r]);
+            m_max[j] = fmaxf(m_max[j], pair_max(mx) * c2);
+          }
+        }
+        exps_t(s0, 0, pn, ps);
+        if constexpr (DP == 64) {
+          // Issue order inside the phase: the four K fragment reads first, then each of the 8 MFMAs
+          // followed by 12 VALU instructions of the exponentials (measured ~5% faster than the
+          // compiler's own order at head dim 64).
+  #pragma unroll
+          for (int i = 0; i < 4; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+  #pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);  // VALU
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        pv_mma(vp);
+        if (STATS) {
+  #pragma unroll
+          for (int j = 0; j < QT; ++j) {
+            float mx = -THERIA_INF;
+  #pragma unroll
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s1[j][r]);
+            m_max[j] = fmaxf(m_max[j], pair_max(mx) * c2);
+          }
+        }
+        exps_t(s1, 1, pn, ps);
+        if constexpr (DP == 64) {
+          // V fragment reads first, then each of the 16 PV MFMAs followed by 6 VALU instructions.
+  #pragma unroll
+          for (int i = 0; i < 8; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+  #pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+            __builtin_amdgcn_sched_group_barrier(0x002, 6, 1);
+          }
+        }
+        bool bad = false;
+  #pragma unroll
+        for (int j = 0; j < QT; ++j) bad |= !(ps[j] <= 0x1p20f);
+        if (__any(bad)) {
+          f32x16_t sc2[QT][2];
+          scores(kc, sc2);
+          exact(sc2, pn, ps);
+        }
+  #pragma unroll
+        for (int j = 0; j < QT; ++j) l_part[j] += ps[j];
+  #pragma unroll
+        for (int j = 0; j < QT; ++j)
+  #pragma unroll
+          for (int t = 0; t < 2; ++t)
+  #pragma unroll
+            for (int cc = 0; cc < 2; ++cc) pf[j][t][cc] = pn[j][t][cc];
+        pf_skip = false;
+      } else {
+        const bool skip = CAUSAL && (k0 > q0w + 32 * QT - 1);  // every key after every query of the wave
+        f32x16_t sc[QT][2];
+        if (!skip) scores(kc, sc);
+        if (k > 0 && !pf_skip) pv_mma(vp);
+        if (!skip) {
+          float ps[QT];
+          mask(sc, k0);
+          if (k == 0) {
+            exact(sc, pn, ps);
+          } else {
+            if (STATS) {
+  #pragma unroll
+              for (int j = 0; j < QT; ++j) m_max[j] = fmaxf(m_max[j], tile_max(sc, j));
+            }
+            exps(sc, m_use, pn, ps);
+            bool bad = false;
+  #pragma unroll
+            for (int j = 0; j < QT; ++j) bad |= !(ps[j] <= 0x1p20f);
+            if (__any(bad)) {
+              f32x16_t sc2[QT][2];
+              scores(kc, sc2);
+              mask(sc2, k0);
+              exact(sc2, pn, ps);
+            }
+          }
+  #pragma unroll
+          for (int j = 0; j < QT; ++j) l_part[j] += ps[j];
+  #pragma unroll
+          for (int j = 0; j < QT; ++j)
+  #pragma unroll
+            for (int t = 0; t < 2; ++t)
+  #pragma unroll
+              for (int cc = 0; cc < 2; ++cc) pf[j][t][cc] = pn[j][t][cc];
+        }
+        pf_skip = skip;
+      }
+    };
+    const std::integral_constant<bool, true> fast;
+    const std::integral_constant<bool, false> general;
+    if (nkt > 0) {
+      // Tile 0 always takes the exact path (m_use = -inf); then the full tiles two at a time, so that
+      // every buffer is a fixed array; then the boundary tiles.
+      step(general, 0, sK0, sV1, sK1, sV0);
+      // fast steps: k < nfull and K(k+1) in range
+      const int nfast = min(nfull, s.M / BN - 1);
+      int k = 1;
+      for (; k + 1 < nfast; k += 2) {
+        step(fast, k, sK1, sV0, sK0, sV1);      // k odd
+        step(fast, k + 1, sK0, sV1, sK1, sV0);  // k + 1 even
+      }
+      if (k < nfast) {
+        step(fast, k, sK1, sV0, sK0, sV1);
+        ++k;
+      }
+      for (; k < nkt; ++k) {
+        const bool odd = k & 1;
+        step(general, k, odd ? sK1 : sK0, odd ? sV0 : sV1, odd ? sK0 : sK1, odd ? sV1 : sV0);
+      }
+      // drain: the last tile's PV
+      wait_vm_all();
+      __syncthreads();
+      if (!pf_skip) pv_mma(((nkt - 1) & 1) ? sV1 : sV0);
+    }
+
+  #pragma unroll
+    for (int j = 0; j < QT; ++j) {
+      const int myq = q0w + 32 * j + li;
+      const float l = pair_sum(l_part[j]);
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+      if (myq < s.T) {
+  #pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+  #pragma unroll
+          for (int qd = 0; qd < 4; ++qd) {
+            const int d0 = dt * 32 + 8 * qd + 4 * g;
+            const float a0 = o[j][dt][4 * qd] * inv, a1 = o[j][dt][4 * qd + 1] * inv;
+            const float a2 = o[j][dt][4 * qd + 2] * inv, a3 = o[j][dt][4 * qd + 3] * inv;
+            if (p.o_f32) {
+              float* O = (float*)p.o.p + b * p.o.sb + h * p.o.sh;
+              store4<float>(O, p.o.sr, myq, d0, DP, a0, a1, a2, a3, true);
+            } else {
+              T* O = (T*)p.o.p + b * p.o.sb + h * p.o.sh;
+              store4<T>(O, p.o.sr, myq, d0, DP, a0, a1, a2, a3, true);
+            }
+          }
+        if (g == 0) {
+          const int64_t row_id = rowbase + myq;
+          p.lse[row_id] = l > 0.f ? (m_use[j] + __builtin_log2f(l)) * kLn2 : -THERIA_INF;
+          if (STATS) {
+            if (p.row_max) p.row_max[row_id] = m_max[j] * kLn2;
+            if (p.row_sum) p.row_sum[row_id] = l > 0.f ? l * fast_exp2(m_use[j] - m_max[j]) : 0.f;
+          }
         }
       }
     }
-  }
+  }  // pass
 }
 
 template <typename T, bool CAUSAL, int NW, int DP>
@@ -407,10 +418,12 @@ static void fwd_pipe_go(const FwdParams& p, int64_t nblk, hipStream_t st) {
 
 template <typename T, bool CAUSAL, int DP>
 static void fwd_pipe_launch(const FwdParams& p, hipStream_t st) {
-  constexpr int QT = DP == 64 ? 2 : 1;
+  constexpr int QT = (DP == 64 && !CAUSAL) ? 2 : 1;
   const int64_t bh = (int64_t)p.s.B * p.s.H;
-  const int64_t nblk8 = (int64_t)((p.s.T + 256 * QT - 1) / (256 * QT)) * bh;
-  const int64_t nblk4 = (int64_t)((p.s.T + 128 * QT - 1) / (128 * QT)) * bh;
+  // workgroups per (batch, head): query blocks, or (causal) pairs of mirrored query blocks
+  auto units = [](int64_t nqb) { return CAUSAL ? (nqb + 1) / 2 : nqb; };
+  const int64_t nblk8 = units((p.s.T + 256 * QT - 1) / (256 * QT)) * bh;
+  const int64_t nblk4 = units((p.s.T + 128 * QT - 1) / (128 * QT)) * bh;
   if (nblk8 >= device_cu_count())
     fwd_pipe_go<T, CAUSAL, 8, DP>(p, nblk8, st);
   else

@@ -8,6 +8,13 @@
 // where O = P V (the saved forward output, or rebuilt in the same pass when it is not supplied).
 // The same kernel yields the G_dO output of the double backward (tangents = cotangents of dQ, dK, dV).
 //
+// 16-bit inputs: the two large terms (P o G) V and c o O of tO cancel, so operand rounding in them is
+// amplified (a bfloat16-rounded P o G gave 0.03 absolute error on a row with four visible keys). Both
+// products are therefore formed from two-term 16-bit splits (hi + lo) of P o G and of P, O is always
+// rebuilt in the pass from the same P (the saved O, rounded to 16 bits, is not used), and P is
+// renormalised by its row sum: the saved lse of a 16-bit forward comes from rounded probabilities, so
+// P rebuilt from it sums to 1 only within ~2^-9. Float32 inputs keep the plain frozen-stats form.
+//
 // Work decomposition as in the forward: one workgroup = 4 waves = 128 query rows, lane per query in
 // the transposed score tiles S^T = K Q^T and G^T = K tq^T + tk Q^T (Q and tq stay in registers as B
 // operands); per 64-key tile, K, tk, V, tv are staged in LDS and the three output products
@@ -68,7 +75,9 @@ __global__ __launch_bounds__(256) void jvp_kernel(const JvpParams p) {
   const float c2 = s.scale * kLog2e;
   const float lse2 = qvalid ? p.lse[row_id] * kLog2e : THERIA_INF;
   const float moff = lse2 == -THERIA_INF ? THERIA_INF : lse2;  // a row without visible keys has P = 0
-  float cpart = 0.f;
+  constexpr bool SPLIT = sizeof(T) == 2;     // hi/lo operands, renormalised P (see the header)
+  constexpr bool REBUILD = SPLIT || !HAS_O;  // O = P V formed in this pass
+  float cpart = 0.f, lpart = 0.f;
 
   int kend = s.M;
   if (CAUSAL) kend = min(s.M, qb * BM + BM);
@@ -116,6 +125,7 @@ __global__ __launch_bounds__(256) void jvp_kernel(const JvpParams p) {
           if (key >= s.M || (CAUSAL && key > myq)) pv = 0.f;
         }
         sc[t][r] = pv;
+        if (SPLIT) lpart += pv;
         const float pg = pv * gm[t][r];
         gm[t][r] = pg;
         cpart += pg;
@@ -124,21 +134,35 @@ __global__ __launch_bounds__(256) void jvp_kernel(const JvpParams p) {
     for (int t = 0; t < NST; ++t)
 #pragma unroll
       for (int cc = 0; cc < NPC; ++cc) {
-        const F pf = acc_frag<T>(sc[t], cc);
-        const F pgf = acc_frag<T>(gm[t], cc);
+        F pf, pgf, pf_lo{}, pgf_lo{};
+        if constexpr (SPLIT) {
+          split_frag<T>(sc[t], cc, pf, pf_lo);
+          split_frag<T>(gm[t], cc, pgf, pgf_lo);
+        } else {
+          pf = acc_frag<T>(sc[t], cc);
+          pgf = acc_frag<T>(gm[t], cc);
+        }
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
           const F vfr = lds_rows<T, KACC>(sV, PITCH, t * 32, cc, dt * 32);
           accA[dt] = MM::mma(vfr, pgf, accA[dt]);
-          if (!HAS_O) accO[dt] = MM::mma(vfr, pf, accO[dt]);
+          if (SPLIT) accA[dt] = MM::mma(vfr, pgf_lo, accA[dt]);
+          if (REBUILD) accO[dt] = MM::mma(vfr, pf, accO[dt]);
+          if (REBUILD && SPLIT) accO[dt] = MM::mma(vfr, pf_lo, accO[dt]);
           if (has_tv) accC[dt] = MM::mma(lds_rows<T, KACC>(stV, PITCH, t * 32, cc, dt * 32), pf, accC[dt]);
         }
       }
   }
 
-  const float cval = pair_sum(cpart) * s.scale;
+  // 16-bit: P / L with L = sum_j P_j, i.e. every term below is divided by L (and O by L as well)
+  float inv = 1.f;
+  if constexpr (SPLIT) {
+    const float L = pair_sum(lpart);
+    inv = L > 0.f ? 1.f / L : 0.f;
+  }
+  const float cval = pair_sum(cpart) * s.scale * inv;
   if (qvalid) {
-    const T* O = HAS_O ? (const T*)p.o.p + b * p.o.sb + h * p.o.sh : nullptr;
+    const T* O = (HAS_O && !REBUILD) ? (const T*)p.o.p + b * p.o.sb + h * p.o.sh : nullptr;
     T* TO = (T*)p.tout.p + b * p.tout.sb + h * p.tout.sh;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
@@ -147,15 +171,16 @@ __global__ __launch_bounds__(256) void jvp_kernel(const JvpParams p) {
         const int d0 = dt * 32 + 8 * qd + 4 * g;
         if (d0 < s.D) {
           f32x4_t ov;
-          if (HAS_O) {
+          if (!REBUILD) {
             ov = load4<T>(O, p.o.sr, myq, d0, s.D, s.vec);
           } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) ov[e] = accO[dt][4 * qd + e];
+            for (int e = 0; e < 4; ++e) ov[e] = accO[dt][4 * qd + e] * inv;
           }
           float r4[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) r4[e] = s.scale * accA[dt][4 * qd + e] - cval * ov[e] + accC[dt][4 * qd + e];
+          for (int e = 0; e < 4; ++e)
+            r4[e] = inv * (s.scale * accA[dt][4 * qd + e] + accC[dt][4 * qd + e]) - cval * ov[e];
           store4<T>(TO, p.tout.sr, myq, d0, s.D, r4[0], r4[1], r4[2], r4[3], s.vec);
         }
       }
