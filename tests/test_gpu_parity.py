@@ -9,6 +9,7 @@ Full-size configs are checked on sampled heads plus size-independent invariants:
 """
 
 import math
+import random
 from pathlib import Path
 
 import numpy as np
@@ -85,16 +86,44 @@ def _ids(c):
 
 @pytest.mark.parametrize("case", CASES, ids=[_ids(c) for c in CASES])
 def test_kernels_match_oracle(case, hip_device):
-    dt, B, H, T, M, D, causal = case
     print(f"[parity] {_ids(case)}", flush=True)
-    dev = hip_device
-    q, qc = make((B, H, T, D), dt, dev, 1)
-    k, kc = make((B, H, M, D), dt, dev, 2)
-    v, vc = make((B, H, M, D), dt, dev, 3)
-    do, doc = make((B, H, T, D), dt, dev, 4)
-    tq, tqc = make((B, H, T, D), dt, dev, 5)
-    tk, tkc = make((B, H, M, D), dt, dev, 6)
-    tv, tvc = make((B, H, M, D), dt, dev, 7)
+    _check_all_entry_points(case, hip_device, seed=1)
+
+
+def _random_cases(n: int = 24, seed: int = 2024):
+    """Seeded random configurations: dtype, head dim 8-128, 1-700 query / key rows, T != M, causal."""
+    rng = random.Random(seed)
+    cases = []
+    for _ in range(n):
+        dt = rng.choice([torch.float32, torch.float16, torch.bfloat16])
+        D = rng.choice([8, 16, 24, 32, 40, 64, 64, 96, 128, 128])
+        T = rng.choice([1, rng.randint(2, 100), rng.randint(100, 700)])
+        M = rng.choice([T, rng.randint(1, 100), rng.randint(100, 700)])
+        B, H = rng.choice([(1, 1), (1, 2), (2, 1), (2, 2)])
+        cases.append((dt, B, H, T, M, D, rng.random() < 0.4))
+    return cases
+
+
+RANDOM_CASES = _random_cases()
+
+
+@pytest.mark.parametrize("case", RANDOM_CASES, ids=[f"r{i}-" + _ids(c) for i, c in enumerate(RANDOM_CASES)])
+def test_random_configurations_match_oracle(case, hip_device):
+    print(f"[parity random] {_ids(case)}", flush=True)
+    _check_all_entry_points(case, hip_device, seed=100)
+
+
+def _check_all_entry_points(case, dev, seed: int):
+    """Forward (O, lse, m, l), backward (with O, from stats, dV only), JVP (saved / rebuilt O, one tangent)
+    and the double backward (all cotangents, one) against the float64 oracle on the same inputs."""
+    dt, B, H, T, M, D, causal = case
+    q, qc = make((B, H, T, D), dt, dev, seed)
+    k, kc = make((B, H, M, D), dt, dev, seed + 1)
+    v, vc = make((B, H, M, D), dt, dev, seed + 2)
+    do, doc = make((B, H, T, D), dt, dev, seed + 3)
+    tq, tqc = make((B, H, T, D), dt, dev, seed + 4)
+    tk, tkc = make((B, H, M, D), dt, dev, seed + 5)
+    tv, tvc = make((B, H, M, D), dt, dev, seed + 6)
     s = 1 / math.sqrt(D)
 
     o, lse, m, l = _ops.fwd(q, k, v, s, causal, stats=True)
