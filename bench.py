@@ -236,7 +236,7 @@ def extras_c4():
     import torch
 
     from theria_amd import _ops
-    from theria_amd.autograd.hip_sdpa import hip_sdpa
+    from theria_amd.autograd.hip_sdpa import hip_sdpa, hip_sdpa_hvp
 
     dev = torch.device("cuda:0")
     B, H, S, D = 8, 8, 512, 64
@@ -258,11 +258,15 @@ def extras_c4():
             return torch.autograd.grad(dot, (qg, kg, vg))
 
         out[f"hvp_ms_{name}"] = round(_time(hvp, 10), 4)
+        # the same HVP from the kernels directly (forward, double backward, backward of J v; no autograd graph)
+        hv = lambda: hip_sdpa_hvp(q, k, v, vq, vk, vv, target=T_, scale=1 / 8.0)  # noqa: E731
+        out[f"hvp_kernels_only_ms_{name}"] = round(_time(hv, 20), 4)
         bb = lambda: _ops.bwd_bwd(q, k, v, o, T_, lse, torch.zeros_like(lse), vq, vk, vv, 1 / 8.0, False)  # noqa: E731
         out[f"double_backward_kernels_ms_{name}"] = round(_time(bb, 20), 4)
     unit = B * H * S * S * D
     out["jvp_tflops_bf16"] = round(10 * unit / (out["jvp_ms_bf16"] * 1e-3) / 1e12, 1)
-    out["config"] = "B8 H8 S512 D64; JVP with saved stats; HVP of 0.5||O-T||^2 via autograd double backward"
+    out["config"] = ("B8 H8 S512 D64; JVP with saved stats; HVP of 0.5||O-T||^2 via autograd double backward "
+                     "(hvp_ms) and from the kernels directly (hvp_kernels_only_ms)")
     return out
 
 

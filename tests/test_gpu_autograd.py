@@ -294,3 +294,37 @@ def test_value_head_dim_differs(D, Dv, causal, hip_device):
     assert sdpa_custom(q, k, v, backend="hip", causal=causal).shape[-1] == Dv
     with pytest.raises(AssertionError):
         sdpa_custom(q, k, v, backend="triton_full_fused")
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("causal", [False, True])
+def test_kernel_only_hvp_matches_oracle_and_autograd(dt, causal, hip_device):
+    """hip_sdpa_hvp (no autograd graph) for sum(O), <W, O> and 0.5 ||O - T||^2, against the oracle and,
+    for the quadratic loss, against autograd double backward through hip_sdpa."""
+    from theria_amd.autograd.hip_sdpa import hip_sdpa_hvp
+
+    dev = hip_device
+    print(f"kernel-only HVP {dt} causal={causal}", flush=True)
+    q, qc = make((2, 2, 70, 64), dt, dev, 101)
+    k, kc = make((2, 2, 90, 64), dt, dev, 102)
+    v, vc = make((2, 2, 90, 64), dt, dev, 103)
+    w, wc = make((2, 2, 70, 64), dt, dev, 104)
+    t_, tc = make((2, 2, 70, 64), dt, dev, 105)
+    u = [make(x.shape, dt, dev, 106 + i, std=0.1) for i, x in enumerate((q, k, v))]
+    uv, uc = [x[0] for x in u], [x[1] for x in u]
+    ones = torch.ones_like(wc)
+    cases = [
+        ("sum", {}, O.hvp_weighted_sum(qc, kc, vc, ones, *uc, causal=causal)),
+        ("weight", {"weight": w}, O.hvp_weighted_sum(qc, kc, vc, wc, *uc, causal=causal)),
+        ("quadratic", {"target": t_}, O.hvp_quadratic(qc, kc, vc, tc, *uc, causal=causal)),
+    ]
+    for name, kw, ref in cases:
+        got = hip_sdpa_hvp(q, k, v, *uv, causal=causal, **kw)
+        for part, a, b in zip("qkv", got, ref):
+            close(a, b, dt, f"hvp {name} {part}")
+    qg, kg, vg = (x.detach().clone().requires_grad_(True) for x in (q, k, v))
+    o = hip_sdpa(qg, kg, vg, causal=causal)
+    g = torch.autograd.grad(0.5 * ((o.float() - t_.float()) ** 2).sum(), (qg, kg, vg), create_graph=True)
+    ag = torch.autograd.grad(sum((a.float() * b.float()).sum() for a, b in zip(g, uv)), (qg, kg, vg))
+    for part, a, b in zip("qkv", hip_sdpa_hvp(q, k, v, *uv, target=t_, causal=causal), ag):
+        close(a, b.detach().double().cpu(), dt, f"hvp vs autograd {part}")

@@ -5,7 +5,7 @@ sdpa_bwd_dk, sdpa_bwd_dv, sdpa_jvp, all running the gfx950 kernels. Importing th
 touch the GPU; the kernel library is loaded on first use.
 """
 
-from ..autograd.hip_sdpa import hip_sdpa, hip_sdpa_with_lse
+from ..autograd.hip_sdpa import hip_sdpa, hip_sdpa_hvp, hip_sdpa_with_lse
 from .explicit import sdpa_bwd, sdpa_bwd_dk, sdpa_bwd_dq, sdpa_bwd_dv, sdpa_jvp
 from .fused import TritonFusedSDPAFunction, sdpa_fused, triton_sdpa_fused, triton_sdpa_fused_autograd
 
@@ -19,6 +19,7 @@ __all__ = [
     "sdpa_fused",
     "hip_sdpa",
     "hip_sdpa_with_lse",
+    "hip_sdpa_hvp",
     "TritonFusedSDPAFunction",
     "triton_sdpa_fused_autograd",
 ]

@@ -1,7 +1,7 @@
 """autograd.Functions: the HIP operator (SDPAOp / SDPABackwardOp) and the pure-PyTorch references."""
 
-from .hip_sdpa import SDPABackwardOp, SDPAOp, hip_sdpa, hip_sdpa_with_lse
+from .hip_sdpa import SDPABackwardOp, SDPAOp, hip_sdpa, hip_sdpa_hvp, hip_sdpa_with_lse
 from .sdpa_custom_function import SDPACustom
 from .sdpa_function import SDPAFunction, sdpa
 
-__all__ = ["SDPAOp", "SDPABackwardOp", "hip_sdpa", "hip_sdpa_with_lse", "SDPACustom", "SDPAFunction", "sdpa"]
+__all__ = ["SDPAOp", "SDPABackwardOp", "hip_sdpa", "hip_sdpa_with_lse", "hip_sdpa_hvp", "SDPACustom", "SDPAFunction", "sdpa"]

@@ -164,4 +164,34 @@ def hip_sdpa_with_lse(q, k, v, *, causal: bool = False, scale: float | None = No
     return (o if o.shape[-1] == dv else o[..., :dv]), lse
 
 
-__all__ = ["SDPAOp", "SDPABackwardOp", "hip_sdpa", "hip_sdpa_with_lse"]
+def hip_sdpa_hvp(q, k, v, vq, vk, vv, *, weight=None, target=None, causal: bool = False, scale: float | None = None):
+    """Hessian-vector product of a scalar loss of O = SDPA(q, k, v) along (vq, vk, vv), from the kernels
+    directly (no autograd graph): the counterpart of the reference's sdpa_hvp
+    (theria/attention/reference_hvp_sdpa.py:46-97), which differentiates sum(O).
+
+    Loss: sum(O) by default; <weight, O> for a constant weight; 0.5 ||O - target||^2 for a target. With
+    dO = dL/dO the HVP is the double backward of the backward map with cotangents (vq, vk, vv), plus, for
+    the quadratic loss, the Gauss-Newton term J^T (J v) = backward(G_dO), since G_dO = J v.
+    Returns (hq, hk, hv) in the input dtype.
+    """
+    if scale is None:
+        scale = _ops.default_scale(q.shape[-1])
+    if weight is not None and target is not None:
+        raise ValueError("hip_sdpa_hvp: give weight or target, not both")
+    with torch.no_grad():
+        o, lse, _, _ = _ops.fwd(q, k, v, float(scale), bool(causal))
+        if target is not None:
+            dout = (o.float() - target.float()).to(o.dtype)
+        elif weight is not None:
+            dout = weight.to(o.dtype)
+        else:
+            dout = torch.ones_like(o)
+        delta = (dout.float() * o.float()).sum(-1)
+        hq, hk, hv, g_do = _ops.bwd_bwd(q, k, v, o, dout, lse, delta, vq, vk, vv, float(scale), bool(causal))
+        if target is None:
+            return hq, hk, hv
+        jq, jk, jv, _ = _ops.bwd(q, k, v, o, lse, g_do.to(o.dtype), float(scale), bool(causal))
+        return hq + jq, hk + jk, hv + jv
+
+
+__all__ = ["SDPAOp", "SDPABackwardOp", "hip_sdpa", "hip_sdpa_with_lse", "hip_sdpa_hvp"]
