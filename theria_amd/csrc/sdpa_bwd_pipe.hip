@@ -108,13 +108,13 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
   const int kw0 = key0 + wave * 32;  // this wave's keys: kw0 + li
 
     F kf[NKC], vf[NKC];
-  #pragma unroll
+#pragma unroll
     for (int c = 0; c < NKC; ++c) {
       kf[c] = gload_frag<T>(K, p.k.sr, kw0 + li, s.M, c, DP, true);
       vf[c] = gload_frag<T>(V, p.v.sr, kw0 + li, s.M, c, DP, true);
     }
     f32x16_t dv[NDT], dk[NDT];
-  #pragma unroll
+#pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
       dv[dt] = zero16();
       dk[dt] = zero16();
@@ -154,13 +154,13 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
     // S = Q K^T and dP = dO V^T - delta for subtile qs (32 queries) of the tile in (tq, to, tr).
     auto sdp = [&](const char* tq, const char* to, const float* tr, int qs, f32x16_t& sc, f32x16_t& dp) {
       sc = zero16();
-  #pragma unroll
+#pragma unroll
       for (int qd = 0; qd < 4; ++qd) {
         const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(tr + BM + 32 * qs + 8 * qd + 4 * g);
-  #pragma unroll
+#pragma unroll
         for (int e = 0; e < 4; ++e) dp[4 * qd + e] = d4[e];
       }
-  #pragma unroll
+#pragma unroll
       for (int c = 0; c < NKC; ++c) {
         sc = MM::mma(swz_cols<T, DP>(tq, 32 * qs + li, c), kf[c], sc);
         dp = MM::mma(swz_cols<T, DP>(to, 32 * qs + li, c), vf[c], dp);
@@ -170,17 +170,17 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
     auto mask = [&](f32x16_t& sc, int q0s) {
       const int mykey = kw0 + li;
       if (kw0 + 31 >= s.M || (CAUSAL && kw0 + 31 > q0s)) {
-  #pragma unroll
+#pragma unroll
         for (int r = 0; r < 16; ++r)
           if (mykey >= s.M || (CAUSAL && mykey > q0s + acc_row(r, g))) sc[r] = -THERIA_INF;
       }
     };
     // P = exp2(S c2 - lse2) and dS = P o dP as 16-bit fragments (KACC chunks 0, 1).
     auto pds = [&](const float* tr, int qs, const f32x16_t& sc, const f32x16_t& dp, F (&pf)[2], F (&df)[2]) {
-  #pragma unroll
+#pragma unroll
       for (int qd = 0; qd < 4; ++qd) {
         const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(tr + 32 * qs + 8 * qd + 4 * g);
-  #pragma unroll
+#pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = 4 * qd + e;
           const float pv = fast_exp2(fmaf(sc[r], c2, -l4[e]));
@@ -191,9 +191,9 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
     };
     // dV += P^T dO and dK += dS^T Q for subtile qs.
     auto dvdk = [&](const char* tq, const char* to, int qs, const F (&pf)[2], const F (&df)[2]) {
-  #pragma unroll
+#pragma unroll
       for (int cc = 0; cc < 2; ++cc)
-  #pragma unroll
+#pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
           dv[dt] = MM::mma(pf[cc], swz_rows<T, DP>(to, 32 * qs, cc, 32 * dt), dv[dt]);
           dk[dt] = MM::mma(df[cc], swz_rows<T, DP>(tq, 32 * qs, cc, 32 * dt), dk[dt]);
@@ -214,7 +214,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
         load_rows(it + 2);
       }
       if constexpr (FAST && OVERLAP) {
-  #pragma unroll
+#pragma unroll
         for (int hf = 0; hf < HALVES; ++hf) {
           f32x16_t s0, p0, s1, p1;
           F pf0[2], df0[2], pf1[2], df1[2];
@@ -230,7 +230,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
           __builtin_amdgcn_sched_barrier(0);
         }
       } else if constexpr (FAST) {
-  #pragma unroll
+#pragma unroll
         for (int qs = 0; qs < 2 * HALVES; ++qs) {
           f32x16_t sc, dp;
           F pf[2], df[2];
@@ -239,7 +239,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
           dvdk(tq, to, qs, pf, df);
         }
       } else {
-  #pragma unroll
+#pragma unroll
         for (int qs = 0; qs < 2 * HALVES; ++qs) {
           const int q0s = q0 + 32 * qs;
           if (q0s >= s.T || (CAUSAL && kw0 > q0s + 31)) continue;  // wave-uniform
@@ -289,10 +289,10 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
     // Epilogue: lane holds column d = dt*32 + li of keys kw0 + acc_row(r, g).
     T* DV = (T*)p.dv.p + b * p.dv.sb + h * p.dv.sh;
     T* DK = p.dk.p ? (T*)p.dk.p + b * p.dk.sb + h * p.dk.sh : nullptr;
-  #pragma unroll
+#pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
       const int d = dt * 32 + li;
-  #pragma unroll
+#pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int key = kw0 + acc_row(r, g);
         if (key < s.M) {
@@ -353,7 +353,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
     const int64_t rowbase = (int64_t)bh * s.T;
 
     F qf[NKC], of[NKC];
-  #pragma unroll
+#pragma unroll
     for (int c = 0; c < NKC; ++c) {
       qf[c] = gload_frag<T>(Q, p.q.sr, myq, s.T, c, DP, true);
       of[c] = gload_frag<T>(dO, p.dout.sr, myq, s.T, c, DP, true);
@@ -365,7 +365,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
       // delta = dO . O over this lane's half of the head dim (the dO fragment's columns), then the pair
       float part = 0.f;
       if (qvalid) {
-  #pragma unroll
+#pragma unroll
         for (int c = 0; c < NKC; ++c) {
           const int col = c * 16 + 8 * g;
           const int64_t off = (int64_t)myq * p.o.sr + col;
@@ -373,12 +373,12 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
             const float* Op = (const float*)p.o.p + b * p.o.sb + h * p.o.sh + off;
             const f32x4_t a0 = *reinterpret_cast<const f32x4_t*>(Op);
             const f32x4_t a1 = *reinterpret_cast<const f32x4_t*>(Op + 4);
-  #pragma unroll
+#pragma unroll
             for (int e = 0; e < 4; ++e) part += a0[e] * (float)of[c][e] + a1[e] * (float)of[c][4 + e];
           } else {
             const F ov = __builtin_bit_cast(F, *reinterpret_cast<const i16x8_t*>((const T*)p.o.p + b * p.o.sb +
                                                                                h * p.o.sh + off));
-  #pragma unroll
+#pragma unroll
             for (int e = 0; e < 8; ++e) part += (float)ov[e] * (float)of[c][e];
           }
         }
@@ -391,7 +391,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
     if (!p.dq.p) continue;  // only the row term was requested (uniform over the grid)
 
     f32x16_t acc[NDT];
-  #pragma unroll
+#pragma unroll
     for (int dt = 0; dt < NDT; ++dt) acc[dt] = zero16();
     const float c2 = s.scale * kLog2e;
 
@@ -410,9 +410,9 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
     // S^T = K Q^T and dP^T = V dO^T - delta for key subtile t of the tile in (tk, tv).
     auto sdp = [&](const char* tk, const char* tv, int t, f32x16_t& sc, f32x16_t& dp) {
       sc = zero16();
-  #pragma unroll
+#pragma unroll
       for (int r = 0; r < 16; ++r) dp[r] = -del;
-  #pragma unroll
+#pragma unroll
       for (int c = 0; c < NKC; ++c) {
         sc = MM::mma(swz_cols<T, DP>(tk, 32 * t + li, c), qf[c], sc);
         dp = MM::mma(swz_cols<T, DP>(tv, 32 * t + li, c), of[c], dp);
@@ -421,20 +421,20 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
     auto mask = [&](f32x16_t& sc, int k0t) {
       if ((k0t + 32 > s.M) || (CAUSAL && k0t + 31 > q0w)) {
         const int lim = CAUSAL ? min(s.M, myq + 1) : s.M;  // first key this query cannot see
-  #pragma unroll
+#pragma unroll
         for (int r = 0; r < 16; ++r)
           if (k0t + acc_row(r, g) >= lim) sc[r] = -THERIA_INF;
       }
     };
     // dS^T = P^T o dP^T as 16-bit fragments (KACC chunks 0, 1)
     auto pds = [&](const f32x16_t& sc, const f32x16_t& dp, F (&df)[2]) {
-  #pragma unroll
+#pragma unroll
       for (int r = 0; r < 16; ++r) df[r >> 3][r & 7] = (T)(fast_exp2(fmaf(sc[r], c2, -lse2)) * dp[r]);
     };
     auto dqm = [&](const char* tk, int t, const F (&df)[2]) {
-  #pragma unroll
+#pragma unroll
       for (int cc = 0; cc < 2; ++cc)
-  #pragma unroll
+#pragma unroll
         for (int dt = 0; dt < NDT; ++dt) acc[dt] = MM::mma(swz_rows<T, DP>(tk, 32 * t, cc, 32 * dt), df[cc], acc[dt]);
     };
 
@@ -448,7 +448,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
         dma.template issue_clamped<NSLAB>(vrsrc, vrs, k0 + BN, s.M, nv);
       }
       if constexpr (FAST && !OVERLAP) {
-  #pragma unroll
+#pragma unroll
         for (int t = 0; t < 2 * HALVES; ++t) {
           f32x16_t sc, dp;
           F df[2];
@@ -457,7 +457,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
           dqm(tk, t, df);
         }
       } else if constexpr (FAST) {
-  #pragma unroll
+#pragma unroll
         for (int hf = 0; hf < HALVES; ++hf) {
           f32x16_t s0, p0, s1, p1;
           F d0[2], d1[2];
@@ -473,7 +473,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
           __builtin_amdgcn_sched_barrier(0);
         }
       } else {
-  #pragma unroll
+#pragma unroll
         for (int t = 0; t < 2 * HALVES; ++t) {
           const int k0t = k0 + 32 * t;
           if (CAUSAL && k0t > q0w + 31) continue;  // every key after every query of the wave (uniform)
@@ -507,9 +507,9 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
 
     if (qvalid) {
       T* DQ = (T*)p.dq.p + b * p.dq.sb + h * p.dq.sh;
-  #pragma unroll
+#pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
-  #pragma unroll
+#pragma unroll
         for (int qd = 0; qd < 4; ++qd) {
           const int d0 = dt * 32 + 8 * qd + 4 * g;
           const f32x16_t& a = acc[dt];

@@ -88,7 +88,7 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
     const rsrc_t krsrc = make_rsrc(K, (uint32_t)s.M * krs);
     const rsrc_t vrsrc = make_rsrc(V, (uint32_t)s.M * vrs);
     uint32_t koff[NSLAB], voff[NSLAB];
-  #pragma unroll
+#pragma unroll
     for (int i = 0; i < NSLAB; ++i) {
       koff[i] = dma.lane_offset(krs, i);
       voff[i] = dma.lane_offset(vrs, i);
@@ -96,16 +96,16 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
     if (nkt > 0) dma.template issue_clamped<NSLAB>(krsrc, krs, 0, s.M, sK0);
 
     F qf[QT][NKC];
-  #pragma unroll
+#pragma unroll
     for (int j = 0; j < QT; ++j)
-  #pragma unroll
+#pragma unroll
       for (int c = 0; c < NKC; ++c) qf[j][c] = gload_frag<T>(Q, p.q.sr, q0w + 32 * j + li, s.T, c, DP, true);
 
     f32x16_t o[QT][NDT];
     float m_use[QT], l_part[QT], m_max[QT];
-  #pragma unroll
+#pragma unroll
     for (int j = 0; j < QT; ++j) {
-  #pragma unroll
+#pragma unroll
       for (int dt = 0; dt < NDT; ++dt) o[j][dt] = zero16();
       m_use[j] = -THERIA_INF;
       l_part[j] = 0.f;
@@ -116,12 +116,12 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
 
     // S^T = K Q^T for both query tiles, key subtile t (32 keys) of the K tile in `kt`.
     auto scores_t = [&](const char* kt, int t, f32x16_t (&st)[QT]) {
-  #pragma unroll
+#pragma unroll
       for (int j = 0; j < QT; ++j) st[j] = zero16();
-  #pragma unroll
+#pragma unroll
       for (int c = 0; c < NKC; ++c) {
         const F kf = swz_cols<T, DP>(kt, 32 * t + li, c);
-  #pragma unroll
+#pragma unroll
         for (int j = 0; j < QT; ++j) st[j] = MM::mma(kf, qf[j][c], st[j]);
       }
     };
@@ -129,7 +129,7 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
       f32x16_t s0[QT], s1[QT];
       scores_t(kt, 0, s0);
       scores_t(kt, 1, s1);
-  #pragma unroll
+#pragma unroll
       for (int j = 0; j < QT; ++j) {
         sc[j][0] = s0[j];
         sc[j][1] = s1[j];
@@ -137,26 +137,26 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
     };
     // O^T += V^T P^T with the previous tile's P and the V tile in `vt`.
     auto pv_mma = [&](const char* vt) __attribute__((always_inline)) {
-  #pragma unroll
+#pragma unroll
       for (int t = 0; t < 2; ++t)
-  #pragma unroll
+#pragma unroll
         for (int cc = 0; cc < 2; ++cc)
-  #pragma unroll
+#pragma unroll
           for (int dt = 0; dt < NDT; ++dt) {
             const F vf = swz_rows<T, DP>(vt, 32 * t, cc, 32 * dt);
-  #pragma unroll
+#pragma unroll
             for (int j = 0; j < QT; ++j) o[j][dt] = MM::mma(vf, pf[j][t][cc], o[j][dt]);
           }
     };
     // Keys out of range, or (causal) after the query, get -inf. Only boundary tiles pay for the test.
     auto mask = [&](f32x16_t (&sc)[QT][2], int k0) {
       if ((k0 + BN > s.M) || (CAUSAL && k0 + BN - 1 > q0w)) {
-  #pragma unroll
+#pragma unroll
         for (int j = 0; j < QT; ++j) {
           const int lim = CAUSAL ? min(s.M, q0w + 32 * j + li + 1) : s.M;  // first key this query cannot see
-  #pragma unroll
+#pragma unroll
           for (int t = 0; t < 2; ++t)
-  #pragma unroll
+#pragma unroll
             for (int r = 0; r < 16; ++r)
               if (k0 + 32 * t + acc_row(r, g) >= lim) sc[j][t][r] = -THERIA_INF;
         }
@@ -164,15 +164,15 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
     };
     // P = exp2(S c2 - off) as 16-bit fragments into pn, and this tile's lane partial row sums into ps.
     auto exps = [&](const f32x16_t (&sc)[QT][2], const float (&off)[QT], F (&pn)[QT][2][2], float (&ps)[QT]) {
-  #pragma unroll
+#pragma unroll
       for (int j = 0; j < QT; ++j) {
         float acc = 0.f;
-  #pragma unroll
+#pragma unroll
         for (int t = 0; t < 2; ++t)
-  #pragma unroll
+#pragma unroll
           for (int cc = 0; cc < 2; ++cc) {
             F f;
-  #pragma unroll
+#pragma unroll
             for (int e = 0; e < 8; ++e) f[e] = (T)fast_exp2(fmaf(sc[j][t][8 * cc + e], c2, -off[j]));
             pn[j][t][cc] = f;
             acc = frag_sum<T>(f, acc);
@@ -182,12 +182,12 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
     };
     // The same for key subtile t only, accumulating the lane partial row sums into ps.
     auto exps_t = [&](const f32x16_t (&st)[QT], int t, F (&pn)[QT][2][2], float (&ps)[QT]) {
-  #pragma unroll
+#pragma unroll
       for (int j = 0; j < QT; ++j)
-  #pragma unroll
+#pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
           F f;
-  #pragma unroll
+#pragma unroll
           for (int e = 0; e < 8; ++e) f[e] = (T)fast_exp2(fmaf(st[j][8 * cc + e], c2, -m_use[j]));
           pn[j][t][cc] = f;
           ps[j] = frag_sum<T>(f, ps[j]);
@@ -195,16 +195,16 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
     };
     auto tile_max = [&](const f32x16_t (&sc)[QT][2], int j) {
       float mx = -THERIA_INF;
-  #pragma unroll
+#pragma unroll
       for (int t = 0; t < 2; ++t)
-  #pragma unroll
+#pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[j][t][r]);
       return pair_max(mx) * c2;
     };
     // Exact path: the running max becomes the offset; O and the row sums are rescaled to it.
     auto exact = [&](const f32x16_t (&sc)[QT][2], F (&pn)[QT][2][2], float (&ps)[QT]) {
       float off[QT];
-  #pragma unroll
+#pragma unroll
       for (int j = 0; j < QT; ++j) {
         const float mx = tile_max(sc, j);
         m_max[j] = fmaxf(m_max[j], mx);
@@ -212,9 +212,9 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
         const float alpha = mnew == -THERIA_INF ? 1.f : fast_exp2(m_use[j] - mnew);
         m_use[j] = mnew;
         l_part[j] *= alpha;
-  #pragma unroll
+#pragma unroll
         for (int dt = 0; dt < NDT; ++dt)
-  #pragma unroll
+#pragma unroll
           for (int r = 0; r < 16; ++r) o[j][dt][r] *= alpha;
         off[j] = mnew == -THERIA_INF ? 0.f : mnew;  // all keys so far masked: P = exp2(-inf) = 0
       }
@@ -243,16 +243,16 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
         //   S(k) subtile 0 | S(k) subtile 1 with exp of subtile 0 | O += V(k-1)^T P(k-1)^T with exp of subtile 1.
         f32x16_t s0[QT], s1[QT];
         float ps[QT];
-  #pragma unroll
+#pragma unroll
         for (int j = 0; j < QT; ++j) ps[j] = 0.f;
         scores_t(kc, 0, s0);
         __builtin_amdgcn_sched_barrier(0);
         scores_t(kc, 1, s1);
         if (STATS) {
-  #pragma unroll
+#pragma unroll
           for (int j = 0; j < QT; ++j) {
             float mx = -THERIA_INF;
-  #pragma unroll
+#pragma unroll
             for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s0[j][r]);
             m_max[j] = fmaxf(m_max[j], pair_max(mx) * c2);
           }
@@ -262,9 +262,9 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
           // Issue order inside the phase: the four K fragment reads first, then each of the 8 MFMAs
           // followed by 12 VALU instructions of the exponentials (measured ~5% faster than the
           // compiler's own order at head dim 64).
-  #pragma unroll
+#pragma unroll
           for (int i = 0; i < 4; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
-  #pragma unroll
+#pragma unroll
           for (int i = 0; i < 8; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
             __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);  // VALU
@@ -273,10 +273,10 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
         __builtin_amdgcn_sched_barrier(0);
         pv_mma(vp);
         if (STATS) {
-  #pragma unroll
+#pragma unroll
           for (int j = 0; j < QT; ++j) {
             float mx = -THERIA_INF;
-  #pragma unroll
+#pragma unroll
             for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s1[j][r]);
             m_max[j] = fmaxf(m_max[j], pair_max(mx) * c2);
           }
@@ -284,29 +284,29 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
         exps_t(s1, 1, pn, ps);
         if constexpr (DP == 64) {
           // V fragment reads first, then each of the 16 PV MFMAs followed by 6 VALU instructions.
-  #pragma unroll
+#pragma unroll
           for (int i = 0; i < 8; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
-  #pragma unroll
+#pragma unroll
           for (int i = 0; i < 16; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
             __builtin_amdgcn_sched_group_barrier(0x002, 6, 1);
           }
         }
         bool bad = false;
-  #pragma unroll
+#pragma unroll
         for (int j = 0; j < QT; ++j) bad |= !(ps[j] <= 0x1p20f);
         if (__any(bad)) {
           f32x16_t sc2[QT][2];
           scores(kc, sc2);
           exact(sc2, pn, ps);
         }
-  #pragma unroll
+#pragma unroll
         for (int j = 0; j < QT; ++j) l_part[j] += ps[j];
-  #pragma unroll
+#pragma unroll
         for (int j = 0; j < QT; ++j)
-  #pragma unroll
+#pragma unroll
           for (int t = 0; t < 2; ++t)
-  #pragma unroll
+#pragma unroll
             for (int cc = 0; cc < 2; ++cc) pf[j][t][cc] = pn[j][t][cc];
         pf_skip = false;
       } else {
@@ -321,12 +321,12 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
             exact(sc, pn, ps);
           } else {
             if (STATS) {
-  #pragma unroll
+#pragma unroll
               for (int j = 0; j < QT; ++j) m_max[j] = fmaxf(m_max[j], tile_max(sc, j));
             }
             exps(sc, m_use, pn, ps);
             bool bad = false;
-  #pragma unroll
+#pragma unroll
             for (int j = 0; j < QT; ++j) bad |= !(ps[j] <= 0x1p20f);
             if (__any(bad)) {
               f32x16_t sc2[QT][2];
@@ -335,13 +335,13 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
               exact(sc2, pn, ps);
             }
           }
-  #pragma unroll
+#pragma unroll
           for (int j = 0; j < QT; ++j) l_part[j] += ps[j];
-  #pragma unroll
+#pragma unroll
           for (int j = 0; j < QT; ++j)
-  #pragma unroll
+#pragma unroll
             for (int t = 0; t < 2; ++t)
-  #pragma unroll
+#pragma unroll
               for (int cc = 0; cc < 2; ++cc) pf[j][t][cc] = pn[j][t][cc];
         }
         pf_skip = skip;
@@ -374,15 +374,15 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
       if (!pf_skip) pv_mma(((nkt - 1) & 1) ? sV1 : sV0);
     }
 
-  #pragma unroll
+#pragma unroll
     for (int j = 0; j < QT; ++j) {
       const int myq = q0w + 32 * j + li;
       const float l = pair_sum(l_part[j]);
       const float inv = l > 0.f ? 1.f / l : 0.f;
       if (myq < s.T) {
-  #pragma unroll
+#pragma unroll
         for (int dt = 0; dt < NDT; ++dt)
-  #pragma unroll
+#pragma unroll
           for (int qd = 0; qd < 4; ++qd) {
             const int d0 = dt * 32 + 8 * qd + 4 * g;
             const float a0 = o[j][dt][4 * qd] * inv, a1 = o[j][dt][4 * qd + 1] * inv;
