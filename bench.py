@@ -1,7 +1,9 @@
 #!/usr/bin/env python
-"""Benchmark of theria_amd's HIP SDPA operator on one MI355X (BASELINE.json metric).
+"""Benchmark of theria_amd's HIP SDPA operator on one MI355X.
 
-A "step" is one forward + backward pass of the SDPA operator over BASELINE config 2
+Metric: SDPA fwd+bwd TFLOP/s and share of the bf16 MFMA peak at B4 H16 S2048 D64; JVP/HVP ms.
+
+A "step" is one forward + backward pass of the SDPA operator over config 2
 (B4 H16 S2048 D64, bfloat16, non-causal, scale 1/8, Q, K, V, dO ~ N(0,1), synthetic, resident in HBM):
 forward kernel (O, lse), then the backward's two kernels (dQ with the row term, then dK/dV). Throughput counts algorithmic FLOPs, FlashAttention convention: 4*B*H*S^2*D forward,
 10*B*H*S^2*D backward (the recomputed QK^T included), 14*B*H*S^2*D per step.
@@ -12,7 +14,7 @@ Printed as ONE JSON line (rank 0): value = TFLOP/s of the whole step, plus
                per launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE runs (profiles/traffic.json);
   cpu_baseline the CPU oracle (oracle/sdpa_oracle.py, the reference's pure-PyTorch math, float32)
                timed on a bounded sample of heads of the same workload on this host's cores;
-  extra        the other BASELINE configs: C3 causal long sequence, C4 JVP / HVP ms, C5 MAML.
+  extra        the other configs: C3 causal long sequence, C4 JVP / HVP ms, C5 MAML.
 One GPU only: --gpus N with N > 1 exits with a message.
 """
 

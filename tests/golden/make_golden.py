@@ -1,4 +1,4 @@
-"""Regenerate tests/golden/c1_fp32.npz: BASELINE config 1 inputs and oracle outputs.
+"""Regenerate tests/golden/c1_fp32.npz: config 1 inputs and oracle outputs.
 
 Config 1: Q, K, V ~ N(0,1), B=2, H=2, S=16, D=8, float32, non-causal, scale 1/sqrt(D); upstream dO,
 tangents (tq, tk, tv), weight W and HVP direction (vq, vk, vv) all ~ N(0,1). Expected values come

@@ -37,7 +37,7 @@ def test_golden_fixture_matches_oracle():
 
 
 def test_golden_fixture_matches_reference_cpu_path_fp32():
-    """Config 1 as the BASELINE states it: the existing pure-PyTorch path in float32, 1e-5."""
+    """Config 1 (B2 H2 S16 D8, float32) on the existing pure-PyTorch path, 1e-5."""
     inp, out = _golden()
     q, k, v = inp["q"], inp["k"], inp["v"]
     tol = dict(rtol=1e-5, atol=1e-5)

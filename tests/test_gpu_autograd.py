@@ -1,7 +1,7 @@
 """The HIP operator through torch.autograd: gradients, forward-mode JVP, HVP by double backward,
 the reference-named entry points, and the second-order boundary (GPU).
 
-Config 4 (BASELINE): B8 H8 S512 D64 in float32 and bfloat16; primals ~ N(0,1), tangents ~ N(0, 0.1^2);
+Config 4: B8 H8 S512 D64 in float32 and bfloat16; primals ~ N(0,1), tangents ~ N(0, 0.1^2);
 HVP of 0.5 ||O - T||^2 with T, v ~ N(0,1) via double backward through the explicit kernels.
 Bars: float32 1e-5 abs/rel, bfloat16/float16 2e-2 abs.
 """

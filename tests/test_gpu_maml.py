@@ -1,5 +1,5 @@
 """Full MAML (create_graph=True) through the HIP operator vs the same model on the pure-PyTorch
-"reference" backend (GPU). BASELINE config 5 (reduced meta-batch): 2-layer, d_model 64, 4-head
+"reference" backend (GPU). Config 5 (reduced meta-batch): 2-layer, d_model 64, 4-head
 token-count classifier, 5 inner SGD steps at lr 0.4. The meta-gradients must agree (attention's
 second-order terms are kept), and full MAML must differ from first-order MAML.
 """

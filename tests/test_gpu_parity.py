@@ -1,6 +1,6 @@
 """GPU parity of the HIP kernels (through the C ABI) against the CPU oracle.
 
-Bars (BASELINE north star): float32 within 1e-5 abs/rel; float16/bfloat16 within 2e-2 abs. Inputs are
+Bars: float32 within 1e-5 abs/rel; float16/bfloat16 within 2e-2 abs. Inputs are
 generated on the CPU with a seeded generator, rounded to the compute dtype, and the oracle receives
 exactly those rounded values in float64 (as the reference's GPU tests do, test_triton_sdpa_dq.py:30-31).
 Full-size configs are checked on sampled heads plus size-independent invariants:
@@ -163,7 +163,7 @@ def _check_all_entry_points(case, dev, seed: int):
 
 
 def test_config1_golden_fixture_fp32(hip_device):
-    """BASELINE config 1 (B2 H2 S16 D8, float32) against the committed fixture, 1e-5."""
+    """Config 1 (B2 H2 S16 D8, float32) against the committed fixture, 1e-5."""
     z = np.load(GOLDEN, allow_pickle=False)
     t = {k: torch.from_numpy(z[k]) for k in z.files}
     dev = hip_device
@@ -221,7 +221,7 @@ def test_strided_inputs(hip_device):
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 def test_config2_full_size(dt, hip_device):
-    """B4 H16 S2048 D64, fwd+bwd; two heads vs the oracle, all heads via invariants."""
+    """Config 2: B4 H16 S2048 D64, fwd+bwd; two heads vs the oracle, all heads via invariants."""
     dev = hip_device
     B, H, S, D = 4, 16, 2048, 64
     print(f"[parity] config2 {dt}", flush=True)
@@ -250,7 +250,7 @@ def test_config2_full_size(dt, hip_device):
 
 
 def test_config3_causal_long_sequence(hip_device):
-    """B1 H32 S8192 D128 causal bf16, inputs 0.5*N(0,1); one head vs the oracle."""
+    """Config 3: B1 H32 S8192 D128 causal bf16, inputs 0.5*N(0,1); one head vs the oracle."""
     dev = hip_device
     B, H, S, D = 1, 32, 8192, 128
     dt = torch.bfloat16

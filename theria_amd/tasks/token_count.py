@@ -1,4 +1,4 @@
-"""Token-count classification tasks for the multi-head MAML benchmark.
+"""Token-count classification tasks for the multi-head MAML benchmark (config 5: 16 tasks, vocab 32, length 64, 5-way).
 
 Not in the reference (its nearest relatives are the prototype tasks of theria/tasks/synthetic_seqcls.py).
 A task partitions the vocabulary at random into `num_classes` class-token sets (sizes differ by at most
