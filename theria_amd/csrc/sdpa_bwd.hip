@@ -388,11 +388,12 @@ struct DqLauncher {
       hipError_t err;
       if (launch_dq_pipe<T, CAUSAL>(p, st, &err)) return err;
     }
-    const int qt = (DQ_QT_MAX >= 2 && DP <= 64 && p.s.T > 128) ? 2 : 1;
+    // Two query tiles per wave only for 16-bit inputs (float32 fragments would spill ~160 VGPRs).
+    const int qt = (DQ_QT_MAX >= 2 && sizeof(T) == 2 && DP <= 64 && p.s.T > 128) ? 2 : 1;
     const int bm = 128 * qt;
     const int64_t nblk = (int64_t)((p.s.T + bm - 1) / bm) * p.s.B * p.s.H;
     if (nblk == 0) return hipSuccess;
-    if constexpr (DP <= 64) {
+    if constexpr (DP <= 64 && sizeof(T) == 2) {
       if (qt == 2) {
         hipLaunchKernelGGL((dq_kernel<T, DP, CAUSAL, 2>), dim3((unsigned)nblk), dim3(256), 0, st, p);
         return hipGetLastError();

@@ -238,11 +238,13 @@ struct FwdLauncher {
       hipError_t err;
       if (launch_fwd_pipe<T, CAUSAL>(p, st, &err)) return err;
     }
-    const int qt = fwd_qt<DP>(p.s.T);
+    // Two query tiles per wave only for 16-bit inputs: with float32 fragments (twice the registers)
+    // that variant spills ~150 VGPRs and runs at half the one-tile rate.
+    const int qt = sizeof(T) == 2 ? fwd_qt<DP>(p.s.T) : 1;
     const int bm = 128 * qt;
     const int64_t nblk = (int64_t)((p.s.T + bm - 1) / bm) * p.s.B * p.s.H;
     if (nblk == 0) return hipSuccess;
-    if constexpr (DP <= 64) {
+    if constexpr (DP <= 64 && sizeof(T) == 2) {
       if (qt == 2) {
         hipLaunchKernelGGL((fwd_kernel<T, DP, CAUSAL, MODE, 2, FWD_BN_QT2>), dim3((unsigned)nblk), dim3(256), 0, st, p);
         return hipGetLastError();
