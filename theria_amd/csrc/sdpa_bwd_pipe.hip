@@ -8,14 +8,16 @@
 // Work decomposition: one workgroup = NW waves, each owning 32 keys (K and V fragments in registers,
 // dK and dV accumulated in registers); the workgroup streams the query tiles (64 or 128 rows) of its head.
 //  * Q and dO tiles reach LDS by DMA (sdpa_lds.hpp) into double buffers with one barrier per tile;
-//    the row terms lse * log2(e) and -delta of the next tile are loaded by the first 64 threads during
+//    the row terms -lse * log2(e) and -delta of the next tile are loaded by the first 64 threads during
 //    the current tile and written beside them.
 //  * Scores are S = Q K^T with this lane's key in the column, so dV += P^T dO and dK += dS^T Q take
 //    P and dS straight from the accumulators (KACC order) and dO^T / Q^T from LDS transpose reads.
 //  * Phase order per 64-row half of a tile, i.e. two 32-query subtiles (scheduling barriers keep it):
 //      S, dP of subtile 0 | S, dP of subtile 1 with exp / dS of subtile 0
 //      | dV, dK of subtile 0 with exp / dS of subtile 1 | dV, dK of subtile 1.
-//  * dP starts from -delta as the MFMA accumulator input, so dS = P o dP is one multiply.
+//  * dP starts from -delta as the MFMA accumulator input, so dS = P o dP is one multiply; K is held
+//    pre-multiplied by scale * log2(e) and S starts from -lse * log2(e), so P = exp2(S) needs no
+//    per-score scaling.
 #include <type_traits>
 
 #include "sdpa_common.hpp"
@@ -74,7 +76,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
   __shared__ __attribute__((aligned(1024))) char sQ1[TILE];
   __shared__ __attribute__((aligned(1024))) char sO0[TILE];
   __shared__ __attribute__((aligned(1024))) char sO1[TILE];
-  __shared__ __attribute__((aligned(16))) float sR0[2 * BM];  // [lse * log2(e) | -delta] of a tile
+  __shared__ __attribute__((aligned(16))) float sR0[2 * BM];  // [-lse * log2(e) | -delta] of a tile
   __shared__ __attribute__((aligned(16))) float sR1[2 * BM];
 
   const Shape& s = p.s;
@@ -110,7 +112,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
     F kf[NKC], vf[NKC];
 #pragma unroll
     for (int c = 0; c < NKC; ++c) {
-      kf[c] = gload_frag<T>(K, p.k.sr, kw0 + li, s.M, c, DP, true);
+      kf[c] = scaled_frag<T>(gload_frag<T>(K, p.k.sr, kw0 + li, s.M, c, DP, true), c2);
       vf[c] = gload_frag<T>(V, p.v.sr, kw0 + li, s.M, c, DP, true);
     }
     f32x16_t dv[NDT], dk[NDT];
@@ -133,14 +135,14 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
     const rsrc_t qrsrc = make_rsrc(Q, (uint32_t)s.T * qrs);
     const rsrc_t orsrc = make_rsrc(dO, (uint32_t)s.T * ors);
 
-    // Row terms of tile `it` for thread tid < BM: lse * log2(e) (rows past the end or without visible
-    // keys: +inf, so P = 0) and -delta.
-    float r_lse = THERIA_INF, r_del = 0.f;
+    // Row terms of tile `it` for thread tid < BM: -lse * log2(e) (rows past the end or without visible
+    // keys: -inf, so P = 0) and -delta.
+    float r_lse = -THERIA_INF, r_del = 0.f;
     auto load_rows = [&](int it) {
       if (tid < BM && it < nqt) {
         const int qq = qbeg + it * BM + tid;
         const float l2 = qq < s.T ? p.lse[rowbase + qq] * kLog2e : THERIA_INF;
-        r_lse = l2 == -THERIA_INF ? THERIA_INF : l2;
+        r_lse = l2 == -THERIA_INF ? -THERIA_INF : -l2;
         r_del = qq < s.T ? -p.delta[rowbase + qq] : 0.f;
       }
     };
@@ -151,14 +153,17 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
       }
     };
 
-    // S = Q K^T and dP = dO V^T - delta for subtile qs (32 queries) of the tile in (tq, to, tr).
+    // S = c2 Q K^T - lse2 and dP = dO V^T - delta for subtile qs (32 queries) of the tile in (tq, to, tr).
     auto sdp = [&](const char* tq, const char* to, const float* tr, int qs, f32x16_t& sc, f32x16_t& dp) {
-      sc = zero16();
 #pragma unroll
       for (int qd = 0; qd < 4; ++qd) {
+        const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(tr + 32 * qs + 8 * qd + 4 * g);
         const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(tr + BM + 32 * qs + 8 * qd + 4 * g);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) dp[4 * qd + e] = d4[e];
+        for (int e = 0; e < 4; ++e) {
+          sc[4 * qd + e] = l4[e];
+          dp[4 * qd + e] = d4[e];
+        }
       }
 #pragma unroll
       for (int c = 0; c < NKC; ++c) {
@@ -175,18 +180,13 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
           if (mykey >= s.M || (CAUSAL && mykey > q0s + acc_row(r, g))) sc[r] = -THERIA_INF;
       }
     };
-    // P = exp2(S c2 - lse2) and dS = P o dP as 16-bit fragments (KACC chunks 0, 1).
-    auto pds = [&](const float* tr, int qs, const f32x16_t& sc, const f32x16_t& dp, F (&pf)[2], F (&df)[2]) {
+    // P = exp2(S) and dS = P o dP as 16-bit fragments (KACC chunks 0, 1).
+    auto pds = [&](const f32x16_t& sc, const f32x16_t& dp, F (&pf)[2], F (&df)[2]) {
 #pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(tr + 32 * qs + 8 * qd + 4 * g);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = 4 * qd + e;
-          const float pv = fast_exp2(fmaf(sc[r], c2, -l4[e]));
-          pf[r >> 3][r & 7] = (T)pv;
-          df[r >> 3][r & 7] = (T)(pv * dp[r]);
-        }
+      for (int r = 0; r < 16; ++r) {
+        const float pv = fast_exp2(sc[r]);
+        pf[r >> 3][r & 7] = (T)pv;
+        df[r >> 3][r & 7] = (T)(pv * dp[r]);
       }
     };
     // dV += P^T dO and dK += dS^T Q for subtile qs.
@@ -221,10 +221,10 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
           sdp(tq, to, tr, 2 * hf, s0, p0);
           __builtin_amdgcn_sched_barrier(0);
           sdp(tq, to, tr, 2 * hf + 1, s1, p1);
-          pds(tr, 2 * hf, s0, p0, pf0, df0);
+          pds(s0, p0, pf0, df0);
           __builtin_amdgcn_sched_barrier(0);
           dvdk(tq, to, 2 * hf, pf0, df0);
-          pds(tr, 2 * hf + 1, s1, p1, pf1, df1);
+          pds(s1, p1, pf1, df1);
           __builtin_amdgcn_sched_barrier(0);
           dvdk(tq, to, 2 * hf + 1, pf1, df1);
           __builtin_amdgcn_sched_barrier(0);
@@ -235,7 +235,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
           f32x16_t sc, dp;
           F pf[2], df[2];
           sdp(tq, to, tr, qs, sc, dp);
-          pds(tr, qs, sc, dp, pf, df);
+          pds(sc, dp, pf, df);
           dvdk(tq, to, qs, pf, df);
         }
       } else {
@@ -247,7 +247,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
           F pf[2], df[2];
           sdp(tq, to, tr, qs, sc, dp);
           mask(sc, q0s);
-          pds(tr, qs, sc, dp, pf, df);
+          pds(sc, dp, pf, df);
           dvdk(tq, to, qs, pf, df);
         }
       }
@@ -393,7 +393,10 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
     f32x16_t acc[NDT];
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) acc[dt] = zero16();
+    // Q pre-multiplied by scale * log2(e) and S^T started from -lse2: P = exp2(S^T) with no per-score scaling.
     const float c2 = s.scale * kLog2e;
+#pragma unroll
+    for (int c = 0; c < NKC; ++c) qf[c] = scaled_frag<T>(qf[c], c2);
 
     int kend = s.M;
     if (CAUSAL) kend = min(s.M, qb * BM + BM);
@@ -407,11 +410,13 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
     const rsrc_t krsrc = make_rsrc(K, (uint32_t)s.M * krs);
     const rsrc_t vrsrc = make_rsrc(V, (uint32_t)s.M * vrs);
 
-    // S^T = K Q^T and dP^T = V dO^T - delta for key subtile t of the tile in (tk, tv).
+    // S^T = c2 K Q^T - lse2 and dP^T = V dO^T - delta for key subtile t of the tile in (tk, tv).
     auto sdp = [&](const char* tk, const char* tv, int t, f32x16_t& sc, f32x16_t& dp) {
-      sc = zero16();
 #pragma unroll
-      for (int r = 0; r < 16; ++r) dp[r] = -del;
+      for (int r = 0; r < 16; ++r) {
+        sc[r] = -lse2;
+        dp[r] = -del;
+      }
 #pragma unroll
       for (int c = 0; c < NKC; ++c) {
         sc = MM::mma(swz_cols<T, DP>(tk, 32 * t + li, c), qf[c], sc);
@@ -429,7 +434,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
     // dS^T = P^T o dP^T as 16-bit fragments (KACC chunks 0, 1)
     auto pds = [&](const f32x16_t& sc, const f32x16_t& dp, F (&df)[2]) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) df[r >> 3][r & 7] = (T)(fast_exp2(fmaf(sc[r], c2, -lse2)) * dp[r]);
+      for (int r = 0; r < 16; ++r) df[r >> 3][r & 7] = (T)(fast_exp2(sc[r]) * dp[r]);
     };
     auto dqm = [&](const char* tk, int t, const F (&df)[2]) {
 #pragma unroll

@@ -175,6 +175,19 @@ __device__ __forceinline__ typename Mfma<T>::frag_t acc_frag(const f32x16_t& a, 
   }
 }
 
+// Fragment with every element multiplied by x (in float32, rounded once to T).
+template <typename T>
+__device__ __forceinline__ typename Mfma<T>::frag_t scaled_frag(const typename Mfma<T>::frag_t& f, float x) {
+  if constexpr (sizeof(T) == 2) {
+    typename Mfma<T>::frag_t r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = (T)((float)f[e] * x);
+    return r;
+  } else {
+    return f * x;
+  }
+}
+
 // Two-term 16-bit split of accumulator chunk c (16-bit T only): hi = round(x), lo = round(x - hi), so
 // hi + lo carries x to ~2^-16 relative and an MFMA pair over (hi, lo) sums x-weighted products with no
 // operand rounding of consequence.
