@@ -42,8 +42,10 @@ TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
 def _args():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    # The GPU runs its first few tens of milliseconds of work after idle at lower clocks; the default
+    # warmup (~0.3 s of steps) reaches the steady state before the timed steps.
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=1000)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU-baseline sample")
     ap.add_argument("--no-extras", action="store_true", help="only the config-2 line (for profiling runs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (for profiling runs)")
@@ -152,11 +154,17 @@ def _cpu_model() -> str:
     return "unknown"
 
 
-def _time(fn, reps: int, warm: int = 3) -> float:
+def _time(fn, reps: int, warm: int = 3, warm_s: float = 0.25) -> float:
+    """Mean ms per call of fn over reps calls, after at least `warm` calls and `warm_s` seconds of warmup."""
     import torch
 
-    for _ in range(warm):
+    t0 = time.perf_counter()
+    n = 0
+    while n < warm or time.perf_counter() - t0 < warm_s:
         fn()
+        n += 1
+        if n % 8 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(reps):

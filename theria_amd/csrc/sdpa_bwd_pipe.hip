@@ -135,21 +135,22 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
     const rsrc_t qrsrc = make_rsrc(Q, (uint32_t)s.T * qrs);
     const rsrc_t orsrc = make_rsrc(dO, (uint32_t)s.T * ors);
 
-    // Row terms of tile `it` for thread tid < BM: -lse * log2(e) (rows past the end or without visible
-    // keys: -inf, so P = 0) and -delta.
-    float r_lse = -THERIA_INF, r_del = 0.f;
+    // Row terms of tile `it` for thread tid < BM, loaded two tiles ahead as raw lse and delta (rows past
+    // the end: lse = +inf) and converted only when stored, so that no instruction waits for these loads
+    // (or for the DMA issued just before them) until the next tile. Stored: -lse * log2(e) (-inf for
+    // rows past the end or without visible keys, so P = 0) and -delta.
+    float r_lse = THERIA_INF, r_del = 0.f;
     auto load_rows = [&](int it) {
       if (tid < BM && it < nqt) {
         const int qq = qbeg + it * BM + tid;
-        const float l2 = qq < s.T ? p.lse[rowbase + qq] * kLog2e : THERIA_INF;
-        r_lse = l2 == -THERIA_INF ? -THERIA_INF : -l2;
-        r_del = qq < s.T ? -p.delta[rowbase + qq] : 0.f;
+        r_lse = qq < s.T ? p.lse[rowbase + qq] : THERIA_INF;
+        r_del = qq < s.T ? p.delta[rowbase + qq] : 0.f;
       }
     };
     auto store_rows = [&](float* sr) {
       if (tid < BM) {
-        sr[tid] = r_lse;
-        sr[BM + tid] = r_del;
+        sr[tid] = __builtin_isinf(r_lse) ? -THERIA_INF : -r_lse * kLog2e;
+        sr[BM + tid] = -r_del;
       }
     };
 
