@@ -396,7 +396,7 @@ def main() -> int:
         "config": {"workload": "sdpa_fwd_bwd", "batch": 4, "heads": 16, "seq_len": 2048, "head_dim": 64, "causal": False},
         "mfma_peak_frac": round(value / PEAK_BF16_TFLOPS, 4),
         "roofline": {
-            "kernel": "dkdv_pipe_kernel<bf16, non-causal, 4 waves> (theria_sdpa_bwd_dkdv)",
+            "kernel": "dkdv_pipe_kernel<bf16, non-causal, 8 waves> (theria_sdpa_bwd_dkdv)",
             "bound": "mfma",
             "achieved": round(achieved, 2),
             "peak": PEAK_BF16_TFLOPS,

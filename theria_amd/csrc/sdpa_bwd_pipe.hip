@@ -29,7 +29,7 @@
 #define DQ_PIPE_NW 4
 #endif
 #ifndef DKDV_PIPE_NW
-#define DKDV_PIPE_NW 4
+#define DKDV_PIPE_NW 4  // head dim 128 (head dim 64 picks 8 or 4 per problem size in the launcher)
 #endif
 // 64-row halves per tile (one barrier per tile): the query tile of dK/dV and the key tile of dQ. At head
 // dim 128 (one wave per SIMD) 128-row tiles halve the barriers, which shortens dK/dV by a quarter; at 64
@@ -561,20 +561,31 @@ bool launch_dkdv_pipe(const DkdvParams& p, hipStream_t st, hipError_t* err) {
   // 32-bit byte offsets inside each (batch, head) slab of Q and dO
   if ((int64_t)p.s.T * p.q.sr * 2 >= (int64_t(1) << 31) || (int64_t)p.s.T * p.dout.sr * 2 >= (int64_t(1) << 31))
     return false;
-  constexpr int NW = DKDV_PIPE_NW;
-  const int64_t nkb = (p.s.M + 32 * NW - 1) / (32 * NW);
-  const int64_t units = (CAUSAL && p.s.D == 64) ? (nkb + 1) / 2 : nkb;  // causal head dim 64: mirrored pairs
-  const int64_t nblk = units * p.s.B * p.s.H;
-  if (nblk == 0) {
+  // workgroups of nw waves (32 keys each): key blocks, or (causal head dim 64) pairs of mirrored blocks
+  auto blocks = [&](int nw) {
+    const int64_t nkb = (p.s.M + 32 * nw - 1) / (32 * nw);
+    return ((CAUSAL && p.s.D == 64) ? (nkb + 1) / 2 : nkb) * p.s.B * p.s.H;
+  };
+  if (blocks(4) == 0) {
     *err = hipSuccess;
     return true;
   }
-  if (p.s.D == 64)
-    hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, NW, 64, true, 2, DKDV64_HALVES>), dim3((unsigned)nblk), dim3(64 * NW), 0,
-                       st, p);
-  else
-    hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, NW, 128, DKDV128_OVERLAP, DKDV128_WPS, DKDV128_HALVES>), dim3((unsigned)nblk),
-                       dim3(64 * NW), 0, st, p);
+  if (p.s.D == 64) {
+    // Eight-wave workgroups (both waves of a SIMD in one workgroup) whenever they still fill every CU:
+    // two independent four-wave workgroups on a CU progress unevenly (the older one is issued first), and
+    // with two rounds of them the CUs that finish early idle through a ~10% tail at config 2.
+    const int64_t nblk8 = blocks(8);
+    if (nblk8 >= device_cu_count())
+      hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, 8, 64, true, 2, DKDV64_HALVES>), dim3((unsigned)nblk8), dim3(64 * 8), 0,
+                         st, p);
+    else
+      hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, 4, 64, true, 2, DKDV64_HALVES>), dim3((unsigned)blocks(4)), dim3(64 * 4),
+                         0, st, p);
+  } else {
+    constexpr int NW = DKDV_PIPE_NW;
+    hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, NW, 128, DKDV128_OVERLAP, DKDV128_WPS, DKDV128_HALVES>),
+                       dim3((unsigned)blocks(NW)), dim3(64 * NW), 0, st, p);
+  }
   *err = hipGetLastError();
   return true;
 }
