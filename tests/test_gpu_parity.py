@@ -271,3 +271,27 @@ def test_config3_causal_long_sequence(hip_device):
     torch.testing.assert_close(dv.double().sum(2), do.double().sum(2), rtol=0, atol=0.5)
     # causal: the first query sees only key 0
     torch.testing.assert_close(o[:, :, 0].float(), v[:, :, 0].float(), rtol=0, atol=1e-2)
+
+
+@pytest.mark.parametrize("S,H,causal", [(1999, 16, False), (1040, 32, True)])
+def test_large_grids_ragged(S, H, causal, hip_device):
+    """Grids large enough that the head-dim-64 dK/dV launcher picks eight-wave workgroups (at least one
+    workgroup per CU), with a ragged sequence length; causal with an odd number of key blocks per head, so
+    one workgroup of each head runs the middle block alone. Two heads vs the oracle, every head via the
+    dV column-sum invariant."""
+    dev = hip_device
+    B, D, dt = 4, 64, torch.bfloat16
+    print(f"[parity] large grid S{S} H{H} causal={causal}", flush=True)
+    q, qc = make((B, H, S, D), dt, dev, 31)
+    k, kc = make((B, H, S, D), dt, dev, 32)
+    v, vc = make((B, H, S, D), dt, dev, 33)
+    do, doc = make((B, H, S, D), dt, dev, 34)
+    s = 1 / 8.0
+    o, lse, _, _ = _ops.fwd(q, k, v, s, causal)
+    dq, dk, dv, _ = _ops.bwd(q, k, v, o, lse, do, s, causal)
+    for b, h in ((0, 1), (B - 1, H - 1)):
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        for name, a, r in zip(("dQ", "dK", "dV"), (dq[sl], dk[sl], dv[sl]),
+                              O.backward(qc[sl], kc[sl], vc[sl], doc[sl], s, causal)):
+            close(a, r, dt, f"{name}[{b},{h}]")
+    torch.testing.assert_close(dv.double().sum(2), do.double().sum(2), rtol=0, atol=0.5)
