@@ -33,9 +33,9 @@
 #endif
 // 64-row halves per tile (one barrier per tile): the query tile of dK/dV and the key tile of dQ. At head
 // dim 128 (one wave per SIMD) 128-row tiles halve the barriers, which shortens dK/dV by a quarter; at 64
-// (two waves per SIMD) the tile height makes no measurable difference.
+// (two waves per SIMD) they shorten dQ by ~1% and change nothing measurable for dK/dV.
 #ifndef DQ64_HALVES
-#define DQ64_HALVES 1
+#define DQ64_HALVES 2
 #endif
 #ifndef DKDV64_HALVES
 #define DKDV64_HALVES 1
