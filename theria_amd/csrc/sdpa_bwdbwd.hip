@@ -15,10 +15,11 @@
 // (Gbar_S = P o (Gbar_P - s_row) with Gbar_P = E1 - r o dP and s_row = t - r z, rearranged so that a
 // single pass over the keys suffices for G_Q.)
 //
-// rows kernel: lane per query (transposed score tiles, as in the forward). One pass over 32-key tiles
-//   accumulates the four D-wide products of the G_Q expression plus r and t, writes G_Q, r, t.
-// cols kernel: lane per key (as in the backward). One pass over 32-query tiles with r, t, z, lse per
-//   row staged in LDS accumulates G_V and G_K in registers.
+// rows kernel: lane per query (transposed score tiles, as in the forward). One pass over key tiles (64
+//   keys as two 32-key subtiles for 16-bit inputs at head dim <= 64, else 32) accumulates the four D-wide products of the G_Q expression plus r and t, writes G_Q, r, t.
+// cols kernel: lane per key (as in the backward). One pass over query tiles (64 queries as two 32-query
+//   subtiles for 16-bit inputs at head dim <= 64, else 32) with r, t, z, lse per row staged in LDS
+//   accumulates G_V and G_K in registers.
 #include "dispatch.hpp"
 #include "sdpa_common.hpp"
 
@@ -29,9 +30,11 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
   constexpr int KC = MM::KC;
-  constexpr int NW = 4, BM = 32 * NW, BN = 32, NT = 64 * NW;
+  constexpr int NW = 4, BM = 32 * NW, NT = 64 * NW;
+  // keys per tile: two 32-key subtiles per pair of barriers where the registers allow (one wave per SIMD)
+  constexpr int BN = (DP == 128 || sizeof(T) == 4) ? 32 : 64;
   constexpr int PITCH = DP + 16 / (int)sizeof(T);
-  constexpr int NDT = DP / 32, NKC = DP / KC, NPC = 32 / KC;
+  constexpr int NDT = DP / 32, NKC = DP / KC, NPC = 32 / KC, NST = BN / 32;
   __shared__ __attribute__((aligned(16))) T sK[BN * PITCH];
   __shared__ __attribute__((aligned(16))) T sV[BN * PITCH];
   __shared__ __attribute__((aligned(16))) T sgK[BN * PITCH];
@@ -99,26 +102,29 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
     if (has_gv) gsgV.store(sgV, PITCH);
     __syncthreads();
     if (kt + 1 < nkt) prefetch(k0 + BN);
-    if (CAUSAL && k0 > q0w + 31) continue;
+#pragma unroll
+    for (int st = 0; st < NST; ++st) {
+    const int k0s = k0 + 32 * st;  // this 32-key subtile
+    if (CAUSAL && k0s > q0w + 31) continue;
 
     f32x16_t sc = zero16(), gm = zero16(), w = zero16(), dpz;
 #pragma unroll
     for (int r = 0; r < 16; ++r) dpz[r] = -z;
 #pragma unroll
     for (int c = 0; c < NKC; ++c) {
-      const F kfr = lds_cols<T, KLIN>(sK, PITCH, li, 0, c);
+      const F kfr = lds_cols<T, KLIN>(sK, PITCH, 32 * st + li, 0, c);
       sc = MM::mma(kfr, qf[c], sc);
-      dpz = MM::mma(lds_cols<T, KLIN>(sV, PITCH, li, 0, c), dof[c], dpz);
+      dpz = MM::mma(lds_cols<T, KLIN>(sV, PITCH, 32 * st + li, 0, c), dof[c], dpz);
       if (has_gq) gm = MM::mma(kfr, gqf[c], gm);
-      if (has_gk) gm = MM::mma(lds_cols<T, KLIN>(sgK, PITCH, li, 0, c), qf[c], gm);
-      if (has_gv) w = MM::mma(lds_cols<T, KLIN>(sgV, PITCH, li, 0, c), dof[c], w);
+      if (has_gk) gm = MM::mma(lds_cols<T, KLIN>(sgK, PITCH, 32 * st + li, 0, c), qf[c], gm);
+      if (has_gv) w = MM::mma(lds_cols<T, KLIN>(sgV, PITCH, 32 * st + li, 0, c), dof[c], w);
     }
-    const bool need_mask = (k0 + BN > s.M) || (CAUSAL && k0 + BN - 1 > q0w);
+    const bool need_mask = (k0s + 32 > s.M) || (CAUSAL && k0s + 31 > q0w);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       float pv = fast_exp2(fmaf(sc[r], c2, -moff));
       if (need_mask) {
-        const int key = k0 + acc_row(r, g);
+        const int key = k0s + acc_row(r, g);
         if (key >= s.M || (CAUSAL && key > myq)) pv = 0.f;
       }
       const float gam = s.scale * gm[r];
@@ -137,13 +143,14 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
       const F dsf = acc_frag<T>(dpz, cc);
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) {
-        const F kr = lds_rows<T, KACC>(sK, PITCH, 0, cc, dt * 32);
+        const F kr = lds_rows<T, KACC>(sK, PITCH, 32 * st, cc, dt * 32);
         x13[dt] = MM::mma(kr, pe1f, x13[dt]);
         x2[dt] = MM::mma(kr, dsf, x2[dt]);
         x4[dt] = MM::mma(kr, pf, x4[dt]);
-        if (has_gk) yk[dt] = MM::mma(lds_rows<T, KACC>(sgK, PITCH, 0, cc, dt * 32), dsf, yk[dt]);
+        if (has_gk) yk[dt] = MM::mma(lds_rows<T, KACC>(sgK, PITCH, 32 * st, cc, dt * 32), dsf, yk[dt]);
       }
     }
+    }  // subtile
   }
 
   const float rr = pair_sum(r_part), tt = pair_sum(t_part);
@@ -176,9 +183,11 @@ __global__ __launch_bounds__(256) void bwdbwd_cols_kernel(const BwdBwdParams p) 
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
   constexpr int KC = MM::KC;
-  constexpr int NW = 4, BN = 32 * NW, BM = 32, NT = 64 * NW;
+  constexpr int NW = 4, BN = 32 * NW, NT = 64 * NW;
+  // queries per tile: two 32-query subtiles per pair of barriers where the registers allow
+  constexpr int BM = (DP == 128 || sizeof(T) == 4) ? 32 : 64;
   constexpr int PITCH = DP + 16 / (int)sizeof(T);
-  constexpr int NDT = DP / 32, NKC = DP / KC, NPC = 32 / KC;
+  constexpr int NDT = DP / 32, NKC = DP / KC, NPC = 32 / KC, NSQ = BM / 32;
   __shared__ __attribute__((aligned(16))) T sQ[BM * PITCH];
   __shared__ __attribute__((aligned(16))) T sdO[BM * PITCH];
   __shared__ __attribute__((aligned(16))) T sgQ[BM * PITCH];
@@ -259,12 +268,16 @@ __global__ __launch_bounds__(256) void bwdbwd_cols_kernel(const BwdBwdParams p) 
     __syncthreads();
     if (it + 1 < nqt) prefetch(q0 + BM);
     if (CAUSAL && kw0 > q0 + BM - 1) continue;
+#pragma unroll
+    for (int sq = 0; sq < NSQ; ++sq) {
+    const int q0s = q0 + 32 * sq;  // this 32-query subtile
+    if (CAUSAL && kw0 > q0s + 31) continue;
 
     f32x16_t sc = zero16(), gm = zero16(), w = zero16(), dpz;
     f32x4_t l4[4], z4[4], r4[4], t4[4];
 #pragma unroll
     for (int qd = 0; qd < 4; ++qd) {
-      const int o = 8 * qd + 4 * g;
+      const int o = 32 * sq + 8 * qd + 4 * g;
       l4[qd] = *reinterpret_cast<const f32x4_t*>(sLse + o);
       z4[qd] = *reinterpret_cast<const f32x4_t*>(sZ + o);
       r4[qd] = *reinterpret_cast<const f32x4_t*>(sR + o);
@@ -274,22 +287,22 @@ __global__ __launch_bounds__(256) void bwdbwd_cols_kernel(const BwdBwdParams p) 
     }
 #pragma unroll
     for (int c = 0; c < NKC; ++c) {
-      const F qfr = lds_cols<T, KLIN>(sQ, PITCH, li, 0, c);
-      const F ofr = lds_cols<T, KLIN>(sdO, PITCH, li, 0, c);
+      const F qfr = lds_cols<T, KLIN>(sQ, PITCH, 32 * sq + li, 0, c);
+      const F ofr = lds_cols<T, KLIN>(sdO, PITCH, 32 * sq + li, 0, c);
       sc = MM::mma(qfr, kf[c], sc);
       dpz = MM::mma(ofr, vf[c], dpz);
-      if (has_gq) gm = MM::mma(lds_cols<T, KLIN>(sgQ, PITCH, li, 0, c), kf[c], gm);
+      if (has_gq) gm = MM::mma(lds_cols<T, KLIN>(sgQ, PITCH, 32 * sq + li, 0, c), kf[c], gm);
       if (has_gk) gm = MM::mma(qfr, gkf[c], gm);
       if (has_gv) w = MM::mma(ofr, gvf[c], w);
     }
-    const bool diag = CAUSAL && (kw0 + 31 > q0);
+    const bool diag = CAUSAL && (kw0 + 31 > q0s);
     f32x16_t gdp, gs;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int qd = r >> 2, e = r & 3;
       float pv = fast_exp2(fmaf(sc[r], c2, -l4[qd][e]));
       if (!kvalid) pv = 0.f;
-      if (diag && mykey > q0 + acc_row(r, g)) pv = 0.f;
+      if (diag && mykey > q0s + acc_row(r, g)) pv = 0.f;
       const float gam = s.scale * gm[r];
       const float ds = pv * dpz[r];
       const float e1 = fmaf(gam, dpz[r], w[r]);
@@ -304,11 +317,12 @@ __global__ __launch_bounds__(256) void bwdbwd_cols_kernel(const BwdBwdParams p) 
       const F dsf = acc_frag<T>(dpz, cc);
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) {
-        accV[dt] = MM::mma(gdpf, lds_rows<T, KACC>(sdO, PITCH, 0, cc, dt * 32), accV[dt]);
-        accK[dt] = MM::mma(gsf, lds_rows<T, KACC>(sQ, PITCH, 0, cc, dt * 32), accK[dt]);
-        if (has_gq) accK[dt] = MM::mma(dsf, lds_rows<T, KACC>(sgQ, PITCH, 0, cc, dt * 32), accK[dt]);
+        accV[dt] = MM::mma(gdpf, lds_rows<T, KACC>(sdO, PITCH, 32 * sq, cc, dt * 32), accV[dt]);
+        accK[dt] = MM::mma(gsf, lds_rows<T, KACC>(sQ, PITCH, 32 * sq, cc, dt * 32), accK[dt]);
+        if (has_gq) accK[dt] = MM::mma(dsf, lds_rows<T, KACC>(sgQ, PITCH, 32 * sq, cc, dt * 32), accK[dt]);
       }
     }
+    }  // subtile
   }
 
   T* OV = (T*)p.out_gv.p + b * p.out_gv.sb + h * p.out_gv.sh;
