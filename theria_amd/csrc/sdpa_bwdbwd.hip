@@ -20,25 +20,38 @@
 // cols kernel: lane per key (as in the backward). One pass over query tiles (64 queries as two 32-query
 //   subtiles for 16-bit inputs at head dim <= 64, else 32) with r, t, z, lse per row staged in LDS
 //   accumulates G_V and G_K in registers.
+#include <initializer_list>
+
 #include "dispatch.hpp"
 #include "sdpa_common.hpp"
+#include "sdpa_lds.hpp"
 
 namespace theria {
 
-template <typename T, int DP, bool CAUSAL>
+// DMA: 16-bit inputs with head dim exactly 64 or 128 and 16-byte-aligned rows. The K, V, gK, gV tiles are
+// then filled by LDS DMA into two sets of unpadded, XOR-swizzled buffers (sdpa_lds.hpp), one barrier per
+// tile with the next tile's copies in flight; otherwise they pass through registers into padded LDS rows
+// (two barriers per tile).
+template <typename T, int DP, bool CAUSAL, bool DMA>
 __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
   constexpr int KC = MM::KC;
   constexpr int NW = 4, BM = 32 * NW, NT = 64 * NW;
-  // keys per tile: two 32-key subtiles per pair of barriers where the registers allow (one wave per SIMD)
-  constexpr int BN = (DP == 128 || sizeof(T) == 4) ? 32 : 64;
+  // keys per tile: two 32-key subtiles per tile where the registers allow (one wave per SIMD)
+  constexpr int BN = (DP == 128 || sizeof(T) == 4 || DMA) ? 32 : 64;
   constexpr int PITCH = DP + 16 / (int)sizeof(T);
   constexpr int NDT = DP / 32, NKC = DP / KC, NPC = 32 / KC, NST = BN / 32;
-  __shared__ __attribute__((aligned(16))) T sK[BN * PITCH];
-  __shared__ __attribute__((aligned(16))) T sV[BN * PITCH];
-  __shared__ __attribute__((aligned(16))) T sgK[BN * PITCH];
-  __shared__ __attribute__((aligned(16))) T sgV[BN * PITCH];
+  constexpr int TB = DMA ? BN * DP * 2 : BN * PITCH * (int)sizeof(T);  // bytes per tile
+  constexpr int TB2 = DMA ? TB : 16;                                    // second set (DMA only)
+  __shared__ __attribute__((aligned(1024))) char sK0[TB];
+  __shared__ __attribute__((aligned(1024))) char sV0[TB];
+  __shared__ __attribute__((aligned(1024))) char sgK0[TB];
+  __shared__ __attribute__((aligned(1024))) char sgV0[TB];
+  __shared__ __attribute__((aligned(1024))) char sK1[TB2];
+  __shared__ __attribute__((aligned(1024))) char sV1[TB2];
+  __shared__ __attribute__((aligned(1024))) char sgK1[TB2];
+  __shared__ __attribute__((aligned(1024))) char sgV1[TB2];
 
   const Shape& s = p.s;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, li = lane & 31, g = lane >> 5;
@@ -85,72 +98,132 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
   int kend = s.M;
   if (CAUSAL) kend = min(s.M, qb * BM + BM);
   const int nkt = (kend + BN - 1) / BN;
-  TileStage<T, BN, DP, NT> gsK, gsV, gsgK, gsgV;
-  auto prefetch = [&](int k0) {
-    gsK.load(K, p.k.sr, k0, s.M, s.D, s.vec);
-    gsV.load(V, p.v.sr, k0, s.M, s.D, s.vec);
-    if (has_gk) gsgK.load(GK, p.gk.sr, k0, s.M, s.D, s.vec);
-    if (has_gv) gsgV.load(GV, p.gv.sr, k0, s.M, s.D, s.vec);
+
+  // Fragment reads: "cols" (k along a tile row, KLIN) and "rows" (k down the tile rows, KACC).
+  auto colsf = [&](const char* t, int row, int c) -> F {
+    if constexpr (DMA)
+      return swz_cols<T, DP>(t, row, c);
+    else
+      return lds_cols<T, KLIN>((const T*)t, PITCH, row, 0, c);
   };
-  if (nkt > 0) prefetch(0);
-  for (int kt = 0; kt < nkt; ++kt) {
+  auto rowsf = [&](const char* t, int kbase, int c, int col0) -> F {
+    if constexpr (DMA)
+      return swz_rows<T, DP>(t, kbase, c, col0);
+    else
+      return lds_rows<T, KACC>((const T*)t, PITCH, kbase, c, col0);
+  };
+
+  // The key tile kt held in (tK, tV, tgK, tgV), as 32-key subtiles.
+  auto compute = [&](int kt, const char* tK, const char* tV, const char* tgK, const char* tgV) {
     const int k0 = kt * BN;
-    __syncthreads();
-    gsK.store(sK, PITCH);
-    gsV.store(sV, PITCH);
-    if (has_gk) gsgK.store(sgK, PITCH);
-    if (has_gv) gsgV.store(sgV, PITCH);
-    __syncthreads();
-    if (kt + 1 < nkt) prefetch(k0 + BN);
 #pragma unroll
     for (int st = 0; st < NST; ++st) {
-    const int k0s = k0 + 32 * st;  // this 32-key subtile
-    if (CAUSAL && k0s > q0w + 31) continue;
+      const int k0s = k0 + 32 * st;  // this 32-key subtile
+      if (CAUSAL && k0s > q0w + 31) continue;
 
-    f32x16_t sc = zero16(), gm = zero16(), w = zero16(), dpz;
+      f32x16_t sc = zero16(), gm = zero16(), w = zero16(), dpz;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) dpz[r] = -z;
+      for (int r = 0; r < 16; ++r) dpz[r] = -z;
 #pragma unroll
-    for (int c = 0; c < NKC; ++c) {
-      const F kfr = lds_cols<T, KLIN>(sK, PITCH, 32 * st + li, 0, c);
-      sc = MM::mma(kfr, qf[c], sc);
-      dpz = MM::mma(lds_cols<T, KLIN>(sV, PITCH, 32 * st + li, 0, c), dof[c], dpz);
-      if (has_gq) gm = MM::mma(kfr, gqf[c], gm);
-      if (has_gk) gm = MM::mma(lds_cols<T, KLIN>(sgK, PITCH, 32 * st + li, 0, c), qf[c], gm);
-      if (has_gv) w = MM::mma(lds_cols<T, KLIN>(sgV, PITCH, 32 * st + li, 0, c), dof[c], w);
-    }
-    const bool need_mask = (k0s + 32 > s.M) || (CAUSAL && k0s + 31 > q0w);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float pv = fast_exp2(fmaf(sc[r], c2, -moff));
-      if (need_mask) {
-        const int key = k0s + acc_row(r, g);
-        if (key >= s.M || (CAUSAL && key > myq)) pv = 0.f;
+      for (int c = 0; c < NKC; ++c) {
+        const F kfr = colsf(tK, 32 * st + li, c);
+        sc = MM::mma(kfr, qf[c], sc);
+        dpz = MM::mma(colsf(tV, 32 * st + li, c), dof[c], dpz);
+        if (has_gq) gm = MM::mma(kfr, gqf[c], gm);
+        if (has_gk) gm = MM::mma(colsf(tgK, 32 * st + li, c), qf[c], gm);
+        if (has_gv) w = MM::mma(colsf(tgV, 32 * st + li, c), dof[c], w);
       }
-      const float gam = s.scale * gm[r];
-      const float e1 = fmaf(gam, dpz[r], w[r]);
-      const float pe1 = pv * e1;
-      r_part = fmaf(pv, gam, r_part);
-      t_part += pe1;
-      sc[r] = pv;
-      gm[r] = pe1;
-      dpz[r] = pv * dpz[r];  // dS
-    }
+      const bool need_mask = (k0s + 32 > s.M) || (CAUSAL && k0s + 31 > q0w);
 #pragma unroll
-    for (int cc = 0; cc < NPC; ++cc) {
-      const F pf = acc_frag<T>(sc, cc);
-      const F pe1f = acc_frag<T>(gm, cc);
-      const F dsf = acc_frag<T>(dpz, cc);
+      for (int r = 0; r < 16; ++r) {
+        float pv = fast_exp2(fmaf(sc[r], c2, -moff));
+        if (need_mask) {
+          const int key = k0s + acc_row(r, g);
+          if (key >= s.M || (CAUSAL && key > myq)) pv = 0.f;
+        }
+        const float gam = s.scale * gm[r];
+        const float e1 = fmaf(gam, dpz[r], w[r]);
+        const float pe1 = pv * e1;
+        r_part = fmaf(pv, gam, r_part);
+        t_part += pe1;
+        sc[r] = pv;
+        gm[r] = pe1;
+        dpz[r] = pv * dpz[r];  // dS
+      }
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-        const F kr = lds_rows<T, KACC>(sK, PITCH, 32 * st, cc, dt * 32);
-        x13[dt] = MM::mma(kr, pe1f, x13[dt]);
-        x2[dt] = MM::mma(kr, dsf, x2[dt]);
-        x4[dt] = MM::mma(kr, pf, x4[dt]);
-        if (has_gk) yk[dt] = MM::mma(lds_rows<T, KACC>(sgK, PITCH, 32 * st, cc, dt * 32), dsf, yk[dt]);
+      for (int cc = 0; cc < NPC; ++cc) {
+        const F pf = acc_frag<T>(sc, cc);
+        const F pe1f = acc_frag<T>(gm, cc);
+        const F dsf = acc_frag<T>(dpz, cc);
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+          const F kr = rowsf(tK, 32 * st, cc, dt * 32);
+          x13[dt] = MM::mma(kr, pe1f, x13[dt]);
+          x2[dt] = MM::mma(kr, dsf, x2[dt]);
+          x4[dt] = MM::mma(kr, pf, x4[dt]);
+          if (has_gk) yk[dt] = MM::mma(rowsf(tgK, 32 * st, cc, dt * 32), dsf, yk[dt]);
+        }
       }
     }
-    }  // subtile
+  };
+
+  if constexpr (DMA) {
+    using Dma = SwzDma<NW, DP>;
+    constexpr int NSLAB = BN / Dma::SLAB_ROWS;
+    static_assert(NSLAB * Dma::SLAB_ROWS == BN, "key tiles must be whole DMA slabs");
+    const Dma dma(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane);
+    // Byte offsets fit in 32 bits: the host only selects this path when each (batch, head) slab of K, V,
+    // gK and gV spans less than 2^31 bytes.
+    const uint32_t krs = (uint32_t)p.k.sr * 2, vrs = (uint32_t)p.v.sr * 2;
+    const uint32_t gkrs = has_gk ? (uint32_t)p.gk.sr * 2 : 0u, gvrs = has_gv ? (uint32_t)p.gv.sr * 2 : 0u;
+    const rsrc_t krsrc = make_rsrc(K, (uint32_t)s.M * krs), vrsrc = make_rsrc(V, (uint32_t)s.M * vrs);
+    const rsrc_t gkrsrc = make_rsrc(has_gk ? (const void*)GK : (const void*)K, (uint32_t)s.M * gkrs);
+    const rsrc_t gvrsrc = make_rsrc(has_gv ? (const void*)GV : (const void*)V, (uint32_t)s.M * gvrs);
+    auto issue = [&](int kt, char* tK, char* tV, char* tgK, char* tgV) {
+      const int k0 = kt * BN;
+      dma.template issue_clamped<NSLAB>(krsrc, krs, k0, s.M, tK);
+      dma.template issue_clamped<NSLAB>(vrsrc, vrs, k0, s.M, tV);
+      if (has_gk) dma.template issue_clamped<NSLAB>(gkrsrc, gkrs, k0, s.M, tgK);
+      if (has_gv) dma.template issue_clamped<NSLAB>(gvrsrc, gvrs, k0, s.M, tgV);
+    };
+    // Tile kt from the set c*; the next tile's copies go to the set n* (read in the previous step, which
+    // every wave has finished at the barrier).
+    auto step = [&](int kt, const char* cK, const char* cV, const char* cgK, const char* cgV, char* nK, char* nV,
+                    char* ngK, char* ngV) {
+      wait_vm_all();
+      __syncthreads();
+      if (kt + 1 < nkt) issue(kt + 1, nK, nV, ngK, ngV);
+      compute(kt, cK, cV, cgK, cgV);
+      __builtin_amdgcn_sched_barrier(0);  // keep the two unrolled steps apart (register pressure)
+    };
+    if (nkt > 0) {
+      issue(0, sK0, sV0, sgK0, sgV0);
+      int kt = 0;
+      for (; kt + 1 < nkt; kt += 2) {
+        step(kt, sK0, sV0, sgK0, sgV0, sK1, sV1, sgK1, sgV1);
+        step(kt + 1, sK1, sV1, sgK1, sgV1, sK0, sV0, sgK0, sgV0);
+      }
+      if (kt < nkt) step(kt, sK0, sV0, sgK0, sgV0, sK1, sV1, sgK1, sgV1);
+    }
+  } else {
+    TileStage<T, BN, DP, NT> gsK, gsV, gsgK, gsgV;
+    auto prefetch = [&](int k0) {
+      gsK.load(K, p.k.sr, k0, s.M, s.D, s.vec);
+      gsV.load(V, p.v.sr, k0, s.M, s.D, s.vec);
+      if (has_gk) gsgK.load(GK, p.gk.sr, k0, s.M, s.D, s.vec);
+      if (has_gv) gsgV.load(GV, p.gv.sr, k0, s.M, s.D, s.vec);
+    };
+    if (nkt > 0) prefetch(0);
+    for (int kt = 0; kt < nkt; ++kt) {
+      __syncthreads();
+      gsK.store((T*)sK0, PITCH);
+      gsV.store((T*)sV0, PITCH);
+      if (has_gk) gsgK.store((T*)sgK0, PITCH);
+      if (has_gv) gsgV.store((T*)sgV0, PITCH);
+      __syncthreads();
+      if (kt + 1 < nkt) prefetch((kt + 1) * BN);
+      compute(kt, sK0, sV0, sgK0, sgV0);
+    }
   }
 
   const float rr = pair_sum(r_part), tt = pair_sum(t_part);
@@ -178,23 +251,30 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
   }
 }
 
-template <typename T, int DP, bool CAUSAL>
+// DMA: as in the rows kernel, for the Q, dO, gQ tiles (the row terms are loaded two tiles ahead by the
+// first BM threads and written beside them one tile ahead).
+template <typename T, int DP, bool CAUSAL, bool DMA>
 __global__ __launch_bounds__(256) void bwdbwd_cols_kernel(const BwdBwdParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
   constexpr int KC = MM::KC;
   constexpr int NW = 4, BN = 32 * NW, NT = 64 * NW;
-  // queries per tile: two 32-query subtiles per pair of barriers where the registers allow
-  constexpr int BM = (DP == 128 || sizeof(T) == 4) ? 32 : 64;
+  // queries per tile: two 32-query subtiles per tile where the registers allow
+  constexpr int BM = (DP == 128 || sizeof(T) == 4 || DMA) ? 32 : 64;
   constexpr int PITCH = DP + 16 / (int)sizeof(T);
   constexpr int NDT = DP / 32, NKC = DP / KC, NPC = 32 / KC, NSQ = BM / 32;
-  __shared__ __attribute__((aligned(16))) T sQ[BM * PITCH];
-  __shared__ __attribute__((aligned(16))) T sdO[BM * PITCH];
-  __shared__ __attribute__((aligned(16))) T sgQ[BM * PITCH];
-  __shared__ __attribute__((aligned(16))) float sLse[BM];
-  __shared__ __attribute__((aligned(16))) float sZ[BM];
-  __shared__ __attribute__((aligned(16))) float sR[BM];
-  __shared__ __attribute__((aligned(16))) float sT[BM];
+  constexpr int TB = DMA ? BM * DP * 2 : BM * PITCH * (int)sizeof(T);  // bytes per tile
+  constexpr int TB2 = DMA ? TB : 16;                                    // second set (DMA only)
+  constexpr int RB2 = DMA ? 4 * BM : 4;
+  __shared__ __attribute__((aligned(1024))) char sQ0[TB];
+  __shared__ __attribute__((aligned(1024))) char sdO0[TB];
+  __shared__ __attribute__((aligned(1024))) char sgQ0[TB];
+  __shared__ __attribute__((aligned(1024))) char sQ1[TB2];
+  __shared__ __attribute__((aligned(1024))) char sdO1[TB2];
+  __shared__ __attribute__((aligned(1024))) char sgQ1[TB2];
+  // row terms [lse * log2(e) | delta | r | t] of a tile
+  __shared__ __attribute__((aligned(16))) float sRow0[4 * BM];
+  __shared__ __attribute__((aligned(16))) float sRow1[RB2];
 
   const Shape& s = p.s;
   const int tid = threadIdx.x;
@@ -236,93 +316,164 @@ __global__ __launch_bounds__(256) void bwdbwd_cols_kernel(const BwdBwdParams p) 
   const int nqt = s.T > qbeg ? (s.T - qbeg + BM - 1) / BM : 0;
   const int64_t rowbase = (int64_t)bh * s.T;
 
-  TileStage<T, BM, DP, NT> gsQ, gsO, gsgQ;
-  float pre[4] = {THERIA_INF, 0.f, 0.f, 0.f};
-  auto prefetch = [&](int q0) {
-    gsQ.load(Q, p.q.sr, q0, s.T, s.D, s.vec);
-    gsO.load(dO, p.dout.sr, q0, s.T, s.D, s.vec);
-    if (has_gq) gsgQ.load(GQ, p.gq.sr, q0, s.T, s.D, s.vec);
-    if (tid < BM) {
-      const int qq = q0 + tid;
+  auto colsf = [&](const char* t, int row, int c) -> F {
+    if constexpr (DMA)
+      return swz_cols<T, DP>(t, row, c);
+    else
+      return lds_cols<T, KLIN>((const T*)t, PITCH, row, 0, c);
+  };
+  auto rowsf = [&](const char* t, int kbase, int c, int col0) -> F {
+    if constexpr (DMA)
+      return swz_rows<T, DP>(t, kbase, c, col0);
+    else
+      return lds_rows<T, KACC>((const T*)t, PITCH, kbase, c, col0);
+  };
+
+  // Row terms of a tile for thread tid < BM, held raw (rows past the end: lse = +inf) and converted when
+  // stored: lse * log2(e) (+inf for rows past the end or without visible keys, so P = 0), delta, r, t.
+  float r_lse = THERIA_INF, r_z = 0.f, r_r = 0.f, r_t = 0.f;
+  auto load_rows = [&](int it) {
+    if (tid < BM && it < nqt) {
+      const int qq = qbeg + it * BM + tid;
       const bool ok = qq < s.T;
-      const float l2 = ok ? p.lse[rowbase + qq] * kLog2e : THERIA_INF;
-      pre[0] = l2 == -THERIA_INF ? THERIA_INF : l2;
-      pre[1] = ok ? p.delta[rowbase + qq] : 0.f;
-      pre[2] = ok ? p.r_row[rowbase + qq] : 0.f;
-      pre[3] = ok ? p.t_row[rowbase + qq] : 0.f;
+      r_lse = ok ? p.lse[rowbase + qq] : THERIA_INF;
+      r_z = ok ? p.delta[rowbase + qq] : 0.f;
+      r_r = ok ? p.r_row[rowbase + qq] : 0.f;
+      r_t = ok ? p.t_row[rowbase + qq] : 0.f;
     }
   };
-  if (nqt > 0) prefetch(qbeg);
-  for (int it = 0; it < nqt; ++it) {
-    const int q0 = qbeg + it * BM;
-    __syncthreads();
-    gsQ.store(sQ, PITCH);
-    gsO.store(sdO, PITCH);
-    if (has_gq) gsgQ.store(sgQ, PITCH);
+  auto store_rows = [&](float* sr) {
     if (tid < BM) {
-      sLse[tid] = pre[0];
-      sZ[tid] = pre[1];
-      sR[tid] = pre[2];
-      sT[tid] = pre[3];
+      sr[tid] = __builtin_isinf(r_lse) ? THERIA_INF : r_lse * kLog2e;
+      sr[BM + tid] = r_z;
+      sr[2 * BM + tid] = r_r;
+      sr[3 * BM + tid] = r_t;
     }
-    __syncthreads();
-    if (it + 1 < nqt) prefetch(q0 + BM);
-    if (CAUSAL && kw0 > q0 + BM - 1) continue;
+  };
+
+  // The query tile it held in (tQ, tO, tgQ) with its row terms in sr, as 32-query subtiles.
+  auto compute = [&](int it, const char* tQ, const char* tO, const char* tgQ, const float* sr) {
+    const int q0 = qbeg + it * BM;
+    if (CAUSAL && kw0 > q0 + BM - 1) return;
 #pragma unroll
     for (int sq = 0; sq < NSQ; ++sq) {
-    const int q0s = q0 + 32 * sq;  // this 32-query subtile
-    if (CAUSAL && kw0 > q0s + 31) continue;
+      const int q0s = q0 + 32 * sq;  // this 32-query subtile
+      if (CAUSAL && kw0 > q0s + 31) continue;
 
-    f32x16_t sc = zero16(), gm = zero16(), w = zero16(), dpz;
-    f32x4_t l4[4], z4[4], r4[4], t4[4];
+      f32x16_t sc = zero16(), gm = zero16(), w = zero16(), dpz;
+      f32x4_t l4[4], z4[4], r4[4], t4[4];
 #pragma unroll
-    for (int qd = 0; qd < 4; ++qd) {
-      const int o = 32 * sq + 8 * qd + 4 * g;
-      l4[qd] = *reinterpret_cast<const f32x4_t*>(sLse + o);
-      z4[qd] = *reinterpret_cast<const f32x4_t*>(sZ + o);
-      r4[qd] = *reinterpret_cast<const f32x4_t*>(sR + o);
-      t4[qd] = *reinterpret_cast<const f32x4_t*>(sT + o);
+      for (int qd = 0; qd < 4; ++qd) {
+        const int o = 32 * sq + 8 * qd + 4 * g;
+        l4[qd] = *reinterpret_cast<const f32x4_t*>(sr + o);
+        z4[qd] = *reinterpret_cast<const f32x4_t*>(sr + BM + o);
+        r4[qd] = *reinterpret_cast<const f32x4_t*>(sr + 2 * BM + o);
+        t4[qd] = *reinterpret_cast<const f32x4_t*>(sr + 3 * BM + o);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) dpz[4 * qd + e] = -z4[qd][e];
-    }
+        for (int e = 0; e < 4; ++e) dpz[4 * qd + e] = -z4[qd][e];
+      }
 #pragma unroll
-    for (int c = 0; c < NKC; ++c) {
-      const F qfr = lds_cols<T, KLIN>(sQ, PITCH, 32 * sq + li, 0, c);
-      const F ofr = lds_cols<T, KLIN>(sdO, PITCH, 32 * sq + li, 0, c);
-      sc = MM::mma(qfr, kf[c], sc);
-      dpz = MM::mma(ofr, vf[c], dpz);
-      if (has_gq) gm = MM::mma(lds_cols<T, KLIN>(sgQ, PITCH, 32 * sq + li, 0, c), kf[c], gm);
-      if (has_gk) gm = MM::mma(qfr, gkf[c], gm);
-      if (has_gv) w = MM::mma(ofr, gvf[c], w);
-    }
-    const bool diag = CAUSAL && (kw0 + 31 > q0s);
-    f32x16_t gdp, gs;
+      for (int c = 0; c < NKC; ++c) {
+        const F qfr = colsf(tQ, 32 * sq + li, c);
+        const F ofr = colsf(tO, 32 * sq + li, c);
+        sc = MM::mma(qfr, kf[c], sc);
+        dpz = MM::mma(ofr, vf[c], dpz);
+        if (has_gq) gm = MM::mma(colsf(tgQ, 32 * sq + li, c), kf[c], gm);
+        if (has_gk) gm = MM::mma(qfr, gkf[c], gm);
+        if (has_gv) w = MM::mma(ofr, gvf[c], w);
+      }
+      const bool diag = CAUSAL && (kw0 + 31 > q0s);
+      f32x16_t gdp, gs;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int qd = r >> 2, e = r & 3;
-      float pv = fast_exp2(fmaf(sc[r], c2, -l4[qd][e]));
-      if (!kvalid) pv = 0.f;
-      if (diag && mykey > q0s + acc_row(r, g)) pv = 0.f;
-      const float gam = s.scale * gm[r];
-      const float ds = pv * dpz[r];
-      const float e1 = fmaf(gam, dpz[r], w[r]);
-      gdp[r] = pv * (gam - r4[qd][e]);
-      gs[r] = pv * e1 - r4[qd][e] * ds - t4[qd][e] * pv;
-      dpz[r] = ds;
-    }
+      for (int r = 0; r < 16; ++r) {
+        const int qd = r >> 2, e = r & 3;
+        float pv = fast_exp2(fmaf(sc[r], c2, -l4[qd][e]));
+        if (!kvalid) pv = 0.f;
+        if (diag && mykey > q0s + acc_row(r, g)) pv = 0.f;
+        const float gam = s.scale * gm[r];
+        const float ds = pv * dpz[r];
+        const float e1 = fmaf(gam, dpz[r], w[r]);
+        gdp[r] = pv * (gam - r4[qd][e]);
+        gs[r] = pv * e1 - r4[qd][e] * ds - t4[qd][e] * pv;
+        dpz[r] = ds;
+      }
 #pragma unroll
-    for (int cc = 0; cc < NPC; ++cc) {
-      const F gdpf = acc_frag<T>(gdp, cc);
-      const F gsf = acc_frag<T>(gs, cc);
-      const F dsf = acc_frag<T>(dpz, cc);
+      for (int cc = 0; cc < NPC; ++cc) {
+        const F gdpf = acc_frag<T>(gdp, cc);
+        const F gsf = acc_frag<T>(gs, cc);
+        const F dsf = acc_frag<T>(dpz, cc);
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-        accV[dt] = MM::mma(gdpf, lds_rows<T, KACC>(sdO, PITCH, 32 * sq, cc, dt * 32), accV[dt]);
-        accK[dt] = MM::mma(gsf, lds_rows<T, KACC>(sQ, PITCH, 32 * sq, cc, dt * 32), accK[dt]);
-        if (has_gq) accK[dt] = MM::mma(dsf, lds_rows<T, KACC>(sgQ, PITCH, 32 * sq, cc, dt * 32), accK[dt]);
+        for (int dt = 0; dt < NDT; ++dt) {
+          accV[dt] = MM::mma(gdpf, rowsf(tO, 32 * sq, cc, dt * 32), accV[dt]);
+          accK[dt] = MM::mma(gsf, rowsf(tQ, 32 * sq, cc, dt * 32), accK[dt]);
+          if (has_gq) accK[dt] = MM::mma(dsf, rowsf(tgQ, 32 * sq, cc, dt * 32), accK[dt]);
+        }
       }
     }
-    }  // subtile
+  };
+
+  if constexpr (DMA) {
+    using Dma = SwzDma<NW, DP>;
+    constexpr int NSLAB = BM / Dma::SLAB_ROWS;
+    static_assert(NSLAB * Dma::SLAB_ROWS == BM, "query tiles must be whole DMA slabs");
+    const Dma dma(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane);
+    // Byte offsets fit in 32 bits: the host only selects this path when each (batch, head) slab of Q, dO
+    // and gQ spans less than 2^31 bytes.
+    const uint32_t qrs = (uint32_t)p.q.sr * 2, ors = (uint32_t)p.dout.sr * 2;
+    const uint32_t gqrs = has_gq ? (uint32_t)p.gq.sr * 2 : 0u;
+    const rsrc_t qrsrc = make_rsrc(Q, (uint32_t)s.T * qrs), orsrc = make_rsrc(dO, (uint32_t)s.T * ors);
+    const rsrc_t gqrsrc = make_rsrc(has_gq ? (const void*)GQ : (const void*)Q, (uint32_t)s.T * gqrs);
+    auto issue = [&](int it, char* tQ, char* tO, char* tgQ) {
+      const int q0 = qbeg + it * BM;
+      dma.template issue_clamped<NSLAB>(qrsrc, qrs, q0, s.T, tQ);
+      dma.template issue_clamped<NSLAB>(orsrc, ors, q0, s.T, tO);
+      if (has_gq) dma.template issue_clamped<NSLAB>(gqrsrc, gqrs, q0, s.T, tgQ);
+    };
+    auto step = [&](int it, const char* cQ, const char* cO, const char* cgQ, const float* cR, char* nQ, char* nO,
+                    char* ngQ, float* nR) {
+      wait_vm_all();
+      __syncthreads();  // tile it (and its row terms) visible; the other set (tile it-1) is free
+      if (it + 1 < nqt) {
+        issue(it + 1, nQ, nO, ngQ);
+        store_rows(nR);
+        load_rows(it + 2);
+      }
+      compute(it, cQ, cO, cgQ, cR);
+      __builtin_amdgcn_sched_barrier(0);  // keep the two unrolled steps apart (register pressure)
+    };
+    if (nqt > 0) {
+      issue(0, sQ0, sdO0, sgQ0);
+      load_rows(0);
+      wait_vm_all();
+      store_rows(sRow0);
+      load_rows(1);
+      int it = 0;
+      for (; it + 1 < nqt; it += 2) {
+        step(it, sQ0, sdO0, sgQ0, sRow0, sQ1, sdO1, sgQ1, sRow1);
+        step(it + 1, sQ1, sdO1, sgQ1, sRow1, sQ0, sdO0, sgQ0, sRow0);
+      }
+      if (it < nqt) step(it, sQ0, sdO0, sgQ0, sRow0, sQ1, sdO1, sgQ1, sRow1);
+    }
+  } else {
+    TileStage<T, BM, DP, NT> gsQ, gsO, gsgQ;
+    auto prefetch = [&](int it) {
+      const int q0 = qbeg + it * BM;
+      gsQ.load(Q, p.q.sr, q0, s.T, s.D, s.vec);
+      gsO.load(dO, p.dout.sr, q0, s.T, s.D, s.vec);
+      if (has_gq) gsgQ.load(GQ, p.gq.sr, q0, s.T, s.D, s.vec);
+      load_rows(it);
+    };
+    if (nqt > 0) prefetch(0);
+    for (int it = 0; it < nqt; ++it) {
+      __syncthreads();
+      gsQ.store((T*)sQ0, PITCH);
+      gsO.store((T*)sdO0, PITCH);
+      if (has_gq) gsgQ.store((T*)sgQ0, PITCH);
+      store_rows(sRow0);
+      __syncthreads();
+      if (it + 1 < nqt) prefetch(it + 1);
+      compute(it, sQ0, sdO0, sgQ0, sRow0);
+    }
   }
 
   T* OV = (T*)p.out_gv.p + b * p.out_gv.sb + h * p.out_gv.sh;
@@ -343,13 +494,29 @@ __global__ __launch_bounds__(256) void bwdbwd_cols_kernel(const BwdBwdParams p) 
   }
 }
 
+// The LDS-DMA tile path applies: 16-bit inputs, head dim exactly DP (64 or 128), 16-byte-aligned views,
+// and every (batch, head) slab of the streamed tensors (rows x row stride) below 2^31 bytes.
+template <typename T, int DP>
+static bool dma_tiles_ok(const BwdBwdParams& p, int64_t rows, std::initializer_list<const View*> streamed) {
+  if (!(sizeof(T) == 2 && (DP == 64 || DP == 128) && p.s.D == DP && p.s.vec)) return false;
+  for (const View* v : streamed)
+    if (v->p && rows * v->sr * 2 >= (int64_t(1) << 31)) return false;
+  return true;
+}
+
 struct RowsLauncher {
   template <typename T, int DP, bool CAUSAL>
   static hipError_t run(const BwdBwdParams& p, hipStream_t st) {
     const int nqb = (p.s.T + 127) / 128;
     const int64_t nblk = (int64_t)nqb * p.s.B * p.s.H;
     if (nblk == 0) return hipSuccess;
-    hipLaunchKernelGGL((bwdbwd_rows_kernel<T, DP, CAUSAL>), dim3((unsigned)nblk), dim3(256), 0, st, p);
+    if constexpr (sizeof(T) == 2 && (DP == 64 || DP == 128)) {
+      if (dma_tiles_ok<T, DP>(p, p.s.M, {&p.k, &p.v, &p.gk, &p.gv})) {
+        hipLaunchKernelGGL((bwdbwd_rows_kernel<T, DP, CAUSAL, true>), dim3((unsigned)nblk), dim3(256), 0, st, p);
+        return hipGetLastError();
+      }
+    }
+    hipLaunchKernelGGL((bwdbwd_rows_kernel<T, DP, CAUSAL, false>), dim3((unsigned)nblk), dim3(256), 0, st, p);
     return hipGetLastError();
   }
 };
@@ -360,7 +527,13 @@ struct ColsLauncher {
     const int nkb = (p.s.M + 127) / 128;
     const int64_t nblk = (int64_t)nkb * p.s.B * p.s.H;
     if (nblk == 0) return hipSuccess;
-    hipLaunchKernelGGL((bwdbwd_cols_kernel<T, DP, CAUSAL>), dim3((unsigned)nblk), dim3(256), 0, st, p);
+    if constexpr (sizeof(T) == 2 && (DP == 64 || DP == 128)) {
+      if (dma_tiles_ok<T, DP>(p, p.s.T, {&p.q, &p.dout, &p.gq})) {
+        hipLaunchKernelGGL((bwdbwd_cols_kernel<T, DP, CAUSAL, true>), dim3((unsigned)nblk), dim3(256), 0, st, p);
+        return hipGetLastError();
+      }
+    }
+    hipLaunchKernelGGL((bwdbwd_cols_kernel<T, DP, CAUSAL, false>), dim3((unsigned)nblk), dim3(256), 0, st, p);
     return hipGetLastError();
   }
 };
