@@ -20,12 +20,18 @@
 // operands); per 64-key tile, K, tk, V, tv are staged in LDS and the three output products
 // (P o G) V, P tv and (if needed) P V accumulate lane-per-query as V^T (.)^T, with V^T / tv^T
 // fragments from the LDS transpose read. A single pass: c_i is folded in at the end.
+#include <initializer_list>
+
 #include "dispatch.hpp"
 #include "sdpa_common.hpp"
+#include "sdpa_lds.hpp"
 
 namespace theria {
 
-template <typename T, int DP, bool CAUSAL, bool HAS_O>
+// DMA: 16-bit inputs with head dim exactly 64 or 128 and 16-byte-aligned rows. The K, tK, V, tV tiles are
+// then filled by LDS DMA into two sets of unpadded, XOR-swizzled buffers (sdpa_lds.hpp), one barrier per
+// tile with the next tile's copies in flight; otherwise they pass through registers into padded LDS rows.
+template <typename T, int DP, bool CAUSAL, bool HAS_O, bool DMA>
 __global__ __launch_bounds__(256) void jvp_kernel(const JvpParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
@@ -34,10 +40,16 @@ __global__ __launch_bounds__(256) void jvp_kernel(const JvpParams p) {
   constexpr int BN = (DP == 128 || sizeof(T) == 4) ? 32 : 64;  // keys per tile (register budget)
   constexpr int PITCH = DP + 16 / (int)sizeof(T);
   constexpr int NDT = DP / 32, NKC = DP / KC, NPC = 32 / KC, NST = BN / 32;
-  __shared__ __attribute__((aligned(16))) T sK[BN * PITCH];
-  __shared__ __attribute__((aligned(16))) T sV[BN * PITCH];
-  __shared__ __attribute__((aligned(16))) T stK[BN * PITCH];
-  __shared__ __attribute__((aligned(16))) T stV[BN * PITCH];
+  constexpr int TB = DMA ? BN * DP * 2 : BN * PITCH * (int)sizeof(T);  // bytes per tile
+  constexpr int TB2 = DMA ? TB : 16;                                    // second set (DMA only)
+  __shared__ __attribute__((aligned(1024))) char sK0[TB];
+  __shared__ __attribute__((aligned(1024))) char sV0[TB];
+  __shared__ __attribute__((aligned(1024))) char stK0[TB];
+  __shared__ __attribute__((aligned(1024))) char stV0[TB];
+  __shared__ __attribute__((aligned(1024))) char sK1[TB2];
+  __shared__ __attribute__((aligned(1024))) char sV1[TB2];
+  __shared__ __attribute__((aligned(1024))) char stK1[TB2];
+  __shared__ __attribute__((aligned(1024))) char stV1[TB2];
 
   const Shape& s = p.s;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, li = lane & 31, g = lane >> 5;
@@ -82,24 +94,23 @@ __global__ __launch_bounds__(256) void jvp_kernel(const JvpParams p) {
   int kend = s.M;
   if (CAUSAL) kend = min(s.M, qb * BM + BM);
   const int nkt = (kend + BN - 1) / BN;
-  TileStage<T, BN, DP, NT> gK, gV, gtK, gtV;
-  auto prefetch = [&](int k0) {
-    gK.load(K, p.k.sr, k0, s.M, s.D, s.vec);
-    gV.load(V, p.v.sr, k0, s.M, s.D, s.vec);
-    if (has_tk) gtK.load(TK, p.tk.sr, k0, s.M, s.D, s.vec);
-    if (has_tv) gtV.load(TV, p.tv.sr, k0, s.M, s.D, s.vec);
+  auto colsf = [&](const char* t, int row, int c) -> F {
+    if constexpr (DMA)
+      return swz_cols<T, DP>(t, row, c);
+    else
+      return lds_cols<T, KLIN>((const T*)t, PITCH, row, 0, c);
   };
-  if (nkt > 0) prefetch(0);
-  for (int kt = 0; kt < nkt; ++kt) {
+  auto rowsf = [&](const char* t, int kbase, int c, int col0) -> F {
+    if constexpr (DMA)
+      return swz_rows<T, DP>(t, kbase, c, col0);
+    else
+      return lds_rows<T, KACC>((const T*)t, PITCH, kbase, c, col0);
+  };
+
+  // The key tile kt held in (tK, tV, ttK, ttV).
+  auto compute = [&](int kt, const char* tK, const char* tV, const char* ttK, const char* ttV) {
     const int k0 = kt * BN;
-    __syncthreads();
-    gK.store(sK, PITCH);
-    gV.store(sV, PITCH);
-    if (has_tk) gtK.store(stK, PITCH);
-    if (has_tv) gtV.store(stV, PITCH);
-    __syncthreads();
-    if (kt + 1 < nkt) prefetch(k0 + BN);
-    if (CAUSAL && k0 > q0w + 31) continue;
+    if (CAUSAL && k0 > q0w + 31) return;
 
     f32x16_t sc[NST], gm[NST];
 #pragma unroll
@@ -108,10 +119,10 @@ __global__ __launch_bounds__(256) void jvp_kernel(const JvpParams p) {
       gm[t] = zero16();
 #pragma unroll
       for (int c = 0; c < NKC; ++c) {
-        const F kfr = lds_cols<T, KLIN>(sK, PITCH, t * 32 + li, 0, c);
+        const F kfr = colsf(tK, t * 32 + li, c);
         sc[t] = MM::mma(kfr, qf[c], sc[t]);
         if (has_tq) gm[t] = MM::mma(kfr, tqf[c], gm[t]);
-        if (has_tk) gm[t] = MM::mma(lds_cols<T, KLIN>(stK, PITCH, t * 32 + li, 0, c), qf[c], gm[t]);
+        if (has_tk) gm[t] = MM::mma(colsf(ttK, t * 32 + li, c), qf[c], gm[t]);
       }
     }
     const bool need_mask = (k0 + BN > s.M) || (CAUSAL && k0 + BN - 1 > q0w);
@@ -144,14 +155,73 @@ __global__ __launch_bounds__(256) void jvp_kernel(const JvpParams p) {
         }
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
-          const F vfr = lds_rows<T, KACC>(sV, PITCH, t * 32, cc, dt * 32);
+          const F vfr = rowsf(tV, t * 32, cc, dt * 32);
           accA[dt] = MM::mma(vfr, pgf, accA[dt]);
           if (SPLIT) accA[dt] = MM::mma(vfr, pgf_lo, accA[dt]);
           if (REBUILD) accO[dt] = MM::mma(vfr, pf, accO[dt]);
           if (REBUILD && SPLIT) accO[dt] = MM::mma(vfr, pf_lo, accO[dt]);
-          if (has_tv) accC[dt] = MM::mma(lds_rows<T, KACC>(stV, PITCH, t * 32, cc, dt * 32), pf, accC[dt]);
+          if (has_tv) accC[dt] = MM::mma(rowsf(ttV, t * 32, cc, dt * 32), pf, accC[dt]);
         }
       }
+  };
+
+  if constexpr (DMA) {
+    using Dma = SwzDma<NW, DP>;
+    constexpr int NSLAB = BN / Dma::SLAB_ROWS;
+    static_assert(NSLAB * Dma::SLAB_ROWS == BN, "key tiles must be whole DMA slabs");
+    const Dma dma(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane);
+    // Byte offsets fit in 32 bits: the host only selects this path when each (batch, head) slab of K, V,
+    // tK and tV spans less than 2^31 bytes.
+    const uint32_t krs = (uint32_t)p.k.sr * 2, vrs = (uint32_t)p.v.sr * 2;
+    const uint32_t tkrs = has_tk ? (uint32_t)p.tk.sr * 2 : 0u, tvrs = has_tv ? (uint32_t)p.tv.sr * 2 : 0u;
+    const rsrc_t krsrc = make_rsrc(K, (uint32_t)s.M * krs), vrsrc = make_rsrc(V, (uint32_t)s.M * vrs);
+    const rsrc_t tkrsrc = make_rsrc(has_tk ? (const void*)TK : (const void*)K, (uint32_t)s.M * tkrs);
+    const rsrc_t tvrsrc = make_rsrc(has_tv ? (const void*)TV : (const void*)V, (uint32_t)s.M * tvrs);
+    auto issue = [&](int kt, char* tK, char* tV, char* ttK, char* ttV) {
+      const int k0 = kt * BN;
+      dma.template issue_clamped<NSLAB>(krsrc, krs, k0, s.M, tK);
+      dma.template issue_clamped<NSLAB>(vrsrc, vrs, k0, s.M, tV);
+      if (has_tk) dma.template issue_clamped<NSLAB>(tkrsrc, tkrs, k0, s.M, ttK);
+      if (has_tv) dma.template issue_clamped<NSLAB>(tvrsrc, tvrs, k0, s.M, ttV);
+    };
+    // Tile kt from the set c*; the next tile's copies go to the set n* (read in the previous step, which
+    // every wave has finished at the barrier).
+    auto step = [&](int kt, const char* cK, const char* cV, const char* ctK, const char* ctV, char* nK, char* nV,
+                    char* ntK, char* ntV) {
+      wait_vm_all();
+      __syncthreads();
+      if (kt + 1 < nkt) issue(kt + 1, nK, nV, ntK, ntV);
+      compute(kt, cK, cV, ctK, ctV);
+      __builtin_amdgcn_sched_barrier(0);  // keep the two unrolled steps apart (register pressure)
+    };
+    if (nkt > 0) {
+      issue(0, sK0, sV0, stK0, stV0);
+      int kt = 0;
+      for (; kt + 1 < nkt; kt += 2) {
+        step(kt, sK0, sV0, stK0, stV0, sK1, sV1, stK1, stV1);
+        step(kt + 1, sK1, sV1, stK1, stV1, sK0, sV0, stK0, stV0);
+      }
+      if (kt < nkt) step(kt, sK0, sV0, stK0, stV0, sK1, sV1, stK1, stV1);
+    }
+  } else {
+    TileStage<T, BN, DP, NT> gK, gV, gtK, gtV;
+    auto prefetch = [&](int k0) {
+      gK.load(K, p.k.sr, k0, s.M, s.D, s.vec);
+      gV.load(V, p.v.sr, k0, s.M, s.D, s.vec);
+      if (has_tk) gtK.load(TK, p.tk.sr, k0, s.M, s.D, s.vec);
+      if (has_tv) gtV.load(TV, p.tv.sr, k0, s.M, s.D, s.vec);
+    };
+    if (nkt > 0) prefetch(0);
+    for (int kt = 0; kt < nkt; ++kt) {
+      __syncthreads();
+      gK.store((T*)sK0, PITCH);
+      gV.store((T*)sV0, PITCH);
+      if (has_tk) gtK.store((T*)stK0, PITCH);
+      if (has_tv) gtV.store((T*)stV0, PITCH);
+      __syncthreads();
+      if (kt + 1 < nkt) prefetch((kt + 1) * BN);
+      compute(kt, sK0, sV0, stK0, stV0);
+    }
   }
 
   // 16-bit: P / L with L = sum_j P_j, i.e. every term below is divided by L (and O by L as well)
@@ -194,7 +264,17 @@ struct JvpLauncher {
     const int nqb = (p.s.T + 127) / 128;
     const int64_t nblk = (int64_t)nqb * p.s.B * p.s.H;
     if (nblk == 0) return hipSuccess;
-    hipLaunchKernelGGL((jvp_kernel<T, DP, CAUSAL, HAS_O>), dim3((unsigned)nblk), dim3(256), 0, st, p);
+    if constexpr (sizeof(T) == 2 && (DP == 64 || DP == 128)) {
+      // LDS-DMA tiles: head dim exactly DP, 16-byte-aligned views, each streamed (batch, head) slab < 2^31 bytes
+      bool ok = p.s.D == DP && p.s.vec;
+      for (const View* v : {&p.k, &p.v, &p.tk, &p.tv})
+        if (v->p && (int64_t)p.s.M * v->sr * 2 >= (int64_t(1) << 31)) ok = false;
+      if (ok) {
+        hipLaunchKernelGGL((jvp_kernel<T, DP, CAUSAL, HAS_O, true>), dim3((unsigned)nblk), dim3(256), 0, st, p);
+        return hipGetLastError();
+      }
+    }
+    hipLaunchKernelGGL((jvp_kernel<T, DP, CAUSAL, HAS_O, false>), dim3((unsigned)nblk), dim3(256), 0, st, p);
     return hipGetLastError();
   }
 };
