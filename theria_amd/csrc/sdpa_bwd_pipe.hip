@@ -574,12 +574,17 @@ bool launch_dkdv_pipe(const DkdvParams& p, hipStream_t st, hipError_t* err) {
     // Eight-wave workgroups (both waves of a SIMD in one workgroup) whenever they still fill every CU:
     // two independent four-wave workgroups on a CU progress unevenly (the older one is issued first), and
     // with two rounds of them the CUs that finish early idle through a ~10% tail at config 2.
-    const int64_t nblk8 = blocks(8);
-    if (nblk8 >= device_cu_count())
+    // Grids that would leave CUs without a four-wave workgroup use two-wave ones (twice as many; per
+    // workgroup they are slower, so only then).
+    const int64_t nblk8 = blocks(8), cus = device_cu_count();
+    if (nblk8 >= cus)
       hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, 8, 64, true, 2, DKDV64_HALVES>), dim3((unsigned)nblk8), dim3(64 * 8), 0,
                          st, p);
-    else
+    else if (blocks(4) >= cus)
       hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, 4, 64, true, 2, DKDV64_HALVES>), dim3((unsigned)blocks(4)), dim3(64 * 4),
+                         0, st, p);
+    else
+      hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, 2, 64, true, 2, DKDV64_HALVES>), dim3((unsigned)blocks(2)), dim3(64 * 2),
                          0, st, p);
   } else {
     constexpr int NW = DKDV_PIPE_NW;

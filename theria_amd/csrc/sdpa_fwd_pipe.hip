@@ -30,15 +30,16 @@
 
 namespace theria {
 
-template <typename T, bool CAUSAL, bool STATS, int NW, int DP>
+// QT query tiles of 32 per wave: two at DP = 64 without the causal mask, where each K / V^T fragment then
+// feeds two MFMAs, unless the grid would then leave CUs without two waves per SIMD; one at DP = 128, where
+// the registers would not allow two, and one with the causal mask, whose paired blocks need the smaller
+// block to fill the GPU.
+template <typename T, bool CAUSAL, bool STATS, int NW, int DP, int QT>
 __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
-  // QT query tiles of 32 per wave (two at DP = 64, where each K / V^T fragment then feeds two MFMAs;
-  // one at DP = 128, where the registers would not allow two, and one with the causal mask, whose paired
-  // blocks need the smaller block to fill the GPU); NKC k-chunks of 16 and NDT output tiles of 32
-  // across the head dim.
-  constexpr int QT = (DP == 64 && !CAUSAL) ? 2 : 1, NKC = DP / 16, NDT = DP / 32;
+  // NKC k-chunks of 16 and NDT output tiles of 32 across the head dim.
+  constexpr int NKC = DP / 16, NDT = DP / 32;
   constexpr int BM = 32 * NW * QT, BN = 64, TILE = BN * 2 * DP;
   // Separate arrays (not one [2][TILE] array) so that the compiler can tell the tile being read from the
   // tile being filled and does not wait for the DMA in flight before every LDS read.
@@ -408,26 +409,35 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
   }  // pass
 }
 
-template <typename T, bool CAUSAL, int NW, int DP>
+template <typename T, bool CAUSAL, int NW, int DP, int QT>
 static void fwd_pipe_go(const FwdParams& p, int64_t nblk, hipStream_t st) {
   if (p.row_max || p.row_sum)
-    hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, true, NW, DP>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p);
+    hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, true, NW, DP, QT>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p);
   else
-    hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, false, NW, DP>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p);
+    hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, false, NW, DP, QT>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p);
 }
 
 template <typename T, bool CAUSAL, int DP>
 static void fwd_pipe_launch(const FwdParams& p, hipStream_t st) {
   constexpr int QT = (DP == 64 && !CAUSAL) ? 2 : 1;
   const int64_t bh = (int64_t)p.s.B * p.s.H;
+  const int64_t cus = device_cu_count();
   // workgroups per (batch, head): query blocks, or (causal) pairs of mirrored query blocks
   auto units = [](int64_t nqb) { return CAUSAL ? (nqb + 1) / 2 : nqb; };
   const int64_t nblk8 = units((p.s.T + 256 * QT - 1) / (256 * QT)) * bh;
   const int64_t nblk4 = units((p.s.T + 128 * QT - 1) / (128 * QT)) * bh;
-  if (nblk8 >= device_cu_count())
-    fwd_pipe_go<T, CAUSAL, 8, DP>(p, nblk8, st);
-  else
-    fwd_pipe_go<T, CAUSAL, 4, DP>(p, nblk4, st);
+  if (nblk8 >= cus) {
+    fwd_pipe_go<T, CAUSAL, 8, DP, QT>(p, nblk8, st);
+    return;
+  }
+  if constexpr (QT == 2) {
+    // Too few query blocks to give every CU two four-wave workgroups: one query tile per wave doubles them.
+    if (nblk4 < 2 * cus) {
+      fwd_pipe_go<T, CAUSAL, 4, DP, 1>(p, units((p.s.T + 127) / 128) * bh, st);
+      return;
+    }
+  }
+  fwd_pipe_go<T, CAUSAL, 4, DP, QT>(p, nblk4, st);
 }
 
 // Launch if the pipelined kernel covers this problem (16-bit, head dim 64 or 128, vector access, more
