@@ -48,6 +48,8 @@ def _args():
     ap.add_argument("--warmup", type=int, default=1000)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU-baseline sample")
     ap.add_argument("--no-extras", action="store_true", help="only the config-2 line (for profiling runs)")
+    ap.add_argument("--extras", default="c2_fp16,c3,c4,c5",
+                    help="comma-separated subset of the other configs to run (c2_fp16, c3, c4, c5)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (for profiling runs)")
     ap.add_argument("--copy-calibration", action="store_true", help="run a plain copy of known size (PMC scaling)")
     return ap.parse_args()
@@ -419,7 +421,10 @@ def main() -> int:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     if not args.no_extras:
         extra = {}
+        wanted = {x.strip() for x in args.extras.split(",") if x.strip()}
         for name, fn in (("c2_fp16", extras_c2_fp16), ("c3", extras_c3), ("c4", extras_c4), ("c5", extras_c5)):
+            if name not in wanted:
+                continue
             try:
                 extra[name] = fn()
             except Exception as exc:  # an extra must not hide the headline line
