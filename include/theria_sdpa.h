@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define THERIA_SDPA_ABI_VERSION 3
+#define THERIA_SDPA_ABI_VERSION 4
 
 enum theria_dtype { THERIA_DTYPE_F32 = 0, THERIA_DTYPE_F16 = 1, THERIA_DTYPE_BF16 = 2 };
 enum theria_status { THERIA_OK = 0, THERIA_ERR_CONTRACT = 1, THERIA_ERR_HIP = 2 };
@@ -124,7 +124,10 @@ int theria_sdpa_jvp(const theria_sdpa_problem_t* p, const theria_tensor_t* q, co
  * The reference has no kernel for this: its HVP is a finite difference of the VJP
  * (theria/attention/hvp_utils.py:30-49) or autograd-in-backward (theria/autograd/sdpa_custom_function.py:32-53).
  * delta is the row term written by theria_sdpa_bwd. Any cotangent may have data == NULL (zero).
- * row_ws is a caller-owned float32 workspace of 2*batch*heads*tq elements.
+ * For 16-bit inputs the row term is recomputed from lse as dO . sum_j P_ij V_j in float32 (into the
+ * workspace), because delta from the 16-bit O differs from sum_j P_ij dP_ij by the rounding of O, which the
+ * second-order terms amplify where they cancel; delta is then not read.
+ * row_ws is a caller-owned float32 workspace of 3*batch*heads*tq elements.
  */
 int theria_sdpa_bwd_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
                         const theria_tensor_t* v, const theria_tensor_t* o, const theria_tensor_t* dout,

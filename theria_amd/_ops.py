@@ -280,7 +280,7 @@ def bwd_bwd(q, k, v, o, do, lse, delta, gq, gk, gv, scale: float, causal: bool):
     out_k = torch.empty((B, H, M, D), dtype=q.dtype, device=dev)
     out_v = torch.empty((B, H, M, D), dtype=q.dtype, device=dev)
     out_do = torch.empty((B, H, T, D), dtype=q.dtype, device=dev)
-    ws = torch.empty((2 * B * H * T,), dtype=torch.float32, device=dev)
+    ws = torch.empty((3 * B * H * T,), dtype=torch.float32, device=dev)
     lib = _lib.load()
     prob = _problem(q, k, scale, causal)
     with _OnDevice(dev):

@@ -385,6 +385,21 @@ THERIA_API int theria_sdpa_bwd_bwd(const theria_sdpa_problem_t* p, const theria_
   bp.delta = delta;
   bp.r_row = row_ws;
   bp.t_row = row_ws + nrows;
+  if (s.dtype != THERIA_DTYPE_F32 && s.T > 0) {
+    // 16-bit inputs: the row term consistent with P(lse), sum_j P_ij dP_ij = dO_i . sum_j P_ij V_j in float32
+    // (mode 1 of the forward kernel), instead of dO . O with the 16-bit O.
+    theria::FwdParams fp{};
+    fp.s = s;
+    fp.q = cv(q);
+    fp.k = cv(k);
+    fp.v = cv(v);
+    fp.dout = cv(dout);
+    fp.lse = const_cast<float*>(lse);
+    fp.delta = row_ws + 2 * nrows;
+    const int rc = hip_status(theria::launch_fwd(fp, 1, st), "theria_sdpa_bwd_bwd (row term)");
+    if (rc != THERIA_OK) return rc;
+    bp.delta = fp.delta;
+  }
   bp.out_gq = mv(out_gq);
   bp.out_gk = mv(out_gk);
   bp.out_gv = mv(out_gv);
