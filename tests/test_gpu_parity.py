@@ -76,6 +76,13 @@ CASES = [
     (torch.float16, 2, 1, 390, 390, 128, True),
     (torch.bfloat16, 1, 2, 200, 330, 64, True),
     (torch.bfloat16, 1, 1, 330, 200, 64, True),
+    # head dims below the pipelined kernels' 64 / 128 (multiples of 8): zero-filled columns past D
+    (torch.bfloat16, 1, 2, 300, 260, 80, False),
+    (torch.float16, 1, 2, 200, 200, 96, True),
+    (torch.bfloat16, 2, 1, 257, 257, 48, True),
+    (torch.bfloat16, 1, 1, 333, 129, 120, False),
+    (torch.float16, 1, 2, 150, 170, 40, False),
+    (torch.bfloat16, 1, 2, 260, 260, 72, True),
 ]
 
 

@@ -1,9 +1,10 @@
-// Pipelined dQ and dK/dV passes of the SDPA backward for 16-bit inputs with head_dim 64 or 128 on gfx950.
+// Pipelined dQ and dK/dV passes of the SDPA backward for 16-bit inputs on gfx950 (head dim a multiple of 8
+// in 40..128, computed at DP = 64 or 128 with the columns past D zero).
 //
 // dkdv_pipe_kernel has the contract of dkdv_kernel (sdpa_bwd.hip): dV = P^T dO and dK = scale dS^T Q with
 // P = exp(scale Q K^T - lse) rebuilt from the saved row statistic and dS = P o (dO V^T - delta)
 // (reference theria/attention/triton_sdpa_backward.py:106-266 and 269-462). It is used when the head
-// dim is 64 or 128 and every view allows 16-byte access; the general kernel covers the rest.
+// dim qualifies and every view allows 16-byte access; the general kernel covers the rest.
 //
 // Work decomposition: one workgroup = NW waves, each owning 32 keys (K and V fragments in registers,
 // dK and dV accumulated in registers); the workgroup streams the query tiles (64 or 128 rows) of its head.
@@ -112,8 +113,8 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
     F kf[NKC], vf[NKC];
 #pragma unroll
     for (int c = 0; c < NKC; ++c) {
-      kf[c] = scaled_frag<T>(gload_frag<T>(K, p.k.sr, kw0 + li, s.M, c, DP, true), c2);
-      vf[c] = gload_frag<T>(V, p.v.sr, kw0 + li, s.M, c, DP, true);
+      kf[c] = scaled_frag<T>(gload_frag<T>(K, p.k.sr, kw0 + li, s.M, c, s.D, true), c2);
+      vf[c] = gload_frag<T>(V, p.v.sr, kw0 + li, s.M, c, s.D, true);
     }
     f32x16_t dv[NDT], dk[NDT];
 #pragma unroll
@@ -130,7 +131,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
     const int ifull = CAUSAL ? min(nqt, (key0 + BN - 1 - qbeg + BM - 1) / BM) : 0;
     const int fend = (key0 + BN <= s.M) ? max(ifull, min(nqt, (s.T - qbeg) / BM)) : ifull;
 
-    const Dma dma(wave, lane);
+    const Dma dma(wave, lane, s.D / 8);  // head dims below DP: zero-filled chunks past D
     const uint32_t qrs = (uint32_t)p.q.sr * 2, ors = (uint32_t)p.dout.sr * 2;
     const rsrc_t qrsrc = make_rsrc(Q, (uint32_t)s.T * qrs);
     const rsrc_t orsrc = make_rsrc(dO, (uint32_t)s.T * ors);
@@ -296,7 +297,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int key = kw0 + acc_row(r, g);
-        if (key < s.M) {
+        if (key < s.M && d < s.D) {
           DV[(int64_t)key * p.dv.sr + d] = (T)dv[dt][r];
           if (DK) DK[(int64_t)key * p.dk.sr + d] = (T)(dk[dt][r] * s.scale);
         }
@@ -356,8 +357,8 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
     F qf[NKC], of[NKC];
 #pragma unroll
     for (int c = 0; c < NKC; ++c) {
-      qf[c] = gload_frag<T>(Q, p.q.sr, myq, s.T, c, DP, true);
-      of[c] = gload_frag<T>(dO, p.dout.sr, myq, s.T, c, DP, true);
+      qf[c] = gload_frag<T>(Q, p.q.sr, myq, s.T, c, s.D, true);
+      of[c] = gload_frag<T>(dO, p.dout.sr, myq, s.T, c, s.D, true);
     }
     const float l2 = qvalid ? p.lse[rowbase + myq] * kLog2e : THERIA_INF;
     const float lse2 = l2 == -THERIA_INF ? THERIA_INF : l2;  // a row without visible keys has P = 0
@@ -369,6 +370,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
 #pragma unroll
         for (int c = 0; c < NKC; ++c) {
           const int col = c * 16 + 8 * g;
+          if (col >= s.D) continue;  // head dim below DP (a multiple of 8): whole 8-column groups only
           const int64_t off = (int64_t)myq * p.o.sr + col;
           if (p.o_f32) {
             const float* Op = (const float*)p.o.p + b * p.o.sb + h * p.o.sh + off;
@@ -406,7 +408,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
     int nfull = s.M / BN;
     if (CAUSAL) nfull = min(nfull, qb * BM / BN);
 
-    const Dma dma(wave, lane);
+    const Dma dma(wave, lane, s.D / 8);  // head dims below DP: zero-filled chunks past D
     const uint32_t krs = (uint32_t)p.k.sr * 2, vrs = (uint32_t)p.v.sr * 2;
     const rsrc_t krsrc = make_rsrc(K, (uint32_t)s.M * krs);
     const rsrc_t vrsrc = make_rsrc(V, (uint32_t)s.M * vrs);
@@ -519,16 +521,20 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
         for (int qd = 0; qd < 4; ++qd) {
           const int d0 = dt * 32 + 8 * qd + 4 * g;
           const f32x16_t& a = acc[dt];
-          store4<T>(DQ, p.dq.sr, myq, d0, DP, a[4 * qd] * s.scale, a[4 * qd + 1] * s.scale, a[4 * qd + 2] * s.scale,
+          store4<T>(DQ, p.dq.sr, myq, d0, s.D, a[4 * qd] * s.scale, a[4 * qd + 1] * s.scale, a[4 * qd + 2] * s.scale,
                     a[4 * qd + 3] * s.scale, true);
         }
     }
   }  // pass
 }
 
+// Head dims the pipelined kernels take: a multiple of 8 in 40..64 (run at DP = 64) or 72..128 (DP = 128);
+// columns past D are zero in every tile and are never stored.
+static bool pipe_head_dim(const Shape& s) { return s.vec && s.D % 8 == 0 && (s.dp == 64 || s.dp == 128) && s.D > 32; }
+
 template <typename T, bool CAUSAL>
 bool launch_dq_pipe(const DqParams& p, hipStream_t st, hipError_t* err) {
-  if (!((p.s.D == 64 || p.s.D == 128) && p.s.vec)) return false;
+  if (!pipe_head_dim(p.s)) return false;
   // 32-bit byte offsets inside each (batch, head) slab of K and V
   if ((int64_t)p.s.M * p.k.sr * 2 >= (int64_t(1) << 31) || (int64_t)p.s.M * p.v.sr * 2 >= (int64_t(1) << 31)) return false;
   constexpr int NW = DQ_PIPE_NW;
@@ -538,7 +544,7 @@ bool launch_dq_pipe(const DqParams& p, hipStream_t st, hipError_t* err) {
     *err = hipSuccess;
     return true;
   }
-  if (p.s.D == 64)
+  if (p.s.dp == 64)
     hipLaunchKernelGGL((dq_pipe_kernel<T, CAUSAL, NW, 64, true, 2, DQ64_HALVES>), dim3((unsigned)nblk), dim3(64 * NW), 0, st,
                        p);
   else
@@ -557,20 +563,20 @@ template bool launch_dq_pipe<_Float16, true>(const DqParams&, hipStream_t, hipEr
 // both wanted); returns false otherwise.
 template <typename T, bool CAUSAL>
 bool launch_dkdv_pipe(const DkdvParams& p, hipStream_t st, hipError_t* err) {
-  if (!((p.s.D == 64 || p.s.D == 128) && p.s.vec && !p.dv_only)) return false;
+  if (!(pipe_head_dim(p.s) && !p.dv_only)) return false;
   // 32-bit byte offsets inside each (batch, head) slab of Q and dO
   if ((int64_t)p.s.T * p.q.sr * 2 >= (int64_t(1) << 31) || (int64_t)p.s.T * p.dout.sr * 2 >= (int64_t(1) << 31))
     return false;
   // workgroups of nw waves (32 keys each): key blocks, or (causal head dim 64) pairs of mirrored blocks
   auto blocks = [&](int nw) {
     const int64_t nkb = (p.s.M + 32 * nw - 1) / (32 * nw);
-    return ((CAUSAL && p.s.D == 64) ? (nkb + 1) / 2 : nkb) * p.s.B * p.s.H;
+    return ((CAUSAL && p.s.dp == 64) ? (nkb + 1) / 2 : nkb) * p.s.B * p.s.H;
   };
   if (blocks(4) == 0) {
     *err = hipSuccess;
     return true;
   }
-  if (p.s.D == 64) {
+  if (p.s.dp == 64) {
     // Eight-wave workgroups (both waves of a SIMD in one workgroup) whenever they still fill every CU:
     // two independent four-wave workgroups on a CU progress unevenly (the older one is issued first), and
     // with two rounds of them the CUs that finish early idle through a ~10% tail at config 2.

@@ -1,8 +1,9 @@
-// Pipelined SDPA forward for 16-bit inputs with head_dim 64 or 128 on gfx950.
+// Pipelined SDPA forward for 16-bit inputs on gfx950.
 //
 // Same contract as fwd_kernel mode 0 (sdpa_fwd.hip): O = softmax(scale Q K^T) V with lse and the
 // optional reference statistics (m, l) (reference theria/attention/triton_qk.py:242-304). It is used when
-// the head dim is exactly 64 or 128, every view allows 16-byte access and there are more than 128 queries.
+// the head dim is a multiple of 8 in 40..128 (computed at DP = 64 or 128, the columns past D zero),
+// every view allows 16-byte access and there are more than 128 queries.
 //
 // Work decomposition: one workgroup = NW waves x QT tiles of 32 queries (QT = 2 at head dim 64, 1 at
 // 128); keys in tiles of 64. Scores are
@@ -81,7 +82,7 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
     if (CAUSAL) nfull = min(nfull, qb * BM / BN);
 
     using Dma = SwzDma<NW, DP>;
-    const Dma dma(wave, lane);
+    const Dma dma(wave, lane, s.D / 8);  // head dims below DP: zero-filled chunks past D
     constexpr int NSLAB = BN / Dma::SLAB_ROWS;
     // Byte offsets fit in 32 bits: the host only selects this kernel when every (batch, head) slab of K
     // and V spans less than 2^31 bytes.
@@ -100,7 +101,7 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
 #pragma unroll
     for (int j = 0; j < QT; ++j)
 #pragma unroll
-      for (int c = 0; c < NKC; ++c) qf[j][c] = gload_frag<T>(Q, p.q.sr, q0w + 32 * j + li, s.T, c, DP, true);
+      for (int c = 0; c < NKC; ++c) qf[j][c] = gload_frag<T>(Q, p.q.sr, q0w + 32 * j + li, s.T, c, s.D, true);
 
     f32x16_t o[QT][NDT];
     float m_use[QT], l_part[QT], m_max[QT];
@@ -390,10 +391,10 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
             const float a2 = o[j][dt][4 * qd + 2] * inv, a3 = o[j][dt][4 * qd + 3] * inv;
             if (p.o_f32) {
               float* O = (float*)p.o.p + b * p.o.sb + h * p.o.sh;
-              store4<float>(O, p.o.sr, myq, d0, DP, a0, a1, a2, a3, true);
+              store4<float>(O, p.o.sr, myq, d0, s.D, a0, a1, a2, a3, true);
             } else {
               T* O = (T*)p.o.p + b * p.o.sb + h * p.o.sh;
-              store4<T>(O, p.o.sr, myq, d0, DP, a0, a1, a2, a3, true);
+              store4<T>(O, p.o.sr, myq, d0, s.D, a0, a1, a2, a3, true);
             }
           }
         if (g == 0) {
@@ -440,18 +441,18 @@ static void fwd_pipe_launch(const FwdParams& p, hipStream_t st) {
   fwd_pipe_go<T, CAUSAL, 4, DP, QT>(p, nblk4, st);
 }
 
-// Launch if the pipelined kernel covers this problem (16-bit, head dim 64 or 128, vector access, more
-// than 128 queries); returns false otherwise.
+// Launch if the pipelined kernel covers this problem (16-bit, head dim a multiple of 8 in 40..64 (run at
+// DP = 64) or 72..128 (DP = 128), vector access, more than 128 queries); returns false otherwise.
 template <typename T, bool CAUSAL>
 bool launch_fwd_pipe(const FwdParams& p, hipStream_t st, hipError_t* err) {
-  if (!((p.s.D == 64 || p.s.D == 128) && p.s.vec && p.s.T > 128)) return false;
+  if (!(p.s.vec && p.s.D % 8 == 0 && p.s.D > 32 && (p.s.dp == 64 || p.s.dp == 128) && p.s.T > 128)) return false;
   // 32-bit byte offsets inside each (batch, head) slab of K and V
   if ((int64_t)p.s.M * p.k.sr * 2 >= (int64_t(1) << 31) || (int64_t)p.s.M * p.v.sr * 2 >= (int64_t(1) << 31)) return false;
   if ((int64_t)p.s.B * p.s.H == 0) {
     *err = hipSuccess;
     return true;
   }
-  if (p.s.D == 64)
+  if (p.s.dp == 64)
     fwd_pipe_launch<T, CAUSAL, 64>(p, st);
   else
     fwd_pipe_launch<T, CAUSAL, 128>(p, st);

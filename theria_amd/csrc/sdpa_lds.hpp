@@ -65,7 +65,10 @@ __device__ __forceinline__ void dma16(rsrc_t rsrc, char* lds, uint32_t voffset, 
 // fills RPW = 1024 / RB rows; wave w fills rows RPW w .. RPW w + RPW - 1 of every slab of RPW * NW rows
 // (bytes [1024 w, 1024 w + 1024) of it). `wave` must be wave-uniform (an SGPR value), since it selects
 // the LDS destination. The copies are buffer_load_dwordx4 ... lds with a per-lane 32-bit offset and a
-// wave-uniform offset for the tile, so no 64-bit address math is needed.
+// wave-uniform offset for the tile, so no 64-bit address math is needed. Rows shorter than DP (a head dim
+// D < DP, a multiple of 8) fill only their nck = D / 8 leading chunks from memory: the lanes of the other
+// chunks use an offset past the end of the buffer (kOutOfRange, >= 2^31 > any buffer the host admits),
+// for which the buffer load returns zero, so the tile's columns D .. DP - 1 read as zero.
 template <int NW, int DP>
 struct SwzDma {
   static constexpr int RB = 2 * DP;            // bytes per row
@@ -76,16 +79,22 @@ struct SwzDma {
   // A lane derives its swizzle from its row inside the slab; that equals the swizzle of the tile row
   // only if slabs start on multiples of the swizzle's period (16 rows).
   static_assert(SLAB_ROWS % 16 == 0, "LDS DMA slabs must span a multiple of 16 rows (more waves per workgroup)");
-  int row;    // row of the slab filled by this lane
-  int chunk;  // logical 16-byte chunk this lane fetches
-  int dst;    // byte offset of this wave's piece in a slab
+  static constexpr uint32_t kOutOfRange = 0x80000000u;
+  int row;     // row of the slab filled by this lane
+  int chunk;   // logical 16-byte chunk this lane fetches
+  int dst;     // byte offset of this wave's piece in a slab
+  bool valid;  // the chunk lies inside the row (chunk < nck)
 
-  __device__ __forceinline__ SwzDma(int wave, int lane)
-      : row(RPW * wave + lane / CPR), chunk((lane % CPR) ^ swz<DP>(RPW * wave + lane / CPR)), dst(1024 * wave) {}
+  __device__ __forceinline__ SwzDma(int wave, int lane, int nck = CPR)
+      : row(RPW * wave + lane / CPR),
+        chunk((lane % CPR) ^ swz<DP>(RPW * wave + lane / CPR)),
+        dst(1024 * wave),
+        valid(chunk < nck) {}
 
-  // Byte offset, from the tile's first row, of what this lane fetches for slab i.
+  // Byte offset, from the tile's first row, of what this lane fetches for slab i (out of range for a chunk
+  // past the row; the tile offset added to it stays below 2^32).
   __device__ __forceinline__ uint32_t lane_offset(uint32_t rs_bytes, int i) const {
-    return (uint32_t)(SLAB_ROWS * i + row) * rs_bytes + chunk * 16;
+    return valid ? (uint32_t)(SLAB_ROWS * i + row) * rs_bytes + chunk * 16 : kOutOfRange;
   }
 
   // Rows [r0, r0 + SLAB_ROWS * NSLAB) all in range: tile_off = r0 * rs_bytes (wave-uniform), off[i] =
@@ -104,7 +113,7 @@ struct SwzDma {
 #pragma unroll
     for (int i = 0; i < NSLAB; ++i) {
       const uint32_t r = (uint32_t)min(r0 + SLAB_ROWS * i + row, nrows - 1);
-      dma16(rsrc, tile + SLAB_BYTES * i + dst, r * rs_bytes + chunk * 16, 0);
+      dma16(rsrc, tile + SLAB_BYTES * i + dst, valid ? r * rs_bytes + chunk * 16 : kOutOfRange, 0);
     }
   }
 };
