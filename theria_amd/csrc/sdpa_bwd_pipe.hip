@@ -63,7 +63,9 @@
 
 namespace theria {
 
-template <typename T, bool CAUSAL, int NW, int DP, bool OVERLAP, int WPS, int HALVES>
+// FD: the head dim is DP itself (compile-time bounds); otherwise the runtime head dim s.D < DP bounds the
+// loads, stores and DMA chunks (both kernels).
+template <typename T, bool CAUSAL, int NW, int DP, bool OVERLAP, int WPS, int HALVES, bool FD>
 __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
@@ -113,8 +115,8 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
     F kf[NKC], vf[NKC];
 #pragma unroll
     for (int c = 0; c < NKC; ++c) {
-      kf[c] = scaled_frag<T>(gload_frag<T>(K, p.k.sr, kw0 + li, s.M, c, s.D, true), c2);
-      vf[c] = gload_frag<T>(V, p.v.sr, kw0 + li, s.M, c, s.D, true);
+      kf[c] = scaled_frag<T>(gload_frag8<T>(K, p.k.sr, kw0 + li, s.M, c, FD ? DP : s.D), c2);
+      vf[c] = gload_frag8<T>(V, p.v.sr, kw0 + li, s.M, c, FD ? DP : s.D);
     }
     f32x16_t dv[NDT], dk[NDT];
 #pragma unroll
@@ -131,7 +133,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
     const int ifull = CAUSAL ? min(nqt, (key0 + BN - 1 - qbeg + BM - 1) / BM) : 0;
     const int fend = (key0 + BN <= s.M) ? max(ifull, min(nqt, (s.T - qbeg) / BM)) : ifull;
 
-    const Dma dma(wave, lane, s.D / 8);  // head dims below DP: zero-filled chunks past D
+    const Dma dma(wave, lane, FD ? DP / 8 : s.D / 8);  // head dims below DP: zero-filled chunks past D
     const uint32_t qrs = (uint32_t)p.q.sr * 2, ors = (uint32_t)p.dout.sr * 2;
     const rsrc_t qrsrc = make_rsrc(Q, (uint32_t)s.T * qrs);
     const rsrc_t orsrc = make_rsrc(dO, (uint32_t)s.T * ors);
@@ -297,7 +299,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int key = kw0 + acc_row(r, g);
-        if (key < s.M && d < s.D) {
+        if (key < s.M && (FD || d < s.D)) {
           DV[(int64_t)key * p.dv.sr + d] = (T)dv[dt][r];
           if (DK) DK[(int64_t)key * p.dk.sr + d] = (T)(dk[dt][r] * s.scale);
         }
@@ -315,7 +317,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
 // 32-key subtiles:
 //   S, dP of subtile 0 | S, dP of subtile 1 with exp / dS of subtile 0
 //   | dQ of subtile 0 with exp / dS of subtile 1 | dQ of subtile 1.
-template <typename T, bool CAUSAL, int NW, int DP, bool OVERLAP, int WPS, int HALVES>
+template <typename T, bool CAUSAL, int NW, int DP, bool OVERLAP, int WPS, int HALVES, bool FD>
 __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
@@ -357,8 +359,8 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
     F qf[NKC], of[NKC];
 #pragma unroll
     for (int c = 0; c < NKC; ++c) {
-      qf[c] = gload_frag<T>(Q, p.q.sr, myq, s.T, c, s.D, true);
-      of[c] = gload_frag<T>(dO, p.dout.sr, myq, s.T, c, s.D, true);
+      qf[c] = gload_frag8<T>(Q, p.q.sr, myq, s.T, c, FD ? DP : s.D);
+      of[c] = gload_frag8<T>(dO, p.dout.sr, myq, s.T, c, FD ? DP : s.D);
     }
     const float l2 = qvalid ? p.lse[rowbase + myq] * kLog2e : THERIA_INF;
     const float lse2 = l2 == -THERIA_INF ? THERIA_INF : l2;  // a row without visible keys has P = 0
@@ -370,7 +372,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
 #pragma unroll
         for (int c = 0; c < NKC; ++c) {
           const int col = c * 16 + 8 * g;
-          if (col >= s.D) continue;  // head dim below DP (a multiple of 8): whole 8-column groups only
+          if (!FD && col >= s.D) continue;  // head dim below DP (a multiple of 8): whole 8-column groups only
           const int64_t off = (int64_t)myq * p.o.sr + col;
           if (p.o_f32) {
             const float* Op = (const float*)p.o.p + b * p.o.sb + h * p.o.sh + off;
@@ -408,7 +410,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
     int nfull = s.M / BN;
     if (CAUSAL) nfull = min(nfull, qb * BM / BN);
 
-    const Dma dma(wave, lane, s.D / 8);  // head dims below DP: zero-filled chunks past D
+    const Dma dma(wave, lane, FD ? DP / 8 : s.D / 8);  // head dims below DP: zero-filled chunks past D
     const uint32_t krs = (uint32_t)p.k.sr * 2, vrs = (uint32_t)p.v.sr * 2;
     const rsrc_t krsrc = make_rsrc(K, (uint32_t)s.M * krs);
     const rsrc_t vrsrc = make_rsrc(V, (uint32_t)s.M * vrs);
@@ -521,11 +523,31 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
         for (int qd = 0; qd < 4; ++qd) {
           const int d0 = dt * 32 + 8 * qd + 4 * g;
           const f32x16_t& a = acc[dt];
-          store4<T>(DQ, p.dq.sr, myq, d0, s.D, a[4 * qd] * s.scale, a[4 * qd + 1] * s.scale, a[4 * qd + 2] * s.scale,
-                    a[4 * qd + 3] * s.scale, true);
+          store4_8<T>(DQ, p.dq.sr, myq, d0, FD ? DP : s.D, a[4 * qd] * s.scale, a[4 * qd + 1] * s.scale, a[4 * qd + 2] * s.scale,
+                      a[4 * qd + 3] * s.scale);
         }
     }
   }  // pass
+}
+
+// Launches with FD = (head dim == DP).
+template <typename T, bool CAUSAL, int NW, int DP, bool OVERLAP, int WPS, int HALVES>
+static void dq_go(const DqParams& p, int64_t nblk, hipStream_t st) {
+  if (p.s.D == DP)
+    hipLaunchKernelGGL((dq_pipe_kernel<T, CAUSAL, NW, DP, OVERLAP, WPS, HALVES, true>), dim3((unsigned)nblk), dim3(64 * NW),
+                       0, st, p);
+  else
+    hipLaunchKernelGGL((dq_pipe_kernel<T, CAUSAL, NW, DP, OVERLAP, WPS, HALVES, false>), dim3((unsigned)nblk), dim3(64 * NW),
+                       0, st, p);
+}
+template <typename T, bool CAUSAL, int NW, int DP, bool OVERLAP, int WPS, int HALVES>
+static void dkdv_go(const DkdvParams& p, int64_t nblk, hipStream_t st) {
+  if (p.s.D == DP)
+    hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, NW, DP, OVERLAP, WPS, HALVES, true>), dim3((unsigned)nblk),
+                       dim3(64 * NW), 0, st, p);
+  else
+    hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, NW, DP, OVERLAP, WPS, HALVES, false>), dim3((unsigned)nblk),
+                       dim3(64 * NW), 0, st, p);
 }
 
 // Head dims the pipelined kernels take: a multiple of 8 in 40..64 (run at DP = 64) or 72..128 (DP = 128);
@@ -545,11 +567,9 @@ bool launch_dq_pipe(const DqParams& p, hipStream_t st, hipError_t* err) {
     return true;
   }
   if (p.s.dp == 64)
-    hipLaunchKernelGGL((dq_pipe_kernel<T, CAUSAL, NW, 64, true, 2, DQ64_HALVES>), dim3((unsigned)nblk), dim3(64 * NW), 0, st,
-                       p);
+    dq_go<T, CAUSAL, NW, 64, true, 2, DQ64_HALVES>(p, nblk, st);
   else
-    hipLaunchKernelGGL((dq_pipe_kernel<T, CAUSAL, NW, 128, DQ128_OVERLAP, DQ128_WPS, DQ128_HALVES>), dim3((unsigned)nblk),
-                       dim3(64 * NW), 0, st, p);
+    dq_go<T, CAUSAL, NW, 128, DQ128_OVERLAP, DQ128_WPS, DQ128_HALVES>(p, nblk, st);
   *err = hipGetLastError();
   return true;
 }
@@ -559,8 +579,8 @@ template bool launch_dq_pipe<__bf16, true>(const DqParams&, hipStream_t, hipErro
 template bool launch_dq_pipe<_Float16, false>(const DqParams&, hipStream_t, hipError_t*);
 template bool launch_dq_pipe<_Float16, true>(const DqParams&, hipStream_t, hipError_t*);
 
-// Launch if the pipelined kernel covers this problem (16-bit, head dim 64, vector access, dK and dV
-// both wanted); returns false otherwise.
+// Launch if the pipelined kernel covers this problem (16-bit, a head dim pipe_head_dim takes, vector
+// access, dK and dV both wanted); returns false otherwise.
 template <typename T, bool CAUSAL>
 bool launch_dkdv_pipe(const DkdvParams& p, hipStream_t st, hipError_t* err) {
   if (!(pipe_head_dim(p.s) && !p.dv_only)) return false;
@@ -584,18 +604,14 @@ bool launch_dkdv_pipe(const DkdvParams& p, hipStream_t st, hipError_t* err) {
     // workgroup they are slower, so only then).
     const int64_t nblk8 = blocks(8), cus = device_cu_count();
     if (nblk8 >= cus)
-      hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, 8, 64, true, 2, DKDV64_HALVES>), dim3((unsigned)nblk8), dim3(64 * 8), 0,
-                         st, p);
+      dkdv_go<T, CAUSAL, 8, 64, true, 2, DKDV64_HALVES>(p, nblk8, st);
     else if (blocks(4) >= cus)
-      hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, 4, 64, true, 2, DKDV64_HALVES>), dim3((unsigned)blocks(4)), dim3(64 * 4),
-                         0, st, p);
+      dkdv_go<T, CAUSAL, 4, 64, true, 2, DKDV64_HALVES>(p, blocks(4), st);
     else
-      hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, 2, 64, true, 2, DKDV64_HALVES>), dim3((unsigned)blocks(2)), dim3(64 * 2),
-                         0, st, p);
+      dkdv_go<T, CAUSAL, 2, 64, true, 2, DKDV64_HALVES>(p, blocks(2), st);
   } else {
     constexpr int NW = DKDV_PIPE_NW;
-    hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, NW, 128, DKDV128_OVERLAP, DKDV128_WPS, DKDV128_HALVES>),
-                       dim3((unsigned)blocks(NW)), dim3(64 * NW), 0, st, p);
+    dkdv_go<T, CAUSAL, NW, 128, DKDV128_OVERLAP, DKDV128_WPS, DKDV128_HALVES>(p, blocks(NW), st);
   }
   *err = hipGetLastError();
   return true;

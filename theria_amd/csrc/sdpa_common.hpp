@@ -335,6 +335,32 @@ __device__ __forceinline__ void store4(T* base, int64_t rs, int row, int col, in
 }
 
 // Load 4 consecutive elements as float (zero beyond D).
+// The same for 16-bit T and a head dim D that is a multiple of 8, with 16-byte aligned rows: a lane's 8
+// columns are all in range or all out of range, so one vector load (or zero) covers them.
+template <typename T>
+__device__ __forceinline__ typename Mfma<T>::frag_t gload_frag8(const T* base, int64_t rs, int row, int nrows, int c,
+                                                               int D) {
+  static_assert(sizeof(T) == 2, "16-bit operands only");
+  const int col = c * 16 + 8 * ((threadIdx.x >> 5) & 1);
+  i16x8_t v = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (row < nrows && col < D) v = *reinterpret_cast<const i16x8_t*>(base + (int64_t)row * rs + col);
+  return __builtin_bit_cast(typename Mfma<T>::frag_t, v);
+}
+
+// store4 for a head dim D that is a multiple of 8 and a column that is a multiple of 4 (vector access).
+template <typename T>
+__device__ __forceinline__ void store4_8(T* base, int64_t rs, int row, int col, int D, float a, float b, float c,
+                                         float d) {
+  if (col >= D) return;
+  T* p = base + (int64_t)row * rs + col;
+  if constexpr (sizeof(T) == 2) {
+    T v[4] = {(T)a, (T)b, (T)c, (T)d};
+    *reinterpret_cast<i16x4_t*>(p) = __builtin_bit_cast(i16x4_t, v);
+  } else {
+    *reinterpret_cast<f32x4_t*>(p) = f32x4_t{a, b, c, d};
+  }
+}
+
 template <typename T>
 __device__ __forceinline__ f32x4_t load4(const T* base, int64_t rs, int row, int col, int D, bool vec) {
   const T* p = base + (int64_t)row * rs + col;

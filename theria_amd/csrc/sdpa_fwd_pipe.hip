@@ -35,7 +35,9 @@ namespace theria {
 // feeds two MFMAs, unless the grid would then leave CUs without two waves per SIMD; one at DP = 128, where
 // the registers would not allow two, and one with the causal mask, whose paired blocks need the smaller
 // block to fill the GPU.
-template <typename T, bool CAUSAL, bool STATS, int NW, int DP, int QT>
+// FD: the head dim is DP itself (compile-time bounds); otherwise the runtime head dim s.D < DP bounds the
+// loads, stores and DMA chunks.
+template <typename T, bool CAUSAL, bool STATS, int NW, int DP, int QT, bool FD>
 __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
@@ -50,6 +52,7 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
   __shared__ __attribute__((aligned(1024))) char sV1[TILE];
 
   const Shape& s = p.s;
+  const int Dh = FD ? DP : s.D;  // head dim
   const int lane = threadIdx.x & 63, li = lane & 31, g = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nqb = (s.T + BM - 1) / BM;
@@ -82,7 +85,7 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
     if (CAUSAL) nfull = min(nfull, qb * BM / BN);
 
     using Dma = SwzDma<NW, DP>;
-    const Dma dma(wave, lane, s.D / 8);  // head dims below DP: zero-filled chunks past D
+    const Dma dma(wave, lane, Dh / 8);  // head dims below DP: zero-filled chunks past D
     constexpr int NSLAB = BN / Dma::SLAB_ROWS;
     // Byte offsets fit in 32 bits: the host only selects this kernel when every (batch, head) slab of K
     // and V spans less than 2^31 bytes.
@@ -101,7 +104,7 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
 #pragma unroll
     for (int j = 0; j < QT; ++j)
 #pragma unroll
-      for (int c = 0; c < NKC; ++c) qf[j][c] = gload_frag<T>(Q, p.q.sr, q0w + 32 * j + li, s.T, c, s.D, true);
+      for (int c = 0; c < NKC; ++c) qf[j][c] = gload_frag8<T>(Q, p.q.sr, q0w + 32 * j + li, s.T, c, Dh);
 
     f32x16_t o[QT][NDT];
     float m_use[QT], l_part[QT], m_max[QT];
@@ -391,10 +394,10 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
             const float a2 = o[j][dt][4 * qd + 2] * inv, a3 = o[j][dt][4 * qd + 3] * inv;
             if (p.o_f32) {
               float* O = (float*)p.o.p + b * p.o.sb + h * p.o.sh;
-              store4<float>(O, p.o.sr, myq, d0, s.D, a0, a1, a2, a3, true);
+              store4_8<float>(O, p.o.sr, myq, d0, Dh, a0, a1, a2, a3);
             } else {
               T* O = (T*)p.o.p + b * p.o.sb + h * p.o.sh;
-              store4<T>(O, p.o.sr, myq, d0, s.D, a0, a1, a2, a3, true);
+              store4_8<T>(O, p.o.sr, myq, d0, Dh, a0, a1, a2, a3);
             }
           }
         if (g == 0) {
@@ -412,10 +415,19 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
 
 template <typename T, bool CAUSAL, int NW, int DP, int QT>
 static void fwd_pipe_go(const FwdParams& p, int64_t nblk, hipStream_t st) {
-  if (p.row_max || p.row_sum)
-    hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, true, NW, DP, QT>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p);
-  else
-    hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, false, NW, DP, QT>), dim3((unsigned)nblk), dim3(64 * NW), 0, st, p);
+  const dim3 grid((unsigned)nblk), block(64 * NW);
+  const bool stats = p.row_max || p.row_sum;
+  if (p.s.D == DP) {
+    if (stats)
+      hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, true, NW, DP, QT, true>), grid, block, 0, st, p);
+    else
+      hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, false, NW, DP, QT, true>), grid, block, 0, st, p);
+  } else {
+    if (stats)
+      hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, true, NW, DP, QT, false>), grid, block, 0, st, p);
+    else
+      hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, false, NW, DP, QT, false>), grid, block, 0, st, p);
+  }
 }
 
 template <typename T, bool CAUSAL, int DP>
