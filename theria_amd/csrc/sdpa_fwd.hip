@@ -226,17 +226,17 @@ __global__ __launch_bounds__(256, (DP <= 64 ? FWD_MINW : 1)) void fwd_kernel(con
 // Query tiles per wave: 2 where the registers allow it and the sequence fills the block.
 template <int DP> constexpr int fwd_qt(int T) { return (FWD_QT_MAX >= 2 && DP <= 64 && T > 128) ? 2 : 1; }
 
-// Pipelined 16-bit head-dim-64 forward (sdpa_fwd_pipe.hip); false when it does not cover the problem.
-template <typename T, bool CAUSAL>
+// Pipelined 16-bit forward and row-term pass (sdpa_fwd_pipe.hip); false when it does not cover the problem.
+template <typename T, bool CAUSAL, int MODE>
 bool launch_fwd_pipe(const FwdParams& p, hipStream_t st, hipError_t* err);
 
 template <int MODE>
 struct FwdLauncher {
   template <typename T, int DP, bool CAUSAL>
   static hipError_t run(const FwdParams& p, hipStream_t st) {
-    if constexpr (MODE == 0 && sizeof(T) == 2 && DP >= 64) {
+    if constexpr (sizeof(T) == 2 && DP >= 64) {
       hipError_t err;
-      if (launch_fwd_pipe<T, CAUSAL>(p, st, &err)) return err;
+      if (launch_fwd_pipe<T, CAUSAL, MODE>(p, st, &err)) return err;
     }
     // Two query tiles per wave only for 16-bit inputs: with float32 fragments (twice the registers)
     // that variant spills ~150 VGPRs and runs at half the one-tile rate.

@@ -1,7 +1,9 @@
 // Pipelined SDPA forward for 16-bit inputs on gfx950.
 //
-// Same contract as fwd_kernel mode 0 (sdpa_fwd.hip): O = softmax(scale Q K^T) V with lse and the
-// optional reference statistics (m, l) (reference theria/attention/triton_qk.py:242-304). It is used when
+// Same contract as fwd_kernel (sdpa_fwd.hip): mode 0, O = softmax(scale Q K^T) V with lse and the optional
+// reference statistics (m, l) (reference theria/attention/triton_qk.py:242-304); mode 1 (ROW), P from a
+// given lse and the backward row term delta_i = dO_i . sum_j P_ij V_j in float32, for the backward entry
+// points that receive the saved statistics but no O and for the double backward. It is used when
 // the head dim is a multiple of 8 in 40..128 (computed at DP = 64 or 128, the columns past D zero),
 // every view allows 16-byte access and there are more than 128 queries.
 //
@@ -37,7 +39,7 @@ namespace theria {
 // block to fill the GPU.
 // FD: the head dim is DP itself (compile-time bounds); otherwise the runtime head dim s.D < DP bounds the
 // loads, stores and DMA chunks.
-template <typename T, bool CAUSAL, bool STATS, int NW, int DP, int QT, bool FD>
+template <typename T, bool CAUSAL, bool STATS, int NW, int DP, int QT, bool FD, bool ROW>
 __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
@@ -115,6 +117,12 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
       m_use[j] = -THERIA_INF;
       l_part[j] = 0.f;
       m_max[j] = -THERIA_INF;
+      if (ROW) {
+        // fixed offset lse * log2(e): P <= 1 on every tile, so the exact path never runs
+        const int myq = q0w + 32 * j + li;
+        const float l2 = myq < s.T ? p.lse[rowbase + myq] * kLog2e : THERIA_INF;
+        m_use[j] = l2 == -THERIA_INF ? THERIA_INF : l2;  // a row without visible keys has P = 0
+      }
     }
     F pf[QT][2][2];  // P of the previous tile as MFMA B fragments: [query tile][32-key subtile][16-key chunk]
     bool pf_skip = false;
@@ -300,7 +308,7 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
         bool bad = false;
 #pragma unroll
         for (int j = 0; j < QT; ++j) bad |= !(ps[j] <= 0x1p20f);
-        if (__any(bad)) {
+        if (!ROW && __any(bad)) {
           f32x16_t sc2[QT][2];
           scores(kc, sc2);
           exact(sc2, pn, ps);
@@ -322,7 +330,7 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
         if (!skip) {
           float ps[QT];
           mask(sc, k0);
-          if (k == 0) {
+          if (k == 0 && !ROW) {
             exact(sc, pn, ps);
           } else {
             if (STATS) {
@@ -333,7 +341,7 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
             bool bad = false;
 #pragma unroll
             for (int j = 0; j < QT; ++j) bad |= !(ps[j] <= 0x1p20f);
-            if (__any(bad)) {
+            if (!ROW && __any(bad)) {
               f32x16_t sc2[QT][2];
               scores(kc, sc2);
               mask(sc2, k0);
@@ -382,6 +390,27 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
 #pragma unroll
     for (int j = 0; j < QT; ++j) {
       const int myq = q0w + 32 * j + li;
+      if constexpr (ROW) {
+        // O is normalised already (P = exp(S - lse)): delta = dO . O over this lane's columns, then the pair
+        if (myq < s.T) {
+          const T* dO = (const T*)p.dout.p + b * p.dout.sb + h * p.dout.sh;
+          float part = 0.f;
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int qd = 0; qd < 4; ++qd) {
+              const int d0 = dt * 32 + 8 * qd + 4 * g;
+              if (FD || d0 < Dh) {
+                const f32x4_t go = load4<T>(dO, p.dout.sr, myq, d0, Dh, true);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) part += go[e] * o[j][dt][4 * qd + e];
+              }
+            }
+          part = pair_sum(part);
+          if (g == 0) p.delta[rowbase + myq] = part;
+        }
+        continue;
+      }
       const float l = pair_sum(l_part[j]);
       const float inv = l > 0.f ? 1.f / l : 0.f;
       if (myq < s.T) {
@@ -413,24 +442,29 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
   }  // pass
 }
 
-template <typename T, bool CAUSAL, int NW, int DP, int QT>
+template <typename T, bool CAUSAL, int NW, int DP, int QT, bool ROW>
 static void fwd_pipe_go(const FwdParams& p, int64_t nblk, hipStream_t st) {
   const dim3 grid((unsigned)nblk), block(64 * NW);
   const bool stats = p.row_max || p.row_sum;
-  if (p.s.D == DP) {
-    if (stats)
-      hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, true, NW, DP, QT, true>), grid, block, 0, st, p);
+  if constexpr (ROW) {
+    if (p.s.D == DP)
+      hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, false, NW, DP, QT, true, true>), grid, block, 0, st, p);
     else
-      hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, false, NW, DP, QT, true>), grid, block, 0, st, p);
+      hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, false, NW, DP, QT, false, true>), grid, block, 0, st, p);
+  } else if (p.s.D == DP) {
+    if (stats)
+      hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, true, NW, DP, QT, true, false>), grid, block, 0, st, p);
+    else
+      hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, false, NW, DP, QT, true, false>), grid, block, 0, st, p);
   } else {
     if (stats)
-      hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, true, NW, DP, QT, false>), grid, block, 0, st, p);
+      hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, true, NW, DP, QT, false, false>), grid, block, 0, st, p);
     else
-      hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, false, NW, DP, QT, false>), grid, block, 0, st, p);
+      hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, false, NW, DP, QT, false, false>), grid, block, 0, st, p);
   }
 }
 
-template <typename T, bool CAUSAL, int DP>
+template <typename T, bool CAUSAL, int DP, bool ROW>
 static void fwd_pipe_launch(const FwdParams& p, hipStream_t st) {
   constexpr int QT = (DP == 64 && !CAUSAL) ? 2 : 1;
   const int64_t bh = (int64_t)p.s.B * p.s.H;
@@ -440,22 +474,23 @@ static void fwd_pipe_launch(const FwdParams& p, hipStream_t st) {
   const int64_t nblk8 = units((p.s.T + 256 * QT - 1) / (256 * QT)) * bh;
   const int64_t nblk4 = units((p.s.T + 128 * QT - 1) / (128 * QT)) * bh;
   if (nblk8 >= cus) {
-    fwd_pipe_go<T, CAUSAL, 8, DP, QT>(p, nblk8, st);
+    fwd_pipe_go<T, CAUSAL, 8, DP, QT, ROW>(p, nblk8, st);
     return;
   }
   if constexpr (QT == 2) {
     // Too few query blocks to give every CU two four-wave workgroups: one query tile per wave doubles them.
     if (nblk4 < 2 * cus) {
-      fwd_pipe_go<T, CAUSAL, 4, DP, 1>(p, units((p.s.T + 127) / 128) * bh, st);
+      fwd_pipe_go<T, CAUSAL, 4, DP, 1, ROW>(p, units((p.s.T + 127) / 128) * bh, st);
       return;
     }
   }
-  fwd_pipe_go<T, CAUSAL, 4, DP, QT>(p, nblk4, st);
+  fwd_pipe_go<T, CAUSAL, 4, DP, QT, ROW>(p, nblk4, st);
 }
 
 // Launch if the pipelined kernel covers this problem (16-bit, head dim a multiple of 8 in 40..64 (run at
-// DP = 64) or 72..128 (DP = 128), vector access, more than 128 queries); returns false otherwise.
-template <typename T, bool CAUSAL>
+// DP = 64) or 72..128 (DP = 128), vector access, more than 128 queries); returns false otherwise. MODE as
+// in fwd_kernel: 0 forward, 1 row term from the given lse.
+template <typename T, bool CAUSAL, int MODE>
 bool launch_fwd_pipe(const FwdParams& p, hipStream_t st, hipError_t* err) {
   if (!(p.s.vec && p.s.D % 8 == 0 && p.s.D > 32 && (p.s.dp == 64 || p.s.dp == 128) && p.s.T > 128)) return false;
   // 32-bit byte offsets inside each (batch, head) slab of K and V
@@ -465,16 +500,20 @@ bool launch_fwd_pipe(const FwdParams& p, hipStream_t st, hipError_t* err) {
     return true;
   }
   if (p.s.dp == 64)
-    fwd_pipe_launch<T, CAUSAL, 64>(p, st);
+    fwd_pipe_launch<T, CAUSAL, 64, MODE == 1>(p, st);
   else
-    fwd_pipe_launch<T, CAUSAL, 128>(p, st);
+    fwd_pipe_launch<T, CAUSAL, 128, MODE == 1>(p, st);
   *err = hipGetLastError();
   return true;
 }
 
-template bool launch_fwd_pipe<__bf16, false>(const FwdParams&, hipStream_t, hipError_t*);
-template bool launch_fwd_pipe<__bf16, true>(const FwdParams&, hipStream_t, hipError_t*);
-template bool launch_fwd_pipe<_Float16, false>(const FwdParams&, hipStream_t, hipError_t*);
-template bool launch_fwd_pipe<_Float16, true>(const FwdParams&, hipStream_t, hipError_t*);
+template bool launch_fwd_pipe<__bf16, false, 0>(const FwdParams&, hipStream_t, hipError_t*);
+template bool launch_fwd_pipe<__bf16, true, 0>(const FwdParams&, hipStream_t, hipError_t*);
+template bool launch_fwd_pipe<_Float16, false, 0>(const FwdParams&, hipStream_t, hipError_t*);
+template bool launch_fwd_pipe<_Float16, true, 0>(const FwdParams&, hipStream_t, hipError_t*);
+template bool launch_fwd_pipe<__bf16, false, 1>(const FwdParams&, hipStream_t, hipError_t*);
+template bool launch_fwd_pipe<__bf16, true, 1>(const FwdParams&, hipStream_t, hipError_t*);
+template bool launch_fwd_pipe<_Float16, false, 1>(const FwdParams&, hipStream_t, hipError_t*);
+template bool launch_fwd_pipe<_Float16, true, 1>(const FwdParams&, hipStream_t, hipError_t*);
 
 }  // namespace theria
