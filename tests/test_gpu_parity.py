@@ -169,6 +169,27 @@ def _check_all_entry_points(case, dev, seed: int):
         close(a, b, dt, name)
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_double_backward_single_visible_key_row(dt, hip_device):
+    """Causal query 0 sees one key, so P = 1 on that row and dS, r - Gam and every second-order term of the
+    row vanish: G_Q[..., 0, :] = 0 in exact arithmetic. The G_Q expression subtracts the products
+    sum_j (P o E1)_ij K_j and t_i sum_j P_ij K_j; with 16-bit operands they cancel only if t is summed from
+    the same rounded P o E1 values (otherwise the row is left with the rounding of E1, ~1e-2 here)."""
+    B, H, T, D = 2, 2, 300, 64
+    q, _ = make((B, H, T, D), dt, hip_device, 21)
+    k, _ = make((B, H, T, D), dt, hip_device, 22)
+    v, _ = make((B, H, T, D), dt, hip_device, 23)
+    do, _ = make((B, H, T, D), dt, hip_device, 24)
+    tq, tk, tv = (make((B, H, T, D), dt, hip_device, 25 + i)[0] for i in range(3))
+    s = 1 / math.sqrt(D)
+    print(f"[single-key row] {dt}", flush=True)
+    o, lse, _, _ = _ops.fwd(q, k, v, s, True)
+    _, _, _, delta = _ops.bwd(q, k, v, o, lse, do, s, True)
+    G = _ops.bwd_bwd(q, k, v, o, do, lse, delta, tq, tk, tv, s, True)
+    row0 = G[0][:, :, 0].float().abs().max().item()
+    assert row0 <= 1e-3, f"G_Q of the single-key row: {row0}"
+
+
 def test_config1_golden_fixture_fp32(hip_device):
     """Config 1 (B2 H2 S16 D8, float32) against the committed fixture, 1e-5."""
     z = np.load(GOLDEN, allow_pickle=False)

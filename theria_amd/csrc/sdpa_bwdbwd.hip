@@ -94,6 +94,9 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
   const float moff = lse2 == -THERIA_INF ? THERIA_INF : lse2;
   const float z = qvalid ? p.delta[row_id] : 0.f;
   float r_part = 0.f, t_part = 0.f;
+  // 16-bit inputs: t summed from the rounded P o E1 operands of the x13 product as well, so that the G_Q terms
+  // x13 - t x4 cancel exactly where they should (a row with one visible key: P = 1, G_Q = 0)
+  float t_frag = 0.f;
 
   int kend = s.M;
   if (CAUSAL) kend = min(s.M, qb * BM + BM);
@@ -155,6 +158,7 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
         const F pf = acc_frag<T>(sc, cc);
         const F pe1f = acc_frag<T>(gm, cc);
         const F dsf = acc_frag<T>(dpz, cc);
+        if constexpr (sizeof(T) == 2) t_frag = frag_sum<T>(pe1f, t_frag);
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
           const F kr = rowsf(tK, 32 * st, cc, dt * 32);
@@ -227,6 +231,7 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
   }
 
   const float rr = pair_sum(r_part), tt = pair_sum(t_part);
+  const float tg = sizeof(T) == 2 ? pair_sum(t_frag) : tt;  // t as G_Q uses it; the cols kernel takes tt
   if (qvalid) {
     T* OG = (T*)p.out_gq.p + b * p.out_gq.sb + h * p.out_gq.sh;
 #pragma unroll
@@ -239,7 +244,7 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int i = 4 * qd + e;
-            r4[e] = s.scale * (x13[dt][i] - rr * x2[dt][i] - tt * x4[dt][i] + yk[dt][i]);
+            r4[e] = s.scale * (x13[dt][i] - rr * x2[dt][i] - tg * x4[dt][i] + yk[dt][i]);
           }
           store4<T>(OG, p.out_gq.sr, myq, d0, s.D, r4[0], r4[1], r4[2], r4[3], s.vec);
         }
