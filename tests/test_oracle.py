@@ -195,6 +195,19 @@ def test_causal_first_row_is_v0():
     torch.testing.assert_close(lse[..., 0], (q[..., 0, :] * k[..., 0, :]).sum(-1) / 2.0, rtol=1e-14, atol=1e-14)
 
 
+def test_causal_first_row_second_order_terms_vanish():
+    """Causal query 0 sees one key, so P = 1 on that row whatever q_0 is: dQ_0 = 0 and the double
+    backward's G_Q row 0 = 0 (the row's softmax has no derivative), while G_Q of later rows is not."""
+    q, k, v = _qkv(1, 2, 6, 6, 4)
+    do = _rand(1, 2, 6, 4, seed=7)
+    gq, gk, gv = (_rand(1, 2, 6, 4, seed=8 + i) for i in range(3))
+    dq, _, _ = O.backward(q, k, v, do, causal=True)
+    assert float(dq[..., 0, :].abs().max()) < 1e-14
+    G = O.double_backward(q, k, v, do, gq, gk, gv, causal=True)
+    assert float(G[0][..., 0, :].abs().max()) < 1e-13
+    assert float(G[0][..., 1:, :].abs().max()) > 1e-3
+
+
 def test_planted_mistake_in_double_backward_is_caught():
     """Dropping the -r o dP term of Gbar_P (a plausible derivation slip) must break autograd parity."""
     q, k, v = (t.requires_grad_(True) for t in _qkv(1, 2, 5, 6, 4))
