@@ -21,6 +21,7 @@
 //   subtiles for 16-bit inputs at head dim <= 64, else 32) with r, t, z, lse per row staged in LDS
 //   accumulates G_V and G_K in registers.
 #include <initializer_list>
+#include <type_traits>
 
 #include "dispatch.hpp"
 #include "sdpa_common.hpp"
@@ -94,9 +95,14 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
   const float moff = lse2 == -THERIA_INF ? THERIA_INF : lse2;
   const float z = qvalid ? p.delta[row_id] : 0.f;
   float r_part = 0.f, t_part = 0.f;
-  // 16-bit inputs: t summed from the rounded P o E1 operands of the x13 product as well, so that the G_Q terms
-  // x13 - t x4 cancel exactly where they should (a row with one visible key: P = 1, G_Q = 0)
-  float t_frag = 0.f;
+  // 16-bit inputs: Gbar_S = P o ((Gam - r)(dP - z) + W - t), and for any row constants cr, ct
+  //   Gbar_S = P o E1c - (r - cr) dS - (t - ct) P  with  E1c = (Gam - cr)(dP - z) + W - ct,
+  // so x13 takes P o E1c and G_Q = s (x13 - (r - cr) x2 - t_c x4 + yk), t_c = sum_j of the rounded P o E1c
+  // operands (= t - ct in exact arithmetic). The centres are r and t over the first key tile (a pre-pass):
+  // on rows with few visible keys, where G_Q is a small difference of large terms, the products then carry
+  // small centred values instead (one visible key gives G_Q = 0 exactly).
+  float t_frag = 0.f, cr = 0.f, ct = 0.f;
+  float c_p = 0.f, c_pg = 0.f, c_pgd = 0.f, c_pd = 0.f, c_pw = 0.f;
 
   int kend = s.M;
   if (CAUSAL) kend = min(s.M, qb * BM + BM);
@@ -117,7 +123,8 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
   };
 
   // The key tile kt held in (tK, tV, tgK, tgV), as 32-key subtiles.
-  auto compute = [&](int kt, const char* tK, const char* tV, const char* tgK, const char* tgV) {
+  auto compute = [&](auto pre_tag, int kt, const char* tK, const char* tV, const char* tgK, const char* tgV) {
+    constexpr bool PRE = decltype(pre_tag)::value;  // centre pre-pass: sums for c only
     const int k0 = kt * BN;
 #pragma unroll
     for (int st = 0; st < NST; ++st) {
@@ -147,12 +154,21 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
         const float gam = s.scale * gm[r];
         const float e1 = fmaf(gam, dpz[r], w[r]);
         const float pe1 = pv * e1;
-        r_part = fmaf(pv, gam, r_part);
-        t_part += pe1;
-        sc[r] = pv;
-        gm[r] = pe1;
-        dpz[r] = pv * dpz[r];  // dS
+        if constexpr (PRE) {
+          c_p += pv;
+          c_pg = fmaf(pv, gam, c_pg);
+          c_pd = fmaf(pv, dpz[r], c_pd);
+          c_pgd = fmaf(pv * gam, dpz[r], c_pgd);
+          c_pw = fmaf(pv, w[r], c_pw);
+        } else {
+          r_part = fmaf(pv, gam, r_part);
+          t_part += pe1;
+          sc[r] = pv;
+          gm[r] = sizeof(T) == 2 ? pv * (fmaf(gam - cr, dpz[r], w[r]) - ct) : pe1;
+          dpz[r] = pv * dpz[r];  // dS
+        }
       }
+      if constexpr (PRE) continue;
 #pragma unroll
       for (int cc = 0; cc < NPC; ++cc) {
         const F pf = acc_frag<T>(sc, cc);
@@ -168,6 +184,17 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
           if (has_gk) yk[dt] = MM::mma(rowsf(tgK, 32 * st, cc, dt * 32), dsf, yk[dt]);
         }
       }
+    }
+  };
+
+  const std::integral_constant<bool, true> pre_pass;
+  const std::integral_constant<bool, false> full_pass;
+  auto set_centre = [&]() {
+    const float sp = pair_sum(c_p), spg = pair_sum(c_pg), spd = pair_sum(c_pd), spgd = pair_sum(c_pgd),
+                spw = pair_sum(c_pw);
+    if (sp > 0.f) {
+      cr = spg / sp;
+      ct = (spgd - cr * spd + spw) / sp;
     }
   };
 
@@ -197,11 +224,17 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
       wait_vm_all();
       __syncthreads();
       if (kt + 1 < nkt) issue(kt + 1, nK, nV, ngK, ngV);
-      compute(kt, cK, cV, cgK, cgV);
+      compute(full_pass, kt, cK, cV, cgK, cgV);
       __builtin_amdgcn_sched_barrier(0);  // keep the two unrolled steps apart (register pressure)
     };
     if (nkt > 0) {
       issue(0, sK0, sV0, sgK0, sgV0);
+      if constexpr (sizeof(T) == 2) {
+        wait_vm_all();
+        __syncthreads();
+        compute(pre_pass, 0, sK0, sV0, sgK0, sgV0);
+        set_centre();
+      }
       int kt = 0;
       for (; kt + 1 < nkt; kt += 2) {
         step(kt, sK0, sV0, sgK0, sgV0, sK1, sV1, sgK1, sgV1);
@@ -218,6 +251,16 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
       if (has_gv) gsgV.load(GV, p.gv.sr, k0, s.M, s.D, s.vec);
     };
     if (nkt > 0) prefetch(0);
+    if (sizeof(T) == 2 && nkt > 0) {
+      // centre pre-pass over tile 0 (the loop stages the same registers again)
+      gsK.store((T*)sK0, PITCH);
+      gsV.store((T*)sV0, PITCH);
+      if (has_gk) gsgK.store((T*)sgK0, PITCH);
+      if (has_gv) gsgV.store((T*)sgV0, PITCH);
+      __syncthreads();
+      compute(pre_pass, 0, sK0, sV0, sgK0, sgV0);
+      set_centre();
+    }
     for (int kt = 0; kt < nkt; ++kt) {
       __syncthreads();
       gsK.store((T*)sK0, PITCH);
@@ -226,12 +269,13 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
       if (has_gv) gsgV.store((T*)sgV0, PITCH);
       __syncthreads();
       if (kt + 1 < nkt) prefetch((kt + 1) * BN);
-      compute(kt, sK0, sV0, sgK0, sgV0);
+      compute(full_pass, kt, sK0, sV0, sgK0, sgV0);
     }
   }
 
   const float rr = pair_sum(r_part), tt = pair_sum(t_part);
-  const float tg = sizeof(T) == 2 ? pair_sum(t_frag) : tt;  // t as G_Q uses it; the cols kernel takes tt
+  const float tg = sizeof(T) == 2 ? pair_sum(t_frag) : tt;  // t_c as G_Q uses it; the cols kernel takes tt
+  const float rg = rr - cr;                                   // r - cr (cr = 0 for float32)
   if (qvalid) {
     T* OG = (T*)p.out_gq.p + b * p.out_gq.sb + h * p.out_gq.sh;
 #pragma unroll
@@ -244,7 +288,7 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int i = 4 * qd + e;
-            r4[e] = s.scale * (x13[dt][i] - rr * x2[dt][i] - tg * x4[dt][i] + yk[dt][i]);
+            r4[e] = s.scale * (x13[dt][i] - rg * x2[dt][i] - tg * x4[dt][i] + yk[dt][i]);
           }
           store4<T>(OG, p.out_gq.sr, myq, d0, s.D, r4[0], r4[1], r4[2], r4[3], s.vec);
         }
