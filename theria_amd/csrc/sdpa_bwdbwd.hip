@@ -98,7 +98,8 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
   // 16-bit inputs: Gbar_S = P o ((Gam - r)(dP - z) + W - t), and for any row constants cr, ct
   //   Gbar_S = P o E1c - (r - cr) dS - (t - ct) P  with  E1c = (Gam - cr)(dP - z) + W - ct,
   // so x13 takes P o E1c and G_Q = s (x13 - (r - cr) x2 - t_c x4 + yk), t_c = sum_j of the rounded P o E1c
-  // operands (= t - ct in exact arithmetic). The centres are r and t over the first key tile (a pre-pass):
+  // operands (= t - ct in exact arithmetic). The centres are r and t over the first key tile (a pre-pass),
+  // used when that tile holds more than half of the row's probability (else cr = ct = 0):
   // on rows with few visible keys, where G_Q is a small difference of large terms, the products then carry
   // small centred values instead (one visible key gives G_Q = 0 exactly).
   float t_frag = 0.f, cr = 0.f, ct = 0.f;
@@ -192,7 +193,8 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
   auto set_centre = [&]() {
     const float sp = pair_sum(c_p), spg = pair_sum(c_pg), spd = pair_sum(c_pd), spgd = pair_sum(c_pgd),
                 spw = pair_sum(c_pw);
-    if (sp > 0.f) {
+    // only where the first tile holds most of the row's probability (its means then stand for the row)
+    if (sp > 0.5f) {
       cr = spg / sp;
       ct = (spgd - cr * spd + spw) / sp;
     }
