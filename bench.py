@@ -46,10 +46,12 @@ def _args():
     # warmup (~0.3 s of steps) reaches the steady state before the timed steps.
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=1000)
+    ap.add_argument("--warmup-seconds", type=float, default=0.5,
+                    help="warm up for at least this long as well as --warmup steps (clock ramp after idle)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU-baseline sample")
     ap.add_argument("--no-extras", action="store_true", help="only the config-2 line (for profiling runs)")
-    ap.add_argument("--extras", default="c2_fp16,c3,c4,c5",
-                    help="comma-separated subset of the other configs to run (c2_fp16, c3, c4, c5)")
+    ap.add_argument("--extras", default="c2_fp16,c3,c4,c5,scores",
+                    help="comma-separated subset of the other configs to run (c2_fp16, c3, c4, c5, scores)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (for profiling runs)")
     ap.add_argument("--copy-calibration", action="store_true", help="run a plain copy of known size (PMC scaling)")
     return ap.parse_args()
@@ -62,37 +64,55 @@ def _rand(shape, dtype, dev, seed, std=1.0):
     return (torch.randn(*shape, generator=g) * std).to(dtype).to(dev)
 
 
-def bench_config2(steps: int, warmup: int):
-    """Timed fwd+bwd steps at config 2; per-kernel HIP-event durations of the three kernels."""
+def _step_fns(q, k, v, do, scale, causal):
+    """One fwd + bwd step as the autograd operator runs it: the forward saves lse, the row maxima m and the
+    rounding residual of O; the dQ kernel forms the row term from O and its residual, then dK/dV."""
     import torch
 
     from theria_amd import _ops
+
+    B, H, S, _ = q.shape
+    prob = _ops._problem(q, k, scale, causal)
+    delta = torch.empty((B, H, S), dtype=torch.float32, device=q.device)
+    dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+
+    def step(ev=None):
+        if ev:
+            ev[0].record()
+        o, lse, m, o_lo = _ops.fwd_for_backward(q, k, v, scale, causal)
+        if ev:
+            ev[1].record()
+        _ops.bwd_dq(prob, q, k, v, o, False, do, lse, delta, dq, o_lo, m)
+        if ev:
+            ev[2].record()
+        _ops.bwd_dkdv(prob, q, k, v, do, lse, delta, dk, dv, m)
+        if ev:
+            ev[3].record()
+
+    return step
+
+
+def bench_config2(steps: int, warmup: int, warmup_s: float):
+    """Timed fwd+bwd steps at config 2; per-kernel HIP-event durations of the three kernels."""
+    import torch
 
     dev = torch.device("cuda:0")
     B, H, S, D = 4, 16, 2048, 64
     dt = torch.bfloat16
     q, k, v, do = (_rand((B, H, S, D), dt, dev, 100 + i) for i in range(4))
     scale = 1.0 / math.sqrt(D)
-    prob = _ops._problem(q, k, scale, False)
-    delta = torch.empty((B, H, S), dtype=torch.float32, device=dev)
-    dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+    step = _step_fns(q, k, v, do, scale, False)
 
-    def step(ev=None):
-        if ev:
-            ev[0].record()
-        o, lse, _, _ = _ops.fwd(q, k, v, scale, False)
-        if ev:
-            ev[1].record()
-        _ops.bwd_dq(prob, q, k, v, o, False, do, lse, delta, dq)
-        if ev:
-            ev[2].record()
-        _ops.bwd_dkdv(prob, q, k, v, do, lse, delta, dk, dv)
-        if ev:
-            ev[3].record()
-
-    for _ in range(warmup):
+    # W steps, and at least warmup_s seconds: the clocks ramp for the first tens of ms after idle
+    t0 = time.perf_counter()
+    n = 0
+    while n < warmup or time.perf_counter() - t0 < warmup_s:
         step()
+        n += 1
+        if n % 64 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
+    warm_s = time.perf_counter() - t0
     t0 = time.perf_counter()
     for _ in range(steps):
         step()
@@ -108,13 +128,27 @@ def bench_config2(steps: int, warmup: int):
     dkdv_ms = statistics.mean(e[2].elapsed_time(e[3]) for e in evs)
     unit = B * H * S * S * D
     return dict(
-        wall_ms=wall * 1e3, fwd_ms=fwd_ms, dq_ms=dq_ms, dkdv_ms=dkdv_ms,
+        wall_ms=wall * 1e3, fwd_ms=fwd_ms, dq_ms=dq_ms, dkdv_ms=dkdv_ms, warmup_steps=n, warmup_s=warm_s,
         flop_step=14 * unit, flop_fwd=4 * unit, flop_bwd=10 * unit,
         # algorithmic work of each backward kernel: dq = S, dP, dQ products (6 B H S^2 D);
         # dkdv = S, dP, dV, dK products (8 B H S^2 D); together 14, of which the FA convention counts 10
         flop_dq=6 * unit, flop_dkdv=8 * unit,
         B=B, H=H, S=S, D=D,
     )
+
+
+def _cpu_threads() -> int:
+    """Host threads for the CPU baseline: every core this process may run on (its affinity mask), capped by
+    OMP_NUM_THREADS when that is set (a GPU box grants one GPU's share of its cores, whatever
+    os.cpu_count() reports for the whole machine)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    cap = os.environ.get("OMP_NUM_THREADS")
+    if cap and cap.isdigit() and int(cap) > 0:
+        n = min(n, int(cap))
+    return max(1, n)
 
 
 def cpu_baseline(budget_s: float):
@@ -124,7 +158,8 @@ def cpu_baseline(budget_s: float):
     from oracle import sdpa_oracle as O
 
     S, D = 2048, 64
-    threads = torch.get_num_threads()
+    threads = _cpu_threads()
+    torch.set_num_threads(threads)
     heads = 0
     t_total = 0.0
     while heads < 64 and (t_total < budget_s or heads == 0):
@@ -142,8 +177,16 @@ def cpu_baseline(budget_s: float):
         "cores": threads,
         "kind": "port",
         "sample": f"{heads} of the 64 (batch, head) slices of config 2 (S2048 D64), fp32 fwd+bwd via the CPU "
-        f"oracle, {t_total:.1f} s; cpu={_cpu_model()}",
+        f"oracle, {t_total:.1f} s; {threads} threads (affinity {_affinity()} of os.cpu_count() {os.cpu_count()}, "
+        f"OMP_NUM_THREADS={os.environ.get('OMP_NUM_THREADS', 'unset')}); cpu={_cpu_model()}",
     }
+
+
+def _affinity() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return -1
 
 
 def _cpu_model() -> str:
@@ -184,16 +227,7 @@ def extras_c2_fp16():
     dev = torch.device("cuda:0")
     B, H, S, D = 4, 16, 2048, 64
     q, k, v, do = (_rand((B, H, S, D), torch.float16, dev, 500 + i) for i in range(4))
-    scale = 1.0 / math.sqrt(D)
-    prob = _ops._problem(q, k, scale, False)
-    delta = torch.empty((B, H, S), dtype=torch.float32, device=dev)
-    dq, dk, dv = (torch.empty_like(q) for _ in range(3))
-
-    def step():
-        o, lse, _, _ = _ops.fwd(q, k, v, scale, False)
-        _ops.bwd_dq(prob, q, k, v, o, False, do, lse, delta, dq)
-        _ops.bwd_dkdv(prob, q, k, v, do, lse, delta, dk, dv)
-
+    step = _step_fns(q, k, v, do, 1.0 / math.sqrt(D), False)
     ms = _time(step, 30, 5)
     return {"config": "B4 H16 S2048 D64 fp16 fwd+bwd", "ms": round(ms, 4),
             "tflops": round(14 * B * H * S * S * D / (ms * 1e-3) / 1e12, 1)}
@@ -211,36 +245,66 @@ def extras_c3():
     do = _rand((B, H, S, D), torch.bfloat16, dev, 303)
     scale = 1 / math.sqrt(D)
 
-    def run():
-        o, lse, _, _ = _ops.fwd(q, k, v, scale, True)
-        _ops.bwd(q, k, v, o, lse, do, scale, True)
-
+    run = _step_fns(q, k, v, do, scale, True)
     ms = _time(run, 5, 2)
     useful = 14 * B * H * (S * (S + 1) / 2) * D  # unmasked elements only
-    # tile accounting of the kernels' schedules (forward: 32-query wave tile x 64-key tile, skipped when
-    # the whole tile is above the diagonal; backward: 32-key wave block x 32-query sub-tile)
-    def count(qt, kt):
-        executed = needed = elems = 0
-        for q0 in range(0, S, qt):
-            for k0 in range(0, S, kt):
-                if k0 <= q0 + qt - 1:
-                    executed += 1
-                    needed += 1
-                    elems += qt * kt
-        return executed, needed, elems
-
-    ef, nf, elf = count(32, 64)
-    eb, nb, elb = count(32, 32)
-    unmasked = S * (S + 1) / 2
+    fwd_t = _causal_tiles(S, 32, 64)  # forward at head dim 128: a wave's 32 queries x a 64-key tile
+    bwd_t = _causal_tiles(S, 32, 32)  # dQ, dK/dV: 32 queries x 32 keys per wave subtile
     return {
         "config": "B1 H32 S8192 D128 causal bf16 fwd+bwd",
         "ms": round(ms, 3),
         "tflops": round(useful / (ms * 1e-3) / 1e12, 1),
-        "tile_skip_efficiency_fwd": round(nf / ef, 4),
-        "tile_skip_efficiency_bwd": round(nb / eb, 4),
-        "useful_flop_fraction_fwd": round(unmasked / elf, 4),
-        "useful_flop_fraction_bwd": round(unmasked / elb, 4),
+        "tile_skip_efficiency_fwd": round(fwd_t["needed"] / fwd_t["executed"], 4),
+        "tile_skip_efficiency_bwd": round(bwd_t["needed"] / bwd_t["executed"], 4),
+        "useful_flop_fraction_fwd": round(fwd_t["useful_fraction"], 4),
+        "useful_flop_fraction_bwd": round(bwd_t["useful_fraction"], 4),
+        "tiles_fwd": {k_: fwd_t[k_] for k_ in ("executed", "needed", "total")},
+        "tiles_bwd": {k_: bwd_t[k_] for k_ in ("executed", "needed", "total")},
     }
+
+
+def _causal_tiles(S: int, qt: int, kt: int) -> dict:
+    """Tile accounting of a causal S x S problem cut into qt-query x kt-key wave tiles.
+
+    executed: tiles whose products the kernels run, by their skip rule (a wave skips a key tile, or a dK/dV
+    wave a query subtile, when its first key lies after the tile's last query: k0 > q0 + qt - 1);
+    needed: tiles holding at least one unmasked (key <= query) element, found from the mask itself.
+    useful_fraction: unmasked elements over the elements of the executed tiles."""
+    import numpy as np
+
+    nq, nk = S // qt, S // kt
+    q0 = np.arange(nq)[:, None] * qt
+    k0 = np.arange(nk)[None, :] * kt
+    executed = k0 <= q0 + qt - 1
+    mask = np.tri(S, S, dtype=bool)  # mask[q, k] = k <= q
+    needed = mask.reshape(nq, qt, nk, kt).any(axis=(1, 3))
+    return {
+        "executed": int(executed.sum()),
+        "needed": int(needed.sum()),
+        "total": nq * nk,
+        "useful_fraction": float(mask.sum()) / float(executed.sum() * qt * kt),
+    }
+
+
+def extras_scores():
+    """The partial-fusion score kernels (sdpa_custom backends triton_qk / triton_qk_softmax) at the config-2
+    shape: ms and HBM GB/s (Q, K read once, the (B,H,S,S) float32 output written once) against 8 TB/s."""
+    import torch
+
+    from theria_amd import _ops
+
+    dev = torch.device("cuda:0")
+    B, H, S, D = 4, 16, 2048, 64
+    q, k = (_rand((B, H, S, D), torch.bfloat16, dev, 600 + i) for i in range(2))
+    out = {"config": "B4 H16 S2048 D64 bf16 in, float32 (B,H,S,S) out", "hbm_peak_gbs": 8000}
+    nbytes = 2 * B * H * S * D * 2 + B * H * S * S * 4
+    for name, fn in (("qk_scores", lambda: _ops.qk_scores(q, k, out_f32=True)),
+                     ("qk_softmax", lambda: _ops.qk_softmax(q, k, 1 / 8.0))):
+        ms = _time(fn, 20)
+        out[f"{name}_ms"] = round(ms, 4)
+        out[f"{name}_gbs"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+    out["bytes_per_call"] = nbytes
+    return out
 
 
 def extras_c4():
@@ -329,13 +393,13 @@ def extras_c5():
     ref.set_attention_backend("reference")
     params_h = list(model.parameters())
     params_r = list(ref.parameters())
-    gh = torch.autograd.grad(meta_loss_on_tasks(model, tasks[:4], inner_lr=0.4, inner_steps=5), params_h)
-    gr = torch.autograd.grad(meta_loss_on_tasks(ref, tasks[:4], inner_lr=0.4, inner_steps=5), params_r)
+    gh = torch.autograd.grad(meta_loss_on_tasks(model, tasks, inner_lr=0.4, inner_steps=5), params_h)
+    gr = torch.autograd.grad(meta_loss_on_tasks(ref, tasks, inner_lr=0.4, inner_steps=5), params_r)
     fh = torch.cat([x.flatten() for x in gh]).double()
     fr = torch.cat([x.flatten() for x in gr]).double()
     res["metagrad_rel_l2_vs_reference"] = float((fh - fr).norm() / fr.norm())
     res["metagrad_cosine_vs_reference"] = float(torch.nn.functional.cosine_similarity(fh, fr, dim=0))
-    gb = torch.autograd.grad(meta_loss_on_tasks_batched(model, tasks[:4], inner_lr=0.4, inner_steps=5), params_h)
+    gb = torch.autograd.grad(meta_loss_on_tasks_batched(model, tasks, inner_lr=0.4, inner_steps=5), params_h)
     fb = torch.cat([x.flatten() for x in gb]).double()
     res["metagrad_rel_l2_task_batched_vs_reference"] = float((fb - fr).norm() / fr.norm())
     return res
@@ -373,7 +437,7 @@ def main() -> int:
     if args.copy_calibration:
         copy_calibration()
         return 0
-    r = bench_config2(args.steps, args.warmup)
+    r = bench_config2(args.steps, args.warmup, args.warmup_seconds)
     value = r["flop_step"] / (r["wall_ms"] * 1e-3) / 1e12
     achieved = r["flop_dkdv"] / (r["dkdv_ms"] * 1e-3) / 1e12
     traffic = None
@@ -389,6 +453,8 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_steps_run": r["warmup_steps"],
+        "warmup_s": round(r["warmup_s"], 3),
         "ms_per_step": round(r["wall_ms"], 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -422,7 +488,8 @@ def main() -> int:
     if not args.no_extras:
         extra = {}
         wanted = {x.strip() for x in args.extras.split(",") if x.strip()}
-        for name, fn in (("c2_fp16", extras_c2_fp16), ("c3", extras_c3), ("c4", extras_c4), ("c5", extras_c5)):
+        for name, fn in (("c2_fp16", extras_c2_fp16), ("c3", extras_c3), ("c4", extras_c4), ("c5", extras_c5),
+                         ("scores", extras_scores)):
             if name not in wanted:
                 continue
             try:

@@ -8,6 +8,8 @@ A plain restatement, on CPU, of the reference's pure-PyTorch path, by closed for
                        saved statistics m, l of the fused kernel (theria/attention/triton_qk.py:280-304,
                        docs/phase9.md:12-16) and lse = m + log l;
   * backward           sdpa_backward_reference (theria/attention/reference_backward_sdpa.py:24-53);
+                       frozen_backward takes P from a given lse like the explicit sdpa_bwd_* kernels
+                       (theria/attention/triton_sdpa_backward.py:106-696);
   * jvp                sdpa_jvp_reference (theria/attention/reference_jvp_sdpa.py:21-44), which equals
                        the frozen-stats sdpa_jvp (theria/attention/triton_sdpa_backward.py:465-503) at
                        exact stats; frozen_jvp takes the stats as given like the latter;
@@ -80,6 +82,24 @@ def backward(q, k, v, dout, scale=None, causal=False, dtype=torch.float64):
     q, k, v, dout = _f64(q, k, v, dout, dtype=dtype)
     s = _scale(q, scale)
     P = probs(q, k, s, causal)
+    dv = P.transpose(-2, -1) @ dout
+    dP = dout @ v.transpose(-2, -1)
+    z = (dP * P).sum(-1, keepdim=True)
+    dS = P * (dP - z)
+    return s * (dS @ k), s * (dS.transpose(-2, -1) @ q), dv
+
+
+def frozen_backward(q, k, v, dout, lse, scale=None, causal=False, dtype=torch.float64):
+    """(dQ, dK, dV) of the frozen-stats backward: the gradient formula of backward() evaluated with
+    P = exp(S - lse) held as given (the reference's sdpa_bwd_dq / _dk / _dv with saved (m, l), lse = m + log l,
+    theria/attention/triton_sdpa_backward.py:106-266, 269-462, 505-696): z = rowsum(dP P), dS = P (dP - z)."""
+    q, k, v, dout, lse = _f64(q, k, v, dout, lse, dtype=dtype)
+    s = _scale(q, scale)
+    S = (q @ k.transpose(-2, -1)) * s
+    msk = _mask(q.shape[-2], k.shape[-2], causal)
+    if msk is not None:
+        S = S.masked_fill(~msk, float("-inf"))
+    P = torch.exp(S - lse.unsqueeze(-1)).nan_to_num(nan=0.0)
     dv = P.transpose(-2, -1) @ dout
     dP = dout @ v.transpose(-2, -1)
     z = (dP * P).sum(-1, keepdim=True)

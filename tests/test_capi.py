@@ -33,6 +33,10 @@ def test_library_exports_every_declared_symbol():
     nm = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True, check=True)
     exported = sorted(set(re.findall(r"\sT\s(theria_\w+)", nm.stdout)))
     assert exported == declared, f"exported {exported} != declared {declared}"
+    # Nothing else: exported kernel stubs (weak template symbols) would bind to another copy of the
+    # library loaded into the same process, which would then launch kernels of a different build.
+    others = [ln.split()[-1] for ln in nm.stdout.splitlines() if ln.split() and not ln.split()[-1].startswith("theria_")]
+    assert not others, f"symbols beyond the C ABI are exported: {others[:5]} ..."
 
 
 def test_abi_version_matches():
@@ -55,12 +59,14 @@ def _call_all(prob):
     lib = _lib.load()
     p = ctypes.byref(prob)
     return {
-        "fwd": lib.theria_sdpa_fwd(p, None, None, None, None, 0, None, None, None, None),
-        "bwd": lib.theria_sdpa_bwd(p, None, None, None, None, 0, None, None, None, None, None, None, None),
-        "bwd_dq": lib.theria_sdpa_bwd_dq(p, None, None, None, None, 0, None, None, None, None, None),
-        "bwd_dkdv": lib.theria_sdpa_bwd_dkdv(p, None, None, None, None, None, None, None, None, None),
-        "bwd_from_stats": lib.theria_sdpa_bwd_from_stats(p, None, None, None, None, None, None, None, None, None, None),
-        "jvp": lib.theria_sdpa_jvp(p, None, None, None, None, None, None, None, None, None, None),
+        "fwd": lib.theria_sdpa_fwd(p, None, None, None, None, 0, None, None, None, None, None),
+        "bwd": lib.theria_sdpa_bwd(p, None, None, None, None, 0, None, None, None, None, None, None, None, None, None),
+        "bwd_dq": lib.theria_sdpa_bwd_dq(p, None, None, None, None, 0, None, None, None, None, None, None, None),
+        "bwd_dkdv": lib.theria_sdpa_bwd_dkdv(p, None, None, None, None, None, None, None, None, None, None),
+        "bwd_from_stats": lib.theria_sdpa_bwd_from_stats(
+            p, None, None, None, None, None, None, None, None, None, None, 0, None
+        ),
+        "jvp": lib.theria_sdpa_jvp(p, None, None, None, None, None, None, None, None, None, 1, None),
         "bwd_bwd": lib.theria_sdpa_bwd_bwd(
             p, None, None, None, None, None, None, None, None, None, None, None, None, None, None, None, None
         ),

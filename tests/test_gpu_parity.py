@@ -40,6 +40,10 @@ def stat_tol(dtype):
 
 
 def close(gpu, ref, dtype, what):
+    _close(gpu, ref, dtype, what)
+
+
+def _close(gpu, ref, dtype, what):
     a = gpu.detach().double().cpu()
     b = ref.double()
     assert a.shape == b.shape, f"{what}: shape {tuple(a.shape)} vs {tuple(b.shape)}"
@@ -124,35 +128,79 @@ def _check_all_entry_points(case, dev, seed: int):
     """Forward (O, lse, m, l), backward (with O, from stats, dV only), JVP (saved / rebuilt O, one tangent)
     and the double backward (all cotangents, one) against the float64 oracle on the same inputs."""
     dt, B, H, T, M, D, causal = case
-    q, qc = make((B, H, T, D), dt, dev, seed)
-    k, kc = make((B, H, M, D), dt, dev, seed + 1)
-    v, vc = make((B, H, M, D), dt, dev, seed + 2)
-    do, doc = make((B, H, T, D), dt, dev, seed + 3)
-    tq, tqc = make((B, H, T, D), dt, dev, seed + 4)
-    tk, tkc = make((B, H, M, D), dt, dev, seed + 5)
-    tv, tvc = make((B, H, M, D), dt, dev, seed + 6)
-    s = 1 / math.sqrt(D)
+    shapes = [(B, H, T, D), (B, H, M, D), (B, H, M, D), (B, H, T, D), (B, H, T, D), (B, H, M, D), (B, H, M, D)]
+    g = [torch.Generator().manual_seed(seed + i) for i in range(7)]
+    ts = [torch.randn(*sh, generator=gi).to(dt) for sh, gi in zip(shapes, g)]
+    check_entry_points_on(dev, dt, causal, *ts)
+
+
+def check_entry_points_on(dev, dt, causal, q, k, v, do, tq, tk, tv, scale=None, fp32_ref_err=None):
+    """Every entry point on the given CPU inputs (already rounded to dt) against the float64 oracle.
+
+    Bars: tol(dt) for outputs in the input dtype; float32 outputs of 16-bit inputs (O with a float32
+    output, lse) carry no output rounding, so they are held to an absolute bound alone: 2e-2 for O (the
+    north star's bar), 4e-3 for lse (the row sum is accumulated from probabilities rounded to 16 bits,
+    each within a relative 2^-8 of its float32 value, so log l is within 2^-8 absolute).
+    fp32_ref_err (float32 only): {quantity: largest error of theria's float32 PyTorch path against the
+    oracle on these inputs}; a quantity listed there may be off by up to twice that error (when it exceeds
+    1e-5), since float32 arithmetic itself cannot reach 1e-5 there."""
+    qc, kc, vc, doc, tqc, tkc, tvc = (t.double() for t in (q, k, v, do, tq, tk, tv))
+    q, k, v, do, tq, tk, tv = (t.to(dev) for t in (q, k, v, do, tq, tk, tv))
+    s = 1 / math.sqrt(q.shape[-1]) if scale is None else scale
+    f32_out = dict(rtol=1e-5, atol=1e-5) if dt == torch.float32 else dict(rtol=0, atol=2e-2)
+    lse_tol = dict(rtol=1e-5, atol=1e-5) if dt == torch.float32 else dict(rtol=0, atol=4e-3)
+
+    def close(gpu, ref, dtype, what):
+        base = what if fp32_ref_err and what in fp32_ref_err else what.split("(")[0]
+        if dtype == torch.float32 and fp32_ref_err and base in fp32_ref_err:
+            a, b = gpu.detach().double().cpu(), ref.double()
+            assert torch.isfinite(a).all(), f"{what}: non-finite output"
+            atol = max(1e-5, 2 * fp32_ref_err[base])
+            torch.testing.assert_close(a, b, rtol=1e-5, atol=atol,
+                                       msg=lambda m_: f"{what} (float32 reference error {fp32_ref_err[base]:.2e}): {m_}")
+        else:
+            _close(gpu, ref, dtype, what)
 
     o, lse, m, l = _ops.fwd(q, k, v, s, causal, stats=True)
-    o32, _, _, _ = _ops.fwd(q, k, v, s, causal, out_fp32=True)
+    o32, lse32, _, _ = _ops.fwd(q, k, v, s, causal, out_fp32=True)
     Or, lser, mr, lr = O.forward(qc, kc, vc, s, causal)
     close(o, Or, dt, "O")
-    close(o32, Or, dt, "O(fp32 out)")
-    torch.testing.assert_close(lse.double().cpu(), lser, **stat_tol(dt))
-    torch.testing.assert_close(m.double().cpu(), mr, rtol=1e-5, atol=1e-5)
-    torch.testing.assert_close(l.double().cpu(), lr, **stat_tol(dt))
+    torch.testing.assert_close(o32.double().cpu(), Or, **f32_out, msg=lambda m_: f"O(fp32 out): {m_}")
+    torch.testing.assert_close(lse.double().cpu(), lser, **lse_tol, msg=lambda m_: f"lse: {m_}")
+    torch.testing.assert_close(lse32.double().cpu(), lser, **lse_tol, msg=lambda m_: f"lse(fp32 out): {m_}")
+    torch.testing.assert_close(m.double().cpu(), mr, rtol=1e-5, atol=1e-5, msg=lambda m_: f"m: {m_}")
+    torch.testing.assert_close(l.double().cpu(), lr, **stat_tol(dt), msg=lambda m_: f"l: {m_}")
 
-    dq, dk, dv, delta = _ops.bwd(q, k, v, o, lse, do, s, causal)
+    # the backward as the autograd operator runs it: the forward's O residual and row maxima
+    _, _, _, o_lo = _ops.fwd_for_backward(q, k, v, s, causal)
+    dq, dk, dv, delta = _ops.bwd(q, k, v, o, lse, do, s, causal, o_lo=o_lo, row_max=m)
     ref = O.backward(qc, kc, vc, doc, s, causal)
     for name, a, b in zip(("dQ", "dK", "dV"), (dq, dk, dv), ref):
         close(a, b, dt, name)
-    close(delta, (doc * o.double().cpu()).sum(-1), torch.float32, "delta")
-
-    sq, sk, sv = _ops.bwd_from_stats(q, k, v, do, lse, s, causal, True, True, True)
-    for name, a, b in zip(("dQ(stats)", "dK(stats)", "dV(stats)"), (sq, sk, sv), ref):
+    o_full = o.double().cpu() + (0 if o_lo is None else o_lo.double().cpu())
+    close(delta, (doc * o_full).sum(-1), torch.float32, "delta")
+    # without row maxima every 16-bit row takes two-term operands
+    aq, ak, av, _ = _ops.bwd(q, k, v, o, lse, do, s, causal, o_lo=o_lo)
+    for name, a, b in zip(("dQ(all split)", "dK(all split)", "dV(all split)"), (aq, ak, av), ref):
         close(a, b, dt, name)
-    _, _, dv_only = _ops.bwd_from_stats(q, k, None, do, lse, s, causal, False, False, True)
-    close(dv_only, ref[2], dt, "dV(no v)")
+
+    # the reference's explicit frozen-stats backward: P = exp(S - lse) for exactly the lse it is given
+    fref = O.frozen_backward(qc, kc, vc, doc, lse.double().cpu(), s, causal)
+    if dt == torch.float32 and fp32_ref_err is not None:
+        # the same formula in float32 arithmetic (exp(S - lse) with S, lse ~ 30 loses ~2^-24 * 30 relative)
+        f32 = O.frozen_backward(qc, kc, vc, doc, lse.double().cpu(), s, causal, dtype=torch.float32)
+        for name, a_, b_ in zip(("dQ(stats)", "dK(stats)", "dV(stats)"), f32, fref):
+            fp32_ref_err[name] = float((a_.double() - b_).abs().max())
+        fp32_ref_err["dV(no v)"] = fp32_ref_err["dV(stats)"]
+    sq, sk, sv = _ops.bwd_from_stats(q, k, v, do, lse, s, causal, True, True, True, row_max=m)
+    for name, a, b in zip(("dQ(stats)", "dK(stats)", "dV(stats)"), (sq, sk, sv), fref):
+        close(a, b, dt, name)
+    _, _, dv_only = _ops.bwd_from_stats(q, k, None, do, lse, s, causal, False, False, True, row_max=m)
+    close(dv_only, fref[2], dt, "dV(no v)")
+    # normalised row term: the exact softmax gradient from the operator's own lse
+    nq, nk, nv = _ops.bwd_from_stats(q, k, v, do, lse, s, causal, True, True, True, row_max=m, normalize=True)
+    for name, a, b in zip(("dQ(stats, normalised)", "dK(stats, normalised)", "dV(stats, normalised)"), (nq, nk, nv), ref):
+        close(a, b, dt, name)
 
     jr = O.jvp(qc, kc, vc, tqc, tkc, tvc, s, causal)
     close(_ops.jvp(q, k, v, o, lse, tq, tk, tv, s, causal), jr, dt, "JVP(saved O)")
@@ -287,8 +335,8 @@ def test_config2_full_size(dt, hip_device):
     v, vc = make((B, H, S, D), dt, dev, 13)
     do, doc = make((B, H, S, D), dt, dev, 14)
     s = 1 / 8.0
-    o, lse, _, _ = _ops.fwd(q, k, v, s, False)
-    dq, dk, dv, _ = _ops.bwd(q, k, v, o, lse, do, s, False)
+    o, lse, m, o_lo = _ops.fwd_for_backward(q, k, v, s, False)
+    dq, dk, dv, _ = _ops.bwd(q, k, v, o, lse, do, s, False, o_lo=o_lo, row_max=m)
     for b, h in ((0, 0), (3, 15)):
         sl = (slice(b, b + 1), slice(h, h + 1))
         Or, lser, _, _ = O.forward(qc[sl], kc[sl], vc[sl], s)
@@ -317,8 +365,8 @@ def test_config3_causal_long_sequence(hip_device):
     v, vc = make((B, H, S, D), dt, dev, 23, std=0.5)
     do, doc = make((B, H, S, D), dt, dev, 24)
     s = 1 / math.sqrt(D)
-    o, lse, _, _ = _ops.fwd(q, k, v, s, True)
-    dq, dk, dv, _ = _ops.bwd(q, k, v, o, lse, do, s, True)
+    o, lse, m, o_lo = _ops.fwd_for_backward(q, k, v, s, True)
+    dq, dk, dv, _ = _ops.bwd(q, k, v, o, lse, do, s, True, o_lo=o_lo, row_max=m)
     h = 7
     sl = (slice(0, 1), slice(h, h + 1))
     Or, _, _, _ = O.forward(qc[sl], kc[sl], vc[sl], s, True)
@@ -344,8 +392,8 @@ def test_large_grids_ragged(S, H, causal, hip_device):
     v, vc = make((B, H, S, D), dt, dev, 33)
     do, doc = make((B, H, S, D), dt, dev, 34)
     s = 1 / 8.0
-    o, lse, _, _ = _ops.fwd(q, k, v, s, causal)
-    dq, dk, dv, _ = _ops.bwd(q, k, v, o, lse, do, s, causal)
+    o, lse, m, o_lo = _ops.fwd_for_backward(q, k, v, s, causal)
+    dq, dk, dv, _ = _ops.bwd(q, k, v, o, lse, do, s, causal, o_lo=o_lo, row_max=m)
     for b, h in ((0, 1), (B - 1, H - 1)):
         sl = (slice(b, b + 1), slice(h, h + 1))
         for name, a, r in zip(("dQ", "dK", "dV"), (dq[sl], dk[sl], dv[sl]),

@@ -1,0 +1,233 @@
+"""GPU parity in the regimes where 16-bit arithmetic is most exposed, against the float64 oracle.
+
+* Peaked rows: q, k ~ N(0, std^2) with std 2 and 3 at head dims 64 and 128, so scaled scores have a spread
+  of ~4-9 and most of a row's probability sits on a few keys (what trained attention produces).
+* Rows whose maximum score lies in a late key tile, 20+ nats above everything before it: the forward kernels'
+  online-softmax rescaling (the exact path of the pipelined kernel, the lazy rescale of the general kernel)
+  runs only on such rows. tests/test_online_softmax_emulation.py shows on the CPU, on the same inputs, that a
+  wrong rescale factor would fail these checks and pass every N(0, 1) case.
+* Few keys per row with many queries (M = 1-18, or causal rows that see only the first keys): each dK/dV
+  element sums hundreds of terms with P = O(1). The cases are those a random sweep of every entry point
+  (seeds 1000 + index, the generator of test_gpu_parity._check_all_entry_points) once failed.
+* The frozen-stats JVP with stats that are not the operator's own (m + 0.1, 1.3 l): P = exp(S - m) / l is
+  held as given (reference theria/attention/triton_sdpa_backward.py:488-503).
+* Broadcast operands (row stride 0), which reach the operator as gradients of reductions.
+
+Bars: as test_gpu_parity (float32 1e-5 abs/rel; 16-bit outputs rtol = atol = 2e-2; float32 outputs of
+16-bit inputs 2e-2 absolute), except that a float32 quantity may be off by twice the error that theria's own
+pure-PyTorch path makes in float32 on the same inputs where that exceeds 1e-5: on peaked rows float32
+arithmetic itself misses 1e-5 against float64 (G_Q 2.9e-5 and G_K 3.7e-5 for textbook attention
+differentiated by torch.autograd at q, k ~ N(0, 9), D = 32).
+"""
+
+import math
+
+import pytest
+import torch
+
+from inputs_planted import peaked, planted_late_key, randn
+from oracle import sdpa_oracle as O
+from test_gpu_parity import _ids, check_entry_points_on, close
+from theria_amd import _ops
+from theria_amd.attention import explicit
+from theria_amd.autograd.hip_sdpa import hip_sdpa
+
+pytestmark = pytest.mark.gpu
+
+
+def fp32_reference_errors(q, k, v, do, tq, tk, tv, causal):
+    """Largest error against the float64 oracle of theria's pure-PyTorch path run in float32 (textbook
+    attention, theria/attention/reference_attention.py:9-19, differentiated by torch.autograd and torch.func),
+    for each quantity the parity check looks at."""
+    s = 1 / math.sqrt(q.shape[-1])
+    qf, kf, vf, dof, tqf, tkf, tvf = (t.float() for t in (q, k, v, do, tq, tk, tv))
+
+    def attn(q_, k_, v_):
+        S = q_ @ k_.transpose(-2, -1) * s
+        if causal:
+            S = S.masked_fill(~torch.ones(S.shape[-2:], dtype=torch.bool).tril(), float("-inf"))
+        return torch.softmax(S, -1) @ v_
+
+    qr, kr, vr = (t.clone().requires_grad_(True) for t in (qf, kf, vf))
+    o = attn(qr, kr, vr)
+    g = torch.autograd.grad(o, (qr, kr, vr), dof, create_graph=True)
+    hh = torch.autograd.grad(g, (qr, kr, vr, ), (tqf, tkf, tvf), retain_graph=True)
+    _, jv = torch.func.jvp(attn, (qf, kf, vf), (tqf, tkf, tvf))
+    d64 = [t.double() for t in (q, k, v, do, tq, tk, tv)]
+    Or = O.forward(*d64[:3], s, causal)[0]
+    gr = O.backward(*d64[:4], s, causal)
+    Gr = O.double_backward(*d64, s, causal)
+    jr = O.jvp(*d64[:3], *d64[4:], s, causal)
+    err = lambda a, b: float((a.detach().double() - b).abs().max())  # noqa: E731
+    out = {"O": err(o, Or), "JVP": err(jv, jr)}
+    out.update({n: err(a, b) for n, a, b in zip(("dQ", "dK", "dV"), g, gr)})
+    out.update({n: err(a, b) for n, a, b in zip(("G_Q", "G_K", "G_V"), hh, Gr[:3])})
+    return out
+
+PEAKED = [
+    # dtype, B, H, T, M, D, causal, std
+    (torch.bfloat16, 1, 2, 300, 300, 64, False, 2.0),
+    (torch.bfloat16, 1, 2, 400, 260, 64, True, 2.0),
+    (torch.float16, 1, 2, 300, 300, 64, False, 2.0),
+    (torch.bfloat16, 1, 2, 260, 300, 128, False, 2.0),
+    (torch.float16, 1, 1, 300, 300, 128, True, 2.0),
+    (torch.float32, 1, 2, 200, 200, 64, False, 2.0),
+    (torch.bfloat16, 1, 2, 300, 300, 64, False, 3.0),
+    (torch.float32, 1, 1, 150, 170, 32, True, 3.0),
+    (torch.bfloat16, 1, 1, 150, 90, 32, False, 3.0),
+]
+
+
+def _pid(c):
+    return _ids(c[:7]) + f"-std{c[7]:g}"
+
+
+@pytest.mark.parametrize("case", PEAKED, ids=[_pid(c) for c in PEAKED])
+def test_peaked_rows_every_entry_point(case, hip_device):
+    dt, B, H, T, M, D, causal, std = case
+    print(f"[peaked] {_pid(case)}", flush=True)
+    q, k, v, do = peaked(B, H, T, M, D, dt, 40, std)
+    tq, tk, tv = (randn(t.shape, 50 + i, 1.0, dt) for i, t in enumerate((q, k, v)))
+    ref_err = fp32_reference_errors(q, k, v, do, tq, tk, tv, causal) if dt == torch.float32 else None
+    check_entry_points_on(hip_device, dt, causal, q, k, v, do, tq, tk, tv, fp32_ref_err=ref_err)
+
+
+PLANTED = [
+    # dtype, B, H, T, M, D, causal, planted key, gap (nats)
+    # pipelined forward (16-bit, head dim 40..128, more than 128 queries): 64-key tiles
+    (torch.bfloat16, 1, 2, 300, 300, 64, False, 290, 24.0),
+    (torch.bfloat16, 1, 2, 300, 330, 64, False, 140, 30.0),
+    (torch.float16, 1, 1, 260, 260, 128, False, 250, 24.0),
+    (torch.bfloat16, 1, 2, 300, 300, 64, True, 100, 24.0),
+    (torch.bfloat16, 1, 1, 520, 520, 48, False, 500, 40.0),
+    # general forward (float32, small head dims, or few queries)
+    (torch.float32, 1, 2, 100, 300, 16, False, 290, 24.0),
+    (torch.float32, 1, 1, 150, 200, 64, True, 70, 24.0),
+    (torch.bfloat16, 1, 2, 100, 300, 32, False, 250, 24.0),
+    (torch.float16, 1, 1, 90, 200, 64, False, 190, 24.0),
+]
+
+
+def _plid(c):
+    return _ids(c[:7]) + f"-key{c[7]}-gap{c[8]:g}"
+
+
+@pytest.mark.parametrize("case", PLANTED, ids=[_plid(c) for c in PLANTED])
+def test_late_row_maximum_rescales(case, hip_device):
+    """O, lse, m, l (and the whole operator) on rows whose maximum lies in a late key tile."""
+    dt, B, H, T, M, D, causal, key, gap = case
+    print(f"[late max] {_plid(case)}", flush=True)
+    s = 1 / math.sqrt(D)
+    q, k, v = planted_late_key(B, H, T, M, D, dt, 60, key, gap, s)
+    do, tq, tk, tv = (randn(t.shape, 70 + i, 1.0, dt) for i, t in enumerate((q, q, k, v)))
+    ref_err = fp32_reference_errors(q, k, v, do, tq, tk, tv, causal) if dt == torch.float32 else None
+    check_entry_points_on(hip_device, dt, causal, q, k, v, do, tq, tk, tv, fp32_ref_err=ref_err)
+    # the planted key carries (nearly) all of the probability on rows that can see it with a positive sign
+    o, _, _, _ = _ops.fwd(q.to(hip_device), k.to(hip_device), v.to(hip_device), s, causal, out_fp32=True)
+    rows = [i for i in range(T) if (i // 7) % 2 == 0 and (not causal or i >= key)]
+    torch.testing.assert_close(o[:, :, rows].cpu(), v[:, :, key : key + 1].float().expand(B, H, len(rows), D),
+                               rtol=0, atol=2e-2)
+
+
+# Cases a random sweep once failed (seed = 1000 + index of the sweep); few keys per row or few visible keys.
+FEW_KEY_SWEEP = [
+    ((torch.bfloat16, 2, 2, 452, 1, 88, True), 1065),
+    ((torch.bfloat16, 1, 2, 501, 8, 56, False), 1090),
+    ((torch.bfloat16, 1, 3, 452, 8, 112, False), 1199),
+    ((torch.bfloat16, 1, 2, 73, 4, 80, False), 1218),
+    ((torch.bfloat16, 1, 2, 343, 12, 56, True), 1337),
+    ((torch.bfloat16, 2, 2, 430, 85, 128, True), 1364),
+    ((torch.bfloat16, 2, 1, 336, 7, 80, False), 1166),
+    ((torch.bfloat16, 1, 2, 191, 191, 88, True), 1254),
+    ((torch.bfloat16, 2, 2, 324, 2, 88, False), 1266),
+    ((torch.bfloat16, 2, 1, 474, 4, 48, False), 1324),
+    ((torch.float32, 2, 1, 876, 5, 80, False), 1379),
+    ((torch.bfloat16, 2, 2, 769, 191, 64, True), 1520),
+    ((torch.bfloat16, 2, 2, 709, 149, 48, True), 1554),
+    ((torch.bfloat16, 1, 3, 791, 14, 96, True), 1664),
+    ((torch.float32, 2, 1, 871, 6, 112, True), 1737),
+    ((torch.bfloat16, 1, 2, 576, 6, 40, True), 1793),
+    ((torch.bfloat16, 2, 2, 864, 702, 40, True), 1077),
+    ((torch.bfloat16, 1, 1, 417, 18, 120, True), 1240),
+    ((torch.bfloat16, 1, 3, 590, 443, 48, True), 1265),
+    ((torch.bfloat16, 1, 3, 548, 1, 112, False), 1392),
+    ((torch.bfloat16, 2, 1, 44, 2, 64, False), 1402),
+    ((torch.bfloat16, 2, 2, 302, 7, 128, True), 1481),
+    ((torch.bfloat16, 1, 3, 709, 6, 128, True), 1489),
+    ((torch.bfloat16, 1, 3, 690, 13, 40, True), 1668),
+    ((torch.bfloat16, 1, 2, 173, 5, 104, False), 1729),
+    ((torch.bfloat16, 1, 3, 62, 2, 56, True), 1851),
+    ((torch.bfloat16, 1, 2, 221, 3, 96, True), 1860),
+    ((torch.bfloat16, 1, 1, 863, 8, 104, False), 1881),
+    ((torch.bfloat16, 2, 2, 53, 53, 112, True), 1992),
+    ((torch.bfloat16, 1, 3, 424, 3, 96, True), 2072),
+    ((torch.bfloat16, 1, 3, 380, 602, 48, True), 2194),
+]
+
+
+@pytest.mark.parametrize("case,seed", FEW_KEY_SWEEP, ids=[f"{_ids(c)}-s{s}" for c, s in FEW_KEY_SWEEP])
+def test_few_keys_per_row_sweep_cases(case, seed, hip_device):
+    print(f"[few keys] {_ids(case)} seed {seed}", flush=True)
+    dt, B, H, T, M, D, causal = case
+    shapes = [(B, H, T, D), (B, H, M, D), (B, H, M, D), (B, H, T, D), (B, H, T, D), (B, H, M, D), (B, H, M, D)]
+    ts = [torch.randn(*sh, generator=torch.Generator().manual_seed(seed + i)).to(dt) for i, sh in enumerate(shapes)]
+    ref_err = fp32_reference_errors(*ts, causal) if dt == torch.float32 else None
+    check_entry_points_on(hip_device, dt, causal, *ts, fp32_ref_err=ref_err)
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("D", [64, 32])
+def test_frozen_jvp_takes_the_given_stats(dt, D, hip_device):
+    """sdpa_jvp(q, k, v, dq, dk, dv, m, l, scale) with perturbed stats equals the frozen-stats formula with
+    exactly those stats, and differs from the JVP at the exact stats."""
+    B, H, T, M = 1, 2, 200, 260
+    print(f"[frozen jvp] {dt} D{D}", flush=True)
+    q, k, v, tq, tk, tv = (randn(sh, 80 + i, 1.0, dt) for i, sh in enumerate([(B, H, T, D), (B, H, M, D), (B, H, M, D)] * 2))
+    s = 1 / math.sqrt(D)
+    dev = hip_device
+    _, _, m, l = _ops.fwd(q.to(dev), k.to(dev), v.to(dev), s, False, stats=True)
+    mp, lp = m + 0.1, l * 1.3
+    out = explicit.sdpa_jvp(*(t.to(dev) for t in (q, k, v, tq, tk, tv)), mp, lp, s)
+    ref = O.frozen_jvp(*(t.double() for t in (q, k, v, tq, tk, tv)), mp.cpu(), lp.cpu(), s)
+    close(out, ref, dt, "frozen JVP (m + 0.1, 1.3 l)")
+    exact = O.jvp(*(t.double() for t in (q, k, v, tq, tk, tv)), s)
+    assert float((ref - exact).abs().max()) > 0.1, "the perturbation must change the frozen JVP"
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_broadcast_row_operands(D, hip_device):
+    """Operands whose row stride is 0: the upstream gradient of O.sum(dim=2) (dO broadcast over the query
+    rows), a tangent broadcast over the rows (JVP) and a broadcast cotangent (double backward)."""
+    dev = hip_device
+    dt = torch.bfloat16
+    B, H, T, M = 2, 2, 300, 280
+    print(f"[broadcast rows] D{D}", flush=True)
+    q, k, v = (randn(sh, 90 + i, 1.0, dt) for i, sh in enumerate([(B, H, T, D), (B, H, M, D), (B, H, M, D)]))
+    s = 1 / math.sqrt(D)
+    qd, kd, vd = (t.to(dev).requires_grad_(True) for t in (q, k, v))
+    w = randn((B, H, D), 94, 1.0, dt)
+    # the gradient of O.sum(dim=2) reaches the operator as w expanded over the rows: strides (H D, D, 0, 1)
+    grads = torch.autograd.grad(hip_sdpa(qd, kd, vd).sum(dim=2), (qd, kd, vd), w.to(dev))
+    do = w.double().unsqueeze(2).expand(B, H, T, D)
+    ref = O.backward(q.double(), k.double(), v.double(), do, s)
+    for name, a, b in zip(("dQ", "dK", "dV"), grads, ref):
+        close(a, b, dt, f"{name} of O.sum(dim=2)")
+    # explicit broadcast views through the ops layer
+    row = randn((B, H, 1, D), 95, 1.0, dt)
+    do_b = row.to(dev).expand(B, H, T, D)
+    tk_b = randn((B, H, 1, D), 96, 1.0, dt).to(dev).expand(B, H, M, D)
+    assert do_b.stride(2) == 0 and tk_b.stride(2) == 0
+    o, lse, _, _ = _ops.fwd(qd.detach(), kd.detach(), vd.detach(), s, False)
+    dq, dk, dv, delta = _ops.bwd(qd.detach(), kd.detach(), vd.detach(), o, lse, do_b, s, False)
+    refb = O.backward(q.double(), k.double(), v.double(), do_b.double().cpu(), s)
+    for name, a, b in zip(("dQ", "dK", "dV"), (dq, dk, dv), refb):
+        close(a, b, dt, f"{name} (dO row stride 0)")
+    tq = randn((B, H, T, D), 97, 1.0, dt)
+    jr = O.jvp(q.double(), k.double(), v.double(), tq.double(), tk_b.double().cpu(), None, s)
+    close(_ops.jvp(qd.detach(), kd.detach(), vd.detach(), o, lse, tq.to(dev), tk_b, None, s, False), jr, dt,
+          "JVP (tk row stride 0)")
+    G = _ops.bwd_bwd(qd.detach(), kd.detach(), vd.detach(), o, do_b, lse, delta, tq.to(dev), tk_b, None, s, False)
+    Gr = O.double_backward(q.double(), k.double(), v.double(), do_b.double().cpu(), tq.double(),
+                           tk_b.double().cpu(), None, s)
+    for name, a, b in zip(("G_Q", "G_K", "G_V", "G_dO"), G, Gr):
+        close(a, b, dt, f"{name} (dO, gK row stride 0)")

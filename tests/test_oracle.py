@@ -90,6 +90,32 @@ def test_frozen_jvp_equals_true_jvp_at_exact_stats():
     torch.testing.assert_close(O.frozen_jvp(q, k, v, tq, tk, tv, m2, l2, s), centred, rtol=1e-12, atol=1e-12)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_frozen_backward_closed_form(causal):
+    """frozen_backward at the exact lse is the true gradient; with lse + c (a per-row shift, i.e. l scaled by
+    e^c) P is scaled by e^-c per row, and the frozen formula then differs from the true gradient by the
+    closed form below (dS_f = e^-c (dS + (1 - e^-c) z P), with z = rowsum(dP P) of the true P)."""
+    q, k, v = _qkv(2, 2, 6, 7, 5, seed=4)
+    do = _rand(*q.shape, seed=8)
+    s = 1 / math.sqrt(5)
+    _, lse, _, _ = O.forward(q, k, v, s, causal)
+    ref = O.backward(q, k, v, do, s, causal)
+    for a_, b_ in zip(O.frozen_backward(q, k, v, do, lse, s, causal), ref):
+        torch.testing.assert_close(a_, b_, rtol=1e-12, atol=1e-12)
+    c = _rand(*lse.shape, seed=9).abs() * 0.5
+    dq_f, dk_f, dv_f = O.frozen_backward(q, k, v, do, lse + c, s, causal)
+    e = torch.exp(-c).unsqueeze(-1)
+    P = O.probs(q, k, s, causal)
+    z = ((do @ v.transpose(-2, -1)) * P).sum(-1, keepdim=True)
+    dq_t, dk_t, dv_t = ref
+    torch.testing.assert_close(dv_f, O.backward(q, k, v, do * e, s, causal)[2], rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(dq_f, e * (dq_t + s * (1 - e) * z * (P @ k)), rtol=1e-12, atol=1e-12)
+    dS = P * ((do @ v.transpose(-2, -1)) - z)
+    torch.testing.assert_close(dk_f, s * ((e * (dS + (1 - e) * z * P)).transpose(-2, -1) @ q), rtol=1e-12, atol=1e-12)
+    # the shift term is not negligible here: a frozen formula without it (e^-c times the true dQ) is far off
+    assert not torch.allclose(dq_f, e * dq_t, rtol=1e-6, atol=1e-6)
+
+
 @pytest.mark.parametrize("B,H,T,M,D,causal", CASES)
 def test_double_backward_matches_autograd(B, H, T, M, D, causal):
     q, k, v = (t.requires_grad_(True) for t in _qkv(B, H, T, M, D))

@@ -16,7 +16,7 @@ import torch  # noqa: F401  (must be imported first: it loads the HIP runtime th
 
 # THERIA_SDPA_LIB overrides the in-tree build (e.g. a library installed elsewhere).
 LIB_PATH = Path(os.environ.get("THERIA_SDPA_LIB") or Path(__file__).resolve().parent / "lib" / "libtheria_sdpa.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 OK, ERR_CONTRACT, ERR_HIP = 0, 1, 2
@@ -58,12 +58,18 @@ _FP = ctypes.POINTER(ctypes.c_float)
 SIGNATURES = {
     "theria_abi_version": ([], ctypes.c_int),
     "theria_last_error": ([], ctypes.c_char_p),
-    "theria_sdpa_fwd": ([_PR, _TV, _TV, _TV, _TV, ctypes.c_int32, _P, _P, _P, _P], ctypes.c_int),
-    "theria_sdpa_bwd": ([_PR, _TV, _TV, _TV, _TV, ctypes.c_int32, _TV, _P, _P, _TV, _TV, _TV, _P], ctypes.c_int),
-    "theria_sdpa_bwd_dq": ([_PR, _TV, _TV, _TV, _TV, ctypes.c_int32, _TV, _P, _P, _TV, _P], ctypes.c_int),
-    "theria_sdpa_bwd_dkdv": ([_PR, _TV, _TV, _TV, _TV, _P, _P, _TV, _TV, _P], ctypes.c_int),
-    "theria_sdpa_bwd_from_stats": ([_PR, _TV, _TV, _TV, _TV, _P, _P, _TV, _TV, _TV, _P], ctypes.c_int),
-    "theria_sdpa_jvp": ([_PR, _TV, _TV, _TV, _TV, _P, _TV, _TV, _TV, _TV, _P], ctypes.c_int),
+    "theria_sdpa_fwd": ([_PR, _TV, _TV, _TV, _TV, ctypes.c_int32, _TV, _P, _P, _P, _P], ctypes.c_int),
+    "theria_sdpa_bwd": (
+        [_PR, _TV, _TV, _TV, _TV, ctypes.c_int32, _TV, _TV, _P, _P, _P, _TV, _TV, _TV, _P],
+        ctypes.c_int,
+    ),
+    "theria_sdpa_bwd_dq": ([_PR, _TV, _TV, _TV, _TV, ctypes.c_int32, _TV, _TV, _P, _P, _P, _TV, _P], ctypes.c_int),
+    "theria_sdpa_bwd_dkdv": ([_PR, _TV, _TV, _TV, _TV, _P, _P, _P, _TV, _TV, _P], ctypes.c_int),
+    "theria_sdpa_bwd_from_stats": (
+        [_PR, _TV, _TV, _TV, _TV, _P, _P, _P, _TV, _TV, _TV, ctypes.c_int32, _P],
+        ctypes.c_int,
+    ),
+    "theria_sdpa_jvp": ([_PR, _TV, _TV, _TV, _TV, _P, _TV, _TV, _TV, _TV, ctypes.c_int32, _P], ctypes.c_int),
     "theria_sdpa_bwd_bwd": (
         [_PR, _TV, _TV, _TV, _TV, _TV, _P, _P, _TV, _TV, _TV, _TV, _TV, _TV, _TV, _P, _P],
         ctypes.c_int,

@@ -145,27 +145,46 @@ def _like_rows(t: torch.Tensor | None, ref: torch.Tensor, rows: int, name: str) 
 
 def fwd(q, k, v, scale: float, causal: bool, out_fp32: bool = False, stats: bool = False):
     """O, lse (and the reference's m, l when stats=True). O is float32 when out_fp32."""
+    o, lse, m, l, _ = _fwd(q, k, v, scale, causal, out_fp32, stats, stats, False)
+    return o, lse, m, l
+
+
+def fwd_for_backward(q, k, v, scale: float, causal: bool, out_fp32: bool = False):
+    """(O, lse, m, O_lo): the forward plus what the backward takes from it. m (row maxima) marks the peaked
+    rows whose 16-bit backward products use two-term operands; O_lo (16-bit inputs with a 16-bit O, else
+    None) is the rounding residual of O, so that the backward's row term dO . O has float32 accuracy."""
+    residual = q.dtype != torch.float32 and not out_fp32
+    o, lse, m, _, o_lo = _fwd(q, k, v, scale, causal, out_fp32, True, False, residual)
+    return o, lse, m, o_lo
+
+
+def _fwd(q, k, v, scale, causal, out_fp32, want_m, want_l, residual):
     check_inputs(q, k, v)
     q, k, v = _rowmajor(q), _rowmajor(k), _rowmajor(v)
     B, H, T, D = q.shape
     dev = q.device
     o = torch.empty((B, H, T, D), dtype=torch.float32 if out_fp32 else q.dtype, device=dev)
+    o_lo = torch.empty((B, H, T, D), dtype=q.dtype, device=dev) if residual else None
     lse = torch.empty((B, H, T), dtype=torch.float32, device=dev)
-    m = torch.empty_like(lse) if stats else None
-    l = torch.empty_like(lse) if stats else None
+    m = torch.empty_like(lse) if want_m else None
+    l = torch.empty_like(lse) if want_l else None
     lib = _lib.load()
     prob = _problem(q, k, scale, causal)
     with _OnDevice(dev):
         rc = lib.theria_sdpa_fwd(
-            ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(o), 1 if out_fp32 else 0, _fp(lse), _fp(m), _fp(l),
-            _stream(dev),
+            ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(o), 1 if out_fp32 else 0, _tv(o_lo), _fp(lse), _fp(m),
+            _fp(l), _stream(dev),
         )
     _lib.check(rc, "theria_sdpa_fwd")
-    return o, lse, m, l
+    return o, lse, m, l, o_lo
 
 
-def bwd(q, k, v, o, lse, do, scale: float, causal: bool, need_dq: bool = True, need_dk: bool = True):
-    """dQ, dK, dV (input dtype) and the row term delta = rowsum(dO * O) (float32)."""
+def bwd(q, k, v, o, lse, do, scale: float, causal: bool, need_dq: bool = True, need_dk: bool = True,
+        o_lo=None, row_max=None):
+    """dQ, dK, dV (input dtype) and the row term delta = rowsum(dO * O) (float32).
+
+    o_lo, row_max: the forward's O residual and row maxima (fwd_for_backward). Without row_max every row
+    of a 16-bit problem takes two-term operands (exact, slower)."""
     check_inputs(q, k, v)
     q, k, v = _rowmajor(q), _rowmajor(k), _rowmajor(v)
     B, H, T, D = q.shape
@@ -178,6 +197,11 @@ def bwd(q, k, v, o, lse, do, scale: float, causal: bool, need_dq: bool = True, n
     if not o_f32 and o.dtype != q.dtype:
         o = o.to(q.dtype)
     lse = lse.contiguous()
+    row_max = None if row_max is None else row_max.contiguous()
+    if o_lo is not None:
+        if o_f32 or o_lo.dtype != q.dtype or tuple(o_lo.shape) != (B, H, T, D):
+            raise AssertionError("o_lo must be the (B,H,T,D) residual of a 16-bit O in the input dtype")
+        o_lo = _rowmajor(o_lo)
     dev = q.device
     delta = torch.empty((B, H, T), dtype=torch.float32, device=dev)
     dq = torch.empty((B, H, T, D), dtype=q.dtype, device=dev) if need_dq else None
@@ -185,31 +209,38 @@ def bwd(q, k, v, o, lse, do, scale: float, causal: bool, need_dq: bool = True, n
     dv = torch.empty((B, H, M, D), dtype=q.dtype, device=dev)
     prob = _problem(q, k, scale, causal)
     with _OnDevice(dev):
-        bwd_dq(prob, q, k, v, o, o_f32, do, lse, delta, dq)
-        bwd_dkdv(prob, q, k, v, do, lse, delta, dk, dv)
+        bwd_dq(prob, q, k, v, o, o_f32, do, lse, delta, dq, o_lo, row_max)
+        bwd_dkdv(prob, q, k, v, do, lse, delta, dk, dv, row_max)
     return dq, dk, dv, delta
 
 
 # The two backward kernels (theria_sdpa_bwd = bwd_dq then bwd_dkdv), on the current stream of the
 # current device. Arguments are already validated and laid out by bwd().
-def bwd_dq(prob, q, k, v, o, o_f32, do, lse, delta, dq) -> None:
-    """dQ; with o given, delta = rowsum(dO * O) is computed and written, else it is read."""
+def bwd_dq(prob, q, k, v, o, o_f32, do, lse, delta, dq, o_lo=None, row_max=None) -> None:
+    """dQ; with o given, delta = rowsum(dO * (O + O_lo)) is computed and written, else it is read."""
     rc = _lib.load().theria_sdpa_bwd_dq(
-        ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(o), 1 if o_f32 else 0, _tv(do), _fp(lse), _fp(delta),
-        _tv(dq), _stream(q.device),
+        ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(o), 1 if o_f32 else 0, _tv(o_lo), _tv(do), _fp(lse),
+        _fp(row_max), _fp(delta), _tv(dq), _stream(q.device),
     )
     _lib.check(rc, "theria_sdpa_bwd_dq")
 
 
-def bwd_dkdv(prob, q, k, v, do, lse, delta, dk, dv) -> None:
+def bwd_dkdv(prob, q, k, v, do, lse, delta, dk, dv, row_max=None) -> None:
     rc = _lib.load().theria_sdpa_bwd_dkdv(
-        ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(do), _fp(lse), _fp(delta), _tv(dk), _tv(dv), _stream(q.device)
+        ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(do), _fp(lse), _fp(row_max), _fp(delta), _tv(dk), _tv(dv),
+        _stream(q.device),
     )
     _lib.check(rc, "theria_sdpa_bwd_dkdv")
 
 
-def bwd_from_stats(q, k, v, do, lse, scale: float, causal: bool, need_dq: bool, need_dk: bool, need_dv: bool):
-    """Backward from saved statistics only (no O). v may be None when only dV is requested."""
+def bwd_from_stats(q, k, v, do, lse, scale: float, causal: bool, need_dq: bool, need_dk: bool, need_dv: bool,
+                   row_max=None, normalize: bool = False):
+    """Backward from saved statistics only (no O). v may be None when only dV is requested. row_max as in
+    bwd (the reference's saved m).
+
+    normalize=False: the reference's frozen-stats backward (P = exp(S - lse) as given, row term
+    sum_j P_ij dP_ij). normalize=True: the row term of the normalised P, i.e. the exact softmax gradient, for
+    the operator's own lse."""
     check_inputs(q, k, v, require_v=v is not None)
     q, k = _rowmajor(q), _rowmajor(k)
     v = _rowmajor(v)
@@ -217,6 +248,7 @@ def bwd_from_stats(q, k, v, do, lse, scale: float, causal: bool, need_dq: bool, 
     M = k.shape[2]
     do = _like_rows(do, q, T, "dout")
     lse = lse.contiguous()
+    row_max = None if row_max is None else row_max.contiguous()
     dev = q.device
     delta = torch.empty((B, H, T), dtype=torch.float32, device=dev) if v is not None else None
     dq = torch.empty((B, H, T, D), dtype=q.dtype, device=dev) if need_dq else None
@@ -226,15 +258,18 @@ def bwd_from_stats(q, k, v, do, lse, scale: float, causal: bool, need_dq: bool, 
     prob = _problem(q, k, scale, causal)
     with _OnDevice(dev):
         rc = lib.theria_sdpa_bwd_from_stats(
-            ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(do), _fp(lse), _fp(delta), _tv(dq), _tv(dk), _tv(dv),
-            _stream(dev),
+            ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(do), _fp(lse), _fp(row_max), _fp(delta), _tv(dq),
+            _tv(dk), _tv(dv), 1 if normalize else 0, _stream(dev),
         )
     _lib.check(rc, "theria_sdpa_bwd_from_stats")
     return dq, dk, (dv if need_dv else None)
 
 
-def jvp(q, k, v, o, lse, tq, tk, tv, scale: float, causal: bool):
-    """Frozen-stats tangent of O along (tq, tk, tv); o=None rebuilds O from lse inside the kernel."""
+def jvp(q, k, v, o, lse, tq, tk, tv, scale: float, causal: bool, normalize: bool = True):
+    """Tangent of O along (tq, tk, tv) with P rebuilt from lse; o=None rebuilds O inside the kernel.
+
+    normalize=True: the JVP of the exact softmax (P divided by its row sum), for the operator's own lse.
+    normalize=False: the reference's frozen-stats JVP, P = exp(S - lse) held as given (o is then not read)."""
     check_inputs(q, k, v)
     q, k, v = _rowmajor(q), _rowmajor(k), _rowmajor(v)
     B, H, T, D = q.shape
@@ -255,7 +290,7 @@ def jvp(q, k, v, o, lse, tq, tk, tv, scale: float, causal: bool):
     with _OnDevice(dev):
         rc = lib.theria_sdpa_jvp(
             ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(o), _fp(lse), _tv(tq), _tv(tk), _tv(tv), _tv(out),
-            _stream(dev),
+            1 if normalize else 0, _stream(dev),
         )
     _lib.check(rc, "theria_sdpa_jvp")
     return out

@@ -66,34 +66,35 @@ def _lse(m, l):
 def sdpa_bwd_dq(q, k, v, dout, m, l, scale):
     """dQ = scale dS K with P rebuilt from (m, l)."""
     _assert_backward_contract(q, k, v, dout, m, l, require_v=True)
-    dq, _, _ = _ops.bwd_from_stats(q, k, v, dout, _lse(m, l), scale, False, True, False, False)
+    dq, _, _ = _ops.bwd_from_stats(q, k, v, dout, _lse(m, l), scale, False, True, False, False, row_max=m.float())
     return dq
 
 
 def sdpa_bwd_dk(q, k, v, dout, m, l, scale):
     """dK = scale dS^T Q with P rebuilt from (m, l)."""
     _assert_backward_contract(q, k, v, dout, m, l, require_v=True)
-    _, dk, _ = _ops.bwd_from_stats(q, k, v, dout, _lse(m, l), scale, False, False, True, False)
+    _, dk, _ = _ops.bwd_from_stats(q, k, v, dout, _lse(m, l), scale, False, False, True, False, row_max=m.float())
     return dk
 
 
 def sdpa_bwd_dv(q, k, dout, m, l, scale):
     """dV = P^T dO with P rebuilt from (m, l); needs no v (triton_sdpa_backward.py:194)."""
     _assert_backward_contract(q, k, None, dout, m, l, require_v=False)
-    _, _, dv = _ops.bwd_from_stats(q, k, None, dout, _lse(m, l), scale, False, False, False, True)
+    _, _, dv = _ops.bwd_from_stats(q, k, None, dout, _lse(m, l), scale, False, False, False, True, row_max=m.float())
     return dv
 
 
 def sdpa_bwd(q, k, v, dout, m, l, scale):
     """All three gradients in one backward pass: (dq, dk, dv)."""
     _assert_backward_contract(q, k, v, dout, m, l, require_v=True)
-    return _ops.bwd_from_stats(q, k, v, dout, _lse(m, l), scale, False, True, True, True)
+    return _ops.bwd_from_stats(q, k, v, dout, _lse(m, l), scale, False, True, True, True, row_max=m.float())
 
 
 def sdpa_jvp(q, k, v, dq, dk, dv, m, l, scale):
-    """Frozen-stats JVP (docs/phase9.md:30-39): dO = P o (dS - rowsum(dS o P)) V + P dv."""
+    """Frozen-stats JVP (docs/phase9.md:30-39): dO = P o (dS - rowsum(dS o P)) V + P dv, with
+    P = exp(S - m) / l held exactly as given (triton_sdpa_backward.py:488-503)."""
     _assert_jvp_contract(q, k, v, dq, dk, dv, m, l)
-    return _ops.jvp(q, k, v, None, _lse(m, l), dq, dk, dv, scale, False)
+    return _ops.jvp(q, k, v, None, _lse(m, l), dq, dk, dv, scale, False, normalize=False)
 
 
 __all__ = ["sdpa_bwd_dq", "sdpa_bwd_dk", "sdpa_bwd_dv", "sdpa_bwd", "sdpa_jvp"]

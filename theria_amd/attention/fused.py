@@ -9,8 +9,10 @@ Widened contract: D <= 128 (reference: D <= 64) and any strides with a contiguou
 
 from __future__ import annotations
 
+import torch
+
 from .. import _ops
-from ..autograd.hip_sdpa import SDPAOp, hip_sdpa
+from ..autograd.hip_sdpa import SDPABackwardOp, hip_sdpa
 
 
 def _fused_guards(q, k, v) -> None:
@@ -38,17 +40,42 @@ def triton_sdpa_fused(q, k, v, return_stats: bool = False):
     return o
 
 
-class TritonFusedSDPAFunction:
-    """Drop-in for the reference's autograd.Function: ``TritonFusedSDPAFunction.apply(q, k, v)``.
-
-    Returns float32 O like the reference. The graph node is SDPAOp, whose backward is differentiable.
-    """
+class TritonFusedSDPAFunction(torch.autograd.Function):
+    """The reference's autograd.Function (triton_qk.py:372-391): ``TritonFusedSDPAFunction.apply(q, k, v)``
+    returns float32 O. Its backward runs the backward kernels through SDPABackwardOp, which is itself
+    differentiable (double backward on the second-order kernels), and its jvp the JVP kernel; the
+    reference's backward runs under no_grad and drops the second-order terms."""
 
     @staticmethod
-    def apply(q, k, v):
+    def forward(q, k, v):
         _fused_guards(q, k, v)
-        o, _ = SDPAOp.apply(q, k, v, _ops.default_scale(q.shape[-1]), False, True)
-        return o
+        return _ops.fwd_for_backward(q, k, v, _ops.default_scale(q.shape[-1]), False, out_fp32=True)
+
+    @staticmethod
+    def setup_context(ctx, inputs, output):
+        q, k, v = inputs
+        o, lse, m, _ = output
+        ctx.scale = _ops.default_scale(q.shape[-1])
+        ctx.mark_non_differentiable(lse, m)
+        ctx.save_for_backward(q, k, v, o, lse, m)
+        ctx.save_for_forward(q, k, v, o, lse)
+
+    @staticmethod
+    def backward(ctx, do, _dlse, _dm, _dolo):
+        if do is None:
+            return None, None, None
+        q, k, v, o, lse, m = ctx.saved_tensors
+        dq, dk, dv = SDPABackwardOp.apply(q, k, v, o.detach(), lse, do, ctx.scale, False, None, m)
+        return dq, dk, dv
+
+    @staticmethod
+    def jvp(ctx, tq, tk, tv):
+        q, k, v, o, lse = ctx.saved_tensors
+        return _ops.jvp(q, k, v, o, lse, tq, tk, tv, ctx.scale, False, normalize=True).float(), None, None, None
+
+    @classmethod
+    def apply(cls, q, k, v):  # O only, as the reference returns
+        return super().apply(q, k, v)[0]
 
 
 def triton_sdpa_fused_autograd(q, k, v):

@@ -67,11 +67,13 @@ def _differentiable_double_backward(q, k, v, dout, gq, gk, gv, scale: float, cau
 
 
 class SDPABackwardOp(torch.autograd.Function):
-    """(q, k, v, o, lse, dout) -> (dq, dk, dv). o and lse are treated as constants of q, k, v."""
+    """(q, k, v, o, lse, dout, scale, causal, o_lo, row_max) -> (dq, dk, dv). o, lse (and the forward's O
+    residual o_lo and row maxima row_max, which the 16-bit backward uses for its row term and peaked rows) are
+    treated as constants of q, k, v."""
 
     @staticmethod
-    def forward(ctx, q, k, v, o, lse, dout, scale, causal):
-        dq, dk, dv, delta = _ops.bwd(q, k, v, o, lse, dout, scale, causal)
+    def forward(ctx, q, k, v, o, lse, dout, scale, causal, o_lo=None, row_max=None):
+        dq, dk, dv, delta = _ops.bwd(q, k, v, o, lse, dout, scale, causal, o_lo=o_lo, row_max=row_max)
         ctx.save_for_backward(q, k, v, o, lse, dout, delta)
         ctx.scale = scale
         ctx.causal = causal
@@ -81,47 +83,47 @@ class SDPABackwardOp(torch.autograd.Function):
     def backward(ctx, gq, gk, gv):
         q, k, v, o, lse, dout, delta = ctx.saved_tensors
         if gq is None and gk is None and gv is None:
-            return None, None, None, None, None, None, None, None
+            return None, None, None, None, None, None, None, None, None, None
         if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (q, k, v, dout, gq, gk, gv)):
             g_q, g_k, g_v, g_do = _differentiable_double_backward(q, k, v, dout, gq, gk, gv, ctx.scale, ctx.causal)
-            return g_q, g_k, g_v, None, None, g_do, None, None
+            return g_q, g_k, g_v, None, None, g_do, None, None, None, None
         g_q, g_k, g_v, g_do = _ops.bwd_bwd(q, k, v, o, dout, lse, delta, gq, gk, gv, ctx.scale, ctx.causal)
-        return g_q, g_k, g_v, None, None, g_do.to(dout.dtype), None, None
+        return g_q, g_k, g_v, None, None, g_do.to(dout.dtype), None, None, None, None
 
 
 class SDPAOp(torch.autograd.Function):
-    """(q, k, v, scale, causal, out_fp32) -> (o, lse)."""
+    """(q, k, v, scale, causal, out_fp32) -> (o, lse, m, o_lo); m (row maxima) and o_lo (the rounding
+    residual of a 16-bit O, or None) are what the backward takes from the forward."""
 
     @staticmethod
     def forward(q, k, v, scale, causal, out_fp32):
-        o, lse, _, _ = _ops.fwd(q, k, v, scale, causal, out_fp32=out_fp32)
-        return o, lse
+        return _ops.fwd_for_backward(q, k, v, scale, causal, out_fp32=out_fp32)
 
     @staticmethod
     def setup_context(ctx, inputs, output):
         q, k, v, scale, causal, out_fp32 = inputs
-        o, lse = output
+        o, lse, m, o_lo = output
         ctx.scale = scale
         ctx.causal = causal
-        ctx.mark_non_differentiable(lse)
-        ctx.save_for_backward(q, k, v, o, lse)
+        ctx.mark_non_differentiable(*(t for t in (lse, m, o_lo) if t is not None))
+        ctx.save_for_backward(q, k, v, o, lse, m, o_lo)
         ctx.save_for_forward(q, k, v, o, lse)
 
     @staticmethod
-    def backward(ctx, do, _dlse):
+    def backward(ctx, do, _dlse, _dm, _dolo):
         if do is None:
             return None, None, None, None, None, None
-        q, k, v, o, lse = ctx.saved_tensors
-        dq, dk, dv = SDPABackwardOp.apply(q, k, v, o.detach(), lse, do, ctx.scale, ctx.causal)
+        q, k, v, o, lse, m, o_lo = ctx.saved_tensors
+        dq, dk, dv = SDPABackwardOp.apply(q, k, v, o.detach(), lse, do, ctx.scale, ctx.causal, o_lo, m)
         return dq, dk, dv, None, None, None
 
     @staticmethod
     def jvp(ctx, tq, tk, tv, _ts, _tc, _tf):
         q, k, v, o, lse = ctx.saved_tensors
-        to = _ops.jvp(q, k, v, o, lse, tq, tk, tv, ctx.scale, ctx.causal)
+        to = _ops.jvp(q, k, v, o, lse, tq, tk, tv, ctx.scale, ctx.causal, normalize=True)
         if to.dtype != o.dtype:
             to = to.to(o.dtype)
-        return to, None
+        return to, None, None, None
 
 
 def _common_head_dim(q, k, v):
@@ -151,7 +153,7 @@ def hip_sdpa(q, k, v, *, causal: bool = False, scale: float | None = None, out_f
     if scale is None:
         scale = _ops.default_scale(q.shape[-1])
     q, k, v, dv = _common_head_dim(q, k, v)
-    o, _ = SDPAOp.apply(q, k, v, float(scale), bool(causal), bool(out_fp32))
+    o = SDPAOp.apply(q, k, v, float(scale), bool(causal), bool(out_fp32))[0]
     return o if o.shape[-1] == dv else o[..., :dv]
 
 
@@ -160,7 +162,7 @@ def hip_sdpa_with_lse(q, k, v, *, causal: bool = False, scale: float | None = No
     if scale is None:
         scale = _ops.default_scale(q.shape[-1])
     q, k, v, dv = _common_head_dim(q, k, v)
-    o, lse = SDPAOp.apply(q, k, v, float(scale), bool(causal), False)
+    o, lse = SDPAOp.apply(q, k, v, float(scale), bool(causal), False)[:2]
     return (o if o.shape[-1] == dv else o[..., :dv]), lse
 
 
@@ -179,7 +181,7 @@ def hip_sdpa_hvp(q, k, v, vq, vk, vv, *, weight=None, target=None, causal: bool 
     if weight is not None and target is not None:
         raise ValueError("hip_sdpa_hvp: give weight or target, not both")
     with torch.no_grad():
-        o, lse, _, _ = _ops.fwd(q, k, v, float(scale), bool(causal))
+        o, lse, m, o_lo = _ops.fwd_for_backward(q, k, v, float(scale), bool(causal))
         if target is not None:
             dout = (o.float() - target.float()).to(o.dtype)
         elif weight is not None:
@@ -190,7 +192,7 @@ def hip_sdpa_hvp(q, k, v, vq, vk, vv, *, weight=None, target=None, causal: bool 
         hq, hk, hv, g_do = _ops.bwd_bwd(q, k, v, o, dout, lse, delta, vq, vk, vv, float(scale), bool(causal))
         if target is None:
             return hq, hk, hv
-        jq, jk, jv, _ = _ops.bwd(q, k, v, o, lse, g_do.to(o.dtype), float(scale), bool(causal))
+        jq, jk, jv, _ = _ops.bwd(q, k, v, o, lse, g_do.to(o.dtype), float(scale), bool(causal), o_lo=o_lo, row_max=m)
         return hq + jq, hk + jk, hv + jv
 
 

@@ -4,7 +4,10 @@ Usage: ``python -m theria_amd.build`` (or ``theria_amd.build.build()``). Every `
 compiled for gfx950 in parallel into ``_build/`` at the repository root and linked into
 ``theria_amd/lib/libtheria_sdpa.so``. The library links against the HIP runtime by its soname
 (libamdhip64.so.7), so inside a process that already imported torch it binds to the runtime torch
-loaded: one HIP runtime per process.
+loaded: one HIP runtime per process. Only the C ABI (``theria_*``) is exported: the host stubs of the
+kernel templates are weak symbols, and exported they would bind to another copy of this library loaded
+into the same process (an older build, say), whose launches would then run these kernels with that
+build's parameter structs.
 """
 
 from __future__ import annotations
@@ -40,6 +43,10 @@ COMMON_FLAGS = [
 ]
 
 
+# Linker version script: export the C ABI, keep every other symbol local to the library.
+EXPORTS = "{\n  global: theria_*;\n  local: *;\n};\n"
+
+
 def _hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and Path(cand).exists():
@@ -70,7 +77,10 @@ def build(verbose: bool = True, jobs: int | None = None) -> Path:
     with _cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(lambda s: _compile(hipcc, s), sources))
     tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    vmap = BUILD_DIR / "exports.map"
+    vmap.write_text(EXPORTS)
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", f"-Wl,--version-script={vmap}", "-o", str(tmp),
+           *map(str, objs)]
     res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{res.stdout}")

@@ -126,8 +126,9 @@ THERIA_API int theria_abi_version(void) { return THERIA_SDPA_ABI_VERSION; }
 THERIA_API const char* theria_last_error(void) { return g_last_error.c_str(); }
 
 THERIA_API int theria_sdpa_fwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
-                               const theria_tensor_t* v, const theria_tensor_t* o, int32_t o_is_f32, float* lse,
-                               float* row_max, float* row_sum, void* stream) {
+                               const theria_tensor_t* v, const theria_tensor_t* o, int32_t o_is_f32,
+                               const theria_tensor_t* o_lo, float* lse, float* row_max, float* row_sum,
+                               void* stream) {
   theria::Shape s;
   std::string err;
   if (!shape_from(p, s, err)) return fail(THERIA_ERR_CONTRACT, err);
@@ -136,7 +137,10 @@ THERIA_API int theria_sdpa_fwd(const theria_sdpa_problem_t* p, const theria_tens
   c.kview(k, "k", true);
   c.kview(v, "v", true);
   c.qview(o, "o", true);
+  c.qview(o_lo, "o_lo", false);
   c.need(lse != nullptr || !c.q_rows, "lse is required");
+  c.need(!(o_lo && o_lo->data) || (s.dtype != THERIA_DTYPE_F32 && !o_is_f32),
+         "o_lo is the residual of a 16-bit O (16-bit inputs, o_is_f32 = 0)");
   if (o_is_f32 && o && (o->stride_b % 4 || o->stride_h % 4 || o->stride_row % 4)) c.vec = false;
   if (!c.err.empty()) return fail(THERIA_ERR_CONTRACT, c.err);
   s.vec = c.vec;
@@ -147,6 +151,7 @@ THERIA_API int theria_sdpa_fwd(const theria_sdpa_problem_t* p, const theria_tens
   fp.k = cv(k);
   fp.v = cv(v);
   fp.o = mv(o);
+  fp.o_lo = mv(o_lo);
   fp.o_f32 = o_is_f32 != 0;
   fp.lse = lse;
   fp.row_max = row_max;
@@ -155,8 +160,9 @@ THERIA_API int theria_sdpa_fwd(const theria_sdpa_problem_t* p, const theria_tens
 }
 
 static int run_dq(const theria::Shape& s, const theria_tensor_t* q, const theria_tensor_t* k,
-                  const theria_tensor_t* v, const theria_tensor_t* o, bool o_f32, const theria_tensor_t* dout,
-                  const float* lse, float* delta, const theria_tensor_t* dq, hipStream_t st) {
+                  const theria_tensor_t* v, const theria_tensor_t* o, bool o_f32, const theria_tensor_t* o_lo,
+                  const theria_tensor_t* dout, const float* lse, const float* row_max, float* delta,
+                  const theria_tensor_t* dq, hipStream_t st) {
   theria::DqParams dp{};
   dp.s = s;
   dp.q = cv(q);
@@ -164,16 +170,19 @@ static int run_dq(const theria::Shape& s, const theria_tensor_t* q, const theria
   dp.v = cv(v);
   dp.dout = cv(dout);
   dp.o = cv(o);
+  dp.o_lo = (o && o->data) ? cv(o_lo) : theria::View{nullptr, 0, 0, 0};
   dp.o_f32 = o_f32;
   dp.lse = lse;
+  dp.row_max = row_max;
   dp.delta = delta;
   dp.dq = mv(dq);
   return hip_status(theria::launch_bwd_dq(dp, st), "theria_sdpa_bwd_dq");
 }
 
 static int run_dkdv(const theria::Shape& s, const theria_tensor_t* q, const theria_tensor_t* k,
-                    const theria_tensor_t* v, const theria_tensor_t* dout, const float* lse, const float* delta,
-                    const theria_tensor_t* dk, const theria_tensor_t* dv, bool dv_only, hipStream_t st) {
+                    const theria_tensor_t* v, const theria_tensor_t* dout, const float* lse, const float* row_max,
+                    const float* delta, const theria_tensor_t* dk, const theria_tensor_t* dv, bool dv_only,
+                    hipStream_t st) {
   theria::DkdvParams kp{};
   kp.s = s;
   kp.q = cv(q);
@@ -181,6 +190,7 @@ static int run_dkdv(const theria::Shape& s, const theria_tensor_t* q, const ther
   kp.v = cv(v);
   kp.dout = cv(dout);
   kp.lse = lse;
+  kp.row_max = row_max;
   kp.delta = delta;
   kp.dk = mv(dk);
   kp.dv = mv(dv);
@@ -190,8 +200,8 @@ static int run_dkdv(const theria::Shape& s, const theria_tensor_t* q, const ther
 
 THERIA_API int theria_sdpa_bwd_dq(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
                                   const theria_tensor_t* v, const theria_tensor_t* o, int32_t o_is_f32,
-                                  const theria_tensor_t* dout, const float* lse, float* delta,
-                                  const theria_tensor_t* dq, void* stream) {
+                                  const theria_tensor_t* o_lo, const theria_tensor_t* dout, const float* lse,
+                                  const float* row_max, float* delta, const theria_tensor_t* dq, void* stream) {
   theria::Shape s;
   std::string err;
   if (!shape_from(p, s, err)) return fail(THERIA_ERR_CONTRACT, err);
@@ -200,21 +210,24 @@ THERIA_API int theria_sdpa_bwd_dq(const theria_sdpa_problem_t* p, const theria_t
   c.kview(k, "k", true);
   c.kview(v, "v", true);
   c.qview(o, "o", false);
+  c.qview(o_lo, "o_lo", false);
   c.qview(dout, "dout", true);
   c.qview(dq, "dq", false);
   c.need(lse != nullptr || !c.q_rows, "lse is required");
   c.need(delta != nullptr || !c.q_rows, "delta is required");
+  c.need(!(o_lo && o_lo->data) || (s.dtype != THERIA_DTYPE_F32 && !o_is_f32), "o_lo is the residual of a 16-bit O");
   if (o_is_f32 && o && (o->stride_b % 4 || o->stride_h % 4 || o->stride_row % 4)) c.vec = false;
   if (!c.err.empty()) return fail(THERIA_ERR_CONTRACT, c.err);
   s.vec = c.vec;
   if (!c.q_rows) return THERIA_OK;
-  return run_dq(s, q, k, v, o, o_is_f32 != 0, dout, lse, delta, dq, (hipStream_t)stream);
+  return run_dq(s, q, k, v, o, o_is_f32 != 0, o_lo, dout, lse, row_max, delta, dq, (hipStream_t)stream);
 }
 
 THERIA_API int theria_sdpa_bwd_dkdv(const theria_sdpa_problem_t* p, const theria_tensor_t* q,
                                     const theria_tensor_t* k, const theria_tensor_t* v,
-                                    const theria_tensor_t* dout, const float* lse, const float* delta,
-                                    const theria_tensor_t* dk, const theria_tensor_t* dv, void* stream) {
+                                    const theria_tensor_t* dout, const float* lse, const float* row_max,
+                                    const float* delta, const theria_tensor_t* dk, const theria_tensor_t* dv,
+                                    void* stream) {
   theria::Shape s;
   std::string err;
   if (!shape_from(p, s, err)) return fail(THERIA_ERR_CONTRACT, err);
@@ -230,14 +243,14 @@ THERIA_API int theria_sdpa_bwd_dkdv(const theria_sdpa_problem_t* p, const theria
   if (!c.err.empty()) return fail(THERIA_ERR_CONTRACT, c.err);
   s.vec = c.vec;
   if (!c.k_rows) return THERIA_OK;
-  return run_dkdv(s, q, k, v, dout, lse, delta, dk, dv, false, (hipStream_t)stream);
+  return run_dkdv(s, q, k, v, dout, lse, row_max, delta, dk, dv, false, (hipStream_t)stream);
 }
 
 THERIA_API int theria_sdpa_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
                                const theria_tensor_t* v, const theria_tensor_t* o, int32_t o_is_f32,
-                               const theria_tensor_t* dout, const float* lse, float* delta_out,
-                               const theria_tensor_t* dq, const theria_tensor_t* dk, const theria_tensor_t* dv,
-                               void* stream) {
+                               const theria_tensor_t* o_lo, const theria_tensor_t* dout, const float* lse,
+                               const float* row_max, float* delta_out, const theria_tensor_t* dq,
+                               const theria_tensor_t* dk, const theria_tensor_t* dv, void* stream) {
   theria::Shape s;
   std::string err;
   if (!shape_from(p, s, err)) return fail(THERIA_ERR_CONTRACT, err);
@@ -246,29 +259,31 @@ THERIA_API int theria_sdpa_bwd(const theria_sdpa_problem_t* p, const theria_tens
   c.kview(k, "k", true);
   c.kview(v, "v", true);
   c.qview(o, "o", true);
+  c.qview(o_lo, "o_lo", false);
   c.qview(dout, "dout", true);
   c.qview(dq, "dq", false);
   c.kview(dk, "dk", false);
   c.kview(dv, "dv", true);
   c.need(lse != nullptr || !c.q_rows, "lse is required");
   c.need(delta_out != nullptr || !c.q_rows, "delta_out is required");
+  c.need(!(o_lo && o_lo->data) || (s.dtype != THERIA_DTYPE_F32 && !o_is_f32), "o_lo is the residual of a 16-bit O");
   if (o_is_f32 && o && (o->stride_b % 4 || o->stride_h % 4 || o->stride_row % 4)) c.vec = false;
   if (!c.err.empty()) return fail(THERIA_ERR_CONTRACT, c.err);
   s.vec = c.vec;
   const hipStream_t st = (hipStream_t)stream;
   if (c.q_rows) {
-    int rc = run_dq(s, q, k, v, o, o_is_f32 != 0, dout, lse, delta_out, dq, st);
+    int rc = run_dq(s, q, k, v, o, o_is_f32 != 0, o_lo, dout, lse, row_max, delta_out, dq, st);
     if (rc != THERIA_OK) return rc;
   }
   if (!c.k_rows) return THERIA_OK;
-  return run_dkdv(s, q, k, v, dout, lse, delta_out, dk, dv, false, st);
+  return run_dkdv(s, q, k, v, dout, lse, row_max, delta_out, dk, dv, false, st);
 }
 
 THERIA_API int theria_sdpa_bwd_from_stats(const theria_sdpa_problem_t* p, const theria_tensor_t* q,
                                           const theria_tensor_t* k, const theria_tensor_t* v,
-                                          const theria_tensor_t* dout, const float* lse, float* delta_out,
-                                          const theria_tensor_t* dq, const theria_tensor_t* dk,
-                                          const theria_tensor_t* dv, void* stream) {
+                                          const theria_tensor_t* dout, const float* lse, const float* row_max,
+                                          float* delta_out, const theria_tensor_t* dq, const theria_tensor_t* dk,
+                                          const theria_tensor_t* dv, int32_t normalize, void* stream) {
   theria::Shape s;
   std::string err;
   if (!shape_from(p, s, err)) return fail(THERIA_ERR_CONTRACT, err);
@@ -297,21 +312,22 @@ THERIA_API int theria_sdpa_bwd_from_stats(const theria_sdpa_problem_t* p, const 
     fp.dout = cv(dout);
     fp.lse = const_cast<float*>(lse);
     fp.delta = delta_out;
+    fp.row_normalize = normalize != 0;
     int rc = hip_status(theria::launch_fwd(fp, 1, st), "theria_sdpa_bwd_from_stats (delta)");
     if (rc != THERIA_OK) return rc;
     if (dq && dq->data) {
-      rc = run_dq(s, q, k, v, nullptr, false, dout, lse, delta_out, dq, st);
+      rc = run_dq(s, q, k, v, nullptr, false, nullptr, dout, lse, row_max, delta_out, dq, st);
       if (rc != THERIA_OK) return rc;
     }
   }
   if (!c.k_rows) return THERIA_OK;
-  return run_dkdv(s, q, k, v, dout, lse, delta_out, dk, dv, dv_only, st);
+  return run_dkdv(s, q, k, v, dout, lse, row_max, delta_out, dk, dv, dv_only, st);
 }
 
 THERIA_API int theria_sdpa_jvp(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
                                const theria_tensor_t* v, const theria_tensor_t* o, const float* lse,
                                const theria_tensor_t* tq, const theria_tensor_t* tk, const theria_tensor_t* tv,
-                               const theria_tensor_t* tout, void* stream) {
+                               const theria_tensor_t* tout, int32_t normalize, void* stream) {
   theria::Shape s;
   std::string err;
   if (!shape_from(p, s, err)) return fail(THERIA_ERR_CONTRACT, err);
@@ -339,6 +355,9 @@ THERIA_API int theria_sdpa_jvp(const theria_sdpa_problem_t* p, const theria_tens
   jp.tv = cv(tv);
   jp.lse = lse;
   jp.tout = mv(tout);
+  jp.normalize = normalize != 0;
+  // The frozen-stats form rebuilds O from the P it is given; a saved O belongs to the exact stats.
+  if (!jp.normalize) jp.o = theria::View{nullptr, 0, 0, 0};
   return hip_status(theria::launch_jvp(jp, (hipStream_t)stream), "theria_sdpa_jvp");
 }
 
@@ -420,6 +439,7 @@ THERIA_API int theria_sdpa_bwd_bwd(const theria_sdpa_problem_t* p, const theria_
   jp.tv = cv(gv);
   jp.lse = lse;
   jp.tout = mv(out_gdout);
+  jp.normalize = true;  // lse is the operator's own: G_dO is the JVP of the exact softmax
   return hip_status(theria::launch_jvp(jp, st), "theria_sdpa_bwd_bwd (dout)");
 }
 

@@ -21,6 +21,8 @@
 // kernels) but removes the LDS round trip of dS, the atomics and the accumulator conversion.
 // Causal: key tiles above a query block (dq) and query tiles before a key block (dkdv) are never
 // visited, fully masked wave tiles skip their MFMAs, and only diagonal tiles are masked element-wise.
+#include <type_traits>
+
 #include "dispatch.hpp"
 #include "sdpa_common.hpp"
 
@@ -68,6 +70,7 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DQ_MINW : 1)) void dq_kernel(const
 
   F qf[QT][NKC], of[QT][NKC];
   float lse2[QT], del[QT];
+  bool peaked = false;  // a row of this wave's largest probability exceeds 1/16 (or no row maxima given)
 #pragma unroll
   for (int j = 0; j < QT; ++j) {
     const int myq = q0w + 32 * j + li;
@@ -77,8 +80,9 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DQ_MINW : 1)) void dq_kernel(const
       qf[j][c] = gload_frag<T>(Q, p.q.sr, myq, s.T, c, s.D, s.vec);
       of[j][c] = gload_frag<T>(dO, p.dout.sr, myq, s.T, c, s.D, s.vec);
     }
-    const float l2 = qvalid ? p.lse[rowbase + myq] * kLog2e : THERIA_INF;
-    lse2[j] = l2 == -THERIA_INF ? THERIA_INF : l2;  // a row without visible keys has P = 0
+    const float lse = qvalid ? p.lse[rowbase + myq] : THERIA_INF;
+    lse2[j] = lse == -THERIA_INF ? THERIA_INF : lse * kLog2e;  // a row without visible keys has P = 0
+    peaked |= qvalid && (!p.row_max || p.row_max[rowbase + myq] - lse > kPeakedLog);
     if (p.o.p) {
       // delta = dO . O over this lane's half of the head dim (the dO fragment's columns), then the pair
       float part = 0.f;
@@ -92,8 +96,10 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DQ_MINW : 1)) void dq_kernel(const
             for (int e = 0; e < 8; ++e) {
               if (col + e < s.D) {
                 const int64_t off = (int64_t)myq * p.o.sr + col + e;
-                const float ov = p.o_f32 ? ((const float*)p.o.p + b * p.o.sb + h * p.o.sh)[off]
-                                         : (float)((const T*)p.o.p + b * p.o.sb + h * p.o.sh)[off];
+                float ov = p.o_f32 ? ((const float*)p.o.p + b * p.o.sb + h * p.o.sh)[off]
+                                   : (float)((const T*)p.o.p + b * p.o.sb + h * p.o.sh)[off];
+                if (p.o_lo.p)  // rounding residual of a 16-bit O
+                  ov += (float)((const T*)p.o_lo.p + b * p.o_lo.sb + h * p.o_lo.sh)[(int64_t)myq * p.o_lo.sr + col + e];
                 part += ov * (float)od[e];
               }
             }
@@ -110,16 +116,74 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DQ_MINW : 1)) void dq_kernel(const
     }
   }
   if (!p.dq.p) return;  // only the row term was requested (uniform over the grid)
-  f32x16_t acc[QT][NDT];
-#pragma unroll
-  for (int j = 0; j < QT; ++j)
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) acc[j][dt] = zero16();
   const float c2 = s.scale * kLog2e;
 
   int kend = s.M;
   if (CAUSAL) kend = min(s.M, qb * BM + BM);
   const int nkt = (kend + BN - 1) / BN;
+
+  // 16-bit, a workgroup holding a peaked row: delta = sum_j P_ij dP_ij / sum_j P_ij formed exactly first (one
+  // more pass over the key tiles): dO . O from the forward's O carries the 16-bit rounding of its P in the PV
+  // product, which a peaked row does not average out. The dK/dV kernel reads the same delta.
+  if constexpr (sizeof(T) == 2) {
+    if (__syncthreads_or(__any(peaked)) && nkt > 0) {
+      float a_part[QT], l_part[QT];
+#pragma unroll
+      for (int j = 0; j < QT; ++j) a_part[j] = l_part[j] = 0.f;
+      TileStage<T, BN, DP, NT> pK, pV;
+      for (int kt = 0; kt < nkt; ++kt) {
+        const int k0 = kt * BN;
+        pK.load(K, p.k.sr, k0, s.M, s.D, s.vec);
+        pV.load(V, p.v.sr, k0, s.M, s.D, s.vec);
+        __syncthreads();
+        pK.store(sK, PITCH);
+        pV.store(sV, PITCH);
+        __syncthreads();
+        if (CAUSAL && k0 > q0w + 32 * QT - 1) continue;
+        f32x16_t sc[QT], dpp[QT];
+#pragma unroll
+        for (int j = 0; j < QT; ++j) sc[j] = dpp[j] = zero16();
+#pragma unroll
+        for (int c = 0; c < NKC; ++c) {
+          const F kfr = lds_cols<T, KLIN>(sK, PITCH, li, 0, c);
+          const F vfr = lds_cols<T, KLIN>(sV, PITCH, li, 0, c);
+#pragma unroll
+          for (int j = 0; j < QT; ++j) {
+            sc[j] = MM::mma(kfr, qf[j][c], sc[j]);
+            dpp[j] = MM::mma(vfr, of[j][c], dpp[j]);
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < QT; ++j) {
+          const int lim = CAUSAL ? min(s.M, q0w + 32 * j + li + 1) : s.M;  // first key this query cannot see
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float pv = k0 + acc_row(r, g) < lim ? fast_exp2(fmaf(sc[j][r], c2, -lse2[j])) : 0.f;
+            a_part[j] = fmaf(pv, dpp[j][r], a_part[j]);
+            l_part[j] += pv;
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < QT; ++j) {
+        const float a = pair_sum(a_part[j]), l = pair_sum(l_part[j]);
+        del[j] = l > 0.f ? a / l : 0.f;
+        const int myq = q0w + 32 * j + li;
+        if (myq < s.T && g == 0) p.delta[rowbase + myq] = del[j];
+      }
+    }
+  }
+
+  f32x16_t acc[QT][NDT];
+#pragma unroll
+  for (int j = 0; j < QT; ++j)
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) acc[j][dt] = zero16();
+
+  // 16-bit: a wave holding a peaked row forms dS as two 16-bit terms (hi + lo) in every product. Both forms
+  // of the loop are inlined (a call that is not would take the register arrays it captures by address).
+  auto run = [&](auto split_tag) __attribute__((always_inline)) {
+  constexpr bool SPLIT = decltype(split_tag)::value;
   TileStage<T, BN, DP, NT> stK, stV;
   if (nkt > 0) {
     stK.load(K, p.k.sr, 0, s.M, s.D, s.vec);
@@ -170,17 +234,32 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DQ_MINW : 1)) void dq_kernel(const
       for (int r = 0; r < 16; ++r) sc[j][r] = fast_exp2(fmaf(sc[j][r], c2, -lse2[j])) * dp[j][r];  // dS^T
 #pragma unroll
     for (int cc = 0; cc < NPC; ++cc) {
-      F dsf[QT];
+      F dsf[QT], dsl[QT];
 #pragma unroll
-      for (int j = 0; j < QT; ++j) dsf[j] = acc_frag<T>(sc[j], cc);
+      for (int j = 0; j < QT; ++j) {
+        if constexpr (SPLIT) {
+          split_frag<T>(sc[j], cc, dsf[j], dsl[j]);
+        } else {
+          dsf[j] = acc_frag<T>(sc[j], cc);
+        }
+      }
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) {
         const F ktf = lds_rows<T, KACC>(sK, PITCH, 0, cc, dt * 32);
 #pragma unroll
-        for (int j = 0; j < QT; ++j) acc[j][dt] = MM::mma(ktf, dsf[j], acc[j][dt]);
+        for (int j = 0; j < QT; ++j) {
+          acc[j][dt] = MM::mma(ktf, dsf[j], acc[j][dt]);
+          if constexpr (SPLIT) acc[j][dt] = MM::mma(ktf, dsl[j], acc[j][dt]);
+        }
       }
     }
   }
+
+  };
+  if (sizeof(T) == 2 && __any(peaked))
+    run(std::integral_constant<bool, sizeof(T) == 2>{});
+  else
+    run(std::integral_constant<bool, false>{});
 
   T* DQ = (T*)p.dq.p + b * p.dq.sb + h * p.dq.sh;
 #pragma unroll
@@ -214,6 +293,7 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DKDV_MINW : 1)) void dkdv_kernel(c
   __shared__ __attribute__((aligned(16))) T sdO[BM * PITCH];
   __shared__ __attribute__((aligned(16))) float sLse[BM];
   __shared__ __attribute__((aligned(16))) float sDel[BM];
+  __shared__ int sPk[1];  // 16-bit: the staged tile holds a peaked row
 
   const Shape& s = p.s;
   const int tid = threadIdx.x;
@@ -260,17 +340,53 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DKDV_MINW : 1)) void dkdv_kernel(c
 
   TileStage<T, BM, DP, NT> stQ, stO;
   float pre_lse = THERIA_INF, pre_del = 0.f;
+  bool pre_pk = false;  // 16-bit: this row's largest probability exceeds 1/16 (or no row maxima given)
   auto prefetch = [&](int q0) {
     stQ.load(Q, p.q.sr, q0, s.T, s.D, s.vec);
     stO.load(dO, p.dout.sr, q0, s.T, s.D, s.vec);
     if (tid < BM) {
       const int qq = q0 + tid;
-      const float l2 = qq < s.T ? p.lse[rowbase + qq] * kLog2e : THERIA_INF;
-      pre_lse = l2 == -THERIA_INF ? THERIA_INF : l2;
+      const float lse = qq < s.T ? p.lse[rowbase + qq] : THERIA_INF;
+      pre_lse = lse == -THERIA_INF ? THERIA_INF : lse * kLog2e;
       pre_del = (qq < s.T && !dv_only) ? -p.delta[rowbase + qq] : 0.f;  // staged negated: dP starts at -delta
+      if constexpr (sizeof(T) == 2) pre_pk = qq < s.T && (!p.row_max || p.row_max[rowbase + qq] - lse > kPeakedLog);
     }
   };
   if (nqt > 0) prefetch(qbeg);
+
+  // S = Q K^T and dP = dO V^T - delta for the 32-row subtile qr0 of the staged tile (masked scores -inf).
+  auto scores = [&](int qr0, int q0t, f32x16_t (&sc)[KT], f32x16_t (&dp)[KT]) {
+    f32x4_t del4[4];
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) del4[qd] = *reinterpret_cast<const f32x4_t*>(sDel + qr0 + 8 * qd + 4 * g);
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+      sc[t] = zero16();
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dp[t][r] = del4[r >> 2][r & 3];
+    }
+#pragma unroll
+    for (int c = 0; c < NKC; ++c) {
+      const F qfr = lds_cols<T, KLIN>(sQ, PITCH, qr0 + li, 0, c);
+#pragma unroll
+      for (int t = 0; t < KT; ++t) sc[t] = MM::mma(qfr, kf[t][c], sc[t]);
+      if constexpr (!DV_ONLY) {
+        const F ofr = lds_cols<T, KLIN>(sdO, PITCH, qr0 + li, 0, c);
+#pragma unroll
+        for (int t = 0; t < KT; ++t) dp[t] = MM::mma(ofr, vf[t][c], dp[t]);
+      }
+    }
+    // Boundary sub-tiles only (a uniform branch): masked scores become -inf, so P = 0 there.
+    if ((kw0 + 32 * KT > s.M) || (CAUSAL && kw0 + 32 * KT - 1 > q0t)) {
+#pragma unroll
+      for (int t = 0; t < KT; ++t) {
+        const int mykey = kw0 + 32 * t + li;
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (mykey >= s.M || (CAUSAL && mykey > q0t + acc_row(r, g))) sc[t][r] = -THERIA_INF;
+      }
+    }
+  };
 
   for (int it = 0; it < nqt; ++it) {
     const int q0 = qbeg + it * BM;
@@ -281,6 +397,12 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DKDV_MINW : 1)) void dkdv_kernel(c
       sLse[tid] = pre_lse;
       sDel[tid] = pre_del;
     }
+    if constexpr (sizeof(T) == 2) {
+      if (wave == 0) {  // BM = 64 rows: wave 0 staged them
+        const bool pk = __any(pre_pk);
+        if (lane == 0) sPk[0] = pk;
+      }
+    }
     __syncthreads();
     if (it + 1 < nqt) prefetch(q0 + BM);
 
@@ -289,40 +411,11 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DKDV_MINW : 1)) void dkdv_kernel(c
       const int qr0 = qt * 32;
       const int q0t = q0 + qr0;
       if (q0t >= s.T || (CAUSAL && kw0 > q0t + 31)) continue;  // wave-uniform
-      f32x4_t lse4[4], del4[4];
+      f32x4_t lse4[4];
 #pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        lse4[qd] = *reinterpret_cast<const f32x4_t*>(sLse + qr0 + 8 * qd + 4 * g);
-        del4[qd] = *reinterpret_cast<const f32x4_t*>(sDel + qr0 + 8 * qd + 4 * g);
-      }
+      for (int qd = 0; qd < 4; ++qd) lse4[qd] = *reinterpret_cast<const f32x4_t*>(sLse + qr0 + 8 * qd + 4 * g);
       f32x16_t sc[KT], dp[KT];
-#pragma unroll
-      for (int t = 0; t < KT; ++t) {
-        sc[t] = zero16();
-#pragma unroll
-        for (int r = 0; r < 16; ++r) dp[t][r] = del4[r >> 2][r & 3];
-      }
-#pragma unroll
-      for (int c = 0; c < NKC; ++c) {
-        const F qfr = lds_cols<T, KLIN>(sQ, PITCH, qr0 + li, 0, c);
-#pragma unroll
-        for (int t = 0; t < KT; ++t) sc[t] = MM::mma(qfr, kf[t][c], sc[t]);
-        if constexpr (!DV_ONLY) {
-          const F ofr = lds_cols<T, KLIN>(sdO, PITCH, qr0 + li, 0, c);
-#pragma unroll
-          for (int t = 0; t < KT; ++t) dp[t] = MM::mma(ofr, vf[t][c], dp[t]);
-        }
-      }
-      // Boundary sub-tiles only (a uniform branch): masked scores become -inf, so P = 0 there.
-      if ((kw0 + 32 * KT > s.M) || (CAUSAL && kw0 + 32 * KT - 1 > q0t)) {
-#pragma unroll
-        for (int t = 0; t < KT; ++t) {
-          const int mykey = kw0 + 32 * t + li;
-#pragma unroll
-          for (int r = 0; r < 16; ++r)
-            if (mykey >= s.M || (CAUSAL && mykey > q0t + acc_row(r, g))) sc[t][r] = -THERIA_INF;
-        }
-      }
+      scores(qr0, q0t, sc, dp);
 #pragma unroll
       for (int t = 0; t < KT; ++t)
 #pragma unroll
@@ -350,6 +443,43 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DKDV_MINW : 1)) void dkdv_kernel(c
             const F da = acc_frag<T>(dp[t], cc);
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt) dk[t][dt] = MM::mma(da, qtr[dt], dk[t][dt]);
+          }
+        }
+      }
+    }
+
+    // 16-bit, a tile holding a peaked row: the residual products, with S and dP formed again, so that P and
+    // dS enter as two 16-bit terms (hi + lo) in total.
+    if constexpr (sizeof(T) == 2) {
+      if (__builtin_amdgcn_readfirstlane(sPk[0])) {
+#pragma unroll
+        for (int qt = 0; qt < NQT; ++qt) {
+          const int qr0 = qt * 32;
+          const int q0t = q0 + qr0;
+          if (q0t >= s.T || (CAUSAL && kw0 > q0t + 31)) continue;  // wave-uniform
+          f32x4_t lse4[4];
+#pragma unroll
+          for (int qd = 0; qd < 4; ++qd) lse4[qd] = *reinterpret_cast<const f32x4_t*>(sLse + qr0 + 8 * qd + 4 * g);
+          f32x16_t sc[KT], dp[KT];
+          scores(qr0, q0t, sc, dp);
+#pragma unroll
+          for (int cc = 0; cc < NPC; ++cc) {
+#pragma unroll
+            for (int t = 0; t < KT; ++t) {
+              F pl, dl;
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                const float pv = fast_exp2(fmaf(sc[t][8 * cc + e], c2, -lse4[(8 * cc + e) >> 2][e & 3]));
+                const float ds = pv * dp[t][8 * cc + e];
+                pl[e] = (T)(pv - (float)(T)pv);
+                dl[e] = (T)(ds - (float)(T)ds);
+              }
+#pragma unroll
+              for (int dt = 0; dt < NDT; ++dt) {
+                dv[t][dt] = MM::mma(pl, lds_rows<T, KACC>(sdO, PITCH, qr0, cc, dt * 32), dv[t][dt]);
+                if constexpr (!DV_ONLY) dk[t][dt] = MM::mma(dl, lds_rows<T, KACC>(sQ, PITCH, qr0, cc, dt * 32), dk[t][dt]);
+              }
+            }
           }
         }
       }

@@ -9,16 +9,19 @@
 // Work decomposition: one workgroup = NW waves, each owning 32 keys (K and V fragments in registers,
 // dK and dV accumulated in registers); the workgroup streams the query tiles (64 or 128 rows) of its head.
 //  * Q and dO tiles reach LDS by DMA (sdpa_lds.hpp) into double buffers with one barrier per tile;
-//    the row terms -lse * log2(e) and -delta of the next tile are loaded by the first 64 threads during
-//    the current tile and written beside them.
+//    the row terms -lse / scale and -delta of the next tile are loaded by the first 64 threads during
+//    the current tile and written beside them, with a flag for a tile holding a peaked row (largest
+//    probability above 1/16): such a tile forms P and dS as two 16-bit terms (hi + lo) and runs its
+//    subtiles one after the other.
 //  * Scores are S = Q K^T with this lane's key in the column, so dV += P^T dO and dK += dS^T Q take
 //    P and dS straight from the accumulators (KACC order) and dO^T / Q^T from LDS transpose reads.
 //  * Phase order per 64-row half of a tile, i.e. two 32-query subtiles (scheduling barriers keep it):
 //      S, dP of subtile 0 | S, dP of subtile 1 with exp / dS of subtile 0
 //      | dV, dK of subtile 0 with exp / dS of subtile 1 | dV, dK of subtile 1.
-//  * dP starts from -delta as the MFMA accumulator input, so dS = P o dP is one multiply; K is held
-//    pre-multiplied by scale * log2(e) and S starts from -lse * log2(e), so P = exp2(S) needs no
-//    per-score scaling.
+//  * dP starts from -delta as the MFMA accumulator input, so dS = P o dP is one multiply; S starts from
+//    -lse / scale, so P = exp2(S * scale * log2(e)) takes one multiply per score. (Holding K pre-multiplied
+//    by scale * log2(e) would save it, but rounds every score's factors once more to 16 bits: P off by up
+//    to ~10% on rows whose scores are large.)
 #include <type_traits>
 
 #include "sdpa_common.hpp"
@@ -79,8 +82,9 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
   __shared__ __attribute__((aligned(1024))) char sQ1[TILE];
   __shared__ __attribute__((aligned(1024))) char sO0[TILE];
   __shared__ __attribute__((aligned(1024))) char sO1[TILE];
-  __shared__ __attribute__((aligned(16))) float sR0[2 * BM];  // [-lse * log2(e) | -delta] of a tile
+  __shared__ __attribute__((aligned(16))) float sR0[2 * BM];  // [-lse / scale | -delta] of a tile
   __shared__ __attribute__((aligned(16))) float sR1[2 * BM];
+  __shared__ int sF0[2], sF1[2];  // per 64-row half: the tile holds a peaked row
 
   const Shape& s = p.s;
   const int tid = threadIdx.x;
@@ -115,7 +119,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
     F kf[NKC], vf[NKC];
 #pragma unroll
     for (int c = 0; c < NKC; ++c) {
-      kf[c] = scaled_frag<T>(gload_frag8<T>(K, p.k.sr, kw0 + li, s.M, c, FD ? DP : s.D), c2);
+      kf[c] = gload_frag8<T>(K, p.k.sr, kw0 + li, s.M, c, FD ? DP : s.D);
       vf[c] = gload_frag8<T>(V, p.v.sr, kw0 + li, s.M, c, FD ? DP : s.D);
     }
     f32x16_t dv[NDT], dk[NDT];
@@ -135,29 +139,37 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
 
     const Dma dma(wave, lane, FD ? DP / 8 : s.D / 8);  // head dims below DP: zero-filled chunks past D
     const uint32_t qrs = (uint32_t)p.q.sr * 2, ors = (uint32_t)p.dout.sr * 2;
-    const rsrc_t qrsrc = make_rsrc(Q, (uint32_t)s.T * qrs);
-    const rsrc_t orsrc = make_rsrc(dO, (uint32_t)s.T * ors);
+    const rsrc_t qrsrc = make_rsrc(Q, (uint32_t)slab_span(s.T, qrs, 2 * (FD ? DP : s.D)));
+    const rsrc_t orsrc = make_rsrc(dO, (uint32_t)slab_span(s.T, ors, 2 * (FD ? DP : s.D)));
 
-    // Row terms of tile `it` for thread tid < BM, loaded two tiles ahead as raw lse and delta (rows past
-    // the end: lse = +inf) and converted only when stored, so that no instruction waits for these loads
-    // (or for the DMA issued just before them) until the next tile. Stored: -lse * log2(e) (-inf for
-    // rows past the end or without visible keys, so P = 0) and -delta.
-    float r_lse = THERIA_INF, r_del = 0.f;
+    // Row terms of tile `it` for thread tid < BM, loaded two tiles ahead as raw lse, row max and delta (rows
+    // past the end: lse = +inf) and converted only when stored, so that no instruction waits for these loads
+    // (or for the DMA issued just before them) until the next tile. Stored: -lse / scale (-inf for rows past
+    // the end or without visible keys, so P = 0), -delta, and per 64-row half whether it holds a peaked row
+    // (every row counts as peaked when the row maxima are not given).
+    float r_lse = THERIA_INF, r_del = 0.f, r_m = -THERIA_INF;
+    const float inv_scale = 1.f / s.scale;
     auto load_rows = [&](int it) {
       if (tid < BM && it < nqt) {
         const int qq = qbeg + it * BM + tid;
         r_lse = qq < s.T ? p.lse[rowbase + qq] : THERIA_INF;
         r_del = qq < s.T ? p.delta[rowbase + qq] : 0.f;
+        r_m = qq < s.T ? (p.row_max ? p.row_max[rowbase + qq] : THERIA_INF) : -THERIA_INF;
       }
     };
-    auto store_rows = [&](float* sr) {
-      if (tid < BM) {
-        sr[tid] = __builtin_isinf(r_lse) ? -THERIA_INF : -r_lse * kLog2e;
+    auto store_rows = [&](float* sr, int* sf) {
+      if (tid < BM) {  // whole waves (BM is a multiple of 64)
+        sr[tid] = __builtin_isinf(r_lse) ? -THERIA_INF : -r_lse * inv_scale;
         sr[BM + tid] = -r_del;
+        const bool pk = __any(r_m - r_lse > kPeakedLog);
+        if (lane == 0) sf[tid >> 6] = pk;
       }
+    };
+    auto peaked_tile = [&](const int* sf) {
+      return __builtin_amdgcn_readfirstlane(BM > 64 ? (sf[0] | sf[1]) : sf[0]) != 0;
     };
 
-    // S = c2 Q K^T - lse2 and dP = dO V^T - delta for subtile qs (32 queries) of the tile in (tq, to, tr).
+    // S = Q K^T - lse / scale and dP = dO V^T - delta for subtile qs (32 queries) of the tile in (tq, to, tr).
     auto sdp = [&](const char* tq, const char* to, const float* tr, int qs, f32x16_t& sc, f32x16_t& dp) {
 #pragma unroll
       for (int qd = 0; qd < 4; ++qd) {
@@ -184,11 +196,11 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
           if (mykey >= s.M || (CAUSAL && mykey > q0s + acc_row(r, g))) sc[r] = -THERIA_INF;
       }
     };
-    // P = exp2(S) and dS = P o dP as 16-bit fragments (KACC chunks 0, 1).
+    // P = exp2(S c2) and dS = P o dP as 16-bit fragments (KACC chunks 0, 1).
     auto pds = [&](const f32x16_t& sc, const f32x16_t& dp, F (&pf)[2], F (&df)[2]) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float pv = fast_exp2(sc[r]);
+        const float pv = fast_exp2(sc[r] * c2);
         pf[r >> 3][r & 7] = (T)pv;
         df[r >> 3][r & 7] = (T)(pv * dp[r]);
       }
@@ -203,20 +215,31 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
           dk[dt] = MM::mma(df[cc], swz_rows<T, DP>(tq, 32 * qs, cc, 32 * dt), dk[dt]);
         }
     };
+    // The residual products of a split subtile: dV += (P - hi(P))^T dO, dK += (dS - hi(dS))^T Q, with the
+    // residuals recomputed from the float32 S and dP (every 16-bit operand then carries ~2^-16 relative).
+    auto dvdk_lo = [&](const char* tq, const char* to, int qs, const f32x16_t& sc, const f32x16_t& dp) {
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc) {
+        F pl, dl;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float pv = fast_exp2(sc[8 * cc + e] * c2);
+          const float ds = pv * dp[8 * cc + e];
+          pl[e] = (T)(pv - (float)(T)pv);
+          dl[e] = (T)(ds - (float)(T)ds);
+        }
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+          dv[dt] = MM::mma(pl, swz_rows<T, DP>(to, 32 * qs, cc, 32 * dt), dv[dt]);
+          dk[dt] = MM::mma(dl, swz_rows<T, DP>(tq, 32 * qs, cc, 32 * dt), dk[dt]);
+        }
+      }
+    };
 
-    // One query tile `it` from buffers (tq, to, tr); the next tile goes to (nq, no, nr).
-    auto step = [&](auto fast_tag, int it, const char* tq, const char* to, const float* tr, char* nq, char* no,
-                    float* nr) {
+    // Subtiles of query tile `it` in (tq, to, tr). FAST: every query in range and every key visible.
+    auto body = [&](auto fast_tag, int it, const char* tq, const char* to, const float* tr) {
       constexpr bool FAST = decltype(fast_tag)::value;
       const int q0 = qbeg + it * BM;
-      wait_vm_all();
-      __syncthreads();  // tile it visible to all waves; the other buffers (tile it-1) are free
-      if (it + 1 < nqt) {
-        dma.template issue_clamped<NSLAB>(qrsrc, qrs, q0 + BM, s.T, nq);
-        dma.template issue_clamped<NSLAB>(orsrc, ors, q0 + BM, s.T, no);
-        store_rows(nr);
-        load_rows(it + 2);
-      }
       if constexpr (FAST && OVERLAP) {
 #pragma unroll
         for (int hf = 0; hf < HALVES; ++hf) {
@@ -233,60 +256,83 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
           dvdk(tq, to, 2 * hf + 1, pf1, df1);
           __builtin_amdgcn_sched_barrier(0);
         }
-      } else if constexpr (FAST) {
-#pragma unroll
-        for (int qs = 0; qs < 2 * HALVES; ++qs) {
-          f32x16_t sc, dp;
-          F pf[2], df[2];
-          sdp(tq, to, tr, qs, sc, dp);
-          pds(sc, dp, pf, df);
-          dvdk(tq, to, qs, pf, df);
-        }
       } else {
 #pragma unroll
         for (int qs = 0; qs < 2 * HALVES; ++qs) {
           const int q0s = q0 + 32 * qs;
-          if (q0s >= s.T || (CAUSAL && kw0 > q0s + 31)) continue;  // wave-uniform
+          if (!FAST && (q0s >= s.T || (CAUSAL && kw0 > q0s + 31))) continue;  // wave-uniform
           f32x16_t sc, dp;
           F pf[2], df[2];
           sdp(tq, to, tr, qs, sc, dp);
-          mask(sc, q0s);
+          if (!FAST) mask(sc, q0s);
           pds(sc, dp, pf, df);
           dvdk(tq, to, qs, pf, df);
         }
       }
     };
+    // The residual pass of a tile holding a peaked row: S and dP are formed again and only the residual
+    // products are added, so the regular pass keeps its schedule and registers.
+    auto residual = [&](auto fast_tag, int it, const char* tq, const char* to, const float* tr) {
+      constexpr bool FAST = decltype(fast_tag)::value;
+      const int q0 = qbeg + it * BM;
+#pragma unroll
+      for (int qs = 0; qs < 2 * HALVES; ++qs) {
+        const int q0s = q0 + 32 * qs;
+        if (!FAST && (q0s >= s.T || (CAUSAL && kw0 > q0s + 31))) continue;  // wave-uniform
+        f32x16_t sc, dp;
+        sdp(tq, to, tr, qs, sc, dp);
+        if (!FAST) mask(sc, q0s);
+        dvdk_lo(tq, to, qs, sc, dp);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
     const std::integral_constant<bool, true> fast;
     const std::integral_constant<bool, false> general;
+
+    // One query tile `it` from buffers (tq, to, tr, tf); the next tile goes to (nq, no, nr, nf).
+    auto step = [&](auto fast_tag, int it, const char* tq, const char* to, const float* tr, const int* tf, char* nq,
+                    char* no, float* nr, int* nf) {
+      const int q0 = qbeg + it * BM;
+      wait_vm_all();
+      __syncthreads();  // tile it visible to all waves; the other buffers (tile it-1) are free
+      if (it + 1 < nqt) {
+        dma.template issue_clamped<NSLAB>(qrsrc, qrs, q0 + BM, s.T, nq);
+        dma.template issue_clamped<NSLAB>(orsrc, ors, q0 + BM, s.T, no);
+        store_rows(nr, nf);
+        load_rows(it + 2);
+      }
+      body(fast_tag, it, tq, to, tr);
+      if (peaked_tile(tf)) residual(fast_tag, it, tq, to, tr);
+    };
 
     if (nqt > 0) {
       dma.template issue_clamped<NSLAB>(qrsrc, qrs, qbeg, s.T, sQ0);
       dma.template issue_clamped<NSLAB>(orsrc, ors, qbeg, s.T, sO0);
       load_rows(0);
       wait_vm_all();
-      store_rows(sR0);
+      store_rows(sR0, sF0);
       load_rows(1);
       int it = 0;
       // causal diagonal tiles first (general), then the full tiles two at a time (fixed buffers), then the rest
       for (; it < ifull; ++it) {
         if (it & 1)
-          step(general, it, sQ1, sO1, sR1, sQ0, sO0, sR0);
+          step(general, it, sQ1, sO1, sR1, sF1, sQ0, sO0, sR0, sF0);
         else
-          step(general, it, sQ0, sO0, sR0, sQ1, sO1, sR1);
+          step(general, it, sQ0, sO0, sR0, sF0, sQ1, sO1, sR1, sF1);
       }
       if (it < fend && (it & 1)) {
-        step(fast, it, sQ1, sO1, sR1, sQ0, sO0, sR0);
+        step(fast, it, sQ1, sO1, sR1, sF1, sQ0, sO0, sR0, sF0);
         ++it;
       }
       for (; it + 1 < fend; it += 2) {
-        step(fast, it, sQ0, sO0, sR0, sQ1, sO1, sR1);
-        step(fast, it + 1, sQ1, sO1, sR1, sQ0, sO0, sR0);
+        step(fast, it, sQ0, sO0, sR0, sF0, sQ1, sO1, sR1, sF1);
+        step(fast, it + 1, sQ1, sO1, sR1, sF1, sQ0, sO0, sR0, sF0);
       }
       for (; it < nqt; ++it) {
         if (it & 1)
-          step(general, it, sQ1, sO1, sR1, sQ0, sO0, sR0);
+          step(general, it, sQ1, sO1, sR1, sF1, sQ0, sO0, sR0, sF0);
         else
-          step(general, it, sQ0, sO0, sR0, sQ1, sO1, sR1);
+          step(general, it, sQ0, sO0, sR0, sF0, sQ1, sO1, sR1, sF1);
       }
     }
 
@@ -313,7 +359,8 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
 // One workgroup = NW waves of 32 queries each (Q and dO fragments, dQ accumulated in registers); K and V
 // tiles of 64 or 128 keys stream through DMA-filled swizzled double buffers, one barrier per tile. Scores
 // are transposed (S^T = K Q^T, this lane's query in the column), so lse and delta are per-lane scalars and
-// dQ^T += K^T dS^T takes dS^T from the accumulators. Phase order per 64-key half of a tile, i.e. two
+// dQ^T += K^T dS^T takes dS^T from the accumulators. A wave holding a peaked row (largest probability above
+// 1/16) forms dS as two 16-bit terms and runs its subtiles one after the other. Phase order per 64-key half of a tile, i.e. two
 // 32-key subtiles:
 //   S, dP of subtile 0 | S, dP of subtile 1 with exp / dS of subtile 0
 //   | dQ of subtile 0 with exp / dS of subtile 1 | dQ of subtile 1.
@@ -362,11 +409,11 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
       qf[c] = gload_frag8<T>(Q, p.q.sr, myq, s.T, c, FD ? DP : s.D);
       of[c] = gload_frag8<T>(dO, p.dout.sr, myq, s.T, c, FD ? DP : s.D);
     }
-    const float l2 = qvalid ? p.lse[rowbase + myq] * kLog2e : THERIA_INF;
-    const float lse2 = l2 == -THERIA_INF ? THERIA_INF : l2;  // a row without visible keys has P = 0
+    const float lse = qvalid ? p.lse[rowbase + myq] : THERIA_INF;
+    const float lse2 = lse == -THERIA_INF ? THERIA_INF : lse * kLog2e;  // a row without visible keys has P = 0
     float del;
     if (p.o.p) {
-      // delta = dO . O over this lane's half of the head dim (the dO fragment's columns), then the pair
+      // delta = dO . (O + O_lo) over this lane's half of the head dim (the dO fragment's columns), then the pair
       float part = 0.f;
       if (qvalid) {
 #pragma unroll
@@ -383,8 +430,12 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
           } else {
             const F ov = __builtin_bit_cast(F, *reinterpret_cast<const i16x8_t*>((const T*)p.o.p + b * p.o.sb +
                                                                                h * p.o.sh + off));
+            F lo{};
+            if (p.o_lo.p)
+              lo = __builtin_bit_cast(F, *reinterpret_cast<const i16x8_t*>((const T*)p.o_lo.p + b * p.o_lo.sb +
+                                                                         h * p.o_lo.sh + (int64_t)myq * p.o_lo.sr + col));
 #pragma unroll
-            for (int e = 0; e < 8; ++e) part += (float)ov[e] * (float)of[c][e];
+            for (int e = 0; e < 8; ++e) part += ((float)ov[e] + (float)lo[e]) * (float)of[c][e];
           }
         }
       }
@@ -395,13 +446,22 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
     }
     if (!p.dq.p) continue;  // only the row term was requested (uniform over the grid)
 
+    // Peaked rows (largest probability above 1/16; every row when the row maxima are not given) take dS as
+    // two 16-bit terms: the whole wave runs the split loop when any of its rows is peaked.
+    const bool peaked = qvalid && (!p.row_max || p.row_max[rowbase + myq] - lse > kPeakedLog);
+    const bool split = __any(peaked);
+    // ... and a workgroup holding a peaked row first forms the row term exactly, delta = sum_j P_ij dP_ij /
+    // sum_j P_ij (below): dO . O from the forward's O carries the 16-bit rounding of the P in its PV
+    // product, which on a peaked row is not averaged out (~2^-9 |dP|), while dS = P o (dP - delta) is a
+    // small difference there. The dK/dV kernel reads the same delta.
+    const bool exact_row_term = __syncthreads_or(split);
+
     f32x16_t acc[NDT];
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) acc[dt] = zero16();
-    // Q pre-multiplied by scale * log2(e) and S^T started from -lse2: P = exp2(S^T) with no per-score scaling.
+    // P = exp2(S^T c2 - lse2) from the exact float32 scores (operands are not rescaled before the product,
+    // which would round every score's factors once more to 16 bits).
     const float c2 = s.scale * kLog2e;
-#pragma unroll
-    for (int c = 0; c < NKC; ++c) qf[c] = scaled_frag<T>(qf[c], c2);
 
     int kend = s.M;
     if (CAUSAL) kend = min(s.M, qb * BM + BM);
@@ -412,14 +472,14 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
 
     const Dma dma(wave, lane, FD ? DP / 8 : s.D / 8);  // head dims below DP: zero-filled chunks past D
     const uint32_t krs = (uint32_t)p.k.sr * 2, vrs = (uint32_t)p.v.sr * 2;
-    const rsrc_t krsrc = make_rsrc(K, (uint32_t)s.M * krs);
-    const rsrc_t vrsrc = make_rsrc(V, (uint32_t)s.M * vrs);
+    const rsrc_t krsrc = make_rsrc(K, (uint32_t)slab_span(s.M, krs, 2 * (FD ? DP : s.D)));
+    const rsrc_t vrsrc = make_rsrc(V, (uint32_t)slab_span(s.M, vrs, 2 * (FD ? DP : s.D)));
 
-    // S^T = c2 K Q^T - lse2 and dP^T = V dO^T - delta for key subtile t of the tile in (tk, tv).
+    // S^T = K Q^T and dP^T = V dO^T - delta for key subtile t of the tile in (tk, tv).
     auto sdp = [&](const char* tk, const char* tv, int t, f32x16_t& sc, f32x16_t& dp) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        sc[r] = -lse2;
+        sc[r] = 0.f;
         dp[r] = -del;
       }
 #pragma unroll
@@ -439,7 +499,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
     // dS^T = P^T o dP^T as 16-bit fragments (KACC chunks 0, 1)
     auto pds = [&](const f32x16_t& sc, const f32x16_t& dp, F (&df)[2]) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) df[r >> 3][r & 7] = (T)(fast_exp2(sc[r]) * dp[r]);
+      for (int r = 0; r < 16; ++r) df[r >> 3][r & 7] = (T)(fast_exp2(fmaf(sc[r], c2, -lse2)) * dp[r]);
     };
     auto dqm = [&](const char* tk, int t, const F (&df)[2]) {
 #pragma unroll
@@ -447,9 +507,26 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) acc[dt] = MM::mma(swz_rows<T, DP>(tk, 32 * t, cc, 32 * dt), df[cc], acc[dt]);
     };
+    // The residual product of a split wave: dQ^T += K^T (dS - hi(dS))^T with the residual recomputed from the
+    // float32 S and dP, so that dS enters as two 16-bit terms in total.
+    auto dqm_lo = [&](const char* tk, int t, const f32x16_t& sc, const f32x16_t& dp) {
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc) {
+        F dl;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float ds = fast_exp2(fmaf(sc[8 * cc + e], c2, -lse2)) * dp[8 * cc + e];
+          dl[e] = (T)(ds - (float)(T)ds);
+        }
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) acc[dt] = MM::mma(swz_rows<T, DP>(tk, 32 * t, cc, 32 * dt), dl, acc[dt]);
+      }
+    };
 
-    auto step = [&](auto fast_tag, int k, const char* tk, const char* tv, char* nk, char* nv) {
+    auto step = [&](auto fast_tag, auto split_tag, int k, const char* tk, const char* tv, char* nk,
+                    char* nv) __attribute__((always_inline)) {
       constexpr bool FAST = decltype(fast_tag)::value;
+      constexpr bool SPLIT = decltype(split_tag)::value;
       const int k0 = k * BN;
       wait_vm_all();
       __syncthreads();  // tile k visible to all waves; the other buffers (tile k-1) are free
@@ -457,16 +534,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
         dma.template issue_clamped<NSLAB>(krsrc, krs, k0 + BN, s.M, nk);
         dma.template issue_clamped<NSLAB>(vrsrc, vrs, k0 + BN, s.M, nv);
       }
-      if constexpr (FAST && !OVERLAP) {
-#pragma unroll
-        for (int t = 0; t < 2 * HALVES; ++t) {
-          f32x16_t sc, dp;
-          F df[2];
-          sdp(tk, tv, t, sc, dp);
-          pds(sc, dp, df);
-          dqm(tk, t, df);
-        }
-      } else if constexpr (FAST) {
+      if constexpr (FAST && OVERLAP && !SPLIT) {
 #pragma unroll
         for (int hf = 0; hf < HALVES; ++hf) {
           f32x16_t s0, p0, s1, p1;
@@ -486,34 +554,84 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
 #pragma unroll
         for (int t = 0; t < 2 * HALVES; ++t) {
           const int k0t = k0 + 32 * t;
-          if (CAUSAL && k0t > q0w + 31) continue;  // every key after every query of the wave (uniform)
+          if (!FAST && CAUSAL && k0t > q0w + 31) continue;  // every key after every query of the wave (uniform)
           f32x16_t sc, dp;
           F df[2];
           sdp(tk, tv, t, sc, dp);
-          mask(sc, k0t);
+          if (!FAST) mask(sc, k0t);
           pds(sc, dp, df);
           dqm(tk, t, df);
+          if constexpr (SPLIT) {
+            dqm_lo(tk, t, sc, dp);
+            __builtin_amdgcn_sched_barrier(0);  // one subtile at a time (registers)
+          }
         }
       }
     };
-    const std::integral_constant<bool, true> fast;
-    const std::integral_constant<bool, false> general;
+    const std::integral_constant<bool, true> fast, with_split;
+    const std::integral_constant<bool, false> general, no_split;
 
-    if (nkt > 0) {
+    // Both forms of the loop are inlined: a call that is not would take every register array it captures
+    // (Q, dO fragments and the dQ accumulators) by address, i.e. into scratch memory.
+    auto loop = [&](auto split_tag) __attribute__((always_inline)) {
+      if (nkt <= 0) return;
       dma.template issue_clamped<NSLAB>(krsrc, krs, 0, s.M, sK0);
       dma.template issue_clamped<NSLAB>(vrsrc, vrs, 0, s.M, sV0);
       int k = 0;
       for (; k + 1 < nfull; k += 2) {
-        step(fast, k, sK0, sV0, sK1, sV1);
-        step(fast, k + 1, sK1, sV1, sK0, sV0);
+        step(fast, split_tag, k, sK0, sV0, sK1, sV1);
+        step(fast, split_tag, k + 1, sK1, sV1, sK0, sV0);
       }
       for (; k < nkt; ++k) {
         if (k & 1)
-          step(general, k, sK1, sV1, sK0, sV0);
+          step(general, split_tag, k, sK1, sV1, sK0, sV0);
         else
-          step(general, k, sK0, sV0, sK1, sV1);
+          step(general, split_tag, k, sK0, sV0, sK1, sV1);
       }
+    };
+    if (exact_row_term && nkt > 0) {
+      // delta = sum_j P_ij dP_ij / sum_j P_ij over every key of the row (one more pass over the key tiles)
+      float a_part = 0.f, l_part = 0.f;
+      dma.template issue_clamped<NSLAB>(krsrc, krs, 0, s.M, sK0);
+      dma.template issue_clamped<NSLAB>(vrsrc, vrs, 0, s.M, sV0);
+      for (int k = 0; k < nkt; ++k) {
+        const int k0 = k * BN;
+        const char* tk = (k & 1) ? sK1 : sK0;
+        const char* tv = (k & 1) ? sV1 : sV0;
+        wait_vm_all();
+        __syncthreads();
+        if (k + 1 < nkt) {
+          dma.template issue_clamped<NSLAB>(krsrc, krs, k0 + BN, s.M, (k & 1) ? sK0 : sK1);
+          dma.template issue_clamped<NSLAB>(vrsrc, vrs, k0 + BN, s.M, (k & 1) ? sV0 : sV1);
+        }
+#pragma unroll
+        for (int t = 0; t < 2 * HALVES; ++t) {
+          const int k0t = k0 + 32 * t;
+          if (CAUSAL && k0t > q0w + 31) continue;  // wave-uniform
+          f32x16_t sc = zero16(), dpp = zero16();
+#pragma unroll
+          for (int c = 0; c < NKC; ++c) {
+            sc = MM::mma(swz_cols<T, DP>(tk, 32 * t + li, c), qf[c], sc);
+            dpp = MM::mma(swz_cols<T, DP>(tv, 32 * t + li, c), of[c], dpp);
+          }
+          mask(sc, k0t);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float pv = fast_exp2(fmaf(sc[r], c2, -lse2));
+            a_part = fmaf(pv, dpp[r], a_part);
+            l_part += pv;
+          }
+        }
+      }
+      __syncthreads();  // every wave is done with the tiles before the main loop refills the buffers
+      const float a = pair_sum(a_part), l = pair_sum(l_part);
+      del = l > 0.f ? a / l : 0.f;
+      if (qvalid && g == 0) p.delta[rowbase + myq] = del;
     }
+    if (split)
+      loop(with_split);
+    else
+      loop(no_split);
 
     if (qvalid) {
       T* DQ = (T*)p.dq.p + b * p.dq.sb + h * p.dq.sh;
@@ -558,7 +676,7 @@ template <typename T, bool CAUSAL>
 bool launch_dq_pipe(const DqParams& p, hipStream_t st, hipError_t* err) {
   if (!pipe_head_dim(p.s)) return false;
   // 32-bit byte offsets inside each (batch, head) slab of K and V
-  if ((int64_t)p.s.M * p.k.sr * 2 >= (int64_t(1) << 31) || (int64_t)p.s.M * p.v.sr * 2 >= (int64_t(1) << 31)) return false;
+  if (!slab_fits_dma(p.s.M, p.k.sr, p.s.D) || !slab_fits_dma(p.s.M, p.v.sr, p.s.D)) return false;
   constexpr int NW = DQ_PIPE_NW;
   const int64_t nqb = (p.s.T + 32 * NW - 1) / (32 * NW);
   const int64_t nblk = (CAUSAL ? (nqb + 1) / 2 : nqb) * p.s.B * p.s.H;  // causal: mirrored pairs
@@ -585,8 +703,7 @@ template <typename T, bool CAUSAL>
 bool launch_dkdv_pipe(const DkdvParams& p, hipStream_t st, hipError_t* err) {
   if (!(pipe_head_dim(p.s) && !p.dv_only)) return false;
   // 32-bit byte offsets inside each (batch, head) slab of Q and dO
-  if ((int64_t)p.s.T * p.q.sr * 2 >= (int64_t(1) << 31) || (int64_t)p.s.T * p.dout.sr * 2 >= (int64_t(1) << 31))
-    return false;
+  if (!slab_fits_dma(p.s.T, p.q.sr, p.s.D) || !slab_fits_dma(p.s.T, p.dout.sr, p.s.D)) return false;
   // workgroups of nw waves (32 keys each): key blocks, or (causal head dim 64) pairs of mirrored blocks
   auto blocks = [&](int nw) {
     const int64_t nkb = (p.s.M + 32 * nw - 1) / (32 * nw);

@@ -209,9 +209,10 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
     // gK and gV spans less than 2^31 bytes.
     const uint32_t krs = (uint32_t)p.k.sr * 2, vrs = (uint32_t)p.v.sr * 2;
     const uint32_t gkrs = has_gk ? (uint32_t)p.gk.sr * 2 : 0u, gvrs = has_gv ? (uint32_t)p.gv.sr * 2 : 0u;
-    const rsrc_t krsrc = make_rsrc(K, (uint32_t)s.M * krs), vrsrc = make_rsrc(V, (uint32_t)s.M * vrs);
-    const rsrc_t gkrsrc = make_rsrc(has_gk ? (const void*)GK : (const void*)K, (uint32_t)s.M * gkrs);
-    const rsrc_t gvrsrc = make_rsrc(has_gv ? (const void*)GV : (const void*)V, (uint32_t)s.M * gvrs);
+    const rsrc_t krsrc = make_rsrc(K, (uint32_t)slab_span(s.M, krs, 2 * DP)),
+                  vrsrc = make_rsrc(V, (uint32_t)slab_span(s.M, vrs, 2 * DP));
+    const rsrc_t gkrsrc = make_rsrc(has_gk ? (const void*)GK : (const void*)K, (uint32_t)slab_span(s.M, gkrs, 2 * DP));
+    const rsrc_t gvrsrc = make_rsrc(has_gv ? (const void*)GV : (const void*)V, (uint32_t)slab_span(s.M, gvrs, 2 * DP));
     auto issue = [&](int kt, char* tK, char* tV, char* tgK, char* tgV) {
       const int k0 = kt * BN;
       dma.template issue_clamped<NSLAB>(krsrc, krs, k0, s.M, tK);
@@ -472,8 +473,9 @@ __global__ __launch_bounds__(256) void bwdbwd_cols_kernel(const BwdBwdParams p) 
     // and gQ spans less than 2^31 bytes.
     const uint32_t qrs = (uint32_t)p.q.sr * 2, ors = (uint32_t)p.dout.sr * 2;
     const uint32_t gqrs = has_gq ? (uint32_t)p.gq.sr * 2 : 0u;
-    const rsrc_t qrsrc = make_rsrc(Q, (uint32_t)s.T * qrs), orsrc = make_rsrc(dO, (uint32_t)s.T * ors);
-    const rsrc_t gqrsrc = make_rsrc(has_gq ? (const void*)GQ : (const void*)Q, (uint32_t)s.T * gqrs);
+    const rsrc_t qrsrc = make_rsrc(Q, (uint32_t)slab_span(s.T, qrs, 2 * DP)),
+                  orsrc = make_rsrc(dO, (uint32_t)slab_span(s.T, ors, 2 * DP));
+    const rsrc_t gqrsrc = make_rsrc(has_gq ? (const void*)GQ : (const void*)Q, (uint32_t)slab_span(s.T, gqrs, 2 * DP));
     auto issue = [&](int it, char* tQ, char* tO, char* tgQ) {
       const int q0 = qbeg + it * BM;
       dma.template issue_clamped<NSLAB>(qrsrc, qrs, q0, s.T, tQ);
@@ -551,7 +553,7 @@ template <typename T, int DP>
 static bool dma_tiles_ok(const BwdBwdParams& p, int64_t rows, std::initializer_list<const View*> streamed) {
   if (!(sizeof(T) == 2 && (DP == 64 || DP == 128) && p.s.D == DP && p.s.vec)) return false;
   for (const View* v : streamed)
-    if (v->p && rows * v->sr * 2 >= (int64_t(1) << 31)) return false;
+    if (v->p && !slab_fits_dma(rows, v->sr, p.s.D)) return false;
   return true;
 }
 

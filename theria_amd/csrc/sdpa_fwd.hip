@@ -4,7 +4,8 @@
 // O = softmax(scale * Q K^T) V with an online softmax, saving lse (and the reference's m, l).
 // Mode 1 rebuilds O_i = sum_j P_ij V_j from a given lse and writes the backward row term
 // delta_i = dO_i . O_i, for the reference's sdpa_bwd_* entry points that receive (m, l) but no O
-// (triton_sdpa_backward.py:312-353 recomputes that term inside its dK kernel).
+// (triton_sdpa_backward.py:312-353 recomputes that term inside its dK kernel); with row_normalize, O is
+// divided by sum_j P_ij first (the operator's own lse: the exact softmax's row term).
 //
 // Work decomposition: one workgroup = 4 waves; each wave owns QT tiles of 32 query rows of one
 // (batch, head) for the whole kernel. The score tile is computed transposed, S^T = K Q^T, so that in
@@ -148,18 +149,29 @@ __global__ __launch_bounds__(256, (DP <= 64 ? FWD_MINW : 1)) void fwd_kernel(con
         }
       l_part[j] += ls;
     }
+    // Mode 1 with 16-bit inputs: P enters the PV product as two 16-bit terms (hi + lo), so the row term
+    // carries ~2^-16 relative rounding instead of 2^-9 (it is a small difference of large terms in dS).
+    constexpr bool SPLIT = MODE == 1 && sizeof(T) == 2;
 #pragma unroll
     for (int t = 0; t < NST; ++t)
 #pragma unroll
       for (int cc = 0; cc < NPC; ++cc) {
-        F pf[QT];
+        F pf[QT], pl[QT];
 #pragma unroll
-        for (int j = 0; j < QT; ++j) pf[j] = acc_frag<T>(sc[j][t], cc);
+        for (int j = 0; j < QT; ++j) {
+          if constexpr (SPLIT)
+            split_frag<T>(sc[j][t], cc, pf[j], pl[j]);
+          else
+            pf[j] = acc_frag<T>(sc[j][t], cc);
+        }
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
           const F vfr = lds_rows<T, KACC>(sV, PITCH, t * 32, cc, dt * 32);
 #pragma unroll
-          for (int j = 0; j < QT; ++j) o[j][dt] = MM::mma(vfr, pf[j], o[j][dt]);
+          for (int j = 0; j < QT; ++j) {
+            o[j][dt] = MM::mma(vfr, pf[j], o[j][dt]);
+            if constexpr (SPLIT) o[j][dt] = MM::mma(vfr, pl[j], o[j][dt]);
+          }
         }
       }
   }
@@ -187,6 +199,11 @@ __global__ __launch_bounds__(256, (DP <= 64 ? FWD_MINW : 1)) void fwd_kernel(con
               } else {
                 T* O = (T*)p.o.p + b * p.o.sb + h * p.o.sh;
                 store4<T>(O, p.o.sr, myq, d0, s.D, a0, a1, a2, a3, s.vec);
+                if (sizeof(T) == 2 && p.o_lo.p) {  // rounding residual of the 16-bit O
+                  T* OL = (T*)p.o_lo.p + b * p.o_lo.sb + h * p.o_lo.sh;
+                  store4<T>(OL, p.o_lo.sr, myq, d0, s.D, a0 - (float)(T)a0, a1 - (float)(T)a1, a2 - (float)(T)a2,
+                            a3 - (float)(T)a3, s.vec);
+                }
               }
             }
           }
@@ -211,6 +228,10 @@ __global__ __launch_bounds__(256, (DP <= 64 ? FWD_MINW : 1)) void fwd_kernel(con
           }
         }
       part = pair_sum(part);
+      if (p.row_normalize) {
+        const float l = pair_sum(l_part[j]);
+        part = l > 0.f ? part / l : 0.f;
+      }
       if (g == 0) p.delta[row_id] = part;
     }
   }

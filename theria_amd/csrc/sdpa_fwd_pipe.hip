@@ -92,8 +92,8 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
     // Byte offsets fit in 32 bits: the host only selects this kernel when every (batch, head) slab of K
     // and V spans less than 2^31 bytes.
     const uint32_t krs = (uint32_t)p.k.sr * 2, vrs = (uint32_t)p.v.sr * 2;
-    const rsrc_t krsrc = make_rsrc(K, (uint32_t)s.M * krs);
-    const rsrc_t vrsrc = make_rsrc(V, (uint32_t)s.M * vrs);
+    const rsrc_t krsrc = make_rsrc(K, (uint32_t)slab_span(s.M, krs, 2 * Dh));
+    const rsrc_t vrsrc = make_rsrc(V, (uint32_t)slab_span(s.M, vrs, 2 * Dh));
     uint32_t koff[NSLAB], voff[NSLAB];
 #pragma unroll
     for (int i = 0; i < NSLAB; ++i) {
@@ -125,6 +125,9 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
       }
     }
     F pf[QT][2][2];  // P of the previous tile as MFMA B fragments: [query tile][32-key subtile][16-key chunk]
+    // ROW: the rounding residuals of those P (P enters the PV product as two 16-bit terms; the row term
+    // delta = dO . sum_j P_ij V_j is a small difference of large terms in dS = P o (dP - delta))
+    F pfl[ROW ? QT : 1][2][2];
     bool pf_skip = false;
 
     // S^T = K Q^T for both query tiles, key subtile t (32 keys) of the K tile in `kt`.
@@ -158,7 +161,10 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
           for (int dt = 0; dt < NDT; ++dt) {
             const F vf = swz_rows<T, DP>(vt, 32 * t, cc, 32 * dt);
 #pragma unroll
-            for (int j = 0; j < QT; ++j) o[j][dt] = MM::mma(vf, pf[j][t][cc], o[j][dt]);
+            for (int j = 0; j < QT; ++j) {
+              o[j][dt] = MM::mma(vf, pf[j][t][cc], o[j][dt]);
+              if constexpr (ROW) o[j][dt] = MM::mma(vf, pfl[j][t][cc], o[j][dt]);
+            }
           }
     };
     // Keys out of range, or (causal) after the query, get -inf. Only boundary tiles pay for the test.
@@ -176,7 +182,8 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
       }
     };
     // P = exp2(S c2 - off) as 16-bit fragments into pn, and this tile's lane partial row sums into ps.
-    auto exps = [&](const f32x16_t (&sc)[QT][2], const float (&off)[QT], F (&pn)[QT][2][2], float (&ps)[QT]) {
+    auto exps = [&](const f32x16_t (&sc)[QT][2], const float (&off)[QT], F (&pn)[QT][2][2],
+                    F (&pnl)[ROW ? QT : 1][2][2], float (&ps)[QT]) __attribute__((always_inline)) {
 #pragma unroll
       for (int j = 0; j < QT; ++j) {
         float acc = 0.f;
@@ -184,26 +191,43 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
         for (int t = 0; t < 2; ++t)
 #pragma unroll
           for (int cc = 0; cc < 2; ++cc) {
-            F f;
+            F f, fl;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) f[e] = (T)fast_exp2(fmaf(sc[j][t][8 * cc + e], c2, -off[j]));
+            for (int e = 0; e < 8; ++e) {
+              const float x = fast_exp2(fmaf(sc[j][t][8 * cc + e], c2, -off[j]));
+              f[e] = (T)x;
+              if constexpr (ROW) fl[e] = (T)(x - (float)f[e]);
+            }
             pn[j][t][cc] = f;
             acc = frag_sum<T>(f, acc);
+            if constexpr (ROW) {
+              pnl[j][t][cc] = fl;
+              acc = frag_sum<T>(fl, acc);
+            }
           }
         ps[j] = acc;
       }
     };
     // The same for key subtile t only, accumulating the lane partial row sums into ps.
-    auto exps_t = [&](const f32x16_t (&st)[QT], int t, F (&pn)[QT][2][2], float (&ps)[QT]) {
+    auto exps_t = [&](const f32x16_t (&st)[QT], int t, F (&pn)[QT][2][2], F (&pnl)[ROW ? QT : 1][2][2],
+                      float (&ps)[QT]) __attribute__((always_inline)) {
 #pragma unroll
       for (int j = 0; j < QT; ++j)
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
-          F f;
+          F f, fl;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) f[e] = (T)fast_exp2(fmaf(st[j][8 * cc + e], c2, -m_use[j]));
+          for (int e = 0; e < 8; ++e) {
+            const float x = fast_exp2(fmaf(st[j][8 * cc + e], c2, -m_use[j]));
+            f[e] = (T)x;
+            if constexpr (ROW) fl[e] = (T)(x - (float)f[e]);
+          }
           pn[j][t][cc] = f;
           ps[j] = frag_sum<T>(f, ps[j]);
+          if constexpr (ROW) {
+            pnl[j][t][cc] = fl;
+            ps[j] = frag_sum<T>(fl, ps[j]);
+          }
         }
     };
     auto tile_max = [&](const f32x16_t (&sc)[QT][2], int j) {
@@ -215,7 +239,8 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
       return pair_max(mx) * c2;
     };
     // Exact path: the running max becomes the offset; O and the row sums are rescaled to it.
-    auto exact = [&](const f32x16_t (&sc)[QT][2], F (&pn)[QT][2][2], float (&ps)[QT]) {
+    auto exact = [&](const f32x16_t (&sc)[QT][2], F (&pn)[QT][2][2], F (&pnl)[ROW ? QT : 1][2][2],
+                     float (&ps)[QT]) __attribute__((always_inline)) {
       float off[QT];
 #pragma unroll
       for (int j = 0; j < QT; ++j) {
@@ -231,7 +256,7 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
           for (int r = 0; r < 16; ++r) o[j][dt][r] *= alpha;
         off[j] = mnew == -THERIA_INF ? 0.f : mnew;  // all keys so far masked: P = exp2(-inf) = 0
       }
-      exps(sc, off, pn, ps);
+      exps(sc, off, pn, pnl, ps);
     };
 
     // One key tile. On entry K(k) and V(k-1) have been requested (one iteration earlier); this step
@@ -250,7 +275,7 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
         if (k + 1 < nkt) dma.template issue_clamped<NSLAB>(krsrc, krs, k0 + BN, s.M, kn);
         dma.template issue_clamped<NSLAB>(vrsrc, vrs, k0, s.M, vn);
       }
-      F pn[QT][2][2];
+      F pn[QT][2][2], pnl[ROW ? QT : 1][2][2];
       if constexpr (FAST) {
         // Phase order (kept by scheduling barriers, which also bound the live registers):
         //   S(k) subtile 0 | S(k) subtile 1 with exp of subtile 0 | O += V(k-1)^T P(k-1)^T with exp of subtile 1.
@@ -270,8 +295,8 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
             m_max[j] = fmaxf(m_max[j], pair_max(mx) * c2);
           }
         }
-        exps_t(s0, 0, pn, ps);
-        if constexpr (DP == 64) {
+        exps_t(s0, 0, pn, pnl, ps);
+        if constexpr (DP == 64 && !ROW) {
           // Issue order inside the phase: the four K fragment reads first, then each of the 8 MFMAs
           // followed by 12 VALU instructions of the exponentials (measured ~5% faster than the
           // compiler's own order at head dim 64).
@@ -294,8 +319,8 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
             m_max[j] = fmaxf(m_max[j], pair_max(mx) * c2);
           }
         }
-        exps_t(s1, 1, pn, ps);
-        if constexpr (DP == 64) {
+        exps_t(s1, 1, pn, pnl, ps);
+        if constexpr (DP == 64 && !ROW) {
           // V fragment reads first, then each of the 16 PV MFMAs followed by 6 VALU instructions.
 #pragma unroll
           for (int i = 0; i < 8; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
@@ -311,7 +336,7 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
         if (!ROW && __any(bad)) {
           f32x16_t sc2[QT][2];
           scores(kc, sc2);
-          exact(sc2, pn, ps);
+          exact(sc2, pn, pnl, ps);
         }
 #pragma unroll
         for (int j = 0; j < QT; ++j) l_part[j] += ps[j];
@@ -320,7 +345,10 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
 #pragma unroll
           for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int cc = 0; cc < 2; ++cc) pf[j][t][cc] = pn[j][t][cc];
+            for (int cc = 0; cc < 2; ++cc) {
+              pf[j][t][cc] = pn[j][t][cc];
+              if constexpr (ROW) pfl[j][t][cc] = pnl[j][t][cc];
+            }
         pf_skip = false;
       } else {
         const bool skip = CAUSAL && (k0 > q0w + 32 * QT - 1);  // every key after every query of the wave
@@ -331,13 +359,13 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
           float ps[QT];
           mask(sc, k0);
           if (k == 0 && !ROW) {
-            exact(sc, pn, ps);
+            exact(sc, pn, pnl, ps);
           } else {
             if (STATS) {
 #pragma unroll
               for (int j = 0; j < QT; ++j) m_max[j] = fmaxf(m_max[j], tile_max(sc, j));
             }
-            exps(sc, m_use, pn, ps);
+            exps(sc, m_use, pn, pnl, ps);
             bool bad = false;
 #pragma unroll
             for (int j = 0; j < QT; ++j) bad |= !(ps[j] <= 0x1p20f);
@@ -345,7 +373,7 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
               f32x16_t sc2[QT][2];
               scores(kc, sc2);
               mask(sc2, k0);
-              exact(sc2, pn, ps);
+              exact(sc2, pn, pnl, ps);
             }
           }
 #pragma unroll
@@ -355,7 +383,10 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
-              for (int cc = 0; cc < 2; ++cc) pf[j][t][cc] = pn[j][t][cc];
+              for (int cc = 0; cc < 2; ++cc) {
+              pf[j][t][cc] = pn[j][t][cc];
+              if constexpr (ROW) pfl[j][t][cc] = pnl[j][t][cc];
+            }
         }
         pf_skip = skip;
       }
@@ -407,6 +438,10 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
               }
             }
           part = pair_sum(part);
+          if (p.row_normalize) {  // the exact softmax's row term: O divided by its own row sum
+            const float l = pair_sum(l_part[j]);
+            part = l > 0.f ? part / l : 0.f;
+          }
           if (g == 0) p.delta[rowbase + myq] = part;
         }
         continue;
@@ -427,6 +462,11 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
             } else {
               T* O = (T*)p.o.p + b * p.o.sb + h * p.o.sh;
               store4_8<T>(O, p.o.sr, myq, d0, Dh, a0, a1, a2, a3);
+              if (p.o_lo.p) {  // rounding residual of the 16-bit O
+                T* OL = (T*)p.o_lo.p + b * p.o_lo.sb + h * p.o_lo.sh;
+                store4_8<T>(OL, p.o_lo.sr, myq, d0, Dh, a0 - (float)(T)a0, a1 - (float)(T)a1, a2 - (float)(T)a2,
+                            a3 - (float)(T)a3);
+              }
             }
           }
         if (g == 0) {
@@ -466,7 +506,9 @@ static void fwd_pipe_go(const FwdParams& p, int64_t nblk, hipStream_t st) {
 
 template <typename T, bool CAUSAL, int DP, bool ROW>
 static void fwd_pipe_launch(const FwdParams& p, hipStream_t st) {
-  constexpr int QT = (DP == 64 && !CAUSAL) ? 2 : 1;
+  // The row-term pass carries two-term P fragments across its software pipeline: one query tile per wave
+  // (two spill ~100 registers).
+  constexpr int QT = (DP == 64 && !CAUSAL && !ROW) ? 2 : 1;
   const int64_t bh = (int64_t)p.s.B * p.s.H;
   const int64_t cus = device_cu_count();
   // workgroups per (batch, head): query blocks, or (causal) pairs of mirrored query blocks
@@ -494,7 +536,7 @@ template <typename T, bool CAUSAL, int MODE>
 bool launch_fwd_pipe(const FwdParams& p, hipStream_t st, hipError_t* err) {
   if (!(p.s.vec && p.s.D % 8 == 0 && p.s.D > 32 && (p.s.dp == 64 || p.s.dp == 128) && p.s.T > 128)) return false;
   // 32-bit byte offsets inside each (batch, head) slab of K and V
-  if ((int64_t)p.s.M * p.k.sr * 2 >= (int64_t(1) << 31) || (int64_t)p.s.M * p.v.sr * 2 >= (int64_t(1) << 31)) return false;
+  if (!slab_fits_dma(p.s.M, p.k.sr, p.s.D) || !slab_fits_dma(p.s.M, p.v.sr, p.s.D)) return false;
   if ((int64_t)p.s.B * p.s.H == 0) {
     *err = hipSuccess;
     return true;

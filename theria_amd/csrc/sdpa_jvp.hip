@@ -10,10 +10,12 @@
 //
 // 16-bit inputs: the two large terms (P o G) V and c o O of tO cancel, so operand rounding in them is
 // amplified (a bfloat16-rounded P o G gave 0.03 absolute error on a row with four visible keys). Both
-// products are therefore formed from two-term 16-bit splits (hi + lo) of P o G and of P, O is always
-// rebuilt in the pass from the same P (the saved O, rounded to 16 bits, is not used), and P is
-// renormalised by its row sum: the saved lse of a 16-bit forward comes from rounded probabilities, so
-// P rebuilt from it sums to 1 only within ~2^-9. Float32 inputs keep the plain frozen-stats form.
+// products are therefore formed from two-term 16-bit splits (hi + lo) of P o G and of P, and O is always
+// rebuilt in the pass from the same P (the saved O, rounded to 16 bits, is not used).
+// p.normalize divides P by its own row sum (every dtype): the JVP of the exact softmax for an lse this
+// library's forward wrote (a 16-bit forward's lse comes from rounded probabilities, so P rebuilt from it
+// sums to 1 only within ~2^-9). Without it P = exp(S - lse) is held exactly as given, which is the
+// reference's frozen-stats contract for caller-supplied (m, l).
 //
 // Work decomposition as in the forward: one workgroup = 4 waves = 128 query rows, lane per query in
 // the transposed score tiles S^T = K Q^T and G^T = K tq^T + tk Q^T (Q and tq stay in registers as B
@@ -136,7 +138,7 @@ __global__ __launch_bounds__(256) void jvp_kernel(const JvpParams p) {
           if (key >= s.M || (CAUSAL && key > myq)) pv = 0.f;
         }
         sc[t][r] = pv;
-        if (SPLIT) lpart += pv;
+        lpart += pv;
         const float pg = pv * gm[t][r];
         gm[t][r] = pg;
         cpart += pg;
@@ -174,9 +176,10 @@ __global__ __launch_bounds__(256) void jvp_kernel(const JvpParams p) {
     // tK and tV spans less than 2^31 bytes.
     const uint32_t krs = (uint32_t)p.k.sr * 2, vrs = (uint32_t)p.v.sr * 2;
     const uint32_t tkrs = has_tk ? (uint32_t)p.tk.sr * 2 : 0u, tvrs = has_tv ? (uint32_t)p.tv.sr * 2 : 0u;
-    const rsrc_t krsrc = make_rsrc(K, (uint32_t)s.M * krs), vrsrc = make_rsrc(V, (uint32_t)s.M * vrs);
-    const rsrc_t tkrsrc = make_rsrc(has_tk ? (const void*)TK : (const void*)K, (uint32_t)s.M * tkrs);
-    const rsrc_t tvrsrc = make_rsrc(has_tv ? (const void*)TV : (const void*)V, (uint32_t)s.M * tvrs);
+    const rsrc_t krsrc = make_rsrc(K, (uint32_t)slab_span(s.M, krs, 2 * DP)),
+                  vrsrc = make_rsrc(V, (uint32_t)slab_span(s.M, vrs, 2 * DP));
+    const rsrc_t tkrsrc = make_rsrc(has_tk ? (const void*)TK : (const void*)K, (uint32_t)slab_span(s.M, tkrs, 2 * DP));
+    const rsrc_t tvrsrc = make_rsrc(has_tv ? (const void*)TV : (const void*)V, (uint32_t)slab_span(s.M, tvrs, 2 * DP));
     auto issue = [&](int kt, char* tK, char* tV, char* ttK, char* ttV) {
       const int k0 = kt * BN;
       dma.template issue_clamped<NSLAB>(krsrc, krs, k0, s.M, tK);
@@ -224,9 +227,9 @@ __global__ __launch_bounds__(256) void jvp_kernel(const JvpParams p) {
     }
   }
 
-  // 16-bit: P / L with L = sum_j P_j, i.e. every term below is divided by L (and O by L as well)
+  // normalize: P / L with L = sum_j P_j, i.e. every term below is divided by L (and a rebuilt O as well)
   float inv = 1.f;
-  if constexpr (SPLIT) {
+  if (p.normalize) {
     const float L = pair_sum(lpart);
     inv = L > 0.f ? 1.f / L : 0.f;
   }
@@ -268,7 +271,7 @@ struct JvpLauncher {
       // LDS-DMA tiles: head dim exactly DP, 16-byte-aligned views, each streamed (batch, head) slab < 2^31 bytes
       bool ok = p.s.D == DP && p.s.vec;
       for (const View* v : {&p.k, &p.v, &p.tk, &p.tv})
-        if (v->p && (int64_t)p.s.M * v->sr * 2 >= (int64_t(1) << 31)) ok = false;
+        if (v->p && !slab_fits_dma(p.s.M, v->sr, p.s.D)) ok = false;
       if (ok) {
         hipLaunchKernelGGL((jvp_kernel<T, DP, CAUSAL, HAS_O, true>), dim3((unsigned)nblk), dim3(256), 0, st, p);
         return hipGetLastError();

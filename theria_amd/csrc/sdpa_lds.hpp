@@ -44,6 +44,19 @@ typedef struct {
 } rsrc_t;
 #endif
 
+// Bytes spanned by `rows` rows of `row_bytes` bytes at a row stride of `rs_bytes`. The stride may be smaller
+// than a row (overlapping rows) or zero (one row broadcast over all of them), so the span is that of the last
+// row's end, not rows * stride. A buffer resource over fewer bytes would read the missing rows as zeros.
+__host__ __device__ __forceinline__ int64_t slab_span(int64_t rows, int64_t rs_bytes, int64_t row_bytes) {
+  return rows > 0 ? (rows - 1) * rs_bytes + row_bytes : 0;
+}
+
+// The DMA kernels address each (batch, head) slab with 32-bit byte offsets (and an out-of-range offset of
+// 2^31 for the chunks past the head dim), so the slab must span less than 2^31 bytes.
+__host__ __device__ __forceinline__ bool slab_fits_dma(int64_t rows, int64_t rs_elems, int64_t head_dim) {
+  return slab_span(rows, 2 * rs_elems, 2 * head_dim) < (int64_t(1) << 31);
+}
+
 // Buffer resource over `bytes` bytes from `base` (raw buffer, stride 0; gfx9 data-format word). Loads
 // beyond `bytes` return zero instead of faulting.
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {

@@ -30,20 +30,30 @@ struct FwdParams {
   Shape s;
   View q, k, v, dout;
   MutView o;
+  MutView o_lo;     // optional (mode 0, 16-bit O): rounding residual O - (float)o in the input dtype
   bool o_f32;
   float* lse;       // mode 0: out; mode 1: in
   float* row_max;   // optional (mode 0)
   float* row_sum;   // optional (mode 0)
   float* delta;     // mode 1: out
+  // mode 1: delta from the normalised O = sum_j P_ij V_j / sum_j P_ij (the exact softmax's row term for the
+  // operator's own lse) instead of sum_j P_ij dP_ij with P as given (the reference's frozen-stats term)
+  bool row_normalize;
 };
 
-// dQ pass of the backward. When o.p is set, delta = rowsum(dO * O) is computed and written to
-// delta; otherwise delta is read.
+// Largest probability of a row above which the 16-bit backward forms P and dS as two 16-bit terms
+// (hi + lo): exp(m - lse) > 1/16, i.e. m - lse > -ln 16.
+constexpr float kPeakedLog = -2.7725887222397811f;
+
+// dQ pass of the backward. When o.p is set, delta = rowsum(dO * (O + O_lo)) is computed and written to
+// delta; otherwise delta is read. row_max (optional): the row maxima m that mark peaked rows (16-bit
+// inputs); absent, every row is treated as peaked.
 struct DqParams {
   Shape s;
-  View q, k, v, dout, o;
+  View q, k, v, dout, o, o_lo;
   bool o_f32;
   const float* lse;
+  const float* row_max;
   float* delta;
   MutView dq;
 };
@@ -53,16 +63,20 @@ struct DkdvParams {
   Shape s;
   View q, k, v, dout;
   const float* lse;
+  const float* row_max;  // as in DqParams
   const float* delta;
   MutView dk, dv;
   bool dv_only;
 };
 
+// normalize: P divided by its own row sum (the exact-softmax JVP, for an lse of this library's forward);
+// otherwise P = exp(S - lse) exactly as given (the reference's frozen-stats JVP).
 struct JvpParams {
   Shape s;
   View q, k, v, o, tq, tk, tv;
   const float* lse;
   MutView tout;
+  bool normalize;
 };
 
 struct BwdBwdParams {
