@@ -79,13 +79,13 @@ def _step_fns(q, k, v, do, scale, causal):
     def step(ev=None):
         if ev:
             ev[0].record()
-        o, lse, m, o_lo = _ops.fwd_for_backward(q, k, v, scale, causal)
+        o, lse, _, _ = _ops.fwd(q, k, v, scale, causal)
         if ev:
             ev[1].record()
-        _ops.bwd_dq(prob, q, k, v, o, False, do, lse, delta, dq, o_lo, m)
+        _ops.bwd_dq(prob, q, k, v, o, False, do, lse, delta, dq)
         if ev:
             ev[2].record()
-        _ops.bwd_dkdv(prob, q, k, v, do, lse, delta, dk, dv, m)
+        _ops.bwd_dkdv(prob, q, k, v, do, lse, delta, dk, dv)
         if ev:
             ev[3].record()
 

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define THERIA_SDPA_ABI_VERSION 5
+#define THERIA_SDPA_ABI_VERSION 6
 
 enum theria_dtype { THERIA_DTYPE_F32 = 0, THERIA_DTYPE_F16 = 1, THERIA_DTYPE_BF16 = 2 };
 enum theria_status { THERIA_OK = 0, THERIA_ERR_CONTRACT = 1, THERIA_ERR_HIP = 2 };
@@ -61,14 +61,14 @@ const char* theria_last_error(void);
  * the input dtype. row_max / row_sum may be NULL; when given they receive the reference's saved
  * statistics m (row max of scaled scores) and l (sum of exp(S - m)) (triton_qk.py:299-304).
  * A query row with no visible key gets O = 0, lse = -inf, m = -inf, l = 0.
- * o_lo may have data == NULL. When given (16-bit inputs with a 16-bit O), it receives the rounding
- * residual of O in the input dtype, o_lo = O - (float)o, so that o + o_lo carries the float32 result to
- * ~2^-16 relative; the backward takes it to form its row term dO . O at float32 accuracy (the reference's
- * forward returns a float32 O, triton_qk.py:321).
+ * 16-bit inputs: the lowest mantissa bit of each finite lse marks a peaked row, one whose largest
+ * probability may exceed 1/4 (set from an upper bound formed from 32-key partial row sums, so it may also
+ * mark a row just below); it moves lse by at most one unit in the last place. The backward entry points
+ * read it (see theria_sdpa_bwd).
  */
 int theria_sdpa_fwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
-                    const theria_tensor_t* v, const theria_tensor_t* o, int32_t o_is_f32, const theria_tensor_t* o_lo,
-                    float* lse, float* row_max, float* row_sum, void* stream);
+                    const theria_tensor_t* v, const theria_tensor_t* o, int32_t o_is_f32, float* lse,
+                    float* row_max, float* row_sum, void* stream);
 
 /*
  * Explicit backward given the forward output O: dQ, dK, dV.
@@ -80,50 +80,53 @@ int theria_sdpa_fwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q, co
  * dq / dk may have data == NULL to skip that output. Deterministic (no atomics, no workspace).
  * theria_sdpa_bwd = theria_sdpa_bwd_dq followed by theria_sdpa_bwd_dkdv on the same stream.
  *
- * o_lo (may be absent): the residual theria_sdpa_fwd wrote for a 16-bit O; delta then uses o + o_lo.
- * row_max (may be NULL): the forward's row maxima m. 16-bit inputs: the probabilities P and the score
- * gradients dS enter the MFMA products as 16-bit operands; on a row whose largest probability
- * exp(m - lse) exceeds 1/16 (a peaked row), each is taken as two 16-bit terms (hi + lo, ~2^-16 relative)
- * so that sums over many such rows stay within the 16-bit bars. NULL treats every row as peaked
- * (always exact operands, slower). Float32 inputs ignore it.
+ * 16-bit inputs: the probabilities P and the score gradients dS enter the MFMA products as 16-bit
+ * operands. On the rows lse flags as peaked (theria_sdpa_fwd), each is taken as two 16-bit terms (hi + lo,
+ * ~2^-16 relative) from the exact float32 scores, so that sums over many such rows stay within the 16-bit
+ * bars, and the row term of every row of a query block (128 or 256 rows) holding a peaked row is formed
+ * exactly, sum_j P_ij dP_ij / sum_j P_ij, in one more pass over the keys (dO . O carries the 16-bit
+ * rounding of the P in the forward's PV product, which a peaked row does not average out). Other rows take
+ * Q or K pre-multiplied by scale * log2(e) in 16 bits. An lse from elsewhere is read the same way: its flag
+ * bits choose the path (every row flagged: always the exact path). Float32 inputs ignore the flags.
  */
 int theria_sdpa_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
                     const theria_tensor_t* v, const theria_tensor_t* o, int32_t o_is_f32,
-                    const theria_tensor_t* o_lo, const theria_tensor_t* dout, const float* lse,
-                    const float* row_max, float* delta_out, const theria_tensor_t* dq, const theria_tensor_t* dk,
-                    const theria_tensor_t* dv, void* stream);
+                    const theria_tensor_t* dout, const float* lse, float* delta_out,
+                    const theria_tensor_t* dq, const theria_tensor_t* dk, const theria_tensor_t* dv, void* stream);
 
 /*
  * The two kernels of theria_sdpa_bwd, for callers that schedule or time them separately.
- *  bwd_dq:   dQ. When o has data, delta = rowsum(dO * O) is computed and written to delta;
- *            when o is absent, delta is read (the row term computed by an earlier call).
- *            dq may be absent: then only delta is produced.
+ *  bwd_dq:   dQ. When o has data, delta = rowsum(dO * O) (or its exact form, as in theria_sdpa_bwd)
+ *            is computed and written to delta; when o is absent, delta is read (the row term computed
+ *            by an earlier call). dq may be absent: then only delta is produced.
  *  bwd_dkdv: dK and dV from delta (dk may be absent).
  */
 int theria_sdpa_bwd_dq(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
                        const theria_tensor_t* v, const theria_tensor_t* o, int32_t o_is_f32,
-                       const theria_tensor_t* o_lo, const theria_tensor_t* dout, const float* lse,
-                       const float* row_max, float* delta, const theria_tensor_t* dq, void* stream);
+                       const theria_tensor_t* dout, const float* lse, float* delta,
+                       const theria_tensor_t* dq, void* stream);
 int theria_sdpa_bwd_dkdv(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
                          const theria_tensor_t* v, const theria_tensor_t* dout, const float* lse,
-                         const float* row_max, const float* delta, const theria_tensor_t* dk,
+                         const float* delta, const theria_tensor_t* dk,
                          const theria_tensor_t* dv, void* stream);
 
 /*
  * Explicit backward from saved statistics only (no O), the reference's sdpa_bwd_* signature
- * (q, k, v, dout, m, l, scale) with lse = m + log(l). The row term is recomputed from P(lse) and V.
+ * (q, k, v, dout, m, l, scale) with lse = m + log(l). The row term is recomputed from P(lse) and
+ * dP = dO V^T in a first pass over the keys (of the dQ kernel, which runs for it even without dq).
  * v may have data == NULL: then only dV is computed (sdpa_bwd_dv takes no v,
  * triton_sdpa_backward.py:194), and dq / dk must be absent. delta_out receives the row term.
- * row_max as in theria_sdpa_bwd (the reference's saved m).
+ * 16-bit inputs: the flag bits of lse choose the exact path as in theria_sdpa_bwd; with the reference's
+ * statistics a row is peaked when l_i < 4 (its largest probability 1 / l_i exceeds 1/4).
  * normalize = 0: the reference's frozen-stats backward, P = exp(S - lse) held as given and the row term
  *   z_i = sum_j P_ij dP_ij (triton_sdpa_backward.py:312-353, 543-585).
- * normalize = 1: the row term from the normalised O = sum_j P_ij V_j / sum_j P_ij, i.e. the exact softmax
- *   gradient's, for an lse this library's forward wrote (a 16-bit forward's lse comes from rounded
+ * normalize = 1: the row term sum_j P_ij dP_ij / sum_j P_ij, i.e. the exact softmax gradient's, for an
+ *   lse this library's forward wrote (a 16-bit forward's lse comes from rounded
  *   probabilities, so P(lse) sums to 1 only within ~2^-9, which the frozen row term passes on to dS).
  */
 int theria_sdpa_bwd_from_stats(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
                                const theria_tensor_t* v, const theria_tensor_t* dout, const float* lse,
-                               const float* row_max, float* delta_out, const theria_tensor_t* dq,
+                               float* delta_out, const theria_tensor_t* dq,
                                const theria_tensor_t* dk, const theria_tensor_t* dv, int32_t normalize,
                                void* stream);
 

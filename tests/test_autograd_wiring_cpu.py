@@ -1,6 +1,6 @@
 """The autograd wiring of the HIP operator (SDPAOp / SDPABackwardOp), checked on the CPU.
 
-The kernel calls (_ops.fwd_for_backward, _ops.bwd, _ops.bwd_bwd, _ops.jvp) are replaced by the float64 oracle, so
+The kernel calls (_ops.fwd, _ops.bwd, _ops.bwd_bwd, _ops.jvp) are replaced by the float64 oracle, so
 what is tested is the graph logic alone: which derivative each node returns, and that derivatives of
 every order equal autograd through textbook attention (oracle.autograd_attention). It also pins which
 path runs: up to second order the double-backward "kernel" is called, and only when the double backward
@@ -22,11 +22,11 @@ H = importlib.import_module("theria_amd.autograd.hip_sdpa")
 def kernels(monkeypatch):
     calls = {"bwd_bwd": 0}
 
-    def fwd_for_backward(q, k, v, scale, causal, out_fp32=False):
-        o, lse, m, _ = O.forward(q, k, v, scale, causal)
-        return o.to(q.dtype), lse, m, None
+    def fwd(q, k, v, scale, causal, out_fp32=False, stats=False):
+        o, lse, m, l = O.forward(q, k, v, scale, causal)
+        return o.to(q.dtype), lse, (m if stats else None), (l if stats else None)
 
-    def bwd(q, k, v, o, lse, dout, scale, causal, o_lo=None, row_max=None):
+    def bwd(q, k, v, o, lse, dout, scale, causal, need_dq=True, need_dk=True):
         dq, dk, dv = O.backward(q, k, v, dout, scale, causal)
         return dq, dk, dv, (dout.double() * o.double()).sum(-1)
 
@@ -39,7 +39,7 @@ def kernels(monkeypatch):
         z = lambda t, like: torch.zeros_like(like) if t is None else t  # noqa: E731
         return O.jvp(q, k, v, z(tq, q), z(tk, k), z(tv, v), scale, causal)
 
-    for name, fn in (("fwd_for_backward", fwd_for_backward), ("bwd", bwd), ("bwd_bwd", bwd_bwd), ("jvp", jvp)):
+    for name, fn in (("fwd", fwd), ("bwd", bwd), ("bwd_bwd", bwd_bwd), ("jvp", jvp)):
         monkeypatch.setattr(_ops, name, fn)
     return calls
 

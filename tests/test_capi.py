@@ -59,13 +59,11 @@ def _call_all(prob):
     lib = _lib.load()
     p = ctypes.byref(prob)
     return {
-        "fwd": lib.theria_sdpa_fwd(p, None, None, None, None, 0, None, None, None, None, None),
-        "bwd": lib.theria_sdpa_bwd(p, None, None, None, None, 0, None, None, None, None, None, None, None, None, None),
-        "bwd_dq": lib.theria_sdpa_bwd_dq(p, None, None, None, None, 0, None, None, None, None, None, None, None),
-        "bwd_dkdv": lib.theria_sdpa_bwd_dkdv(p, None, None, None, None, None, None, None, None, None, None),
-        "bwd_from_stats": lib.theria_sdpa_bwd_from_stats(
-            p, None, None, None, None, None, None, None, None, None, None, 0, None
-        ),
+        "fwd": lib.theria_sdpa_fwd(p, None, None, None, None, 0, None, None, None, None),
+        "bwd": lib.theria_sdpa_bwd(p, None, None, None, None, 0, None, None, None, None, None, None, None),
+        "bwd_dq": lib.theria_sdpa_bwd_dq(p, None, None, None, None, 0, None, None, None, None, None),
+        "bwd_dkdv": lib.theria_sdpa_bwd_dkdv(p, None, None, None, None, None, None, None, None, None),
+        "bwd_from_stats": lib.theria_sdpa_bwd_from_stats(p, None, None, None, None, None, None, None, None, None, 0, None),
         "jvp": lib.theria_sdpa_jvp(p, None, None, None, None, None, None, None, None, None, 1, None),
         "bwd_bwd": lib.theria_sdpa_bwd_bwd(
             p, None, None, None, None, None, None, None, None, None, None, None, None, None, None, None, None

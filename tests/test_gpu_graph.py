@@ -37,8 +37,8 @@ def test_graph_replay_matches_eager(case, hip_device):
     s = 1.0 / math.sqrt(D)
 
     def step():
-        o, lse, m, o_lo = _ops.fwd_for_backward(q, k, v, s, causal)
-        dq, dk, dv, delta = _ops.bwd(q, k, v, o, lse, do, s, causal, o_lo=o_lo, row_max=m)
+        o, lse, _, _ = _ops.fwd(q, k, v, s, causal)
+        dq, dk, dv, delta = _ops.bwd(q, k, v, o, lse, do, s, causal)
         return o, lse, dq, dk, dv, delta
 
     ref = [t.clone() for t in step()]

@@ -134,6 +134,12 @@ def _check_all_entry_points(case, dev, seed: int):
     check_entry_points_on(dev, dt, causal, *ts)
 
 
+def flag_all(lse):
+    """lse with the peaked-row flag set on every finite entry (the backward's exact path everywhere)."""
+    bits = lse.view(torch.int32)
+    return torch.where(torch.isfinite(lse), bits | 1, bits).view(torch.float32)
+
+
 def check_entry_points_on(dev, dt, causal, q, k, v, do, tq, tk, tv, scale=None, fp32_ref_err=None):
     """Every entry point on the given CPU inputs (already rounded to dt) against the float64 oracle.
 
@@ -171,16 +177,27 @@ def check_entry_points_on(dev, dt, causal, q, k, v, do, tq, tk, tv, scale=None, 
     torch.testing.assert_close(m.double().cpu(), mr, rtol=1e-5, atol=1e-5, msg=lambda m_: f"m: {m_}")
     torch.testing.assert_close(l.double().cpu(), lr, **stat_tol(dt), msg=lambda m_: f"l: {m_}")
 
-    # the backward as the autograd operator runs it: the forward's O residual and row maxima
-    _, _, _, o_lo = _ops.fwd_for_backward(q, k, v, s, causal)
-    dq, dk, dv, delta = _ops.bwd(q, k, v, o, lse, do, s, causal, o_lo=o_lo, row_max=m)
+    if dt != torch.float32:
+        # the forward flags every row whose largest probability exceeds 1/4 (its bound may flag a few more)
+        flagged = (lse.cpu().view(torch.int32) & 1).bool()
+        pmax = (mr - lser).exp()
+        missed = (pmax > 0.25 * (1 + 1e-3)) & ~flagged
+        assert not missed.any(), f"peaked rows not flagged in lse: {int(missed.sum())}"
+    else:
+        assert torch.equal(lse.cpu(), lse32.cpu()), "float32 lse carries no flags"
+
+    # the backward as the autograd operator runs it: the forward's lse with its peaked-row flags
+    dq, dk, dv, delta = _ops.bwd(q, k, v, o, lse, do, s, causal)
     ref = O.backward(qc, kc, vc, doc, s, causal)
     for name, a, b in zip(("dQ", "dK", "dV"), (dq, dk, dv), ref):
         close(a, b, dt, name)
-    o_full = o.double().cpu() + (0 if o_lo is None else o_lo.double().cpu())
-    close(delta, (doc * o_full).sum(-1), torch.float32, "delta")
-    # without row maxima every 16-bit row takes two-term operands
-    aq, ak, av, _ = _ops.bwd(q, k, v, o, lse, do, s, causal, o_lo=o_lo)
+    # the row term: dO . O, or its exact form sum_j P_ij dP_ij / sum_j P_ij on query blocks holding a peaked
+    # row; both equal the oracle's dO . O_exact within the float32-output bar
+    torch.testing.assert_close(delta.double().cpu(), (doc * Or).sum(-1), **f32_out, msg=lambda m_: f"delta: {m_}")
+    # every 16-bit row flagged peaked: two-term operands and the exact row term everywhere
+    aq, ak, av, adelta = _ops.bwd(q, k, v, o, flag_all(lse) if dt != torch.float32 else lse, do, s, causal)
+    torch.testing.assert_close(adelta.double().cpu(), (doc * Or).sum(-1), **f32_out,
+                               msg=lambda m_: f"delta(all peaked): {m_}")
     for name, a, b in zip(("dQ(all split)", "dK(all split)", "dV(all split)"), (aq, ak, av), ref):
         close(a, b, dt, name)
 
@@ -192,13 +209,13 @@ def check_entry_points_on(dev, dt, causal, q, k, v, do, tq, tk, tv, scale=None, 
         for name, a_, b_ in zip(("dQ(stats)", "dK(stats)", "dV(stats)"), f32, fref):
             fp32_ref_err[name] = float((a_.double() - b_).abs().max())
         fp32_ref_err["dV(no v)"] = fp32_ref_err["dV(stats)"]
-    sq, sk, sv = _ops.bwd_from_stats(q, k, v, do, lse, s, causal, True, True, True, row_max=m)
+    sq, sk, sv = _ops.bwd_from_stats(q, k, v, do, lse, s, causal, True, True, True)
     for name, a, b in zip(("dQ(stats)", "dK(stats)", "dV(stats)"), (sq, sk, sv), fref):
         close(a, b, dt, name)
-    _, _, dv_only = _ops.bwd_from_stats(q, k, None, do, lse, s, causal, False, False, True, row_max=m)
+    _, _, dv_only = _ops.bwd_from_stats(q, k, None, do, lse, s, causal, False, False, True)
     close(dv_only, fref[2], dt, "dV(no v)")
     # normalised row term: the exact softmax gradient from the operator's own lse
-    nq, nk, nv = _ops.bwd_from_stats(q, k, v, do, lse, s, causal, True, True, True, row_max=m, normalize=True)
+    nq, nk, nv = _ops.bwd_from_stats(q, k, v, do, lse, s, causal, True, True, True, normalize=True)
     for name, a, b in zip(("dQ(stats, normalised)", "dK(stats, normalised)", "dV(stats, normalised)"), (nq, nk, nv), ref):
         close(a, b, dt, name)
 
@@ -335,8 +352,8 @@ def test_config2_full_size(dt, hip_device):
     v, vc = make((B, H, S, D), dt, dev, 13)
     do, doc = make((B, H, S, D), dt, dev, 14)
     s = 1 / 8.0
-    o, lse, m, o_lo = _ops.fwd_for_backward(q, k, v, s, False)
-    dq, dk, dv, _ = _ops.bwd(q, k, v, o, lse, do, s, False, o_lo=o_lo, row_max=m)
+    o, lse, _, _ = _ops.fwd(q, k, v, s, False)
+    dq, dk, dv, _ = _ops.bwd(q, k, v, o, lse, do, s, False)
     for b, h in ((0, 0), (3, 15)):
         sl = (slice(b, b + 1), slice(h, h + 1))
         Or, lser, _, _ = O.forward(qc[sl], kc[sl], vc[sl], s)
@@ -365,8 +382,8 @@ def test_config3_causal_long_sequence(hip_device):
     v, vc = make((B, H, S, D), dt, dev, 23, std=0.5)
     do, doc = make((B, H, S, D), dt, dev, 24)
     s = 1 / math.sqrt(D)
-    o, lse, m, o_lo = _ops.fwd_for_backward(q, k, v, s, True)
-    dq, dk, dv, _ = _ops.bwd(q, k, v, o, lse, do, s, True, o_lo=o_lo, row_max=m)
+    o, lse, _, _ = _ops.fwd(q, k, v, s, True)
+    dq, dk, dv, _ = _ops.bwd(q, k, v, o, lse, do, s, True)
     h = 7
     sl = (slice(0, 1), slice(h, h + 1))
     Or, _, _, _ = O.forward(qc[sl], kc[sl], vc[sl], s, True)
@@ -392,8 +409,8 @@ def test_large_grids_ragged(S, H, causal, hip_device):
     v, vc = make((B, H, S, D), dt, dev, 33)
     do, doc = make((B, H, S, D), dt, dev, 34)
     s = 1 / 8.0
-    o, lse, m, o_lo = _ops.fwd_for_backward(q, k, v, s, causal)
-    dq, dk, dv, _ = _ops.bwd(q, k, v, o, lse, do, s, causal, o_lo=o_lo, row_max=m)
+    o, lse, _, _ = _ops.fwd(q, k, v, s, causal)
+    dq, dk, dv, _ = _ops.bwd(q, k, v, o, lse, do, s, causal)
     for b, h in ((0, 1), (B - 1, H - 1)):
         sl = (slice(b, b + 1), slice(h, h + 1))
         for name, a, r in zip(("dQ", "dK", "dV"), (dq[sl], dk[sl], dv[sl]),

@@ -16,7 +16,7 @@ import torch  # noqa: F401  (must be imported first: it loads the HIP runtime th
 
 # THERIA_SDPA_LIB overrides the in-tree build (e.g. a library installed elsewhere).
 LIB_PATH = Path(os.environ.get("THERIA_SDPA_LIB") or Path(__file__).resolve().parent / "lib" / "libtheria_sdpa.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 OK, ERR_CONTRACT, ERR_HIP = 0, 1, 2
@@ -58,15 +58,15 @@ _FP = ctypes.POINTER(ctypes.c_float)
 SIGNATURES = {
     "theria_abi_version": ([], ctypes.c_int),
     "theria_last_error": ([], ctypes.c_char_p),
-    "theria_sdpa_fwd": ([_PR, _TV, _TV, _TV, _TV, ctypes.c_int32, _TV, _P, _P, _P, _P], ctypes.c_int),
+    "theria_sdpa_fwd": ([_PR, _TV, _TV, _TV, _TV, ctypes.c_int32, _P, _P, _P, _P], ctypes.c_int),
     "theria_sdpa_bwd": (
-        [_PR, _TV, _TV, _TV, _TV, ctypes.c_int32, _TV, _TV, _P, _P, _P, _TV, _TV, _TV, _P],
+        [_PR, _TV, _TV, _TV, _TV, ctypes.c_int32, _TV, _P, _P, _TV, _TV, _TV, _P],
         ctypes.c_int,
     ),
-    "theria_sdpa_bwd_dq": ([_PR, _TV, _TV, _TV, _TV, ctypes.c_int32, _TV, _TV, _P, _P, _P, _TV, _P], ctypes.c_int),
-    "theria_sdpa_bwd_dkdv": ([_PR, _TV, _TV, _TV, _TV, _P, _P, _P, _TV, _TV, _P], ctypes.c_int),
+    "theria_sdpa_bwd_dq": ([_PR, _TV, _TV, _TV, _TV, ctypes.c_int32, _TV, _P, _P, _TV, _P], ctypes.c_int),
+    "theria_sdpa_bwd_dkdv": ([_PR, _TV, _TV, _TV, _TV, _P, _P, _TV, _TV, _P], ctypes.c_int),
     "theria_sdpa_bwd_from_stats": (
-        [_PR, _TV, _TV, _TV, _TV, _P, _P, _P, _TV, _TV, _TV, ctypes.c_int32, _P],
+        [_PR, _TV, _TV, _TV, _TV, _P, _P, _TV, _TV, _TV, ctypes.c_int32, _P],
         ctypes.c_int,
     ),
     "theria_sdpa_jvp": ([_PR, _TV, _TV, _TV, _TV, _P, _TV, _TV, _TV, _TV, ctypes.c_int32, _P], ctypes.c_int),
@@ -100,7 +100,7 @@ def load(path: str | os.PathLike | None = None):
                 f"theria_amd: {p} is not built. Run `python -m theria_amd.build` (needs hipcc) before "
                 "using the HIP SDPA operators; there is no fallback path."
             )
-        lib = ctypes.CDLL(str(p), mode=ctypes.RTLD_GLOBAL)
+        lib = ctypes.CDLL(str(p), mode=ctypes.RTLD_LOCAL)
         for name, (argtypes, restype) in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.argtypes = argtypes

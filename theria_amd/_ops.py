@@ -144,27 +144,30 @@ def _like_rows(t: torch.Tensor | None, ref: torch.Tensor, rows: int, name: str) 
 
 
 def fwd(q, k, v, scale: float, causal: bool, out_fp32: bool = False, stats: bool = False):
-    """O, lse (and the reference's m, l when stats=True). O is float32 when out_fp32."""
-    o, lse, m, l, _ = _fwd(q, k, v, scale, causal, out_fp32, stats, stats, False)
-    return o, lse, m, l
+    """O, lse (and the reference's m, l when stats=True). O is float32 when out_fp32. With 16-bit inputs the
+    lowest mantissa bit of lse flags the peaked rows (largest probability above 1/4), which the backward
+    takes on its exact path."""
+    return _fwd(q, k, v, scale, causal, out_fp32, stats, stats)
 
 
-def fwd_for_backward(q, k, v, scale: float, causal: bool, out_fp32: bool = False):
-    """(O, lse, m, O_lo): the forward plus what the backward takes from it. m (row maxima) marks the peaked
-    rows whose 16-bit backward products use two-term operands; O_lo (16-bit inputs with a 16-bit O, else
-    None) is the rounding residual of O, so that the backward's row term dO . O has float32 accuracy."""
-    residual = q.dtype != torch.float32 and not out_fp32
-    o, lse, m, _, o_lo = _fwd(q, k, v, scale, causal, out_fp32, True, False, residual)
-    return o, lse, m, o_lo
+def lse_from_stats(m, l, peaked_bits: bool = True):
+    """lse = m + log(l) (float32) from the reference's saved statistics, with the peaked-row flag of the
+    16-bit backward in its lowest mantissa bit: a row is peaked when its largest probability 1 / l exceeds
+    1/4, i.e. l < 4. Infinite entries (rows without visible keys) are left as they are."""
+    lse = (m.float() + torch.log(l.float())).contiguous()
+    if peaked_bits:
+        bits = lse.view(torch.int32)
+        flagged = (bits & ~1) | (l.float() < 4.0).to(torch.int32)
+        lse = torch.where(torch.isfinite(lse), flagged, bits).view(torch.float32)
+    return lse
 
 
-def _fwd(q, k, v, scale, causal, out_fp32, want_m, want_l, residual):
+def _fwd(q, k, v, scale, causal, out_fp32, want_m, want_l):
     check_inputs(q, k, v)
     q, k, v = _rowmajor(q), _rowmajor(k), _rowmajor(v)
     B, H, T, D = q.shape
     dev = q.device
     o = torch.empty((B, H, T, D), dtype=torch.float32 if out_fp32 else q.dtype, device=dev)
-    o_lo = torch.empty((B, H, T, D), dtype=q.dtype, device=dev) if residual else None
     lse = torch.empty((B, H, T), dtype=torch.float32, device=dev)
     m = torch.empty_like(lse) if want_m else None
     l = torch.empty_like(lse) if want_l else None
@@ -172,19 +175,16 @@ def _fwd(q, k, v, scale, causal, out_fp32, want_m, want_l, residual):
     prob = _problem(q, k, scale, causal)
     with _OnDevice(dev):
         rc = lib.theria_sdpa_fwd(
-            ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(o), 1 if out_fp32 else 0, _tv(o_lo), _fp(lse), _fp(m),
-            _fp(l), _stream(dev),
+            ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(o), 1 if out_fp32 else 0, _fp(lse), _fp(m), _fp(l),
+            _stream(dev),
         )
     _lib.check(rc, "theria_sdpa_fwd")
-    return o, lse, m, l, o_lo
+    return o, lse, m, l
 
 
-def bwd(q, k, v, o, lse, do, scale: float, causal: bool, need_dq: bool = True, need_dk: bool = True,
-        o_lo=None, row_max=None):
-    """dQ, dK, dV (input dtype) and the row term delta = rowsum(dO * O) (float32).
-
-    o_lo, row_max: the forward's O residual and row maxima (fwd_for_backward). Without row_max every row
-    of a 16-bit problem takes two-term operands (exact, slower)."""
+def bwd(q, k, v, o, lse, do, scale: float, causal: bool, need_dq: bool = True, need_dk: bool = True):
+    """dQ, dK, dV (input dtype) and the row term delta = rowsum(dO * O) (float32; formed exactly on query
+    blocks that hold a row flagged peaked in lse)."""
     check_inputs(q, k, v)
     q, k, v = _rowmajor(q), _rowmajor(k), _rowmajor(v)
     B, H, T, D = q.shape
@@ -197,11 +197,6 @@ def bwd(q, k, v, o, lse, do, scale: float, causal: bool, need_dq: bool = True, n
     if not o_f32 and o.dtype != q.dtype:
         o = o.to(q.dtype)
     lse = lse.contiguous()
-    row_max = None if row_max is None else row_max.contiguous()
-    if o_lo is not None:
-        if o_f32 or o_lo.dtype != q.dtype or tuple(o_lo.shape) != (B, H, T, D):
-            raise AssertionError("o_lo must be the (B,H,T,D) residual of a 16-bit O in the input dtype")
-        o_lo = _rowmajor(o_lo)
     dev = q.device
     delta = torch.empty((B, H, T), dtype=torch.float32, device=dev)
     dq = torch.empty((B, H, T, D), dtype=q.dtype, device=dev) if need_dq else None
@@ -209,34 +204,34 @@ def bwd(q, k, v, o, lse, do, scale: float, causal: bool, need_dq: bool = True, n
     dv = torch.empty((B, H, M, D), dtype=q.dtype, device=dev)
     prob = _problem(q, k, scale, causal)
     with _OnDevice(dev):
-        bwd_dq(prob, q, k, v, o, o_f32, do, lse, delta, dq, o_lo, row_max)
-        bwd_dkdv(prob, q, k, v, do, lse, delta, dk, dv, row_max)
+        bwd_dq(prob, q, k, v, o, o_f32, do, lse, delta, dq)
+        bwd_dkdv(prob, q, k, v, do, lse, delta, dk, dv)
     return dq, dk, dv, delta
 
 
 # The two backward kernels (theria_sdpa_bwd = bwd_dq then bwd_dkdv), on the current stream of the
 # current device. Arguments are already validated and laid out by bwd().
-def bwd_dq(prob, q, k, v, o, o_f32, do, lse, delta, dq, o_lo=None, row_max=None) -> None:
-    """dQ; with o given, delta = rowsum(dO * (O + O_lo)) is computed and written, else it is read."""
+def bwd_dq(prob, q, k, v, o, o_f32, do, lse, delta, dq) -> None:
+    """dQ; with o given, the row term delta is computed and written, else it is read."""
     rc = _lib.load().theria_sdpa_bwd_dq(
-        ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(o), 1 if o_f32 else 0, _tv(o_lo), _tv(do), _fp(lse),
-        _fp(row_max), _fp(delta), _tv(dq), _stream(q.device),
+        ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(o), 1 if o_f32 else 0, _tv(do), _fp(lse), _fp(delta),
+        _tv(dq), _stream(q.device),
     )
     _lib.check(rc, "theria_sdpa_bwd_dq")
 
 
-def bwd_dkdv(prob, q, k, v, do, lse, delta, dk, dv, row_max=None) -> None:
+def bwd_dkdv(prob, q, k, v, do, lse, delta, dk, dv) -> None:
     rc = _lib.load().theria_sdpa_bwd_dkdv(
-        ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(do), _fp(lse), _fp(row_max), _fp(delta), _tv(dk), _tv(dv),
+        ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(do), _fp(lse), _fp(delta), _tv(dk), _tv(dv),
         _stream(q.device),
     )
     _lib.check(rc, "theria_sdpa_bwd_dkdv")
 
 
 def bwd_from_stats(q, k, v, do, lse, scale: float, causal: bool, need_dq: bool, need_dk: bool, need_dv: bool,
-                   row_max=None, normalize: bool = False):
-    """Backward from saved statistics only (no O). v may be None when only dV is requested. row_max as in
-    bwd (the reference's saved m).
+                   normalize: bool = False):
+    """Backward from saved statistics only (no O). v may be None when only dV is requested. lse carries the
+    peaked-row flags as in bwd (lse_from_stats sets them from the reference's m, l).
 
     normalize=False: the reference's frozen-stats backward (P = exp(S - lse) as given, row term
     sum_j P_ij dP_ij). normalize=True: the row term of the normalised P, i.e. the exact softmax gradient, for
@@ -248,7 +243,6 @@ def bwd_from_stats(q, k, v, do, lse, scale: float, causal: bool, need_dq: bool, 
     M = k.shape[2]
     do = _like_rows(do, q, T, "dout")
     lse = lse.contiguous()
-    row_max = None if row_max is None else row_max.contiguous()
     dev = q.device
     delta = torch.empty((B, H, T), dtype=torch.float32, device=dev) if v is not None else None
     dq = torch.empty((B, H, T, D), dtype=q.dtype, device=dev) if need_dq else None
@@ -258,8 +252,8 @@ def bwd_from_stats(q, k, v, do, lse, scale: float, causal: bool, need_dq: bool, 
     prob = _problem(q, k, scale, causal)
     with _OnDevice(dev):
         rc = lib.theria_sdpa_bwd_from_stats(
-            ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(do), _fp(lse), _fp(row_max), _fp(delta), _tv(dq),
-            _tv(dk), _tv(dv), 1 if normalize else 0, _stream(dev),
+            ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(do), _fp(lse), _fp(delta), _tv(dq), _tv(dk),
+            _tv(dv), 1 if normalize else 0, _stream(dev),
         )
     _lib.check(rc, "theria_sdpa_bwd_from_stats")
     return dq, dk, (dv if need_dv else None)

@@ -60,34 +60,34 @@ def _assert_jvp_contract(q, k, v, dq, dk, dv, m, l):
 
 
 def _lse(m, l):
-    return (m.float() + torch.log(l.float())).contiguous()
+    return _ops.lse_from_stats(m, l)
 
 
 def sdpa_bwd_dq(q, k, v, dout, m, l, scale):
     """dQ = scale dS K with P rebuilt from (m, l)."""
     _assert_backward_contract(q, k, v, dout, m, l, require_v=True)
-    dq, _, _ = _ops.bwd_from_stats(q, k, v, dout, _lse(m, l), scale, False, True, False, False, row_max=m.float())
+    dq, _, _ = _ops.bwd_from_stats(q, k, v, dout, _lse(m, l), scale, False, True, False, False)
     return dq
 
 
 def sdpa_bwd_dk(q, k, v, dout, m, l, scale):
     """dK = scale dS^T Q with P rebuilt from (m, l)."""
     _assert_backward_contract(q, k, v, dout, m, l, require_v=True)
-    _, dk, _ = _ops.bwd_from_stats(q, k, v, dout, _lse(m, l), scale, False, False, True, False, row_max=m.float())
+    _, dk, _ = _ops.bwd_from_stats(q, k, v, dout, _lse(m, l), scale, False, False, True, False)
     return dk
 
 
 def sdpa_bwd_dv(q, k, dout, m, l, scale):
     """dV = P^T dO with P rebuilt from (m, l); needs no v (triton_sdpa_backward.py:194)."""
     _assert_backward_contract(q, k, None, dout, m, l, require_v=False)
-    _, _, dv = _ops.bwd_from_stats(q, k, None, dout, _lse(m, l), scale, False, False, False, True, row_max=m.float())
+    _, _, dv = _ops.bwd_from_stats(q, k, None, dout, _lse(m, l), scale, False, False, False, True)
     return dv
 
 
 def sdpa_bwd(q, k, v, dout, m, l, scale):
     """All three gradients in one backward pass: (dq, dk, dv)."""
     _assert_backward_contract(q, k, v, dout, m, l, require_v=True)
-    return _ops.bwd_from_stats(q, k, v, dout, _lse(m, l), scale, False, True, True, True, row_max=m.float())
+    return _ops.bwd_from_stats(q, k, v, dout, _lse(m, l), scale, False, True, True, True)
 
 
 def sdpa_jvp(q, k, v, dq, dk, dv, m, l, scale):

@@ -49,29 +49,29 @@ class TritonFusedSDPAFunction(torch.autograd.Function):
     @staticmethod
     def forward(q, k, v):
         _fused_guards(q, k, v)
-        return _ops.fwd_for_backward(q, k, v, _ops.default_scale(q.shape[-1]), False, out_fp32=True)
+        return _ops.fwd(q, k, v, _ops.default_scale(q.shape[-1]), False, out_fp32=True)[:2]
 
     @staticmethod
     def setup_context(ctx, inputs, output):
         q, k, v = inputs
-        o, lse, m, _ = output
+        o, lse = output
         ctx.scale = _ops.default_scale(q.shape[-1])
-        ctx.mark_non_differentiable(lse, m)
-        ctx.save_for_backward(q, k, v, o, lse, m)
+        ctx.mark_non_differentiable(lse)
+        ctx.save_for_backward(q, k, v, o, lse)
         ctx.save_for_forward(q, k, v, o, lse)
 
     @staticmethod
-    def backward(ctx, do, _dlse, _dm, _dolo):
+    def backward(ctx, do, _dlse):
         if do is None:
             return None, None, None
-        q, k, v, o, lse, m = ctx.saved_tensors
-        dq, dk, dv = SDPABackwardOp.apply(q, k, v, o.detach(), lse, do, ctx.scale, False, None, m)
+        q, k, v, o, lse = ctx.saved_tensors
+        dq, dk, dv = SDPABackwardOp.apply(q, k, v, o.detach(), lse, do, ctx.scale, False)
         return dq, dk, dv
 
     @staticmethod
     def jvp(ctx, tq, tk, tv):
         q, k, v, o, lse = ctx.saved_tensors
-        return _ops.jvp(q, k, v, o, lse, tq, tk, tv, ctx.scale, False, normalize=True).float(), None, None, None
+        return _ops.jvp(q, k, v, o, lse, tq, tk, tv, ctx.scale, False, normalize=True).float(), None
 
     @classmethod
     def apply(cls, q, k, v):  # O only, as the reference returns

@@ -15,9 +15,9 @@ from .. import _ops
 def _explicit_grads_sum(q, k, v):
     """Gradients of sum(O) with respect to q, k, v through the HIP forward + backward."""
     scale = _ops.default_scale(q.shape[-1])
-    o, lse, m, _ = _ops.fwd_for_backward(q, k, v, scale, False, out_fp32=True)
+    o, lse, _, _ = _ops.fwd(q, k, v, scale, False, out_fp32=True)
     dout = torch.ones(o.shape, dtype=q.dtype, device=q.device)
-    dq, dk, dv, _ = _ops.bwd(q, k, v, o, lse, dout, scale, False, row_max=m)
+    dq, dk, dv, _ = _ops.bwd(q, k, v, o, lse, dout, scale, False)
     return dq, dk, dv
 
 

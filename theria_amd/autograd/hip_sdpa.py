@@ -67,13 +67,12 @@ def _differentiable_double_backward(q, k, v, dout, gq, gk, gv, scale: float, cau
 
 
 class SDPABackwardOp(torch.autograd.Function):
-    """(q, k, v, o, lse, dout, scale, causal, o_lo, row_max) -> (dq, dk, dv). o, lse (and the forward's O
-    residual o_lo and row maxima row_max, which the 16-bit backward uses for its row term and peaked rows) are
-    treated as constants of q, k, v."""
+    """(q, k, v, o, lse, dout, scale, causal) -> (dq, dk, dv). o and lse (whose flag bits mark the peaked rows
+    of the 16-bit backward) are treated as constants of q, k, v."""
 
     @staticmethod
-    def forward(ctx, q, k, v, o, lse, dout, scale, causal, o_lo=None, row_max=None):
-        dq, dk, dv, delta = _ops.bwd(q, k, v, o, lse, dout, scale, causal, o_lo=o_lo, row_max=row_max)
+    def forward(ctx, q, k, v, o, lse, dout, scale, causal):
+        dq, dk, dv, delta = _ops.bwd(q, k, v, o, lse, dout, scale, causal)
         ctx.save_for_backward(q, k, v, o, lse, dout, delta)
         ctx.scale = scale
         ctx.causal = causal
@@ -83,38 +82,37 @@ class SDPABackwardOp(torch.autograd.Function):
     def backward(ctx, gq, gk, gv):
         q, k, v, o, lse, dout, delta = ctx.saved_tensors
         if gq is None and gk is None and gv is None:
-            return None, None, None, None, None, None, None, None, None, None
+            return None, None, None, None, None, None, None, None
         if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (q, k, v, dout, gq, gk, gv)):
             g_q, g_k, g_v, g_do = _differentiable_double_backward(q, k, v, dout, gq, gk, gv, ctx.scale, ctx.causal)
-            return g_q, g_k, g_v, None, None, g_do, None, None, None, None
+            return g_q, g_k, g_v, None, None, g_do, None, None
         g_q, g_k, g_v, g_do = _ops.bwd_bwd(q, k, v, o, dout, lse, delta, gq, gk, gv, ctx.scale, ctx.causal)
-        return g_q, g_k, g_v, None, None, g_do.to(dout.dtype), None, None, None, None
+        return g_q, g_k, g_v, None, None, g_do.to(dout.dtype), None, None
 
 
 class SDPAOp(torch.autograd.Function):
-    """(q, k, v, scale, causal, out_fp32) -> (o, lse, m, o_lo); m (row maxima) and o_lo (the rounding
-    residual of a 16-bit O, or None) are what the backward takes from the forward."""
+    """(q, k, v, scale, causal, out_fp32) -> (o, lse)."""
 
     @staticmethod
     def forward(q, k, v, scale, causal, out_fp32):
-        return _ops.fwd_for_backward(q, k, v, scale, causal, out_fp32=out_fp32)
+        return _ops.fwd(q, k, v, scale, causal, out_fp32=out_fp32)[:2]
 
     @staticmethod
     def setup_context(ctx, inputs, output):
         q, k, v, scale, causal, out_fp32 = inputs
-        o, lse, m, o_lo = output
+        o, lse = output
         ctx.scale = scale
         ctx.causal = causal
-        ctx.mark_non_differentiable(*(t for t in (lse, m, o_lo) if t is not None))
-        ctx.save_for_backward(q, k, v, o, lse, m, o_lo)
+        ctx.mark_non_differentiable(lse)
+        ctx.save_for_backward(q, k, v, o, lse)
         ctx.save_for_forward(q, k, v, o, lse)
 
     @staticmethod
-    def backward(ctx, do, _dlse, _dm, _dolo):
+    def backward(ctx, do, _dlse):
         if do is None:
             return None, None, None, None, None, None
-        q, k, v, o, lse, m, o_lo = ctx.saved_tensors
-        dq, dk, dv = SDPABackwardOp.apply(q, k, v, o.detach(), lse, do, ctx.scale, ctx.causal, o_lo, m)
+        q, k, v, o, lse = ctx.saved_tensors
+        dq, dk, dv = SDPABackwardOp.apply(q, k, v, o.detach(), lse, do, ctx.scale, ctx.causal)
         return dq, dk, dv, None, None, None
 
     @staticmethod
@@ -123,7 +121,7 @@ class SDPAOp(torch.autograd.Function):
         to = _ops.jvp(q, k, v, o, lse, tq, tk, tv, ctx.scale, ctx.causal, normalize=True)
         if to.dtype != o.dtype:
             to = to.to(o.dtype)
-        return to, None, None, None
+        return to, None
 
 
 def _common_head_dim(q, k, v):
@@ -181,7 +179,7 @@ def hip_sdpa_hvp(q, k, v, vq, vk, vv, *, weight=None, target=None, causal: bool 
     if weight is not None and target is not None:
         raise ValueError("hip_sdpa_hvp: give weight or target, not both")
     with torch.no_grad():
-        o, lse, m, o_lo = _ops.fwd_for_backward(q, k, v, float(scale), bool(causal))
+        o, lse, _, _ = _ops.fwd(q, k, v, float(scale), bool(causal))
         if target is not None:
             dout = (o.float() - target.float()).to(o.dtype)
         elif weight is not None:
@@ -192,7 +190,7 @@ def hip_sdpa_hvp(q, k, v, vq, vk, vv, *, weight=None, target=None, causal: bool 
         hq, hk, hv, g_do = _ops.bwd_bwd(q, k, v, o, dout, lse, delta, vq, vk, vv, float(scale), bool(causal))
         if target is None:
             return hq, hk, hv
-        jq, jk, jv, _ = _ops.bwd(q, k, v, o, lse, g_do.to(o.dtype), float(scale), bool(causal), o_lo=o_lo, row_max=m)
+        jq, jk, jv, _ = _ops.bwd(q, k, v, o, lse, g_do.to(o.dtype), float(scale), bool(causal))
         return hq + jq, hk + jk, hv + jv
 
 

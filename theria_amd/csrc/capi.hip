@@ -126,9 +126,8 @@ THERIA_API int theria_abi_version(void) { return THERIA_SDPA_ABI_VERSION; }
 THERIA_API const char* theria_last_error(void) { return g_last_error.c_str(); }
 
 THERIA_API int theria_sdpa_fwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
-                               const theria_tensor_t* v, const theria_tensor_t* o, int32_t o_is_f32,
-                               const theria_tensor_t* o_lo, float* lse, float* row_max, float* row_sum,
-                               void* stream) {
+                               const theria_tensor_t* v, const theria_tensor_t* o, int32_t o_is_f32, float* lse,
+                               float* row_max, float* row_sum, void* stream) {
   theria::Shape s;
   std::string err;
   if (!shape_from(p, s, err)) return fail(THERIA_ERR_CONTRACT, err);
@@ -137,10 +136,7 @@ THERIA_API int theria_sdpa_fwd(const theria_sdpa_problem_t* p, const theria_tens
   c.kview(k, "k", true);
   c.kview(v, "v", true);
   c.qview(o, "o", true);
-  c.qview(o_lo, "o_lo", false);
   c.need(lse != nullptr || !c.q_rows, "lse is required");
-  c.need(!(o_lo && o_lo->data) || (s.dtype != THERIA_DTYPE_F32 && !o_is_f32),
-         "o_lo is the residual of a 16-bit O (16-bit inputs, o_is_f32 = 0)");
   if (o_is_f32 && o && (o->stride_b % 4 || o->stride_h % 4 || o->stride_row % 4)) c.vec = false;
   if (!c.err.empty()) return fail(THERIA_ERR_CONTRACT, c.err);
   s.vec = c.vec;
@@ -151,18 +147,18 @@ THERIA_API int theria_sdpa_fwd(const theria_sdpa_problem_t* p, const theria_tens
   fp.k = cv(k);
   fp.v = cv(v);
   fp.o = mv(o);
-  fp.o_lo = mv(o_lo);
   fp.o_f32 = o_is_f32 != 0;
   fp.lse = lse;
   fp.row_max = row_max;
   fp.row_sum = row_sum;
-  return hip_status(theria::launch_fwd(fp, 0, (hipStream_t)stream), "theria_sdpa_fwd");
+  return hip_status(theria::launch_fwd(fp, (hipStream_t)stream), "theria_sdpa_fwd");
 }
 
+// The dQ kernel; row_term (theria::RowTerm) says how it obtains the row term it writes to (or reads from) delta.
 static int run_dq(const theria::Shape& s, const theria_tensor_t* q, const theria_tensor_t* k,
-                  const theria_tensor_t* v, const theria_tensor_t* o, bool o_f32, const theria_tensor_t* o_lo,
-                  const theria_tensor_t* dout, const float* lse, const float* row_max, float* delta,
-                  const theria_tensor_t* dq, hipStream_t st) {
+                  const theria_tensor_t* v, const theria_tensor_t* o, bool o_f32, int row_term,
+                  const theria_tensor_t* dout, const float* lse, float* delta,
+                  const theria_tensor_t* dq, hipStream_t st, const char* what) {
   theria::DqParams dp{};
   dp.s = s;
   dp.q = cv(q);
@@ -170,17 +166,16 @@ static int run_dq(const theria::Shape& s, const theria_tensor_t* q, const theria
   dp.v = cv(v);
   dp.dout = cv(dout);
   dp.o = cv(o);
-  dp.o_lo = (o && o->data) ? cv(o_lo) : theria::View{nullptr, 0, 0, 0};
   dp.o_f32 = o_f32;
+  dp.row_term = row_term;
   dp.lse = lse;
-  dp.row_max = row_max;
   dp.delta = delta;
   dp.dq = mv(dq);
-  return hip_status(theria::launch_bwd_dq(dp, st), "theria_sdpa_bwd_dq");
+  return hip_status(theria::launch_bwd_dq(dp, st), what);
 }
 
 static int run_dkdv(const theria::Shape& s, const theria_tensor_t* q, const theria_tensor_t* k,
-                    const theria_tensor_t* v, const theria_tensor_t* dout, const float* lse, const float* row_max,
+                    const theria_tensor_t* v, const theria_tensor_t* dout, const float* lse,
                     const float* delta, const theria_tensor_t* dk, const theria_tensor_t* dv, bool dv_only,
                     hipStream_t st) {
   theria::DkdvParams kp{};
@@ -190,7 +185,6 @@ static int run_dkdv(const theria::Shape& s, const theria_tensor_t* q, const ther
   kp.v = cv(v);
   kp.dout = cv(dout);
   kp.lse = lse;
-  kp.row_max = row_max;
   kp.delta = delta;
   kp.dk = mv(dk);
   kp.dv = mv(dv);
@@ -200,8 +194,8 @@ static int run_dkdv(const theria::Shape& s, const theria_tensor_t* q, const ther
 
 THERIA_API int theria_sdpa_bwd_dq(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
                                   const theria_tensor_t* v, const theria_tensor_t* o, int32_t o_is_f32,
-                                  const theria_tensor_t* o_lo, const theria_tensor_t* dout, const float* lse,
-                                  const float* row_max, float* delta, const theria_tensor_t* dq, void* stream) {
+                                  const theria_tensor_t* dout, const float* lse, float* delta,
+                                  const theria_tensor_t* dq, void* stream) {
   theria::Shape s;
   std::string err;
   if (!shape_from(p, s, err)) return fail(THERIA_ERR_CONTRACT, err);
@@ -210,22 +204,22 @@ THERIA_API int theria_sdpa_bwd_dq(const theria_sdpa_problem_t* p, const theria_t
   c.kview(k, "k", true);
   c.kview(v, "v", true);
   c.qview(o, "o", false);
-  c.qview(o_lo, "o_lo", false);
   c.qview(dout, "dout", true);
   c.qview(dq, "dq", false);
   c.need(lse != nullptr || !c.q_rows, "lse is required");
   c.need(delta != nullptr || !c.q_rows, "delta is required");
-  c.need(!(o_lo && o_lo->data) || (s.dtype != THERIA_DTYPE_F32 && !o_is_f32), "o_lo is the residual of a 16-bit O");
   if (o_is_f32 && o && (o->stride_b % 4 || o->stride_h % 4 || o->stride_row % 4)) c.vec = false;
   if (!c.err.empty()) return fail(THERIA_ERR_CONTRACT, c.err);
   s.vec = c.vec;
   if (!c.q_rows) return THERIA_OK;
-  return run_dq(s, q, k, v, o, o_is_f32 != 0, o_lo, dout, lse, row_max, delta, dq, (hipStream_t)stream);
+  const int rt = (o && o->data) ? theria::kRowFromO : theria::kRowGiven;
+  return run_dq(s, q, k, v, o, o_is_f32 != 0, rt, dout, lse, delta, dq, (hipStream_t)stream,
+                "theria_sdpa_bwd_dq");
 }
 
 THERIA_API int theria_sdpa_bwd_dkdv(const theria_sdpa_problem_t* p, const theria_tensor_t* q,
                                     const theria_tensor_t* k, const theria_tensor_t* v,
-                                    const theria_tensor_t* dout, const float* lse, const float* row_max,
+                                    const theria_tensor_t* dout, const float* lse,
                                     const float* delta, const theria_tensor_t* dk, const theria_tensor_t* dv,
                                     void* stream) {
   theria::Shape s;
@@ -243,14 +237,14 @@ THERIA_API int theria_sdpa_bwd_dkdv(const theria_sdpa_problem_t* p, const theria
   if (!c.err.empty()) return fail(THERIA_ERR_CONTRACT, c.err);
   s.vec = c.vec;
   if (!c.k_rows) return THERIA_OK;
-  return run_dkdv(s, q, k, v, dout, lse, row_max, delta, dk, dv, false, (hipStream_t)stream);
+  return run_dkdv(s, q, k, v, dout, lse, delta, dk, dv, false, (hipStream_t)stream);
 }
 
 THERIA_API int theria_sdpa_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
                                const theria_tensor_t* v, const theria_tensor_t* o, int32_t o_is_f32,
-                               const theria_tensor_t* o_lo, const theria_tensor_t* dout, const float* lse,
-                               const float* row_max, float* delta_out, const theria_tensor_t* dq,
-                               const theria_tensor_t* dk, const theria_tensor_t* dv, void* stream) {
+                               const theria_tensor_t* dout, const float* lse,
+                               float* delta_out, const theria_tensor_t* dq, const theria_tensor_t* dk,
+                               const theria_tensor_t* dv, void* stream) {
   theria::Shape s;
   std::string err;
   if (!shape_from(p, s, err)) return fail(THERIA_ERR_CONTRACT, err);
@@ -259,29 +253,28 @@ THERIA_API int theria_sdpa_bwd(const theria_sdpa_problem_t* p, const theria_tens
   c.kview(k, "k", true);
   c.kview(v, "v", true);
   c.qview(o, "o", true);
-  c.qview(o_lo, "o_lo", false);
   c.qview(dout, "dout", true);
   c.qview(dq, "dq", false);
   c.kview(dk, "dk", false);
   c.kview(dv, "dv", true);
   c.need(lse != nullptr || !c.q_rows, "lse is required");
   c.need(delta_out != nullptr || !c.q_rows, "delta_out is required");
-  c.need(!(o_lo && o_lo->data) || (s.dtype != THERIA_DTYPE_F32 && !o_is_f32), "o_lo is the residual of a 16-bit O");
   if (o_is_f32 && o && (o->stride_b % 4 || o->stride_h % 4 || o->stride_row % 4)) c.vec = false;
   if (!c.err.empty()) return fail(THERIA_ERR_CONTRACT, c.err);
   s.vec = c.vec;
   const hipStream_t st = (hipStream_t)stream;
   if (c.q_rows) {
-    int rc = run_dq(s, q, k, v, o, o_is_f32 != 0, o_lo, dout, lse, row_max, delta_out, dq, st);
+    int rc = run_dq(s, q, k, v, o, o_is_f32 != 0, theria::kRowFromO, dout, lse, delta_out, dq, st,
+                    "theria_sdpa_bwd (dq)");
     if (rc != THERIA_OK) return rc;
   }
   if (!c.k_rows) return THERIA_OK;
-  return run_dkdv(s, q, k, v, dout, lse, row_max, delta_out, dk, dv, false, st);
+  return run_dkdv(s, q, k, v, dout, lse, delta_out, dk, dv, false, st);
 }
 
 THERIA_API int theria_sdpa_bwd_from_stats(const theria_sdpa_problem_t* p, const theria_tensor_t* q,
                                           const theria_tensor_t* k, const theria_tensor_t* v,
-                                          const theria_tensor_t* dout, const float* lse, const float* row_max,
+                                          const theria_tensor_t* dout, const float* lse,
                                           float* delta_out, const theria_tensor_t* dq, const theria_tensor_t* dk,
                                           const theria_tensor_t* dv, int32_t normalize, void* stream) {
   theria::Shape s;
@@ -303,25 +296,14 @@ THERIA_API int theria_sdpa_bwd_from_stats(const theria_sdpa_problem_t* p, const 
   s.vec = c.vec;
   const hipStream_t st = (hipStream_t)stream;
   if (!dv_only && c.q_rows) {
-    // row term from P(lse) and V (mode 1 of the forward kernel), then dQ with that delta
-    theria::FwdParams fp{};
-    fp.s = s;
-    fp.q = cv(q);
-    fp.k = cv(k);
-    fp.v = cv(v);
-    fp.dout = cv(dout);
-    fp.lse = const_cast<float*>(lse);
-    fp.delta = delta_out;
-    fp.row_normalize = normalize != 0;
-    int rc = hip_status(theria::launch_fwd(fp, 1, st), "theria_sdpa_bwd_from_stats (delta)");
+    // the dQ kernel forms the row term from P(lse) and dP in a first pass over the keys (and dQ when asked)
+    const int rt = normalize ? theria::kRowNormalized : theria::kRowFrozen;
+    const int rc = run_dq(s, q, k, v, nullptr, false, rt, dout, lse, delta_out, dq, st,
+                          "theria_sdpa_bwd_from_stats (dq)");
     if (rc != THERIA_OK) return rc;
-    if (dq && dq->data) {
-      rc = run_dq(s, q, k, v, nullptr, false, nullptr, dout, lse, row_max, delta_out, dq, st);
-      if (rc != THERIA_OK) return rc;
-    }
   }
   if (!c.k_rows) return THERIA_OK;
-  return run_dkdv(s, q, k, v, dout, lse, row_max, delta_out, dk, dv, dv_only, st);
+  return run_dkdv(s, q, k, v, dout, lse, delta_out, dk, dv, dv_only, st);
 }
 
 THERIA_API int theria_sdpa_jvp(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
@@ -405,19 +387,13 @@ THERIA_API int theria_sdpa_bwd_bwd(const theria_sdpa_problem_t* p, const theria_
   bp.r_row = row_ws;
   bp.t_row = row_ws + nrows;
   if (s.dtype != THERIA_DTYPE_F32 && s.T > 0) {
-    // 16-bit inputs: the row term consistent with P(lse), sum_j P_ij dP_ij = dO_i . sum_j P_ij V_j in float32
-    // (mode 1 of the forward kernel), instead of dO . O with the 16-bit O.
-    theria::FwdParams fp{};
-    fp.s = s;
-    fp.q = cv(q);
-    fp.k = cv(k);
-    fp.v = cv(v);
-    fp.dout = cv(dout);
-    fp.lse = const_cast<float*>(lse);
-    fp.delta = row_ws + 2 * nrows;
-    const int rc = hip_status(theria::launch_fwd(fp, 1, st), "theria_sdpa_bwd_bwd (row term)");
+    // 16-bit inputs: the row term consistent with P(lse), sum_j P_ij dP_ij in float32 (the row-term pass of
+    // the dQ kernel), instead of dO . O with the 16-bit O.
+    float* rt_delta = row_ws + 2 * nrows;
+    const int rc = run_dq(s, q, k, v, nullptr, false, theria::kRowFrozen, dout, lse, rt_delta, nullptr, st,
+                          "theria_sdpa_bwd_bwd (row term)");
     if (rc != THERIA_OK) return rc;
-    bp.delta = fp.delta;
+    bp.delta = rt_delta;
   }
   bp.out_gq = mv(out_gq);
   bp.out_gk = mv(out_gk);

@@ -70,7 +70,7 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DQ_MINW : 1)) void dq_kernel(const
 
   F qf[QT][NKC], of[QT][NKC];
   float lse2[QT], del[QT];
-  bool peaked = false;  // a row of this wave's largest probability exceeds 1/16 (or no row maxima given)
+  bool peaked = false;  // a row of this wave is flagged peaked in its lse
 #pragma unroll
   for (int j = 0; j < QT; ++j) {
     const int myq = q0w + 32 * j + li;
@@ -82,8 +82,9 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DQ_MINW : 1)) void dq_kernel(const
     }
     const float lse = qvalid ? p.lse[rowbase + myq] : THERIA_INF;
     lse2[j] = lse == -THERIA_INF ? THERIA_INF : lse * kLog2e;  // a row without visible keys has P = 0
-    peaked |= qvalid && (!p.row_max || p.row_max[rowbase + myq] - lse > kPeakedLog);
-    if (p.o.p) {
+    peaked |= qvalid && lse_peaked(lse);
+    del[j] = 0.f;
+    if (p.row_term == kRowFromO) {
       // delta = dO . O over this lane's half of the head dim (the dO fragment's columns), then the pair
       float part = 0.f;
       if (qvalid) {
@@ -96,10 +97,8 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DQ_MINW : 1)) void dq_kernel(const
             for (int e = 0; e < 8; ++e) {
               if (col + e < s.D) {
                 const int64_t off = (int64_t)myq * p.o.sr + col + e;
-                float ov = p.o_f32 ? ((const float*)p.o.p + b * p.o.sb + h * p.o.sh)[off]
-                                   : (float)((const T*)p.o.p + b * p.o.sb + h * p.o.sh)[off];
-                if (p.o_lo.p)  // rounding residual of a 16-bit O
-                  ov += (float)((const T*)p.o_lo.p + b * p.o_lo.sb + h * p.o_lo.sh)[(int64_t)myq * p.o_lo.sr + col + e];
+                const float ov = p.o_f32 ? ((const float*)p.o.p + b * p.o.sb + h * p.o.sh)[off]
+                                         : (float)((const T*)p.o.p + b * p.o.sb + h * p.o.sh)[off];
                 part += ov * (float)od[e];
               }
             }
@@ -111,68 +110,69 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DQ_MINW : 1)) void dq_kernel(const
       }
       del[j] = pair_sum(part);
       if (qvalid && g == 0) p.delta[rowbase + myq] = del[j];
-    } else {
+    } else if (p.row_term == kRowGiven) {
       del[j] = qvalid ? p.delta[rowbase + myq] : 0.f;
     }
   }
-  if (!p.dq.p) return;  // only the row term was requested (uniform over the grid)
+  if (!p.dq.p && p.row_term < kRowFrozen) return;  // only dO . O was requested (uniform over the grid)
   const float c2 = s.scale * kLog2e;
 
   int kend = s.M;
   if (CAUSAL) kend = min(s.M, qb * BM + BM);
   const int nkt = (kend + BN - 1) / BN;
 
-  // 16-bit, a workgroup holding a peaked row: delta = sum_j P_ij dP_ij / sum_j P_ij formed exactly first (one
-  // more pass over the key tiles): dO . O from the forward's O carries the 16-bit rounding of its P in the PV
-  // product, which a peaked row does not average out. The dK/dV kernel reads the same delta.
-  if constexpr (sizeof(T) == 2) {
-    if (__syncthreads_or(__any(peaked)) && nkt > 0) {
-      float a_part[QT], l_part[QT];
+  // The row term from a pass over the key tiles: always for the frozen / normalised forms, and (16-bit) for a
+  // workgroup holding a peaked row in place of dO . O, whose 16-bit P rounding in the forward's PV product
+  // a peaked row does not average out. The dK/dV kernel reads the same delta.
+  bool exact_row_term = p.row_term >= kRowFrozen;
+  if (sizeof(T) == 2 && p.row_term == kRowFromO) exact_row_term = __syncthreads_or(__any(peaked));
+  if (exact_row_term) {
+    float a_part[QT], l_part[QT];
 #pragma unroll
-      for (int j = 0; j < QT; ++j) a_part[j] = l_part[j] = 0.f;
-      TileStage<T, BN, DP, NT> pK, pV;
-      for (int kt = 0; kt < nkt; ++kt) {
-        const int k0 = kt * BN;
-        pK.load(K, p.k.sr, k0, s.M, s.D, s.vec);
-        pV.load(V, p.v.sr, k0, s.M, s.D, s.vec);
-        __syncthreads();
-        pK.store(sK, PITCH);
-        pV.store(sV, PITCH);
-        __syncthreads();
-        if (CAUSAL && k0 > q0w + 32 * QT - 1) continue;
-        f32x16_t sc[QT], dpp[QT];
+    for (int j = 0; j < QT; ++j) a_part[j] = l_part[j] = 0.f;
+    TileStage<T, BN, DP, NT> pK, pV;
+    for (int kt = 0; kt < nkt; ++kt) {
+      const int k0 = kt * BN;
+      pK.load(K, p.k.sr, k0, s.M, s.D, s.vec);
+      pV.load(V, p.v.sr, k0, s.M, s.D, s.vec);
+      __syncthreads();
+      pK.store(sK, PITCH);
+      pV.store(sV, PITCH);
+      __syncthreads();
+      if (CAUSAL && k0 > q0w + 32 * QT - 1) continue;
+      f32x16_t sc[QT], dpp[QT];
 #pragma unroll
-        for (int j = 0; j < QT; ++j) sc[j] = dpp[j] = zero16();
+      for (int j = 0; j < QT; ++j) sc[j] = dpp[j] = zero16();
 #pragma unroll
-        for (int c = 0; c < NKC; ++c) {
-          const F kfr = lds_cols<T, KLIN>(sK, PITCH, li, 0, c);
-          const F vfr = lds_cols<T, KLIN>(sV, PITCH, li, 0, c);
-#pragma unroll
-          for (int j = 0; j < QT; ++j) {
-            sc[j] = MM::mma(kfr, qf[j][c], sc[j]);
-            dpp[j] = MM::mma(vfr, of[j][c], dpp[j]);
-          }
-        }
+      for (int c = 0; c < NKC; ++c) {
+        const F kfr = lds_cols<T, KLIN>(sK, PITCH, li, 0, c);
+        const F vfr = lds_cols<T, KLIN>(sV, PITCH, li, 0, c);
 #pragma unroll
         for (int j = 0; j < QT; ++j) {
-          const int lim = CAUSAL ? min(s.M, q0w + 32 * j + li + 1) : s.M;  // first key this query cannot see
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float pv = k0 + acc_row(r, g) < lim ? fast_exp2(fmaf(sc[j][r], c2, -lse2[j])) : 0.f;
-            a_part[j] = fmaf(pv, dpp[j][r], a_part[j]);
-            l_part[j] += pv;
-          }
+          sc[j] = MM::mma(kfr, qf[j][c], sc[j]);
+          dpp[j] = MM::mma(vfr, of[j][c], dpp[j]);
         }
       }
 #pragma unroll
       for (int j = 0; j < QT; ++j) {
-        const float a = pair_sum(a_part[j]), l = pair_sum(l_part[j]);
-        del[j] = l > 0.f ? a / l : 0.f;
-        const int myq = q0w + 32 * j + li;
-        if (myq < s.T && g == 0) p.delta[rowbase + myq] = del[j];
+        const int lim = CAUSAL ? min(s.M, q0w + 32 * j + li + 1) : s.M;  // first key this query cannot see
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float pv = k0 + acc_row(r, g) < lim ? fast_exp2(fmaf(sc[j][r], c2, -lse2[j])) : 0.f;
+          a_part[j] = fmaf(pv, dpp[j][r], a_part[j]);
+          l_part[j] += pv;
+        }
       }
     }
+#pragma unroll
+    for (int j = 0; j < QT; ++j) {
+      const float a = pair_sum(a_part[j]), l = pair_sum(l_part[j]);
+      del[j] = p.row_term == kRowFrozen ? a : (l > 0.f ? a / l : 0.f);
+      const int myq = q0w + 32 * j + li;
+      if (myq < s.T && g == 0) p.delta[rowbase + myq] = del[j];
+    }
   }
+  if (!p.dq.p) return;  // only the row term was requested
 
   f32x16_t acc[QT][NDT];
 #pragma unroll
@@ -340,7 +340,7 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DKDV_MINW : 1)) void dkdv_kernel(c
 
   TileStage<T, BM, DP, NT> stQ, stO;
   float pre_lse = THERIA_INF, pre_del = 0.f;
-  bool pre_pk = false;  // 16-bit: this row's largest probability exceeds 1/16 (or no row maxima given)
+  bool pre_pk = false;  // 16-bit: this row is flagged peaked in its lse
   auto prefetch = [&](int q0) {
     stQ.load(Q, p.q.sr, q0, s.T, s.D, s.vec);
     stO.load(dO, p.dout.sr, q0, s.T, s.D, s.vec);
@@ -349,7 +349,7 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DKDV_MINW : 1)) void dkdv_kernel(c
       const float lse = qq < s.T ? p.lse[rowbase + qq] : THERIA_INF;
       pre_lse = lse == -THERIA_INF ? THERIA_INF : lse * kLog2e;
       pre_del = (qq < s.T && !dv_only) ? -p.delta[rowbase + qq] : 0.f;  // staged negated: dP starts at -delta
-      if constexpr (sizeof(T) == 2) pre_pk = qq < s.T && (!p.row_max || p.row_max[rowbase + qq] - lse > kPeakedLog);
+      if constexpr (sizeof(T) == 2) pre_pk = qq < s.T && lse_peaked(lse);
     }
   };
   if (nqt > 0) prefetch(qbeg);

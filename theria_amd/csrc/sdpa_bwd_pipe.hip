@@ -68,7 +68,12 @@ namespace theria {
 
 // FD: the head dim is DP itself (compile-time bounds); otherwise the runtime head dim s.D < DP bounds the
 // loads, stores and DMA chunks (both kernels).
-template <typename T, bool CAUSAL, int NW, int DP, bool OVERLAP, int WPS, int HALVES, bool FD>
+// Two launches share the query tiles of every key block: PEAKED = false runs the tiles without a peaked row
+// (flagged in lse: largest probability above 1/4) with K pre-multiplied by scale * log2(e) and S started from -lse2, so
+// P = exp2(S); PEAKED = true then finds the tiles holding a peaked row (a scan of the lse flags), runs
+// them from the exact float32 scores with P and dS as two 16-bit terms each, and adds its sums to dK, dV.
+// Keeping the two apart keeps the common kernel's registers and schedule.
+template <typename T, bool CAUSAL, int NW, int DP, bool OVERLAP, int WPS, int HALVES, bool FD, bool PEAKED>
 __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
@@ -82,7 +87,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
   __shared__ __attribute__((aligned(1024))) char sQ1[TILE];
   __shared__ __attribute__((aligned(1024))) char sO0[TILE];
   __shared__ __attribute__((aligned(1024))) char sO1[TILE];
-  __shared__ __attribute__((aligned(16))) float sR0[2 * BM];  // [-lse / scale | -delta] of a tile
+  __shared__ __attribute__((aligned(16))) float sR0[2 * BM];  // [-lse * log2(e) | -delta] of a tile
   __shared__ __attribute__((aligned(16))) float sR1[2 * BM];
   __shared__ int sF0[2], sF1[2];  // per 64-row half: the tile holds a peaked row
 
@@ -116,11 +121,18 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
   const int key0 = kb * BN;
   const int kw0 = key0 + wave * 32;  // this wave's keys: kw0 + li
 
+    // K pre-multiplied by scale * log2(e) and S started from -lse * log2(e): P = exp2(S) with no per-score
+    // scaling. The peaked launch forms the exact scores from K itself, and loads V only once it has found a
+    // tile to run.
     F kf[NKC], vf[NKC];
+    auto load_v = [&]() {
 #pragma unroll
-    for (int c = 0; c < NKC; ++c) {
-      kf[c] = gload_frag8<T>(K, p.k.sr, kw0 + li, s.M, c, FD ? DP : s.D);
-      vf[c] = gload_frag8<T>(V, p.v.sr, kw0 + li, s.M, c, FD ? DP : s.D);
+      for (int c = 0; c < NKC; ++c) vf[c] = gload_frag8<T>(V, p.v.sr, kw0 + li, s.M, c, FD ? DP : s.D);
+    };
+    if (!PEAKED) {
+#pragma unroll
+      for (int c = 0; c < NKC; ++c) kf[c] = scaled_frag<T>(gload_frag8<T>(K, p.k.sr, kw0 + li, s.M, c, FD ? DP : s.D), c2);
+      load_v();
     }
     f32x16_t dv[NDT], dk[NDT];
 #pragma unroll
@@ -141,27 +153,34 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
     const uint32_t qrs = (uint32_t)p.q.sr * 2, ors = (uint32_t)p.dout.sr * 2;
     const rsrc_t qrsrc = make_rsrc(Q, (uint32_t)slab_span(s.T, qrs, 2 * (FD ? DP : s.D)));
     const rsrc_t orsrc = make_rsrc(dO, (uint32_t)slab_span(s.T, ors, 2 * (FD ? DP : s.D)));
+    // K unscaled for the exact body: chunk c of key kw0 + li by a buffer load (zeros past the head dim and the
+    // last key), so that no per-chunk address stays live across the tile loop.
+    const uint32_t krs = (uint32_t)p.k.sr * 2;
+    const rsrc_t krsrc = make_rsrc(K, (uint32_t)slab_span(s.M, krs, 2 * (FD ? DP : s.D)));
+    auto kraw = [&](int c) {
+      const int key = kw0 + li, col = c * 16 + 8 * g;
+      const bool ok = key < s.M && (FD || col < s.D);
+      return __builtin_bit_cast(F, buf_load16(krsrc, ok ? (uint32_t)key * krs + 2 * col : 0x80000000u, 0));
+    };
 
-    // Row terms of tile `it` for thread tid < BM, loaded two tiles ahead as raw lse, row max and delta (rows
-    // past the end: lse = +inf) and converted only when stored, so that no instruction waits for these loads
-    // (or for the DMA issued just before them) until the next tile. Stored: -lse / scale (-inf for rows past
-    // the end or without visible keys, so P = 0), -delta, and per 64-row half whether it holds a peaked row
-    // (every row counts as peaked when the row maxima are not given).
-    float r_lse = THERIA_INF, r_del = 0.f, r_m = -THERIA_INF;
-    const float inv_scale = 1.f / s.scale;
+    // Row terms of tile `it` for thread tid < BM, loaded two tiles ahead as raw lse and delta (rows past the
+    // end: lse = +inf) and converted only when stored, so that no instruction waits for these loads (or for
+    // the DMA issued just before them) until the next tile. Stored: -lse * log2(e) (-inf for rows past the
+    // end or without visible keys, so P = 0), -delta, and per 64-row half whether it holds a row flagged
+    // peaked in its lse.
+    float r_lse = THERIA_INF, r_del = 0.f;
     auto load_rows = [&](int it) {
       if (tid < BM && it < nqt) {
         const int qq = qbeg + it * BM + tid;
         r_lse = qq < s.T ? p.lse[rowbase + qq] : THERIA_INF;
         r_del = qq < s.T ? p.delta[rowbase + qq] : 0.f;
-        r_m = qq < s.T ? (p.row_max ? p.row_max[rowbase + qq] : THERIA_INF) : -THERIA_INF;
       }
     };
     auto store_rows = [&](float* sr, int* sf) {
       if (tid < BM) {  // whole waves (BM is a multiple of 64)
-        sr[tid] = __builtin_isinf(r_lse) ? -THERIA_INF : -r_lse * inv_scale;
+        sr[tid] = __builtin_isinf(r_lse) ? -THERIA_INF : -r_lse * kLog2e;
         sr[BM + tid] = -r_del;
-        const bool pk = __any(r_m - r_lse > kPeakedLog);
+        const bool pk = __any(lse_peaked(r_lse));
         if (lane == 0) sf[tid >> 6] = pk;
       }
     };
@@ -169,7 +188,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
       return __builtin_amdgcn_readfirstlane(BM > 64 ? (sf[0] | sf[1]) : sf[0]) != 0;
     };
 
-    // S = Q K^T - lse / scale and dP = dO V^T - delta for subtile qs (32 queries) of the tile in (tq, to, tr).
+    // S = c2 Q K^T - lse2 and dP = dO V^T - delta for subtile qs (32 queries) of the tile in (tq, to, tr).
     auto sdp = [&](const char* tq, const char* to, const float* tr, int qs, f32x16_t& sc, f32x16_t& dp) {
 #pragma unroll
       for (int qd = 0; qd < 4; ++qd) {
@@ -196,11 +215,11 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
           if (mykey >= s.M || (CAUSAL && mykey > q0s + acc_row(r, g))) sc[r] = -THERIA_INF;
       }
     };
-    // P = exp2(S c2) and dS = P o dP as 16-bit fragments (KACC chunks 0, 1).
+    // P = exp2(S) and dS = P o dP as 16-bit fragments (KACC chunks 0, 1).
     auto pds = [&](const f32x16_t& sc, const f32x16_t& dp, F (&pf)[2], F (&df)[2]) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float pv = fast_exp2(sc[r] * c2);
+        const float pv = fast_exp2(sc[r]);
         pf[r >> 3][r & 7] = (T)pv;
         df[r >> 3][r & 7] = (T)(pv * dp[r]);
       }
@@ -215,27 +234,6 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
           dk[dt] = MM::mma(df[cc], swz_rows<T, DP>(tq, 32 * qs, cc, 32 * dt), dk[dt]);
         }
     };
-    // The residual products of a split subtile: dV += (P - hi(P))^T dO, dK += (dS - hi(dS))^T Q, with the
-    // residuals recomputed from the float32 S and dP (every 16-bit operand then carries ~2^-16 relative).
-    auto dvdk_lo = [&](const char* tq, const char* to, int qs, const f32x16_t& sc, const f32x16_t& dp) {
-#pragma unroll
-      for (int cc = 0; cc < 2; ++cc) {
-        F pl, dl;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float pv = fast_exp2(sc[8 * cc + e] * c2);
-          const float ds = pv * dp[8 * cc + e];
-          pl[e] = (T)(pv - (float)(T)pv);
-          dl[e] = (T)(ds - (float)(T)ds);
-        }
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-          dv[dt] = MM::mma(pl, swz_rows<T, DP>(to, 32 * qs, cc, 32 * dt), dv[dt]);
-          dk[dt] = MM::mma(dl, swz_rows<T, DP>(tq, 32 * qs, cc, 32 * dt), dk[dt]);
-        }
-      }
-    };
-
     // Subtiles of query tile `it` in (tq, to, tr). FAST: every query in range and every key visible.
     auto body = [&](auto fast_tag, int it, const char* tq, const char* to, const float* tr) {
       constexpr bool FAST = decltype(fast_tag)::value;
@@ -270,19 +268,57 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
         }
       }
     };
-    // The residual pass of a tile holding a peaked row: S and dP are formed again and only the residual
-    // products are added, so the regular pass keeps its schedule and registers.
-    auto residual = [&](auto fast_tag, int it, const char* tq, const char* to, const float* tr) {
+    // A tile holding a peaked row instead: the exact float32 scores (from K reloaded unscaled, seeded with
+    // -lse2 through the FMA) and P, dS as two 16-bit terms each (hi + lo, ~2^-16 relative), subtiles one after
+    // the other.
+    auto exact_body = [&](auto fast_tag, int it, const char* tq, const char* to, const float* tr) {
       constexpr bool FAST = decltype(fast_tag)::value;
       const int q0 = qbeg + it * BM;
 #pragma unroll
       for (int qs = 0; qs < 2 * HALVES; ++qs) {
         const int q0s = q0 + 32 * qs;
         if (!FAST && (q0s >= s.T || (CAUSAL && kw0 > q0s + 31))) continue;  // wave-uniform
-        f32x16_t sc, dp;
-        sdp(tq, to, tr, qs, sc, dp);
-        if (!FAST) mask(sc, q0s);
-        dvdk_lo(tq, to, qs, sc, dp);
+        f32x16_t se = zero16(), dp;
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+          const f32x4_t d4 = *reinterpret_cast<const f32x4_t*>(tr + BM + 32 * qs + 8 * qd + 4 * g);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) dp[4 * qd + e] = d4[e];
+        }
+#pragma unroll
+        for (int c = 0; c < NKC; ++c) {
+          se = MM::mma(swz_cols<T, DP>(tq, 32 * qs + li, c), kraw(c), se);
+          dp = MM::mma(swz_cols<T, DP>(to, 32 * qs + li, c), vf[c], dp);
+        }
+#pragma unroll
+        for (int qd = 0; qd < 4; ++qd) {
+          const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(tr + 32 * qs + 8 * qd + 4 * g);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) se[4 * qd + e] = fmaf(se[4 * qd + e], c2, l4[e]);
+        }
+        if (!FAST) mask(se, q0s);
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+          F ph, pl, dh, dl;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float pv = fast_exp2(se[8 * cc + e]);
+            const float ds = pv * dp[8 * cc + e];
+            ph[e] = (T)pv;
+            pl[e] = (T)(pv - (float)ph[e]);
+            dh[e] = (T)ds;
+            dl[e] = (T)(ds - (float)dh[e]);
+          }
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) {
+            const F ro = swz_rows<T, DP>(to, 32 * qs, cc, 32 * dt);
+            dv[dt] = MM::mma(ph, ro, dv[dt]);
+            dv[dt] = MM::mma(pl, ro, dv[dt]);
+            const F rq = swz_rows<T, DP>(tq, 32 * qs, cc, 32 * dt);
+            dk[dt] = MM::mma(dh, rq, dk[dt]);
+            dk[dt] = MM::mma(dl, rq, dk[dt]);
+          }
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
     };
@@ -301,9 +337,72 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
         store_rows(nr, nf);
         load_rows(it + 2);
       }
-      body(fast_tag, it, tq, to, tr);
-      if (peaked_tile(tf)) residual(fast_tag, it, tq, to, tr);
+      if (!peaked_tile(tf)) body(fast_tag, it, tq, to, tr);  // the peaked launch takes the others
     };
+
+    if constexpr (PEAKED) {
+      // Tiles holding a peaked row, found 64 at a time from the lse flags, one after the other.
+      __shared__ int sPk[64];
+      bool touched = false;  // uniform
+      for (int t0 = 0; t0 < nqt; t0 += 64) {
+        const int nt = min(64, nqt - t0);
+        __syncthreads();  // every thread is done with the previous flags
+        if (tid < 64) sPk[tid] = 0;
+        __syncthreads();
+        // every row of the chunk (at most 64 tiles) in one batch of loads per thread
+        constexpr int RPT = (64 * BM + 64 * NW - 1) / (64 * NW);
+        const int r0 = qbeg + t0 * BM, r1 = min(s.T, qbeg + (t0 + nt) * BM);
+        float lv[RPT];
+#pragma unroll
+        for (int j = 0; j < RPT; ++j) {
+          const int r = r0 + tid + 64 * NW * j;
+          lv[j] = r < r1 ? p.lse[rowbase + r] : THERIA_INF;  // rows past the end: no flag
+        }
+#pragma unroll
+        for (int j = 0; j < RPT; ++j)
+          if (lse_peaked(lv[j])) sPk[(tid + 64 * NW * j) / BM] = 1;
+        __syncthreads();
+        for (int i = 0; i < nt; ++i) {
+          if (!sPk[i]) continue;  // uniform: every thread reads the same flag
+          if (!touched) load_v();
+          const int it = t0 + i;
+          dma.template issue_clamped<NSLAB>(qrsrc, qrs, qbeg + it * BM, s.T, sQ0);
+          dma.template issue_clamped<NSLAB>(orsrc, ors, qbeg + it * BM, s.T, sO0);
+          load_rows(it);
+          wait_vm_all();
+          store_rows(sR0, sF0);
+          __syncthreads();
+          if (it >= ifull && it < fend)
+            exact_body(fast, it, sQ0, sO0, sR0);
+          else
+            exact_body(general, it, sQ0, sO0, sR0);
+          __syncthreads();  // the tile buffers are free again
+          touched = true;
+        }
+      }
+      // Add this launch's sums to what the common launch stored (same stream, so it has completed).
+      if (touched) {
+        T* DV = (T*)p.dv.p + b * p.dv.sb + h * p.dv.sh;
+        T* DK = p.dk.p ? (T*)p.dk.p + b * p.dk.sb + h * p.dk.sh : nullptr;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+          const int d = dt * 32 + li;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = kw0 + acc_row(r, g);
+            if (key < s.M && (FD || d < s.D)) {
+              T* pv = DV + (int64_t)key * p.dv.sr + d;
+              *pv = (T)((float)*pv + dv[dt][r]);
+              if (DK) {
+                T* pk = DK + (int64_t)key * p.dk.sr + d;
+                *pk = (T)((float)*pk + dk[dt][r] * s.scale);
+              }
+            }
+          }
+        }
+      }
+      continue;
+    }
 
     if (nqt > 0) {
       dma.template issue_clamped<NSLAB>(qrsrc, qrs, qbeg, s.T, sQ0);
@@ -359,12 +458,16 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
 // One workgroup = NW waves of 32 queries each (Q and dO fragments, dQ accumulated in registers); K and V
 // tiles of 64 or 128 keys stream through DMA-filled swizzled double buffers, one barrier per tile. Scores
 // are transposed (S^T = K Q^T, this lane's query in the column), so lse and delta are per-lane scalars and
-// dQ^T += K^T dS^T takes dS^T from the accumulators. A wave holding a peaked row (largest probability above
-// 1/16) forms dS as two 16-bit terms and runs its subtiles one after the other. Phase order per 64-key half of a tile, i.e. two
-// 32-key subtiles:
+// dQ^T += K^T dS^T takes dS^T from the accumulators. Phase order per 64-key half of a tile, i.e. two 32-key
+// subtiles:
 //   S, dP of subtile 0 | S, dP of subtile 1 with exp / dS of subtile 0
 //   | dQ of subtile 0 with exp / dS of subtile 1 | dQ of subtile 1.
-template <typename T, bool CAUSAL, int NW, int DP, bool OVERLAP, int WPS, int HALVES, bool FD>
+// Two launches share the query blocks: PEAKED = false takes the blocks without a peaked row (flagged in lse:
+// largest probability above 1/4): Q pre-multiplied by scale * log2(e), S^T started from -lse2, P = exp2(S^T), the
+// row term dO . O. PEAKED = true takes the others (and every block for the frozen / normalised row terms):
+// the row term from a pass over the keys, exact float32 scores and dS as two 16-bit terms in the waves
+// holding a peaked row. Keeping the two apart keeps the common kernel's registers and schedule.
+template <typename T, bool CAUSAL, int NW, int DP, bool OVERLAP, int WPS, int HALVES, bool FD, bool PEAKED>
 __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
@@ -403,17 +506,25 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
     const bool qvalid = myq < s.T;
     const int64_t rowbase = (int64_t)bh * s.T;
 
+    const float lse = qvalid ? p.lse[rowbase + myq] : THERIA_INF;
+    const float lse2 = lse == -THERIA_INF ? THERIA_INF : lse * kLog2e;  // a row without visible keys has P = 0
+    const int rt = p.row_term;
+    // Rows flagged peaked in lse: the whole wave runs the split loop when any of its rows is, and the block
+    // belongs to the peaked launch.
+    const bool peaked = qvalid && lse_peaked(lse);
+    const bool split = __any(peaked);
+    const bool block_peaked = rt >= kRowFrozen || __syncthreads_or(split);
+    if (block_peaked != PEAKED) continue;  // uniform over the workgroup
+
     F qf[NKC], of[NKC];
 #pragma unroll
     for (int c = 0; c < NKC; ++c) {
       qf[c] = gload_frag8<T>(Q, p.q.sr, myq, s.T, c, FD ? DP : s.D);
       of[c] = gload_frag8<T>(dO, p.dout.sr, myq, s.T, c, FD ? DP : s.D);
     }
-    const float lse = qvalid ? p.lse[rowbase + myq] : THERIA_INF;
-    const float lse2 = lse == -THERIA_INF ? THERIA_INF : lse * kLog2e;  // a row without visible keys has P = 0
-    float del;
-    if (p.o.p) {
-      // delta = dO . (O + O_lo) over this lane's half of the head dim (the dO fragment's columns), then the pair
+    float del = 0.f;
+    if (!PEAKED && rt == kRowFromO) {
+      // delta = dO . O over this lane's half of the head dim (the dO fragment's columns), then the pair
       float part = 0.f;
       if (qvalid) {
 #pragma unroll
@@ -430,37 +541,23 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
           } else {
             const F ov = __builtin_bit_cast(F, *reinterpret_cast<const i16x8_t*>((const T*)p.o.p + b * p.o.sb +
                                                                                h * p.o.sh + off));
-            F lo{};
-            if (p.o_lo.p)
-              lo = __builtin_bit_cast(F, *reinterpret_cast<const i16x8_t*>((const T*)p.o_lo.p + b * p.o_lo.sb +
-                                                                         h * p.o_lo.sh + (int64_t)myq * p.o_lo.sr + col));
 #pragma unroll
-            for (int e = 0; e < 8; ++e) part += ((float)ov[e] + (float)lo[e]) * (float)of[c][e];
+            for (int e = 0; e < 8; ++e) part += (float)ov[e] * (float)of[c][e];
           }
         }
       }
       del = pair_sum(part);
       if (qvalid && g == 0) p.delta[rowbase + myq] = del;
-    } else {
+    } else if (rt == kRowGiven) {
       del = qvalid ? p.delta[rowbase + myq] : 0.f;
     }
-    if (!p.dq.p) continue;  // only the row term was requested (uniform over the grid)
-
-    // Peaked rows (largest probability above 1/16; every row when the row maxima are not given) take dS as
-    // two 16-bit terms: the whole wave runs the split loop when any of its rows is peaked.
-    const bool peaked = qvalid && (!p.row_max || p.row_max[rowbase + myq] - lse > kPeakedLog);
-    const bool split = __any(peaked);
-    // ... and a workgroup holding a peaked row first forms the row term exactly, delta = sum_j P_ij dP_ij /
-    // sum_j P_ij (below): dO . O from the forward's O carries the 16-bit rounding of the P in its PV
-    // product, which on a peaked row is not averaged out (~2^-9 |dP|), while dS = P o (dP - delta) is a
-    // small difference there. The dK/dV kernel reads the same delta.
-    const bool exact_row_term = __syncthreads_or(split);
+    if (!PEAKED && !p.dq.p) continue;  // only dO . O was requested (uniform over the grid)
 
     f32x16_t acc[NDT];
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) acc[dt] = zero16();
-    // P = exp2(S^T c2 - lse2) from the exact float32 scores (operands are not rescaled before the product,
-    // which would round every score's factors once more to 16 bits).
+    // c2 = scale * log2(e): split waves form P = exp2(S^T c2 - lse2) from the exact float32 scores; the others
+    // hold Q pre-multiplied by c2 (one more 16-bit rounding of each score's factors, ~2^-9 of the score).
     const float c2 = s.scale * kLog2e;
 
     int kend = s.M;
@@ -476,10 +573,13 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
     const rsrc_t vrsrc = make_rsrc(V, (uint32_t)slab_span(s.M, vrs, 2 * (FD ? DP : s.D)));
 
     // S^T = K Q^T and dP^T = V dO^T - delta for key subtile t of the tile in (tk, tv).
-    auto sdp = [&](const char* tk, const char* tv, int t, f32x16_t& sc, f32x16_t& dp) {
+    // Split waves: S^T = K Q^T exactly; other waves: Q is pre-multiplied by scale * log2(e) (below) and S^T
+    // starts from -lse2, so P = exp2(S^T) with no per-score scaling.
+    auto sdp = [&](auto split_tag, const char* tk, const char* tv, int t, f32x16_t& sc, f32x16_t& dp) {
+      constexpr bool SPLIT = decltype(split_tag)::value;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        sc[r] = 0.f;
+        sc[r] = SPLIT ? 0.f : -lse2;
         dp[r] = -del;
       }
 #pragma unroll
@@ -497,9 +597,11 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
       }
     };
     // dS^T = P^T o dP^T as 16-bit fragments (KACC chunks 0, 1)
-    auto pds = [&](const f32x16_t& sc, const f32x16_t& dp, F (&df)[2]) {
+    auto pds = [&](auto split_tag, const f32x16_t& sc, const f32x16_t& dp, F (&df)[2]) {
+      constexpr bool SPLIT = decltype(split_tag)::value;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) df[r >> 3][r & 7] = (T)(fast_exp2(fmaf(sc[r], c2, -lse2)) * dp[r]);
+      for (int r = 0; r < 16; ++r)
+        df[r >> 3][r & 7] = (T)(fast_exp2(SPLIT ? fmaf(sc[r], c2, -lse2) : sc[r]) * dp[r]);
     };
     auto dqm = [&](const char* tk, int t, const F (&df)[2]) {
 #pragma unroll
@@ -539,13 +641,13 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
         for (int hf = 0; hf < HALVES; ++hf) {
           f32x16_t s0, p0, s1, p1;
           F d0[2], d1[2];
-          sdp(tk, tv, 2 * hf, s0, p0);
+          sdp(split_tag, tk, tv, 2 * hf, s0, p0);
           __builtin_amdgcn_sched_barrier(0);
-          sdp(tk, tv, 2 * hf + 1, s1, p1);
-          pds(s0, p0, d0);
+          sdp(split_tag, tk, tv, 2 * hf + 1, s1, p1);
+          pds(split_tag, s0, p0, d0);
           __builtin_amdgcn_sched_barrier(0);
           dqm(tk, 2 * hf, d0);
-          pds(s1, p1, d1);
+          pds(split_tag, s1, p1, d1);
           __builtin_amdgcn_sched_barrier(0);
           dqm(tk, 2 * hf + 1, d1);
           __builtin_amdgcn_sched_barrier(0);
@@ -557,9 +659,9 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
           if (!FAST && CAUSAL && k0t > q0w + 31) continue;  // every key after every query of the wave (uniform)
           f32x16_t sc, dp;
           F df[2];
-          sdp(tk, tv, t, sc, dp);
+          sdp(split_tag, tk, tv, t, sc, dp);
           if (!FAST) mask(sc, k0t);
-          pds(sc, dp, df);
+          pds(split_tag, sc, dp, df);
           dqm(tk, t, df);
           if constexpr (SPLIT) {
             dqm_lo(tk, t, sc, dp);
@@ -589,11 +691,16 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
           step(general, split_tag, k, sK0, sV0, sK1, sV1);
       }
     };
-    if (exact_row_term && nkt > 0) {
-      // delta = sum_j P_ij dP_ij / sum_j P_ij over every key of the row (one more pass over the key tiles)
+    // Peaked launch: the row term from a pass over the keys, for the frozen / normalised forms and in place of
+    // dO . O, whose 16-bit P rounding in the forward's PV product (~2^-9 |dP|) a peaked row does not average
+    // out while dS = P o (dP - delta) is a small difference there.
+    if (PEAKED && rt != kRowGiven) {
+      // a = sum_j P_ij dP_ij and l = sum_j P_ij over every key of the row (one more pass over the key tiles)
       float a_part = 0.f, l_part = 0.f;
-      dma.template issue_clamped<NSLAB>(krsrc, krs, 0, s.M, sK0);
-      dma.template issue_clamped<NSLAB>(vrsrc, vrs, 0, s.M, sV0);
+      if (nkt > 0) {
+        dma.template issue_clamped<NSLAB>(krsrc, krs, 0, s.M, sK0);
+        dma.template issue_clamped<NSLAB>(vrsrc, vrs, 0, s.M, sV0);
+      }
       for (int k = 0; k < nkt; ++k) {
         const int k0 = k * BN;
         const char* tk = (k & 1) ? sK1 : sK0;
@@ -625,13 +732,17 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
       }
       __syncthreads();  // every wave is done with the tiles before the main loop refills the buffers
       const float a = pair_sum(a_part), l = pair_sum(l_part);
-      del = l > 0.f ? a / l : 0.f;
+      del = rt == kRowFrozen ? a : (l > 0.f ? a / l : 0.f);
       if (qvalid && g == 0) p.delta[rowbase + myq] = del;
     }
-    if (split)
+    if (!p.dq.p) continue;  // only the row term was requested
+    if (PEAKED && split) {
       loop(with_split);
-    else
+    } else {
+#pragma unroll
+      for (int c = 0; c < NKC; ++c) qf[c] = scaled_frag<T>(qf[c], c2);
       loop(no_split);
+    }
 
     if (qvalid) {
       T* DQ = (T*)p.dq.p + b * p.dq.sb + h * p.dq.sh;
@@ -648,24 +759,37 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
   }  // pass
 }
 
-// Launches with FD = (head dim == DP).
+// Launches with FD = (head dim == DP): the common launch (unless every block takes the row-term pass), then the
+// peaked launch.
+template <typename T, bool CAUSAL, int NW, int DP, bool OVERLAP, int WPS, int HALVES, bool FD>
+static void dq_go_fd(const DqParams& p, int64_t nblk, hipStream_t st) {
+  if (p.row_term < kRowFrozen)
+    hipLaunchKernelGGL((dq_pipe_kernel<T, CAUSAL, NW, DP, OVERLAP, WPS, HALVES, FD, false>), dim3((unsigned)nblk),
+                       dim3(64 * NW), 0, st, p);
+  hipLaunchKernelGGL((dq_pipe_kernel<T, CAUSAL, NW, DP, OVERLAP, WPS, HALVES, FD, true>), dim3((unsigned)nblk),
+                     dim3(64 * NW), 0, st, p);
+}
 template <typename T, bool CAUSAL, int NW, int DP, bool OVERLAP, int WPS, int HALVES>
 static void dq_go(const DqParams& p, int64_t nblk, hipStream_t st) {
   if (p.s.D == DP)
-    hipLaunchKernelGGL((dq_pipe_kernel<T, CAUSAL, NW, DP, OVERLAP, WPS, HALVES, true>), dim3((unsigned)nblk), dim3(64 * NW),
-                       0, st, p);
+    dq_go_fd<T, CAUSAL, NW, DP, OVERLAP, WPS, HALVES, true>(p, nblk, st);
   else
-    hipLaunchKernelGGL((dq_pipe_kernel<T, CAUSAL, NW, DP, OVERLAP, WPS, HALVES, false>), dim3((unsigned)nblk), dim3(64 * NW),
-                       0, st, p);
+    dq_go_fd<T, CAUSAL, NW, DP, OVERLAP, WPS, HALVES, false>(p, nblk, st);
+}
+// The common launch, then the peaked launch (which adds to what the first stored).
+template <typename T, bool CAUSAL, int NW, int DP, bool OVERLAP, int WPS, int HALVES, bool FD>
+static void dkdv_go_fd(const DkdvParams& p, int64_t nblk, hipStream_t st) {
+  hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, NW, DP, OVERLAP, WPS, HALVES, FD, false>), dim3((unsigned)nblk),
+                     dim3(64 * NW), 0, st, p);
+  hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, NW, DP, OVERLAP, WPS, HALVES, FD, true>), dim3((unsigned)nblk),
+                     dim3(64 * NW), 0, st, p);
 }
 template <typename T, bool CAUSAL, int NW, int DP, bool OVERLAP, int WPS, int HALVES>
 static void dkdv_go(const DkdvParams& p, int64_t nblk, hipStream_t st) {
   if (p.s.D == DP)
-    hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, NW, DP, OVERLAP, WPS, HALVES, true>), dim3((unsigned)nblk),
-                       dim3(64 * NW), 0, st, p);
+    dkdv_go_fd<T, CAUSAL, NW, DP, OVERLAP, WPS, HALVES, true>(p, nblk, st);
   else
-    hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, NW, DP, OVERLAP, WPS, HALVES, false>), dim3((unsigned)nblk),
-                       dim3(64 * NW), 0, st, p);
+    dkdv_go_fd<T, CAUSAL, NW, DP, OVERLAP, WPS, HALVES, false>(p, nblk, st);
 }
 
 // Head dims the pipelined kernels take: a multiple of 8 in 40..64 (run at DP = 64) or 72..128 (DP = 128);
@@ -702,8 +826,10 @@ template bool launch_dq_pipe<_Float16, true>(const DqParams&, hipStream_t, hipEr
 template <typename T, bool CAUSAL>
 bool launch_dkdv_pipe(const DkdvParams& p, hipStream_t st, hipError_t* err) {
   if (!(pipe_head_dim(p.s) && !p.dv_only)) return false;
-  // 32-bit byte offsets inside each (batch, head) slab of Q and dO
-  if (!slab_fits_dma(p.s.T, p.q.sr, p.s.D) || !slab_fits_dma(p.s.T, p.dout.sr, p.s.D)) return false;
+  // 32-bit byte offsets inside each (batch, head) slab of Q, dO and K
+  if (!slab_fits_dma(p.s.T, p.q.sr, p.s.D) || !slab_fits_dma(p.s.T, p.dout.sr, p.s.D) ||
+      !slab_fits_dma(p.s.M, p.k.sr, p.s.D))
+    return false;
   // workgroups of nw waves (32 keys each): key blocks, or (causal head dim 64) pairs of mirrored blocks
   auto blocks = [&](int nw) {
     const int64_t nkb = (p.s.M + 32 * nw - 1) / (32 * nw);

@@ -97,6 +97,19 @@ __device__ __forceinline__ float pair_sum(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Peaked rows. With 16-bit inputs the lowest mantissa bit of each lse the forward writes marks a row whose
+// largest probability may exceed 1/4 (kPeakedFrac); the backward kernels read it to take their exact path
+// there (two-term 16-bit operands, the row term from a pass over the keys). Setting the bit moves lse by at
+// most one unit in the last place. Infinite lse (rows without visible keys) carries no flag.
+constexpr float kPeakedFrac = 0.25f;
+__device__ __forceinline__ float lse_with_flag(float lse, bool peaked) {
+  if (!__builtin_isfinite(lse)) return lse;
+  return __uint_as_float((__float_as_uint(lse) & ~1u) | (peaked ? 1u : 0u));
+}
+__device__ __forceinline__ bool lse_peaked(float lse) {
+  return __builtin_isfinite(lse) && (__float_as_uint(lse) & 1u);
+}
+
 // ----------------------------------------------------------------------------------------------
 // k-index mapping of fragment element 0 / element EPL/2 for 16-bit types, and the single element of
 // float32 fragments. c is the chunk index (KC wide), g the lane half.

@@ -1,11 +1,7 @@
 // Fused SDPA forward for gfx950.
 //
-// Forward (mode 0) replaces _fused_sdpa_kernel (reference theria/attention/triton_qk.py:242-304):
+// Replaces _fused_sdpa_kernel (reference theria/attention/triton_qk.py:242-304):
 // O = softmax(scale * Q K^T) V with an online softmax, saving lse (and the reference's m, l).
-// Mode 1 rebuilds O_i = sum_j P_ij V_j from a given lse and writes the backward row term
-// delta_i = dO_i . O_i, for the reference's sdpa_bwd_* entry points that receive (m, l) but no O
-// (triton_sdpa_backward.py:312-353 recomputes that term inside its dK kernel); with row_normalize, O is
-// divided by sum_j P_ij first (the operator's own lse: the exact softmax's row term).
 //
 // Work decomposition: one workgroup = 4 waves; each wave owns QT tiles of 32 query rows of one
 // (batch, head) for the whole kernel. The score tile is computed transposed, S^T = K Q^T, so that in
@@ -27,7 +23,7 @@
 
 namespace theria {
 
-template <typename T, int DP, bool CAUSAL, int MODE, int QT, int BN>
+template <typename T, int DP, bool CAUSAL, int QT, int BN>
 __global__ __launch_bounds__(256, (DP <= 64 ? FWD_MINW : 1)) void fwd_kernel(const FwdParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
@@ -65,7 +61,6 @@ __global__ __launch_bounds__(256, (DP <= 64 ? FWD_MINW : 1)) void fwd_kernel(con
     m_use[j] = -THERIA_INF;  // offset of P in the log2 domain
     m_max[j] = -THERIA_INF;  // exact running row max (log2 domain)
     l_part[j] = 0.f;         // this lane's share of the row sum
-    if (MODE == 1) m_use[j] = myq < s.T ? p.lse[rowbase + myq] * kLog2e : THERIA_INF;
   }
   const float c2 = s.scale * kLog2e;
 
@@ -116,7 +111,7 @@ __global__ __launch_bounds__(256, (DP <= 64 ? FWD_MINW : 1)) void fwd_kernel(con
     }
 #pragma unroll
     for (int j = 0; j < QT; ++j) {
-      if (MODE == 0) {
+      {
         float mx = -THERIA_INF;
 #pragma unroll
         for (int t = 0; t < NST; ++t)
@@ -135,9 +130,8 @@ __global__ __launch_bounds__(256, (DP <= 64 ? FWD_MINW : 1)) void fwd_kernel(con
             for (int r = 0; r < 16; ++r) o[j][dt][r] *= alpha;
         }
       }
-      // m_use is -inf only while every key seen so far is masked (then every score is -inf and
-      // P = 0); in mode 1 a row without visible keys has lse = -inf and P must be 0 as well.
-      const float moff = (m_use[j] == -THERIA_INF) ? (MODE == 0 ? 0.f : THERIA_INF) : m_use[j];
+      // m_use is -inf only while every key seen so far is masked (then every score is -inf and P = 0)
+      const float moff = m_use[j] == -THERIA_INF ? 0.f : m_use[j];
       float ls = 0.f;
 #pragma unroll
       for (int t = 0; t < NST; ++t)
@@ -149,29 +143,18 @@ __global__ __launch_bounds__(256, (DP <= 64 ? FWD_MINW : 1)) void fwd_kernel(con
         }
       l_part[j] += ls;
     }
-    // Mode 1 with 16-bit inputs: P enters the PV product as two 16-bit terms (hi + lo), so the row term
-    // carries ~2^-16 relative rounding instead of 2^-9 (it is a small difference of large terms in dS).
-    constexpr bool SPLIT = MODE == 1 && sizeof(T) == 2;
 #pragma unroll
     for (int t = 0; t < NST; ++t)
 #pragma unroll
       for (int cc = 0; cc < NPC; ++cc) {
-        F pf[QT], pl[QT];
+        F pf[QT];
 #pragma unroll
-        for (int j = 0; j < QT; ++j) {
-          if constexpr (SPLIT)
-            split_frag<T>(sc[j][t], cc, pf[j], pl[j]);
-          else
-            pf[j] = acc_frag<T>(sc[j][t], cc);
-        }
+        for (int j = 0; j < QT; ++j) pf[j] = acc_frag<T>(sc[j][t], cc);
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
           const F vfr = lds_rows<T, KACC>(sV, PITCH, t * 32, cc, dt * 32);
 #pragma unroll
-          for (int j = 0; j < QT; ++j) {
-            o[j][dt] = MM::mma(vfr, pf[j], o[j][dt]);
-            if constexpr (SPLIT) o[j][dt] = MM::mma(vfr, pl[j], o[j][dt]);
-          }
+          for (int j = 0; j < QT; ++j) o[j][dt] = MM::mma(vfr, pf[j], o[j][dt]);
         }
       }
   }
@@ -181,7 +164,7 @@ __global__ __launch_bounds__(256, (DP <= 64 ? FWD_MINW : 1)) void fwd_kernel(con
     const int myq = q0w + 32 * j + li;
     const bool qvalid = myq < s.T;
     const int64_t row_id = rowbase + myq;
-    if (MODE == 0) {
+    {
       const float l = pair_sum(l_part[j]);
       const float inv = l > 0.f ? 1.f / l : 0.f;
       if (qvalid) {
@@ -199,40 +182,18 @@ __global__ __launch_bounds__(256, (DP <= 64 ? FWD_MINW : 1)) void fwd_kernel(con
               } else {
                 T* O = (T*)p.o.p + b * p.o.sb + h * p.o.sh;
                 store4<T>(O, p.o.sr, myq, d0, s.D, a0, a1, a2, a3, s.vec);
-                if (sizeof(T) == 2 && p.o_lo.p) {  // rounding residual of the 16-bit O
-                  T* OL = (T*)p.o_lo.p + b * p.o_lo.sb + h * p.o_lo.sh;
-                  store4<T>(OL, p.o_lo.sr, myq, d0, s.D, a0 - (float)(T)a0, a1 - (float)(T)a1, a2 - (float)(T)a2,
-                            a3 - (float)(T)a3, s.vec);
-                }
               }
             }
           }
         if (g == 0) {
-          p.lse[row_id] = l > 0.f ? (m_use[j] + __builtin_log2f(l)) * kLn2 : -THERIA_INF;
+          // 16-bit: flag a peaked row, largest probability exp2(m_max - m_use) / l above 1/4 (log2: -2)
+          const float lse2 = m_use[j] + __builtin_log2f(l);
+          const bool peaked = sizeof(T) == 2 && m_max[j] - lse2 > -2.f;
+          p.lse[row_id] = l > 0.f ? (sizeof(T) == 2 ? lse_with_flag(lse2 * kLn2, peaked) : lse2 * kLn2) : -THERIA_INF;
           if (p.row_max) p.row_max[row_id] = m_max[j] * kLn2;
           if (p.row_sum) p.row_sum[row_id] = l > 0.f ? l * fast_exp2(m_use[j] - m_max[j]) : 0.f;
         }
       }
-    } else if (qvalid) {
-      const T* dO = (const T*)p.dout.p + b * p.dout.sb + h * p.dout.sh;
-      float part = 0.f;
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-        for (int qd = 0; qd < 4; ++qd) {
-          const int d0 = dt * 32 + 8 * qd + 4 * g;
-          if (d0 < s.D) {
-            const f32x4_t go = load4<T>(dO, p.dout.sr, myq, d0, s.D, s.vec);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) part += go[e] * o[j][dt][4 * qd + e];
-          }
-        }
-      part = pair_sum(part);
-      if (p.row_normalize) {
-        const float l = pair_sum(l_part[j]);
-        part = l > 0.f ? part / l : 0.f;
-      }
-      if (g == 0) p.delta[row_id] = part;
     }
   }
 }
@@ -247,17 +208,16 @@ __global__ __launch_bounds__(256, (DP <= 64 ? FWD_MINW : 1)) void fwd_kernel(con
 // Query tiles per wave: 2 where the registers allow it and the sequence fills the block.
 template <int DP> constexpr int fwd_qt(int T) { return (FWD_QT_MAX >= 2 && DP <= 64 && T > 128) ? 2 : 1; }
 
-// Pipelined 16-bit forward and row-term pass (sdpa_fwd_pipe.hip); false when it does not cover the problem.
-template <typename T, bool CAUSAL, int MODE>
+// Pipelined 16-bit forward (sdpa_fwd_pipe.hip); false when it does not cover the problem.
+template <typename T, bool CAUSAL>
 bool launch_fwd_pipe(const FwdParams& p, hipStream_t st, hipError_t* err);
 
-template <int MODE>
 struct FwdLauncher {
   template <typename T, int DP, bool CAUSAL>
   static hipError_t run(const FwdParams& p, hipStream_t st) {
     if constexpr (sizeof(T) == 2 && DP >= 64) {
       hipError_t err;
-      if (launch_fwd_pipe<T, CAUSAL, MODE>(p, st, &err)) return err;
+      if (launch_fwd_pipe<T, CAUSAL>(p, st, &err)) return err;
     }
     // Two query tiles per wave only for 16-bit inputs: with float32 fragments (twice the registers)
     // that variant spills ~150 VGPRs and runs at half the one-tile rate.
@@ -267,17 +227,15 @@ struct FwdLauncher {
     if (nblk == 0) return hipSuccess;
     if constexpr (DP <= 64 && sizeof(T) == 2) {
       if (qt == 2) {
-        hipLaunchKernelGGL((fwd_kernel<T, DP, CAUSAL, MODE, 2, FWD_BN_QT2>), dim3((unsigned)nblk), dim3(256), 0, st, p);
+        hipLaunchKernelGGL((fwd_kernel<T, DP, CAUSAL, 2, FWD_BN_QT2>), dim3((unsigned)nblk), dim3(256), 0, st, p);
         return hipGetLastError();
       }
     }
-    hipLaunchKernelGGL((fwd_kernel<T, DP, CAUSAL, MODE, 1, 64>), dim3((unsigned)nblk), dim3(256), 0, st, p);
+    hipLaunchKernelGGL((fwd_kernel<T, DP, CAUSAL, 1, 64>), dim3((unsigned)nblk), dim3(256), 0, st, p);
     return hipGetLastError();
   }
 };
 
-hipError_t launch_fwd(const FwdParams& p, int mode, hipStream_t st) {
-  return mode == 0 ? dispatch_all<FwdLauncher<0>>(p, st) : dispatch_all<FwdLauncher<1>>(p, st);
-}
+hipError_t launch_fwd(const FwdParams& p, hipStream_t st) { return dispatch_all<FwdLauncher>(p, st); }
 
 }  // namespace theria

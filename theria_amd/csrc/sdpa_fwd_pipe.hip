@@ -1,9 +1,7 @@
 // Pipelined SDPA forward for 16-bit inputs on gfx950.
 //
-// Same contract as fwd_kernel (sdpa_fwd.hip): mode 0, O = softmax(scale Q K^T) V with lse and the optional
-// reference statistics (m, l) (reference theria/attention/triton_qk.py:242-304); mode 1 (ROW), P from a
-// given lse and the backward row term delta_i = dO_i . sum_j P_ij V_j in float32, for the backward entry
-// points that receive the saved statistics but no O and for the double backward. It is used when
+// Same contract as fwd_kernel (sdpa_fwd.hip): O = softmax(scale Q K^T) V with lse and the optional
+// reference statistics (m, l) (reference theria/attention/triton_qk.py:242-304). It is used when
 // the head dim is a multiple of 8 in 40..128 (computed at DP = 64 or 128, the columns past D zero),
 // every view allows 16-byte access and there are more than 128 queries.
 //
@@ -39,7 +37,7 @@ namespace theria {
 // block to fill the GPU.
 // FD: the head dim is DP itself (compile-time bounds); otherwise the runtime head dim s.D < DP bounds the
 // loads, stores and DMA chunks.
-template <typename T, bool CAUSAL, bool STATS, int NW, int DP, int QT, bool FD, bool ROW>
+template <typename T, bool CAUSAL, bool STATS, int NW, int DP, int QT, bool FD>
 __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
@@ -109,7 +107,9 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
       for (int c = 0; c < NKC; ++c) qf[j][c] = gload_frag8<T>(Q, p.q.sr, q0w + 32 * j + li, s.T, c, Dh);
 
     f32x16_t o[QT][NDT];
-    float m_use[QT], l_part[QT], m_max[QT];
+    // pk_max: the largest lane partial row sum of any tile (32 keys, relative to the current offset), an upper
+    // bound of the row's largest P that costs one max per tile; it marks the peaked rows in lse.
+    float m_use[QT], l_part[QT], m_max[QT], pk_max[QT];
 #pragma unroll
     for (int j = 0; j < QT; ++j) {
 #pragma unroll
@@ -117,17 +117,9 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
       m_use[j] = -THERIA_INF;
       l_part[j] = 0.f;
       m_max[j] = -THERIA_INF;
-      if (ROW) {
-        // fixed offset lse * log2(e): P <= 1 on every tile, so the exact path never runs
-        const int myq = q0w + 32 * j + li;
-        const float l2 = myq < s.T ? p.lse[rowbase + myq] * kLog2e : THERIA_INF;
-        m_use[j] = l2 == -THERIA_INF ? THERIA_INF : l2;  // a row without visible keys has P = 0
-      }
+      pk_max[j] = 0.f;
     }
     F pf[QT][2][2];  // P of the previous tile as MFMA B fragments: [query tile][32-key subtile][16-key chunk]
-    // ROW: the rounding residuals of those P (P enters the PV product as two 16-bit terms; the row term
-    // delta = dO . sum_j P_ij V_j is a small difference of large terms in dS = P o (dP - delta))
-    F pfl[ROW ? QT : 1][2][2];
     bool pf_skip = false;
 
     // S^T = K Q^T for both query tiles, key subtile t (32 keys) of the K tile in `kt`.
@@ -161,10 +153,7 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
           for (int dt = 0; dt < NDT; ++dt) {
             const F vf = swz_rows<T, DP>(vt, 32 * t, cc, 32 * dt);
 #pragma unroll
-            for (int j = 0; j < QT; ++j) {
-              o[j][dt] = MM::mma(vf, pf[j][t][cc], o[j][dt]);
-              if constexpr (ROW) o[j][dt] = MM::mma(vf, pfl[j][t][cc], o[j][dt]);
-            }
+            for (int j = 0; j < QT; ++j) o[j][dt] = MM::mma(vf, pf[j][t][cc], o[j][dt]);
           }
     };
     // Keys out of range, or (causal) after the query, get -inf. Only boundary tiles pay for the test.
@@ -182,8 +171,7 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
       }
     };
     // P = exp2(S c2 - off) as 16-bit fragments into pn, and this tile's lane partial row sums into ps.
-    auto exps = [&](const f32x16_t (&sc)[QT][2], const float (&off)[QT], F (&pn)[QT][2][2],
-                    F (&pnl)[ROW ? QT : 1][2][2], float (&ps)[QT]) __attribute__((always_inline)) {
+    auto exps = [&](const f32x16_t (&sc)[QT][2], const float (&off)[QT], F (&pn)[QT][2][2], float (&ps)[QT]) {
 #pragma unroll
       for (int j = 0; j < QT; ++j) {
         float acc = 0.f;
@@ -191,43 +179,26 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
         for (int t = 0; t < 2; ++t)
 #pragma unroll
           for (int cc = 0; cc < 2; ++cc) {
-            F f, fl;
+            F f;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const float x = fast_exp2(fmaf(sc[j][t][8 * cc + e], c2, -off[j]));
-              f[e] = (T)x;
-              if constexpr (ROW) fl[e] = (T)(x - (float)f[e]);
-            }
+            for (int e = 0; e < 8; ++e) f[e] = (T)fast_exp2(fmaf(sc[j][t][8 * cc + e], c2, -off[j]));
             pn[j][t][cc] = f;
             acc = frag_sum<T>(f, acc);
-            if constexpr (ROW) {
-              pnl[j][t][cc] = fl;
-              acc = frag_sum<T>(fl, acc);
-            }
           }
         ps[j] = acc;
       }
     };
     // The same for key subtile t only, accumulating the lane partial row sums into ps.
-    auto exps_t = [&](const f32x16_t (&st)[QT], int t, F (&pn)[QT][2][2], F (&pnl)[ROW ? QT : 1][2][2],
-                      float (&ps)[QT]) __attribute__((always_inline)) {
+    auto exps_t = [&](const f32x16_t (&st)[QT], int t, F (&pn)[QT][2][2], float (&ps)[QT]) {
 #pragma unroll
       for (int j = 0; j < QT; ++j)
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
-          F f, fl;
+          F f;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float x = fast_exp2(fmaf(st[j][8 * cc + e], c2, -m_use[j]));
-            f[e] = (T)x;
-            if constexpr (ROW) fl[e] = (T)(x - (float)f[e]);
-          }
+          for (int e = 0; e < 8; ++e) f[e] = (T)fast_exp2(fmaf(st[j][8 * cc + e], c2, -m_use[j]));
           pn[j][t][cc] = f;
           ps[j] = frag_sum<T>(f, ps[j]);
-          if constexpr (ROW) {
-            pnl[j][t][cc] = fl;
-            ps[j] = frag_sum<T>(fl, ps[j]);
-          }
         }
     };
     auto tile_max = [&](const f32x16_t (&sc)[QT][2], int j) {
@@ -239,8 +210,7 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
       return pair_max(mx) * c2;
     };
     // Exact path: the running max becomes the offset; O and the row sums are rescaled to it.
-    auto exact = [&](const f32x16_t (&sc)[QT][2], F (&pn)[QT][2][2], F (&pnl)[ROW ? QT : 1][2][2],
-                     float (&ps)[QT]) __attribute__((always_inline)) {
+    auto exact = [&](const f32x16_t (&sc)[QT][2], F (&pn)[QT][2][2], float (&ps)[QT]) {
       float off[QT];
 #pragma unroll
       for (int j = 0; j < QT; ++j) {
@@ -250,13 +220,14 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
         const float alpha = mnew == -THERIA_INF ? 1.f : fast_exp2(m_use[j] - mnew);
         m_use[j] = mnew;
         l_part[j] *= alpha;
+        pk_max[j] *= alpha;
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
           for (int r = 0; r < 16; ++r) o[j][dt][r] *= alpha;
         off[j] = mnew == -THERIA_INF ? 0.f : mnew;  // all keys so far masked: P = exp2(-inf) = 0
       }
-      exps(sc, off, pn, pnl, ps);
+      exps(sc, off, pn, ps);
     };
 
     // One key tile. On entry K(k) and V(k-1) have been requested (one iteration earlier); this step
@@ -275,7 +246,7 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
         if (k + 1 < nkt) dma.template issue_clamped<NSLAB>(krsrc, krs, k0 + BN, s.M, kn);
         dma.template issue_clamped<NSLAB>(vrsrc, vrs, k0, s.M, vn);
       }
-      F pn[QT][2][2], pnl[ROW ? QT : 1][2][2];
+      F pn[QT][2][2];
       if constexpr (FAST) {
         // Phase order (kept by scheduling barriers, which also bound the live registers):
         //   S(k) subtile 0 | S(k) subtile 1 with exp of subtile 0 | O += V(k-1)^T P(k-1)^T with exp of subtile 1.
@@ -295,8 +266,8 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
             m_max[j] = fmaxf(m_max[j], pair_max(mx) * c2);
           }
         }
-        exps_t(s0, 0, pn, pnl, ps);
-        if constexpr (DP == 64 && !ROW) {
+        exps_t(s0, 0, pn, ps);
+        if constexpr (DP == 64) {
           // Issue order inside the phase: the four K fragment reads first, then each of the 8 MFMAs
           // followed by 12 VALU instructions of the exponentials (measured ~5% faster than the
           // compiler's own order at head dim 64).
@@ -319,8 +290,8 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
             m_max[j] = fmaxf(m_max[j], pair_max(mx) * c2);
           }
         }
-        exps_t(s1, 1, pn, pnl, ps);
-        if constexpr (DP == 64 && !ROW) {
+        exps_t(s1, 1, pn, ps);
+        if constexpr (DP == 64) {
           // V fragment reads first, then each of the 16 PV MFMAs followed by 6 VALU instructions.
 #pragma unroll
           for (int i = 0; i < 8; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
@@ -333,22 +304,22 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
         bool bad = false;
 #pragma unroll
         for (int j = 0; j < QT; ++j) bad |= !(ps[j] <= 0x1p20f);
-        if (!ROW && __any(bad)) {
+        if (__any(bad)) {
           f32x16_t sc2[QT][2];
           scores(kc, sc2);
-          exact(sc2, pn, pnl, ps);
+          exact(sc2, pn, ps);
         }
 #pragma unroll
-        for (int j = 0; j < QT; ++j) l_part[j] += ps[j];
+        for (int j = 0; j < QT; ++j) {
+          l_part[j] += ps[j];
+          pk_max[j] = fmaxf(pk_max[j], ps[j]);
+        }
 #pragma unroll
         for (int j = 0; j < QT; ++j)
 #pragma unroll
           for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int cc = 0; cc < 2; ++cc) {
-              pf[j][t][cc] = pn[j][t][cc];
-              if constexpr (ROW) pfl[j][t][cc] = pnl[j][t][cc];
-            }
+            for (int cc = 0; cc < 2; ++cc) pf[j][t][cc] = pn[j][t][cc];
         pf_skip = false;
       } else {
         const bool skip = CAUSAL && (k0 > q0w + 32 * QT - 1);  // every key after every query of the wave
@@ -358,35 +329,35 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
         if (!skip) {
           float ps[QT];
           mask(sc, k0);
-          if (k == 0 && !ROW) {
-            exact(sc, pn, pnl, ps);
+          if (k == 0) {
+            exact(sc, pn, ps);
           } else {
             if (STATS) {
 #pragma unroll
               for (int j = 0; j < QT; ++j) m_max[j] = fmaxf(m_max[j], tile_max(sc, j));
             }
-            exps(sc, m_use, pn, pnl, ps);
+            exps(sc, m_use, pn, ps);
             bool bad = false;
 #pragma unroll
             for (int j = 0; j < QT; ++j) bad |= !(ps[j] <= 0x1p20f);
-            if (!ROW && __any(bad)) {
+            if (__any(bad)) {
               f32x16_t sc2[QT][2];
               scores(kc, sc2);
               mask(sc2, k0);
-              exact(sc2, pn, pnl, ps);
+              exact(sc2, pn, ps);
             }
           }
 #pragma unroll
-          for (int j = 0; j < QT; ++j) l_part[j] += ps[j];
+          for (int j = 0; j < QT; ++j) {
+            l_part[j] += ps[j];
+            pk_max[j] = fmaxf(pk_max[j], ps[j]);
+          }
 #pragma unroll
           for (int j = 0; j < QT; ++j)
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
-              for (int cc = 0; cc < 2; ++cc) {
-              pf[j][t][cc] = pn[j][t][cc];
-              if constexpr (ROW) pfl[j][t][cc] = pnl[j][t][cc];
-            }
+              for (int cc = 0; cc < 2; ++cc) pf[j][t][cc] = pn[j][t][cc];
         }
         pf_skip = skip;
       }
@@ -421,33 +392,10 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
 #pragma unroll
     for (int j = 0; j < QT; ++j) {
       const int myq = q0w + 32 * j + li;
-      if constexpr (ROW) {
-        // O is normalised already (P = exp(S - lse)): delta = dO . O over this lane's columns, then the pair
-        if (myq < s.T) {
-          const T* dO = (const T*)p.dout.p + b * p.dout.sb + h * p.dout.sh;
-          float part = 0.f;
-#pragma unroll
-          for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-            for (int qd = 0; qd < 4; ++qd) {
-              const int d0 = dt * 32 + 8 * qd + 4 * g;
-              if (FD || d0 < Dh) {
-                const f32x4_t go = load4<T>(dO, p.dout.sr, myq, d0, Dh, true);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) part += go[e] * o[j][dt][4 * qd + e];
-              }
-            }
-          part = pair_sum(part);
-          if (p.row_normalize) {  // the exact softmax's row term: O divided by its own row sum
-            const float l = pair_sum(l_part[j]);
-            part = l > 0.f ? part / l : 0.f;
-          }
-          if (g == 0) p.delta[rowbase + myq] = part;
-        }
-        continue;
-      }
       const float l = pair_sum(l_part[j]);
       const float inv = l > 0.f ? 1.f / l : 0.f;
+      // cross-lane, so taken by every lane before the per-row branches
+      const bool peaked = pair_max(pk_max[j]) > kPeakedFrac * l;
       if (myq < s.T) {
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt)
@@ -462,16 +410,11 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
             } else {
               T* O = (T*)p.o.p + b * p.o.sb + h * p.o.sh;
               store4_8<T>(O, p.o.sr, myq, d0, Dh, a0, a1, a2, a3);
-              if (p.o_lo.p) {  // rounding residual of the 16-bit O
-                T* OL = (T*)p.o_lo.p + b * p.o_lo.sb + h * p.o_lo.sh;
-                store4_8<T>(OL, p.o_lo.sr, myq, d0, Dh, a0 - (float)(T)a0, a1 - (float)(T)a1, a2 - (float)(T)a2,
-                            a3 - (float)(T)a3);
-              }
             }
           }
         if (g == 0) {
           const int64_t row_id = rowbase + myq;
-          p.lse[row_id] = l > 0.f ? (m_use[j] + __builtin_log2f(l)) * kLn2 : -THERIA_INF;
+          p.lse[row_id] = l > 0.f ? lse_with_flag((m_use[j] + __builtin_log2f(l)) * kLn2, peaked) : -THERIA_INF;
           if (STATS) {
             if (p.row_max) p.row_max[row_id] = m_max[j] * kLn2;
             if (p.row_sum) p.row_sum[row_id] = l > 0.f ? l * fast_exp2(m_use[j] - m_max[j]) : 0.f;
@@ -482,33 +425,26 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
   }  // pass
 }
 
-template <typename T, bool CAUSAL, int NW, int DP, int QT, bool ROW>
+template <typename T, bool CAUSAL, int NW, int DP, int QT>
 static void fwd_pipe_go(const FwdParams& p, int64_t nblk, hipStream_t st) {
   const dim3 grid((unsigned)nblk), block(64 * NW);
   const bool stats = p.row_max || p.row_sum;
-  if constexpr (ROW) {
-    if (p.s.D == DP)
-      hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, false, NW, DP, QT, true, true>), grid, block, 0, st, p);
-    else
-      hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, false, NW, DP, QT, false, true>), grid, block, 0, st, p);
-  } else if (p.s.D == DP) {
+  if (p.s.D == DP) {
     if (stats)
-      hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, true, NW, DP, QT, true, false>), grid, block, 0, st, p);
+      hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, true, NW, DP, QT, true>), grid, block, 0, st, p);
     else
-      hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, false, NW, DP, QT, true, false>), grid, block, 0, st, p);
+      hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, false, NW, DP, QT, true>), grid, block, 0, st, p);
   } else {
     if (stats)
-      hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, true, NW, DP, QT, false, false>), grid, block, 0, st, p);
+      hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, true, NW, DP, QT, false>), grid, block, 0, st, p);
     else
-      hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, false, NW, DP, QT, false, false>), grid, block, 0, st, p);
+      hipLaunchKernelGGL((fwd_pipe_kernel<T, CAUSAL, false, NW, DP, QT, false>), grid, block, 0, st, p);
   }
 }
 
-template <typename T, bool CAUSAL, int DP, bool ROW>
+template <typename T, bool CAUSAL, int DP>
 static void fwd_pipe_launch(const FwdParams& p, hipStream_t st) {
-  // The row-term pass carries two-term P fragments across its software pipeline: one query tile per wave
-  // (two spill ~100 registers).
-  constexpr int QT = (DP == 64 && !CAUSAL && !ROW) ? 2 : 1;
+  constexpr int QT = (DP == 64 && !CAUSAL) ? 2 : 1;
   const int64_t bh = (int64_t)p.s.B * p.s.H;
   const int64_t cus = device_cu_count();
   // workgroups per (batch, head): query blocks, or (causal) pairs of mirrored query blocks
@@ -516,23 +452,22 @@ static void fwd_pipe_launch(const FwdParams& p, hipStream_t st) {
   const int64_t nblk8 = units((p.s.T + 256 * QT - 1) / (256 * QT)) * bh;
   const int64_t nblk4 = units((p.s.T + 128 * QT - 1) / (128 * QT)) * bh;
   if (nblk8 >= cus) {
-    fwd_pipe_go<T, CAUSAL, 8, DP, QT, ROW>(p, nblk8, st);
+    fwd_pipe_go<T, CAUSAL, 8, DP, QT>(p, nblk8, st);
     return;
   }
   if constexpr (QT == 2) {
     // Too few query blocks to give every CU two four-wave workgroups: one query tile per wave doubles them.
     if (nblk4 < 2 * cus) {
-      fwd_pipe_go<T, CAUSAL, 4, DP, 1, ROW>(p, units((p.s.T + 127) / 128) * bh, st);
+      fwd_pipe_go<T, CAUSAL, 4, DP, 1>(p, units((p.s.T + 127) / 128) * bh, st);
       return;
     }
   }
-  fwd_pipe_go<T, CAUSAL, 4, DP, QT, ROW>(p, nblk4, st);
+  fwd_pipe_go<T, CAUSAL, 4, DP, QT>(p, nblk4, st);
 }
 
 // Launch if the pipelined kernel covers this problem (16-bit, head dim a multiple of 8 in 40..64 (run at
-// DP = 64) or 72..128 (DP = 128), vector access, more than 128 queries); returns false otherwise. MODE as
-// in fwd_kernel: 0 forward, 1 row term from the given lse.
-template <typename T, bool CAUSAL, int MODE>
+// DP = 64) or 72..128 (DP = 128), vector access, more than 128 queries); returns false otherwise.
+template <typename T, bool CAUSAL>
 bool launch_fwd_pipe(const FwdParams& p, hipStream_t st, hipError_t* err) {
   if (!(p.s.vec && p.s.D % 8 == 0 && p.s.D > 32 && (p.s.dp == 64 || p.s.dp == 128) && p.s.T > 128)) return false;
   // 32-bit byte offsets inside each (batch, head) slab of K and V
@@ -542,20 +477,16 @@ bool launch_fwd_pipe(const FwdParams& p, hipStream_t st, hipError_t* err) {
     return true;
   }
   if (p.s.dp == 64)
-    fwd_pipe_launch<T, CAUSAL, 64, MODE == 1>(p, st);
+    fwd_pipe_launch<T, CAUSAL, 64>(p, st);
   else
-    fwd_pipe_launch<T, CAUSAL, 128, MODE == 1>(p, st);
+    fwd_pipe_launch<T, CAUSAL, 128>(p, st);
   *err = hipGetLastError();
   return true;
 }
 
-template bool launch_fwd_pipe<__bf16, false, 0>(const FwdParams&, hipStream_t, hipError_t*);
-template bool launch_fwd_pipe<__bf16, true, 0>(const FwdParams&, hipStream_t, hipError_t*);
-template bool launch_fwd_pipe<_Float16, false, 0>(const FwdParams&, hipStream_t, hipError_t*);
-template bool launch_fwd_pipe<_Float16, true, 0>(const FwdParams&, hipStream_t, hipError_t*);
-template bool launch_fwd_pipe<__bf16, false, 1>(const FwdParams&, hipStream_t, hipError_t*);
-template bool launch_fwd_pipe<__bf16, true, 1>(const FwdParams&, hipStream_t, hipError_t*);
-template bool launch_fwd_pipe<_Float16, false, 1>(const FwdParams&, hipStream_t, hipError_t*);
-template bool launch_fwd_pipe<_Float16, true, 1>(const FwdParams&, hipStream_t, hipError_t*);
+template bool launch_fwd_pipe<__bf16, false>(const FwdParams&, hipStream_t, hipError_t*);
+template bool launch_fwd_pipe<__bf16, true>(const FwdParams&, hipStream_t, hipError_t*);
+template bool launch_fwd_pipe<_Float16, false>(const FwdParams&, hipStream_t, hipError_t*);
+template bool launch_fwd_pipe<_Float16, true>(const FwdParams&, hipStream_t, hipError_t*);
 
 }  // namespace theria

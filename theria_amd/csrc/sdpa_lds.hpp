@@ -67,6 +67,15 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
 #endif
 }
 
+// 16 bytes per lane from the buffer at voffset + soffset into registers (zeros beyond the resource's range).
+__device__ __forceinline__ i16x8_t buf_load16(rsrc_t rsrc, uint32_t voffset, uint32_t soffset) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_bit_cast(i16x8_t, __builtin_amdgcn_raw_buffer_load_b128(rsrc, voffset, soffset, 0));
+#else
+  return i16x8_t{};
+#endif
+}
+
 // One 16-byte-per-lane LDS DMA: lane l's 16 bytes at voffset + soffset in the buffer go to lds + 16 l.
 __device__ __forceinline__ void dma16(rsrc_t rsrc, char* lds, uint32_t voffset, uint32_t soffset) {
 #if defined(__HIP_DEVICE_COMPILE__)

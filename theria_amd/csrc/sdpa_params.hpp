@@ -25,35 +25,35 @@ struct Shape {
   bool vec;   // every view allows 16-byte vector access
 };
 
-// Forward (mode 0) or row term from saved stats (mode 1: delta_i = dO_i . sum_j P_ij V_j).
+// Forward: O, lse and the optional reference statistics m (row_max) and l (row_sum).
 struct FwdParams {
   Shape s;
-  View q, k, v, dout;
+  View q, k, v;
   MutView o;
-  MutView o_lo;     // optional (mode 0, 16-bit O): rounding residual O - (float)o in the input dtype
   bool o_f32;
-  float* lse;       // mode 0: out; mode 1: in
-  float* row_max;   // optional (mode 0)
-  float* row_sum;   // optional (mode 0)
-  float* delta;     // mode 1: out
-  // mode 1: delta from the normalised O = sum_j P_ij V_j / sum_j P_ij (the exact softmax's row term for the
-  // operator's own lse) instead of sum_j P_ij dP_ij with P as given (the reference's frozen-stats term)
-  bool row_normalize;
+  float* lse;
+  float* row_max;  // optional
+  float* row_sum;  // optional
 };
 
-// Largest probability of a row above which the 16-bit backward forms P and dS as two 16-bit terms
-// (hi + lo): exp(m - lse) > 1/16, i.e. m - lse > -ln 16.
-constexpr float kPeakedLog = -2.7725887222397811f;
+// How the dQ kernel obtains the row term delta_i of dS = P o (dP - delta), which it writes to delta (the
+// dK / dV kernel reads it there):
+enum RowTerm : int {
+  kRowFromO = 0,    // dO_i . O_i from the given O; with 16-bit inputs a workgroup holding a peaked row (flagged
+                    // in its lse) forms it exactly instead (as kRowNormalized): the 16-bit P of the forward's
+                    // PV product leave ~2^-9 |dP| in dO . O, which a peaked row does not average out
+  kRowGiven = 1,    // read from delta
+  kRowFrozen = 2,   // sum_j P_ij dP_ij with P = exp(S - lse) exactly as given (frozen statistics)
+  kRowNormalized = 3,  // sum_j P_ij dP_ij / sum_j P_ij: the exact softmax's row term for this lse
+};
 
-// dQ pass of the backward. When o.p is set, delta = rowsum(dO * (O + O_lo)) is computed and written to
-// delta; otherwise delta is read. row_max (optional): the row maxima m that mark peaked rows (16-bit
-// inputs); absent, every row is treated as peaked.
+// dQ pass of the backward (dq.p may be null: the row term only). 16-bit inputs: peaked rows are flagged in lse.
 struct DqParams {
   Shape s;
-  View q, k, v, dout, o, o_lo;
+  View q, k, v, dout, o;
   bool o_f32;
+  int row_term;  // RowTerm
   const float* lse;
-  const float* row_max;
   float* delta;
   MutView dq;
 };
@@ -62,8 +62,7 @@ struct DqParams {
 struct DkdvParams {
   Shape s;
   View q, k, v, dout;
-  const float* lse;
-  const float* row_max;  // as in DqParams
+  const float* lse;  // 16-bit inputs: peaked rows flagged
   const float* delta;
   MutView dk, dv;
   bool dv_only;
@@ -102,7 +101,7 @@ struct ScoresParams {
 // Compute units of the current device (cached per device).
 int device_cu_count();
 
-hipError_t launch_fwd(const FwdParams& p, int mode, hipStream_t st);
+hipError_t launch_fwd(const FwdParams& p, hipStream_t st);
 hipError_t launch_bwd_dq(const DqParams& p, hipStream_t st);
 hipError_t launch_bwd_dkdv(const DkdvParams& p, hipStream_t st);
 hipError_t launch_jvp(const JvpParams& p, hipStream_t st);
