@@ -140,7 +140,7 @@ def flag_all(lse):
     return torch.where(torch.isfinite(lse), bits | 1, bits).view(torch.float32)
 
 
-def check_entry_points_on(dev, dt, causal, q, k, v, do, tq, tk, tv, scale=None, fp32_ref_err=None):
+def check_entry_points_on(dev, dt, causal, q, k, v, do, tq, tk, tv, scale=None, fp32_ref_err=None, orders=(1, 2)):
     """Every entry point on the given CPU inputs (already rounded to dt) against the float64 oracle.
 
     Bars: tol(dt) for outputs in the input dtype; float32 outputs of 16-bit inputs (O with a float32
@@ -149,7 +149,9 @@ def check_entry_points_on(dev, dt, causal, q, k, v, do, tq, tk, tv, scale=None, 
     each within a relative 2^-8 of its float32 value, so log l is within 2^-8 absolute).
     fp32_ref_err (float32 only): {quantity: largest error of theria's float32 PyTorch path against the
     oracle on these inputs}; a quantity listed there may be off by up to twice that error (when it exceeds
-    1e-5), since float32 arithmetic itself cannot reach 1e-5 there."""
+    1e-5), since float32 arithmetic itself cannot reach 1e-5 there.
+    orders: 1 checks the forward, backward and JVP entry points, 2 the double backward (the forward is checked
+    either way)."""
     qc, kc, vc, doc, tqc, tkc, tvc = (t.double() for t in (q, k, v, do, tq, tk, tv))
     q, k, v, do, tq, tk, tv = (t.to(dev) for t in (q, k, v, do, tq, tk, tv))
     s = 1 / math.sqrt(q.shape[-1]) if scale is None else scale
@@ -176,6 +178,21 @@ def check_entry_points_on(dev, dt, causal, q, k, v, do, tq, tk, tv, scale=None, 
     torch.testing.assert_close(lse32.double().cpu(), lser, **lse_tol, msg=lambda m_: f"lse(fp32 out): {m_}")
     torch.testing.assert_close(m.double().cpu(), mr, rtol=1e-5, atol=1e-5, msg=lambda m_: f"m: {m_}")
     torch.testing.assert_close(l.double().cpu(), lr, **stat_tol(dt), msg=lambda m_: f"l: {m_}")
+
+    def second_order(delta):
+        G = _ops.bwd_bwd(q, k, v, o, do, lse, delta, tq, tk, tv, s, causal)
+        Gr = O.double_backward(qc, kc, vc, doc, tqc, tkc, tvc, s, causal)
+        for name, a, b in zip(("G_Q", "G_K", "G_V", "G_dO"), G, Gr):
+            close(a, b, dt, name)
+        G2 = _ops.bwd_bwd(q, k, v, o, do, lse, delta, None, tk, None, s, causal)
+        G2r = O.double_backward(qc, kc, vc, doc, None, tkc, None, s, causal)
+        for name, a, b in zip(("G_Q(gk)", "G_K(gk)", "G_V(gk)", "G_dO(gk)"), G2, G2r):
+            close(a, b, dt, name)
+
+    if 1 not in orders:
+        if 2 in orders:
+            second_order(_ops.bwd(q, k, v, o, lse, do, s, causal)[3])
+        return
 
     if dt != torch.float32:
         # the forward flags every row whose largest probability exceeds 1/4 (its bound may flag a few more)
@@ -223,15 +240,8 @@ def check_entry_points_on(dev, dt, causal, q, k, v, do, tq, tk, tv, scale=None, 
     close(_ops.jvp(q, k, v, o, lse, tq, tk, tv, s, causal), jr, dt, "JVP(saved O)")
     close(_ops.jvp(q, k, v, None, lse, tq, tk, tv, s, causal), jr, dt, "JVP(rebuilt O)")
     close(_ops.jvp(q, k, v, o, lse, tq, None, None, s, causal), O.jvp(qc, kc, vc, tqc, None, None, s, causal), dt, "JVP(tq only)")
-
-    G = _ops.bwd_bwd(q, k, v, o, do, lse, delta, tq, tk, tv, s, causal)
-    Gr = O.double_backward(qc, kc, vc, doc, tqc, tkc, tvc, s, causal)
-    for name, a, b in zip(("G_Q", "G_K", "G_V", "G_dO"), G, Gr):
-        close(a, b, dt, name)
-    G2 = _ops.bwd_bwd(q, k, v, o, do, lse, delta, None, tk, None, s, causal)
-    G2r = O.double_backward(qc, kc, vc, doc, None, tkc, None, s, causal)
-    for name, a, b in zip(("G_Q(gk)", "G_K(gk)", "G_V(gk)", "G_dO(gk)"), G2, G2r):
-        close(a, b, dt, name)
+    if 2 in orders:
+        second_order(delta)
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
