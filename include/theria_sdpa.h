@@ -153,8 +153,8 @@ int theria_sdpa_jvp(const theria_sdpa_problem_t* p, const theria_tensor_t* q, co
  * The reference has no kernel for this: its HVP is a finite difference of the VJP
  * (theria/attention/hvp_utils.py:30-49) or autograd-in-backward (theria/autograd/sdpa_custom_function.py:32-53).
  * delta is the row term written by theria_sdpa_bwd. Any cotangent may have data == NULL (zero).
- * For 16-bit inputs the row term is recomputed from lse as dO . sum_j P_ij V_j in float32 (into the
- * workspace), because delta from the 16-bit O differs from sum_j P_ij dP_ij by the rounding of O, which the
+ * For 16-bit inputs the row term is recomputed from lse as sum_j P_ij dP_ij in float32 (into the
+ * workspace), because delta from the 16-bit O differs from it by the rounding of O, which the
  * second-order terms amplify where they cancel; delta is then not read.
  * row_ws is a caller-owned float32 workspace of 3*batch*heads*tq elements.
  */
@@ -163,6 +163,22 @@ int theria_sdpa_bwd_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q
                         const float* lse, const float* delta, const theria_tensor_t* gq, const theria_tensor_t* gk,
                         const theria_tensor_t* gv, const theria_tensor_t* out_gq, const theria_tensor_t* out_gk,
                         const theria_tensor_t* out_gv, const theria_tensor_t* out_gdout, float* row_ws, void* stream);
+
+/*
+ * theria_sdpa_bwd_bwd without a workspace argument and without any allocation. It has no counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). The row workspace is a static device array of 3 * 2^20 floats (12 MiB)
+ * that each GPU the library runs on holds until the process ends, so 3 * batch * heads * tq must not exceed
+ * 3 * 2^20 (a larger problem is rejected with THERIA_ERR_CONTRACT). Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (other streams, other threads) race and must be serialised by the
+ * caller. Results equal theria_sdpa_bwd_bwd's bit for bit.
+ */
+int theria_sdpa_bwd_bwd_noalloc(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
+                                const theria_tensor_t* v, const theria_tensor_t* o, const theria_tensor_t* dout,
+                                const float* lse, const float* delta, const theria_tensor_t* gq,
+                                const theria_tensor_t* gk, const theria_tensor_t* gv, const theria_tensor_t* out_gq,
+                                const theria_tensor_t* out_gk, const theria_tensor_t* out_gv,
+                                const theria_tensor_t* out_gdout, void* stream);
 
 /*
  * Materialised scores for the partial-fusion sdpa_custom backends (theria/attention/custom.py:30-49).

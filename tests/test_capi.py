@@ -68,6 +68,9 @@ def _call_all(prob):
         "bwd_bwd": lib.theria_sdpa_bwd_bwd(
             p, None, None, None, None, None, None, None, None, None, None, None, None, None, None, None, None
         ),
+        "bwd_bwd_noalloc": lib.theria_sdpa_bwd_bwd_noalloc(
+            p, None, None, None, None, None, None, None, None, None, None, None, None, None, None, None
+        ),
         "qk_scores": lib.theria_qk_scores(p, None, None, None, 1, None),
         "qk_softmax": lib.theria_qk_softmax(p, None, None, None, None),
     }

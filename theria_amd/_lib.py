@@ -74,6 +74,10 @@ SIGNATURES = {
         [_PR, _TV, _TV, _TV, _TV, _TV, _P, _P, _TV, _TV, _TV, _TV, _TV, _TV, _TV, _P, _P],
         ctypes.c_int,
     ),
+    "theria_sdpa_bwd_bwd_noalloc": (
+        [_PR, _TV, _TV, _TV, _TV, _TV, _P, _P, _TV, _TV, _TV, _TV, _TV, _TV, _TV, _P],
+        ctypes.c_int,
+    ),
     "theria_qk_scores": ([_PR, _TV, _TV, _P, ctypes.c_int32, _P], ctypes.c_int),
     "theria_qk_softmax": ([_PR, _TV, _TV, _P, _P], ctypes.c_int),
 }

@@ -290,8 +290,11 @@ def jvp(q, k, v, o, lse, tq, tk, tv, scale: float, causal: bool, normalize: bool
     return out
 
 
-def bwd_bwd(q, k, v, o, do, lse, delta, gq, gk, gv, scale: float, causal: bool):
-    """(G_Q, G_K, G_V, G_dO): VJP of the backward map with cotangents (gq, gk, gv) (None = zero)."""
+def bwd_bwd(q, k, v, o, do, lse, delta, gq, gk, gv, scale: float, causal: bool, noalloc: bool = False):
+    """(G_Q, G_K, G_V, G_dO): VJP of the backward map with cotangents (gq, gk, gv) (None = zero).
+
+    noalloc: run theria_sdpa_bwd_bwd_noalloc, whose row workspace is the library's static device array
+    (3 * B * H * T up to 3 * 2^20), instead of a workspace allocated here."""
     check_inputs(q, k, v)
     q, k, v = _rowmajor(q), _rowmajor(k), _rowmajor(v)
     B, H, T, D = q.shape
@@ -309,15 +312,17 @@ def bwd_bwd(q, k, v, o, do, lse, delta, gq, gk, gv, scale: float, causal: bool):
     out_k = torch.empty((B, H, M, D), dtype=q.dtype, device=dev)
     out_v = torch.empty((B, H, M, D), dtype=q.dtype, device=dev)
     out_do = torch.empty((B, H, T, D), dtype=q.dtype, device=dev)
-    ws = torch.empty((3 * B * H * T,), dtype=torch.float32, device=dev)
     lib = _lib.load()
     prob = _problem(q, k, scale, causal)
+    args = (ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(o), _tv(do), _fp(lse), _fp(delta), _tv(gq), _tv(gk),
+            _tv(gv), _tv(out_q), _tv(out_k), _tv(out_v), _tv(out_do))
     with _OnDevice(dev):
-        rc = lib.theria_sdpa_bwd_bwd(
-            ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(o), _tv(do), _fp(lse), _fp(delta), _tv(gq), _tv(gk),
-            _tv(gv), _tv(out_q), _tv(out_k), _tv(out_v), _tv(out_do), _fp(ws), _stream(dev),
-        )
-    _lib.check(rc, "theria_sdpa_bwd_bwd")
+        if noalloc:
+            rc = lib.theria_sdpa_bwd_bwd_noalloc(*args, _stream(dev))
+        else:
+            ws = torch.empty((3 * B * H * T,), dtype=torch.float32, device=dev)
+            rc = lib.theria_sdpa_bwd_bwd(*args, _fp(ws), _stream(dev))
+    _lib.check(rc, "theria_sdpa_bwd_bwd_noalloc" if noalloc else "theria_sdpa_bwd_bwd")
     return out_q, out_k, out_v, out_do
 
 

@@ -3,6 +3,7 @@
 #include <atomic>
 #include <cmath>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "../../include/theria_sdpa.h"
@@ -120,6 +121,37 @@ int device_cu_count() {
 }
 
 }  // namespace theria
+
+// Static row workspace of theria_sdpa_bwd_bwd_noalloc: kScratchFloats floats (12 MiB) on every device the
+// library runs on, held until the process ends. Its name is only a host-side stand-in; the device address is
+// looked up once per device (with that device current) and kept in g_scratch_ptr. The kernels overwrite
+// every element they later read (r, t and the row term), so nothing is cleared; two calls that overlap on
+// one device race on it.
+constexpr int64_t kScratchFloats = int64_t(3) << 20;
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_on_current_device(float** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e, "theria_sdpa_bwd_bwd_noalloc (hipGetDevice)");
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(THERIA_ERR_CONTRACT, "theria_sdpa_bwd_bwd_noalloc: device index beyond " + std::to_string(kMaxDevices));
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_status(e, "theria_sdpa_bwd_bwd_noalloc (hipGetSymbolAddress)");
+    g_scratch_ptr[dev] = static_cast<float*>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return THERIA_OK;
+}
+}  // namespace
 
 THERIA_API int theria_abi_version(void) { return THERIA_SDPA_ABI_VERSION; }
 
@@ -343,12 +375,14 @@ THERIA_API int theria_sdpa_jvp(const theria_sdpa_problem_t* p, const theria_tens
   return hip_status(theria::launch_jvp(jp, (hipStream_t)stream), "theria_sdpa_jvp");
 }
 
-THERIA_API int theria_sdpa_bwd_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
-                                   const theria_tensor_t* v, const theria_tensor_t* o, const theria_tensor_t* dout,
-                                   const float* lse, const float* delta, const theria_tensor_t* gq,
-                                   const theria_tensor_t* gk, const theria_tensor_t* gv, const theria_tensor_t* out_gq,
-                                   const theria_tensor_t* out_gk, const theria_tensor_t* out_gv,
-                                   const theria_tensor_t* out_gdout, float* row_ws, void* stream) {
+// The double backward with its row workspace either given (row_ws) or, for the allocation-free entry point
+// (noalloc), the calling device's static scratch array.
+static int run_bwd_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
+                       const theria_tensor_t* v, const theria_tensor_t* o, const theria_tensor_t* dout,
+                       const float* lse, const float* delta, const theria_tensor_t* gq, const theria_tensor_t* gk,
+                       const theria_tensor_t* gv, const theria_tensor_t* out_gq, const theria_tensor_t* out_gk,
+                       const theria_tensor_t* out_gv, const theria_tensor_t* out_gdout, float* row_ws, bool noalloc,
+                       void* stream) {
   theria::Shape s;
   std::string err;
   if (!shape_from(p, s, err)) return fail(THERIA_ERR_CONTRACT, err);
@@ -367,12 +401,20 @@ THERIA_API int theria_sdpa_bwd_bwd(const theria_sdpa_problem_t* p, const theria_
   c.qview(out_gdout, "out_gdout", true);
   c.need(lse != nullptr || !c.q_rows, "lse is required");
   c.need(delta != nullptr || !c.q_rows, "delta is required");
-  c.need(row_ws != nullptr || !c.q_rows, "row_ws is required");
+  c.need(noalloc || row_ws != nullptr || !c.q_rows, "row_ws is required");
   if (!c.err.empty()) return fail(THERIA_ERR_CONTRACT, c.err);
   s.vec = c.vec;
   if (s.B == 0 || s.H == 0) return THERIA_OK;
   const hipStream_t st = (hipStream_t)stream;
   const int64_t nrows = (int64_t)s.B * s.H * s.T;
+  if (noalloc) {
+    if (3 * nrows > kScratchFloats)
+      return fail(THERIA_ERR_CONTRACT, "theria_sdpa_bwd_bwd_noalloc: 3 * batch * heads * tq = " +
+                                           std::to_string(3 * nrows) + " floats exceeds the static scratch of " +
+                                           std::to_string(kScratchFloats) + " (use theria_sdpa_bwd_bwd with row_ws)");
+    const int rc = scratch_on_current_device(&row_ws);
+    if (rc != THERIA_OK) return rc;
+  }
   theria::BwdBwdParams bp{};
   bp.s = s;
   bp.q = cv(q);
@@ -417,6 +459,27 @@ THERIA_API int theria_sdpa_bwd_bwd(const theria_sdpa_problem_t* p, const theria_
   jp.tout = mv(out_gdout);
   jp.normalize = true;  // lse is the operator's own: G_dO is the JVP of the exact softmax
   return hip_status(theria::launch_jvp(jp, st), "theria_sdpa_bwd_bwd (dout)");
+}
+
+THERIA_API int theria_sdpa_bwd_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
+                                   const theria_tensor_t* v, const theria_tensor_t* o, const theria_tensor_t* dout,
+                                   const float* lse, const float* delta, const theria_tensor_t* gq,
+                                   const theria_tensor_t* gk, const theria_tensor_t* gv, const theria_tensor_t* out_gq,
+                                   const theria_tensor_t* out_gk, const theria_tensor_t* out_gv,
+                                   const theria_tensor_t* out_gdout, float* row_ws, void* stream) {
+  return run_bwd_bwd(p, q, k, v, o, dout, lse, delta, gq, gk, gv, out_gq, out_gk, out_gv, out_gdout, row_ws, false,
+                     stream);
+}
+
+THERIA_API int theria_sdpa_bwd_bwd_noalloc(const theria_sdpa_problem_t* p, const theria_tensor_t* q,
+                                           const theria_tensor_t* k, const theria_tensor_t* v, const theria_tensor_t* o,
+                                           const theria_tensor_t* dout, const float* lse, const float* delta,
+                                           const theria_tensor_t* gq, const theria_tensor_t* gk,
+                                           const theria_tensor_t* gv, const theria_tensor_t* out_gq,
+                                           const theria_tensor_t* out_gk, const theria_tensor_t* out_gv,
+                                           const theria_tensor_t* out_gdout, void* stream) {
+  return run_bwd_bwd(p, q, k, v, o, dout, lse, delta, gq, gk, gv, out_gq, out_gk, out_gv, out_gdout, nullptr, true,
+                     stream);
 }
 
 // Partial-fusion score kernels: the problem's v-related fields are unused; causal must be 0.
