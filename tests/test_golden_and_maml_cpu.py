@@ -11,7 +11,7 @@ from oracle import sdpa_oracle as O
 from theria_amd.attention.reference import reference_attention, sdpa_backward_reference, sdpa_jvp_reference
 from theria_amd.maml import meta_loss_on_tasks
 from theria_amd.models import BackendAttentionModel, MHAClassifier, MHAConfig, TinyAttentionConfig, TinyAttentionModel
-from theria_amd.tasks import label_sequences, sample_token_count_task, task_sampler
+from theria_amd.tasks import label_sequences, sample_token_count_task, teacher_readout_task
 
 GOLDEN = Path(__file__).resolve().parent / "golden" / "c1_fp32.npz"
 
@@ -53,8 +53,9 @@ def test_golden_fixture_matches_reference_cpu_path_fp32():
 
 
 def _toy_tasks(n, D=8, seed=0):
-    torch.manual_seed(seed)
-    return [task_sampler(B_s=4, B_q=4, T=6, D=D, num_classes=3, dtype=torch.float64) for _ in range(n)]
+    g = torch.Generator().manual_seed(seed)
+    return [teacher_readout_task(support=4, query=4, T=6, D=D, num_classes=3, generator=g, dtype=torch.float64)
+            for _ in range(n)]
 
 
 def test_maml_full_differs_from_first_order():

@@ -1,7 +1,8 @@
 """Full MAML (create_graph=True) through the HIP operator vs the same model on the pure-PyTorch
-"reference" backend (GPU). Config 5 (reduced meta-batch): 2-layer, d_model 64, 4-head
-token-count classifier, 5 inner SGD steps at lr 0.4. The meta-gradients must agree (attention's
-second-order terms are kept), and full MAML must differ from first-order MAML.
+"reference" backend (GPU). Config 5 at its full meta-batch of 16 tasks: 2-layer, d_model 64, 4-head
+token-count classifier, 5 inner SGD steps at lr 0.4. The meta-gradients must agree to a relative L2 of
+1e-5 (attention's second-order terms are kept; float32 accumulation differences between the two backends
+measure ~4e-6), and full MAML must differ from first-order MAML.
 """
 
 import copy
@@ -11,9 +12,12 @@ import torch
 
 from theria_amd.maml import meta_loss_on_tasks, meta_loss_on_tasks_batched
 from theria_amd.models import BackendAttentionModel, MHAClassifier, MHAConfig, TinyAttentionConfig
-from theria_amd.tasks import sample_token_count_task, task_sampler
+from theria_amd.tasks import sample_token_count_task, teacher_readout_task
 
 pytestmark = pytest.mark.gpu
+
+META_BATCH = 16
+REL_L2 = 1e-5
 
 
 def _flat(grads):
@@ -33,14 +37,14 @@ def test_config5_full_maml_metagradient_matches_reference_backend(hip_device):
     hip_model = copy.deepcopy(ref_model)
     hip_model.set_attention_backend("hip")
     g = torch.Generator().manual_seed(0)
-    tasks = [sample_token_count_task(generator=g, device=dev)[0] for _ in range(4)]
+    tasks = [sample_token_count_task(generator=g, device=dev)[0] for _ in range(META_BATCH)]
     l_ref, g_ref = _metagrad(ref_model, tasks)
     l_hip, g_hip = _metagrad(hip_model, tasks)
     torch.testing.assert_close(l_hip.double(), l_ref.double(), rtol=1e-4, atol=1e-5)
     rel = float((g_hip - g_ref).norm() / g_ref.norm())
     cos = float(torch.nn.functional.cosine_similarity(g_hip, g_ref, dim=0))
     print(f"[maml] config5 rel_l2={rel:.3e} cosine={cos:.8f}", flush=True)
-    assert rel < 1e-3 and cos > 0.99999
+    assert rel < REL_L2 and cos > 0.99999
     _, g_fo = _metagrad(hip_model, tasks, fo=True)
     assert float((g_hip - g_fo).norm() / g_hip.norm()) > 1e-3
 
@@ -52,13 +56,13 @@ def test_phase10_model_full_vs_reference(hip_device):
     ref_model = BackendAttentionModel(TinyAttentionConfig(), backend="reference").to(dev)
     hip_model = copy.deepcopy(ref_model)
     hip_model.set_attention_backend("triton_fused")
-    torch.manual_seed(1)
-    tasks = [task_sampler(device=dev) for _ in range(2)]
+    g = torch.Generator().manual_seed(1)
+    tasks = [teacher_readout_task(generator=g, device=dev) for _ in range(2)]
     _, g_ref = _metagrad(ref_model, tasks, inner_lr=0.1)
     _, g_hip = _metagrad(hip_model, tasks, inner_lr=0.1)
     rel = float((g_hip - g_ref).norm() / g_ref.norm())
     print(f"[maml] phase10 rel_l2={rel:.3e}", flush=True)
-    assert rel < 1e-3
+    assert rel < REL_L2
 
 
 def test_config5_task_batched_full_maml_matches_reference_loop(hip_device):
@@ -70,7 +74,7 @@ def test_config5_task_batched_full_maml_matches_reference_loop(hip_device):
     hip_model = copy.deepcopy(ref_model)
     hip_model.set_attention_backend("hip")
     g = torch.Generator().manual_seed(0)
-    tasks = [sample_token_count_task(generator=g, device=dev)[0] for _ in range(4)]
+    tasks = [sample_token_count_task(generator=g, device=dev)[0] for _ in range(META_BATCH)]
     params = list(hip_model.parameters())
     for fo in (False, True):
         l_ref, g_ref = _metagrad(ref_model, tasks, fo=fo)
@@ -79,7 +83,7 @@ def test_config5_task_batched_full_maml_matches_reference_loop(hip_device):
         torch.testing.assert_close(loss.detach().double(), l_ref.double(), rtol=1e-4, atol=1e-5)
         rel = float((g_hip - g_ref).norm() / g_ref.norm())
         print(f"[maml] task-batched fo={fo} rel_l2={rel:.3e}", flush=True)
-        assert rel < 1e-3
+        assert rel < REL_L2
 
 
 def test_graphed_task_batched_meta_step_matches_eager(hip_device):

@@ -18,7 +18,7 @@ import torch
 from theria_amd.attention.custom import sdpa_custom
 from theria_amd.maml.diagnostics import attention_second_order_ok, meta_gradient_probe
 from theria_amd.models.tiny_attention import BackendAttentionModel, TinyAttentionConfig
-from theria_amd.tasks.synthetic_seqcls import task_sampler
+from theria_amd.tasks import teacher_readout_task
 
 pytestmark = pytest.mark.gpu
 
@@ -39,7 +39,8 @@ def test_meta_probe_hip_matches_reference_backend(backend, inner_steps, hip_devi
     torch.manual_seed(0)
     ref_model = BackendAttentionModel(TinyAttentionConfig(d_model=64, num_classes=5), backend="reference")
     ref_model = ref_model.to(hip_device)
-    task = task_sampler(B_s=16, B_q=16, T=32, D=64, num_classes=5, device=hip_device)
+    task = teacher_readout_task(support=16, query=16, T=32, D=64, num_classes=5, device=hip_device,
+                                generator=torch.Generator().manual_seed(0))
     model = copy.deepcopy(ref_model)
     model.set_attention_backend(backend)
     ref = meta_gradient_probe(ref_model, task, inner_steps=inner_steps, inner_lr=0.4)

@@ -18,7 +18,7 @@ from theria_amd.attention.custom import sdpa_custom
 from theria_amd.attention.reference import reference_attention
 from theria_amd.maml.diagnostics import attention_second_order_ok, meta_gradient_probe
 from theria_amd.models.tiny_attention import BackendAttentionModel, TinyAttentionConfig
-from theria_amd.tasks.synthetic_seqcls import task_sampler
+from theria_amd.tasks import teacher_readout_task
 
 
 def detach_output(fn):
@@ -96,7 +96,8 @@ def test_attention_probe_rejects_planted_mistakes(bad):
 def _model_and_task(seed=0):
     torch.manual_seed(seed)
     model = BackendAttentionModel(TinyAttentionConfig(d_model=16, num_classes=3), backend="reference")
-    task = task_sampler(B_s=8, B_q=8, T=6, D=16, num_classes=3)
+    task = teacher_readout_task(support=8, query=8, T=6, D=16, num_classes=3,
+                                generator=torch.Generator().manual_seed(seed))
     return model, task
 
 

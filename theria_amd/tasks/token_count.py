@@ -1,6 +1,6 @@
 """Token-count classification tasks for the multi-head MAML benchmark (config 5: 16 tasks, vocab 32, length 64, 5-way).
 
-Not in the reference (its nearest relatives are the prototype tasks of theria/tasks/synthetic_seqcls.py).
+Not in the reference.
 A task partitions the vocabulary at random into `num_classes` class-token sets (sizes differ by at most
 one). A sequence is `seq_len` token ids drawn uniformly from the vocabulary; its label is the class
 whose tokens occur most often in it, ties going to the lowest class index. Support and query sets are
@@ -12,7 +12,7 @@ from __future__ import annotations
 
 import torch
 
-from .synthetic_seqcls import TaskBatch
+from .batch import TaskBatch
 
 
 def label_sequences(tokens: torch.Tensor, token_class: torch.Tensor, num_classes: int) -> torch.Tensor:
