@@ -294,6 +294,31 @@ def test_double_backward_few_key_rows(case, seed, hip_device):
     close(G[0], Gr[0], dt, "G_Q")
 
 
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_dv_only_backward_float32(D, causal, hip_device):
+    """The dV-only backward (no V: the reference's sdpa_bwd_dv) in float32 at head dims 64 and 128 with
+    several query tiles, the regime where an earlier runtime-flag form of it returned wrong dV; here the
+    DV_ONLY variant of the dK/dV kernel, through the explicit API, against the frozen-stats oracle."""
+    from theria_amd.attention import explicit
+
+    print(f"[dv only] fp32 D{D} causal={causal}", flush=True)
+    B, H, T, M = 1, 2, 200, 170 if not causal else 200
+    g = torch.Generator().manual_seed(7 + D)
+    q, k, v, do = (torch.randn(B, H, n, D, generator=g) for n in (T, M, M, T))
+    s = 1 / math.sqrt(D)
+    dev = hip_device
+    _, lse, m, l = _ops.fwd(q.to(dev), k.to(dev), v.to(dev), s, causal, stats=True)
+    ref = O.frozen_backward(q.double(), k.double(), v.double(), do.double(), lse.double().cpu(), s, causal)[2]
+    _, _, dv = _ops.bwd_from_stats(q.to(dev), k.to(dev), None, do.to(dev), lse, s, causal, False, False, True)
+    _close(dv, ref, torch.float32, "dV(no v)")
+    if not causal:  # the reference's sdpa_bwd_dv(q, k, dout, m, l, scale) takes no causal flag
+        dv2 = explicit.sdpa_bwd_dv(q.to(dev), k.to(dev), do.to(dev), m, l, s)
+        lse_ml = (m.double() + torch.log(l.double())).cpu()
+        ref2 = O.frozen_backward(q.double(), k.double(), v.double(), do.double(), lse_ml, s, causal)[2]
+        _close(dv2, ref2, torch.float32, "sdpa_bwd_dv")
+
+
 def test_config1_golden_fixture_fp32(hip_device):
     """Config 1 (B2 H2 S16 D8, float32) against the committed fixture, 1e-5."""
     z = np.load(GOLDEN, allow_pickle=False)
