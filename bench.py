@@ -5,14 +5,13 @@ Metric: SDPA fwd+bwd TFLOP/s and share of the bf16 MFMA peak at B4 H16 S2048 D64
 
 A "step" is one forward + backward pass of the SDPA operator over config 2
 (B4 H16 S2048 D64, bfloat16, non-causal, scale 1/8, Q, K, V, dO ~ N(0,1), synthetic, resident in HBM):
-forward kernel (O, lse), then the backward's two kernels (dQ with the row term, then dK/dV), each run as
-a common launch and a launch for the query blocks / tiles holding peaked rows (none at config 2, where that
-launch only checks the lse flags). Throughput counts algorithmic FLOPs, FlashAttention convention: 4*B*H*S^2*D forward,
+forward kernel (O, lse), then the backward's two kernels (dQ with the row term, then dK/dV); query blocks /
+tiles holding peaked rows (flagged in lse; none at config 2) take an exact path inside the same launches. Throughput counts algorithmic FLOPs, FlashAttention convention: 4*B*H*S^2*D forward,
 10*B*H*S^2*D backward (the recomputed QK^T included), 14*B*H*S^2*D per step.
 
 Printed as ONE JSON line (rank 0): value = TFLOP/s of the whole step, plus
-  roofline     the dominant kernel (the backward's dK/dV kernel), its algorithmic FLOPs per call over the
-               average HIP-event duration of theria_sdpa_bwd_dkdv (both of its launches), against the dense bf16 MFMA peak; traffic = HBM bytes
+  roofline     the dominant kernel (the backward's dK/dV kernel), its algorithmic FLOPs per launch over the
+               average HIP-event duration of theria_sdpa_bwd_dkdv (one launch), against the dense bf16 MFMA peak; traffic = HBM bytes
                per launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE runs (profiles/traffic.json);
   cpu_baseline the CPU oracle (oracle/sdpa_oracle.py, the reference's pure-PyTorch math, float32)
                timed on a bounded sample of heads of the same workload on this host's cores;
@@ -466,7 +465,7 @@ def main() -> int:
         "config": {"workload": "sdpa_fwd_bwd", "batch": 4, "heads": 16, "seq_len": 2048, "head_dim": 64, "causal": False},
         "mfma_peak_frac": round(value / PEAK_BF16_TFLOPS, 4),
         "roofline": {
-            "kernel": "dkdv_pipe_kernel<bf16, non-causal, 8 waves>, common + peaked launches (theria_sdpa_bwd_dkdv)",
+            "kernel": "dkdv_pipe_kernel<bf16, non-causal, 8 waves> (theria_sdpa_bwd_dkdv)",
             "bound": "mfma",
             "achieved": round(achieved, 2),
             "peak": PEAK_BF16_TFLOPS,

@@ -68,12 +68,12 @@ namespace theria {
 
 // FD: the head dim is DP itself (compile-time bounds); otherwise the runtime head dim s.D < DP bounds the
 // loads, stores and DMA chunks (both kernels).
-// Two launches share the query tiles of every key block: PEAKED = false runs the tiles without a peaked row
-// (flagged in lse: largest probability above 1/4) with K pre-multiplied by scale * log2(e) and S started from -lse2, so
-// P = exp2(S); PEAKED = true then finds the tiles holding a peaked row (a scan of the lse flags), runs
-// them from the exact float32 scores with P and dS as two 16-bit terms each, and adds its sums to dK, dV.
-// Keeping the two apart keeps the common kernel's registers and schedule.
-template <typename T, bool CAUSAL, int NW, int DP, bool OVERLAP, int WPS, int HALVES, bool FD, bool PEAKED>
+// dkdv_pipe_kernel runs the query tiles without a peaked row (flagged in lse: largest probability above 1/4)
+// with K pre-multiplied by scale * log2(e) and S started from -lse2, so P = exp2(S), and skips the others;
+// after the last tile, a workgroup that skipped any finds them again (a scan of the lse flags) and runs them
+// from the exact float32 scores with P and dS as two 16-bit terms each, into the same dK, dV accumulators.
+// Running them apart from the tile loop keeps the loop's registers and schedule.
+template <typename T, bool CAUSAL, int NW, int DP, bool OVERLAP, int WPS, int HALVES, bool FD>
 __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
@@ -122,18 +122,15 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
   const int kw0 = key0 + wave * 32;  // this wave's keys: kw0 + li
 
     // K pre-multiplied by scale * log2(e) and S started from -lse * log2(e): P = exp2(S) with no per-score
-    // scaling. The peaked launch forms the exact scores from K itself, and loads V only once it has found a
-    // tile to run.
+    // scaling. The tiles holding a peaked row form the exact scores from K itself (kraw below).
     F kf[NKC], vf[NKC];
     auto load_v = [&]() {
 #pragma unroll
       for (int c = 0; c < NKC; ++c) vf[c] = gload_frag8<T>(V, p.v.sr, kw0 + li, s.M, c, FD ? DP : s.D);
     };
-    if (!PEAKED) {
 #pragma unroll
-      for (int c = 0; c < NKC; ++c) kf[c] = scaled_frag<T>(gload_frag8<T>(K, p.k.sr, kw0 + li, s.M, c, FD ? DP : s.D), c2);
-      load_v();
-    }
+    for (int c = 0; c < NKC; ++c) kf[c] = scaled_frag<T>(gload_frag8<T>(K, p.k.sr, kw0 + li, s.M, c, FD ? DP : s.D), c2);
+    load_v();
     f32x16_t dv[NDT], dk[NDT];
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
@@ -325,6 +322,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
     const std::integral_constant<bool, true> fast;
     const std::integral_constant<bool, false> general;
 
+    bool pk_any = false;  // uniform: a tile holding a peaked row was skipped
     // One query tile `it` from buffers (tq, to, tr, tf); the next tile goes to (nq, no, nr, nf).
     auto step = [&](auto fast_tag, int it, const char* tq, const char* to, const float* tr, const int* tf, char* nq,
                     char* no, float* nr, int* nf) {
@@ -337,10 +335,13 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
         store_rows(nr, nf);
         load_rows(it + 2);
       }
-      if (!peaked_tile(tf)) body(fast_tag, it, tq, to, tr);  // the peaked launch takes the others
+      const bool pk = peaked_tile(tf);
+      pk_any |= pk;  // run after the loop
+      if (!pk) body(fast_tag, it, tq, to, tr);
     };
 
-    if constexpr (PEAKED) {
+    // The tiles holding a peaked row, run from the exact scores into dK, dV; returns whether any ran (uniform).
+    auto peaked_tiles = [&]() __attribute__((always_inline)) {
       // Tiles holding a peaked row, found 64 at a time from the lse flags, one after the other.
       __shared__ int sPk[64];
       bool touched = false;  // uniform
@@ -364,7 +365,6 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
         __syncthreads();
         for (int i = 0; i < nt; ++i) {
           if (!sPk[i]) continue;  // uniform: every thread reads the same flag
-          if (!touched) load_v();
           const int it = t0 + i;
           dma.template issue_clamped<NSLAB>(qrsrc, qrs, qbeg + it * BM, s.T, sQ0);
           dma.template issue_clamped<NSLAB>(orsrc, ors, qbeg + it * BM, s.T, sO0);
@@ -380,30 +380,8 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
           touched = true;
         }
       }
-      // Add this launch's sums to what the common launch stored (same stream, so it has completed).
-      if (touched) {
-        T* DV = (T*)p.dv.p + b * p.dv.sb + h * p.dv.sh;
-        T* DK = p.dk.p ? (T*)p.dk.p + b * p.dk.sb + h * p.dk.sh : nullptr;
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-          const int d = dt * 32 + li;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = kw0 + acc_row(r, g);
-            if (key < s.M && (FD || d < s.D)) {
-              T* pv = DV + (int64_t)key * p.dv.sr + d;
-              *pv = (T)((float)*pv + dv[dt][r]);
-              if (DK) {
-                T* pk = DK + (int64_t)key * p.dk.sr + d;
-                *pk = (T)((float)*pk + dk[dt][r] * s.scale);
-              }
-            }
-          }
-        }
-      }
-      continue;
-    }
-
+      return touched;
+    };
     if (nqt > 0) {
       dma.template issue_clamped<NSLAB>(qrsrc, qrs, qbeg, s.T, sQ0);
       dma.template issue_clamped<NSLAB>(orsrc, ors, qbeg, s.T, sO0);
@@ -434,6 +412,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
           step(general, it, sQ0, sO0, sR0, sF0, sQ1, sO1, sR1, sF1);
       }
     }
+    if (pk_any) peaked_tiles();  // into the same accumulators
 
     // Epilogue: lane holds column d = dt*32 + li of keys kw0 + acc_row(r, g).
     T* DV = (T*)p.dv.p + b * p.dv.sb + h * p.dv.sh;
@@ -462,12 +441,14 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
 // subtiles:
 //   S, dP of subtile 0 | S, dP of subtile 1 with exp / dS of subtile 0
 //   | dQ of subtile 0 with exp / dS of subtile 1 | dQ of subtile 1.
-// Two launches share the query blocks: PEAKED = false takes the blocks without a peaked row (flagged in lse:
-// largest probability above 1/4): Q pre-multiplied by scale * log2(e), S^T started from -lse2, P = exp2(S^T), the
-// row term dO . O. PEAKED = true takes the others (and every block for the frozen / normalised row terms):
-// the row term from a pass over the keys, exact float32 scores and dS as two 16-bit terms in the waves
-// holding a peaked row. Keeping the two apart keeps the common kernel's registers and schedule.
-template <typename T, bool CAUSAL, int NW, int DP, bool OVERLAP, int WPS, int HALVES, bool FD, bool PEAKED>
+// Two paths per query block. The common one takes the blocks without a peaked row (flagged in lse: largest
+// probability above 1/4): Q pre-multiplied by scale * log2(e), S^T started from -lse2, P = exp2(S^T), the row
+// term dO . O. The peaked one takes the others (and every block for the frozen / normalised row terms): the
+// row term from a pass over the keys, exact float32 scores and dS as two 16-bit terms in the waves holding a
+// peaked row. PK = 2 compiles both and takes each block's own (one launch); PK = 0 / 1 compile one each, for
+// two launches: at head dim 128 the second path's registers change the common path's schedule (~20% slower
+// at config 3), at head dim 64 the common path's loop compiles to the same instructions either way.
+template <typename T, bool CAUSAL, int NW, int DP, bool OVERLAP, int WPS, int HALVES, bool FD, int PK>
 __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
@@ -510,11 +491,15 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
     const float lse2 = lse == -THERIA_INF ? THERIA_INF : lse * kLog2e;  // a row without visible keys has P = 0
     const int rt = p.row_term;
     // Rows flagged peaked in lse: the whole wave runs the split loop when any of its rows is, and the block
-    // belongs to the peaked launch.
+    // takes the peaked path.
     const bool peaked = qvalid && lse_peaked(lse);
     const bool split = __any(peaked);
     const bool block_peaked = rt >= kRowFrozen || __syncthreads_or(split);
-    if (block_peaked != PEAKED) continue;  // uniform over the workgroup
+    if (PK != 2 && block_peaked != (PK == 1)) continue;  // uniform over the workgroup
+
+    // The block's work for one path (PEAKED: compile-time); the fused kernel (PK = 2) picks it per block.
+    auto run = [&](auto peaked_tag) __attribute__((always_inline)) {
+    constexpr bool PEAKED = decltype(peaked_tag)::value;
 
     F qf[NKC], of[NKC];
 #pragma unroll
@@ -551,7 +536,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
     } else if (rt == kRowGiven) {
       del = qvalid ? p.delta[rowbase + myq] : 0.f;
     }
-    if (!PEAKED && !p.dq.p) continue;  // only dO . O was requested (uniform over the grid)
+    if (!PEAKED && !p.dq.p) return;  // only dO . O was requested (uniform over the grid)
 
     f32x16_t acc[NDT];
 #pragma unroll
@@ -735,7 +720,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
       del = rt == kRowFrozen ? a : (l > 0.f ? a / l : 0.f);
       if (qvalid && g == 0) p.delta[rowbase + myq] = del;
     }
-    if (!p.dq.p) continue;  // only the row term was requested
+    if (!p.dq.p) return;  // only the row term was requested
     if (PEAKED && split) {
       loop(with_split);
     } else {
@@ -756,18 +741,34 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
                       a[4 * qd + 3] * s.scale);
         }
     }
+    };  // run
+    if constexpr (PK == 0) {
+      run(std::false_type{});
+    } else if constexpr (PK == 1) {
+      run(std::true_type{});
+    } else {
+      if (block_peaked)
+        run(std::true_type{});
+      else
+        run(std::false_type{});
+    }
   }  // pass
 }
 
-// Launches with FD = (head dim == DP): the common launch (unless every block takes the row-term pass), then the
-// peaked launch.
+// Launches with FD = (head dim == DP): one fused launch at head dim 64; at 128 the common launch (unless every
+// block takes the row-term pass), then the peaked launch.
 template <typename T, bool CAUSAL, int NW, int DP, bool OVERLAP, int WPS, int HALVES, bool FD>
 static void dq_go_fd(const DqParams& p, int64_t nblk, hipStream_t st) {
-  if (p.row_term < kRowFrozen)
-    hipLaunchKernelGGL((dq_pipe_kernel<T, CAUSAL, NW, DP, OVERLAP, WPS, HALVES, FD, false>), dim3((unsigned)nblk),
+  if constexpr (DP == 64) {
+    hipLaunchKernelGGL((dq_pipe_kernel<T, CAUSAL, NW, DP, OVERLAP, WPS, HALVES, FD, 2>), dim3((unsigned)nblk),
                        dim3(64 * NW), 0, st, p);
-  hipLaunchKernelGGL((dq_pipe_kernel<T, CAUSAL, NW, DP, OVERLAP, WPS, HALVES, FD, true>), dim3((unsigned)nblk),
-                     dim3(64 * NW), 0, st, p);
+  } else {
+    if (p.row_term < kRowFrozen)
+      hipLaunchKernelGGL((dq_pipe_kernel<T, CAUSAL, NW, DP, OVERLAP, WPS, HALVES, FD, 0>), dim3((unsigned)nblk),
+                         dim3(64 * NW), 0, st, p);
+    hipLaunchKernelGGL((dq_pipe_kernel<T, CAUSAL, NW, DP, OVERLAP, WPS, HALVES, FD, 1>), dim3((unsigned)nblk),
+                       dim3(64 * NW), 0, st, p);
+  }
 }
 template <typename T, bool CAUSAL, int NW, int DP, bool OVERLAP, int WPS, int HALVES>
 static void dq_go(const DqParams& p, int64_t nblk, hipStream_t st) {
@@ -776,12 +777,9 @@ static void dq_go(const DqParams& p, int64_t nblk, hipStream_t st) {
   else
     dq_go_fd<T, CAUSAL, NW, DP, OVERLAP, WPS, HALVES, false>(p, nblk, st);
 }
-// The common launch, then the peaked launch (which adds to what the first stored).
 template <typename T, bool CAUSAL, int NW, int DP, bool OVERLAP, int WPS, int HALVES, bool FD>
 static void dkdv_go_fd(const DkdvParams& p, int64_t nblk, hipStream_t st) {
-  hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, NW, DP, OVERLAP, WPS, HALVES, FD, false>), dim3((unsigned)nblk),
-                     dim3(64 * NW), 0, st, p);
-  hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, NW, DP, OVERLAP, WPS, HALVES, FD, true>), dim3((unsigned)nblk),
+  hipLaunchKernelGGL((dkdv_pipe_kernel<T, CAUSAL, NW, DP, OVERLAP, WPS, HALVES, FD>), dim3((unsigned)nblk),
                      dim3(64 * NW), 0, st, p);
 }
 template <typename T, bool CAUSAL, int NW, int DP, bool OVERLAP, int WPS, int HALVES>
