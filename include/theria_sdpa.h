@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define THERIA_SDPA_ABI_VERSION 6
+#define THERIA_SDPA_ABI_VERSION 7
 
 enum theria_dtype { THERIA_DTYPE_F32 = 0, THERIA_DTYPE_F16 = 1, THERIA_DTYPE_BF16 = 2 };
 enum theria_status { THERIA_OK = 0, THERIA_ERR_CONTRACT = 1, THERIA_ERR_HIP = 2 };
@@ -153,10 +153,13 @@ int theria_sdpa_jvp(const theria_sdpa_problem_t* p, const theria_tensor_t* q, co
  * The reference has no kernel for this: its HVP is a finite difference of the VJP
  * (theria/attention/hvp_utils.py:30-49) or autograd-in-backward (theria/autograd/sdpa_custom_function.py:32-53).
  * delta is the row term written by theria_sdpa_bwd. Any cotangent may have data == NULL (zero).
- * For 16-bit inputs the row term is recomputed from lse as sum_j P_ij dP_ij in float32 (into the
- * workspace), because delta from the 16-bit O differs from it by the rounding of O, which the
- * second-order terms amplify where they cancel; delta is then not read.
- * row_ws is a caller-owned float32 workspace of 3*batch*heads*tq elements.
+ * For 16-bit inputs a pass over the keys recomputes, into the workspace, the row normaliser
+ * lse + ln(sum_j P_ij) (a 16-bit forward's lse comes from rounded probabilities, so P rebuilt from it sums to
+ * one only within ~2^-9) and the row term sum_j P_ij dP_ij / sum_j P_ij in float32 (delta from the 16-bit O
+ * differs from it by the rounding of O); the second-order terms amplify both where they cancel. delta is
+ * then not read. Query blocks / tiles holding a row flagged peaked in lse form G_Q from two passes and
+ * enter the G_Q, G_K, G_V products as two 16-bit terms.
+ * row_ws is a caller-owned float32 workspace of 4*batch*heads*tq elements.
  */
 int theria_sdpa_bwd_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
                         const theria_tensor_t* v, const theria_tensor_t* o, const theria_tensor_t* dout,
@@ -167,9 +170,9 @@ int theria_sdpa_bwd_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q
 /*
  * theria_sdpa_bwd_bwd without a workspace argument and without any allocation. It has no counterpart in the
  * reference: it is for callers that cannot allocate (code under HIP graph capture, tight serving loops,
- * harnesses that forbid hipMalloc). The row workspace is a static device array of 3 * 2^20 floats (12 MiB)
- * that each GPU the library runs on holds until the process ends, so 3 * batch * heads * tq must not exceed
- * 3 * 2^20 (a larger problem is rejected with THERIA_ERR_CONTRACT). Every call on one GPU shares that GPU's
+ * harnesses that forbid hipMalloc). The row workspace is a static device array of 4 * 2^20 floats (16 MiB)
+ * that each GPU the library runs on holds until the process ends, so 4 * batch * heads * tq must not exceed
+ * 4 * 2^20 (a larger problem is rejected with THERIA_ERR_CONTRACT). Every call on one GPU shares that GPU's
  * array: calls that overlap on one GPU (other streams, other threads) race and must be serialised by the
  * caller. Results equal theria_sdpa_bwd_bwd's bit for bit.
  */

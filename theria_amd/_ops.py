@@ -294,7 +294,7 @@ def bwd_bwd(q, k, v, o, do, lse, delta, gq, gk, gv, scale: float, causal: bool, 
     """(G_Q, G_K, G_V, G_dO): VJP of the backward map with cotangents (gq, gk, gv) (None = zero).
 
     noalloc: run theria_sdpa_bwd_bwd_noalloc, whose row workspace is the library's static device array
-    (3 * B * H * T up to 3 * 2^20), instead of a workspace allocated here."""
+    (4 * B * H * T up to 4 * 2^20), instead of a workspace allocated here."""
     check_inputs(q, k, v)
     q, k, v = _rowmajor(q), _rowmajor(k), _rowmajor(v)
     B, H, T, D = q.shape
@@ -320,7 +320,7 @@ def bwd_bwd(q, k, v, o, do, lse, delta, gq, gk, gv, scale: float, causal: bool, 
         if noalloc:
             rc = lib.theria_sdpa_bwd_bwd_noalloc(*args, _stream(dev))
         else:
-            ws = torch.empty((3 * B * H * T,), dtype=torch.float32, device=dev)
+            ws = torch.empty((4 * B * H * T,), dtype=torch.float32, device=dev)
             rc = lib.theria_sdpa_bwd_bwd(*args, _fp(ws), _stream(dev))
     _lib.check(rc, "theria_sdpa_bwd_bwd_noalloc" if noalloc else "theria_sdpa_bwd_bwd")
     return out_q, out_k, out_v, out_do

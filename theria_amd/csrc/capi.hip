@@ -122,12 +122,12 @@ int device_cu_count() {
 
 }  // namespace theria
 
-// Static row workspace of theria_sdpa_bwd_bwd_noalloc: kScratchFloats floats (12 MiB) on every device the
+// Static row workspace of theria_sdpa_bwd_bwd_noalloc: kScratchFloats floats (16 MiB) on every device the
 // library runs on, held until the process ends. Its name is only a host-side stand-in; the device address is
 // looked up once per device (with that device current) and kept in g_scratch_ptr. The kernels overwrite
-// every element they later read (r, t and the row term), so nothing is cleared; two calls that overlap on
+// every element they later read (r, t, the row term and the normaliser), so nothing is cleared; two calls that overlap on
 // one device race on it.
-constexpr int64_t kScratchFloats = int64_t(3) << 20;
+constexpr int64_t kScratchFloats = int64_t(4) << 20;
 static __device__ __align__(256) float scratch[kScratchFloats];
 
 namespace {
@@ -190,7 +190,7 @@ THERIA_API int theria_sdpa_fwd(const theria_sdpa_problem_t* p, const theria_tens
 static int run_dq(const theria::Shape& s, const theria_tensor_t* q, const theria_tensor_t* k,
                   const theria_tensor_t* v, const theria_tensor_t* o, bool o_f32, int row_term,
                   const theria_tensor_t* dout, const float* lse, float* delta,
-                  const theria_tensor_t* dq, hipStream_t st, const char* what) {
+                  const theria_tensor_t* dq, hipStream_t st, const char* what, float* lse_out = nullptr) {
   theria::DqParams dp{};
   dp.s = s;
   dp.q = cv(q);
@@ -203,6 +203,7 @@ static int run_dq(const theria::Shape& s, const theria_tensor_t* q, const theria
   dp.lse = lse;
   dp.delta = delta;
   dp.dq = mv(dq);
+  dp.lse_out = lse_out;
   return hip_status(theria::launch_bwd_dq(dp, st), what);
 }
 
@@ -408,9 +409,9 @@ static int run_bwd_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q,
   const hipStream_t st = (hipStream_t)stream;
   const int64_t nrows = (int64_t)s.B * s.H * s.T;
   if (noalloc) {
-    if (3 * nrows > kScratchFloats)
-      return fail(THERIA_ERR_CONTRACT, "theria_sdpa_bwd_bwd_noalloc: 3 * batch * heads * tq = " +
-                                           std::to_string(3 * nrows) + " floats exceeds the static scratch of " +
+    if (4 * nrows > kScratchFloats)
+      return fail(THERIA_ERR_CONTRACT, "theria_sdpa_bwd_bwd_noalloc: 4 * batch * heads * tq = " +
+                                           std::to_string(4 * nrows) + " floats exceeds the static scratch of " +
                                            std::to_string(kScratchFloats) + " (use theria_sdpa_bwd_bwd with row_ws)");
     const int rc = scratch_on_current_device(&row_ws);
     if (rc != THERIA_OK) return rc;
@@ -429,13 +430,18 @@ static int run_bwd_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q,
   bp.r_row = row_ws;
   bp.t_row = row_ws + nrows;
   if (s.dtype != THERIA_DTYPE_F32 && s.T > 0) {
-    // 16-bit inputs: the row term consistent with P(lse), sum_j P_ij dP_ij in float32 (the row-term pass of
-    // the dQ kernel), instead of dO . O with the 16-bit O.
+    // 16-bit inputs: a 16-bit forward's lse comes from rounded probabilities, so P rebuilt from it sums to one
+    // only within ~2^-9, and on peaked rows the second-order terms (Gam - r, dP - z, E1 - t) are differences
+    // that such a scale error does not cancel from. The row-term pass of the dQ kernel forms the exact
+    // normaliser: lse + ln(sum_j P_ij) for the row and column kernels, and z = sum_j P_ij dP_ij / sum_j P_ij in
+    // float32 instead of dO . O with the 16-bit O.
     float* rt_delta = row_ws + 2 * nrows;
-    const int rc = run_dq(s, q, k, v, nullptr, false, theria::kRowFrozen, dout, lse, rt_delta, nullptr, st,
-                          "theria_sdpa_bwd_bwd (row term)");
+    float* lse_c = row_ws + 3 * nrows;
+    const int rc = run_dq(s, q, k, v, nullptr, false, theria::kRowNormalized, dout, lse, rt_delta, nullptr, st,
+                          "theria_sdpa_bwd_bwd (row term)", lse_c);
     if (rc != THERIA_OK) return rc;
     bp.delta = rt_delta;
+    bp.lse = lse_c;
   }
   bp.out_gq = mv(out_gq);
   bp.out_gk = mv(out_gk);

@@ -127,9 +127,9 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DQ_MINW : 1)) void dq_kernel(const
   bool exact_row_term = p.row_term >= kRowFrozen;
   if (sizeof(T) == 2 && p.row_term == kRowFromO) exact_row_term = __syncthreads_or(__any(peaked));
   if (exact_row_term) {
-    float a_part[QT], l_part[QT];
+    float a_part[QT], l_part[QT], p_mx[QT];
 #pragma unroll
-    for (int j = 0; j < QT; ++j) a_part[j] = l_part[j] = 0.f;
+    for (int j = 0; j < QT; ++j) a_part[j] = l_part[j] = p_mx[j] = 0.f;
     TileStage<T, BN, DP, NT> pK, pV;
     for (int kt = 0; kt < nkt; ++kt) {
       const int k0 = kt * BN;
@@ -161,15 +161,22 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DQ_MINW : 1)) void dq_kernel(const
           const float pv = k0 + acc_row(r, g) < lim ? fast_exp2(fmaf(sc[j][r], c2, -lse2[j])) : 0.f;
           a_part[j] = fmaf(pv, dpp[j][r], a_part[j]);
           l_part[j] += pv;
+          p_mx[j] = fmaxf(p_mx[j], pv);
         }
       }
     }
 #pragma unroll
     for (int j = 0; j < QT; ++j) {
-      const float a = pair_sum(a_part[j]), l = pair_sum(l_part[j]);
+      const float a = pair_sum(a_part[j]), l = pair_sum(l_part[j]), pm = pair_max(p_mx[j]);
       del[j] = p.row_term == kRowFrozen ? a : (l > 0.f ? a / l : 0.f);
       const int myq = q0w + 32 * j + li;
-      if (myq < s.T && g == 0) p.delta[rowbase + myq] = del[j];
+      if (myq < s.T && g == 0) {
+        p.delta[rowbase + myq] = del[j];
+        if (p.lse_out) {  // flagged from the exact largest probability
+          const float lin = p.lse[rowbase + myq];
+          p.lse_out[rowbase + myq] = l > 0.f ? lse_with_flag(lin + __builtin_log2f(l) * kLn2, pm > kPeakedFrac * l) : lin;
+        }
+      }
     }
   }
   if (!p.dq.p) return;  // only the row term was requested

@@ -681,7 +681,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
     // out while dS = P o (dP - delta) is a small difference there.
     if (PEAKED && rt != kRowGiven) {
       // a = sum_j P_ij dP_ij and l = sum_j P_ij over every key of the row (one more pass over the key tiles)
-      float a_part = 0.f, l_part = 0.f;
+      float a_part = 0.f, l_part = 0.f, p_mx = 0.f;
       if (nkt > 0) {
         dma.template issue_clamped<NSLAB>(krsrc, krs, 0, s.M, sK0);
         dma.template issue_clamped<NSLAB>(vrsrc, vrs, 0, s.M, sV0);
@@ -712,13 +712,18 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
             const float pv = fast_exp2(fmaf(sc[r], c2, -lse2));
             a_part = fmaf(pv, dpp[r], a_part);
             l_part += pv;
+            p_mx = fmaxf(p_mx, pv);
           }
         }
       }
       __syncthreads();  // every wave is done with the tiles before the main loop refills the buffers
-      const float a = pair_sum(a_part), l = pair_sum(l_part);
+      const float a = pair_sum(a_part), l = pair_sum(l_part), pm = pair_max(p_mx);
       del = rt == kRowFrozen ? a : (l > 0.f ? a / l : 0.f);
-      if (qvalid && g == 0) p.delta[rowbase + myq] = del;
+      if (qvalid && g == 0) {
+        p.delta[rowbase + myq] = del;
+        if (p.lse_out)  // flagged from the exact largest probability
+          p.lse_out[rowbase + myq] = l > 0.f ? lse_with_flag(lse + __builtin_log2f(l) * kLn2, pm > kPeakedFrac * l) : lse;
+      }
     }
     if (!p.dq.p) return;  // only the row term was requested
     if (PEAKED && split) {

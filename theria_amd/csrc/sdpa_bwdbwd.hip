@@ -17,9 +17,13 @@
 //
 // rows kernel: lane per query (transposed score tiles, as in the forward). One pass over key tiles (64
 //   keys as two 32-key subtiles for 16-bit inputs at head dim <= 64, else 32) accumulates the four D-wide products of the G_Q expression plus r and t, writes G_Q, r, t.
+//   16-bit workgroups holding a row flagged peaked in lse instead make two passes: r and t first, then
+//   Gbar_S = P o ((Gam - r)(dP - z) + W - t) formed in float32 and, with dS, entered as two 16-bit terms
+//   (hi + lo), so that G_Q = s (Gbar_S K + dS gK) is no longer a small difference of large products.
 // cols kernel: lane per key (as in the backward). One pass over query tiles (64 queries as two 32-query
 //   subtiles for 16-bit inputs at head dim <= 64, else 32) with r, t, z, lse per row staged in LDS
-//   accumulates G_V and G_K in registers.
+//   accumulates G_V and G_K in registers. 16-bit query tiles holding a row flagged peaked enter
+//   Gbar_dP, Gbar_S and dS as two 16-bit terms each (their sums over many queries are small there).
 #include <initializer_list>
 #include <type_traits>
 
@@ -33,7 +37,9 @@ namespace theria {
 // then filled by LDS DMA into two sets of unpadded, XOR-swizzled buffers (sdpa_lds.hpp), one barrier per
 // tile with the next tile's copies in flight; otherwise they pass through registers into padded LDS rows
 // (two barriers per tile).
-template <typename T, int DP, bool CAUSAL, bool DMA>
+// EXACT: the second launch of 16-bit problems, which redoes only the workgroups holding a row flagged peaked in
+// lse in the two-pass form (overwriting G_Q, r, t); apart, the first launch keeps its registers and schedule.
+template <typename T, int DP, bool CAUSAL, bool DMA, bool EXACT>
 __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
@@ -74,6 +80,10 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
   const int myq = q0w + li;
   const bool qvalid = myq < s.T;
   const int64_t row_id = (int64_t)bh * s.T + myq;
+  // 16-bit, second launch: the workgroups holding a row flagged peaked in lse, in the two-pass form (uniform)
+  static_assert(!EXACT || sizeof(T) == 2, "the two-pass form is for 16-bit inputs");
+  const bool two_pass = EXACT && __syncthreads_or(qvalid && lse_peaked(p.lse[row_id]));
+  if (EXACT && !two_pass) return;
 
   F qf[NKC], dof[NKC], gqf[NKC];
 #pragma unroll
@@ -103,6 +113,7 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
   // on rows with few visible keys, where G_Q is a small difference of large terms, the products then carry
   // small centred values instead (one visible key gives G_Q = 0 exactly).
   float t_frag = 0.f, cr = 0.f, ct = 0.f;
+  float rx = 0.f, tx = 0.f;  // exact row terms of the two-pass form
   float c_p = 0.f, c_pg = 0.f, c_pgd = 0.f, c_pd = 0.f, c_pw = 0.f;
 
   int kend = s.M;
@@ -124,8 +135,12 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
   };
 
   // The key tile kt held in (tK, tV, tgK, tgV), as 32-key subtiles.
-  auto compute = [&](auto pre_tag, int kt, const char* tK, const char* tV, const char* tgK, const char* tgV) {
-    constexpr bool PRE = decltype(pre_tag)::value;  // centre pre-pass: sums for c only
+  // PASS: 0 centre pre-pass (sums for c only), 1 the common pass, 2 exact row terms r, t only, 3 the exact
+  // pass (Gbar_S from r, t; 16-bit only).
+  auto compute = [&](auto pass_tag, int kt, const char* tK, const char* tV, const char* tgK,
+                     const char* tgV) __attribute__((always_inline)) {
+    constexpr int PASS = decltype(pass_tag)::value;
+    constexpr bool PRE = PASS == 0;
     const int k0 = kt * BN;
 #pragma unroll
     for (int st = 0; st < NST; ++st) {
@@ -161,6 +176,12 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
           c_pd = fmaf(pv, dpz[r], c_pd);
           c_pgd = fmaf(pv * gam, dpz[r], c_pgd);
           c_pw = fmaf(pv, w[r], c_pw);
+        } else if constexpr (PASS == 2) {
+          r_part = fmaf(pv, gam, r_part);
+          t_part += pe1;
+        } else if constexpr (PASS == 3) {
+          gm[r] = pv * (fmaf(gam - rx, dpz[r], w[r]) - tx);  // Gbar_S
+          dpz[r] = pv * dpz[r];                              // dS
         } else {
           r_part = fmaf(pv, gam, r_part);
           t_part += pe1;
@@ -169,7 +190,27 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
           dpz[r] = pv * dpz[r];  // dS
         }
       }
-      if constexpr (PRE) continue;
+      if constexpr (PRE || PASS == 2) continue;
+      if constexpr (PASS == 3 && sizeof(T) == 2) {
+#pragma unroll
+        for (int cc = 0; cc < NPC; ++cc) {
+          F gh, gl, dh, dl;
+          split_frag<T>(gm, cc, gh, gl);
+          split_frag<T>(dpz, cc, dh, dl);
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) {
+            const F kr = rowsf(tK, 32 * st, cc, dt * 32);
+            x13[dt] = MM::mma(kr, gh, x13[dt]);
+            x13[dt] = MM::mma(kr, gl, x13[dt]);
+            if (has_gk) {
+              const F gkr = rowsf(tgK, 32 * st, cc, dt * 32);
+              yk[dt] = MM::mma(gkr, dh, yk[dt]);
+              yk[dt] = MM::mma(gkr, dl, yk[dt]);
+            }
+          }
+        }
+        continue;
+      }
 #pragma unroll
       for (int cc = 0; cc < NPC; ++cc) {
         const F pf = acc_frag<T>(sc, cc);
@@ -188,8 +229,14 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
     }
   };
 
-  const std::integral_constant<bool, true> pre_pass;
-  const std::integral_constant<bool, false> full_pass;
+  const std::integral_constant<int, 0> pre_pass;
+  const std::integral_constant<int, 1> full_pass;
+  const std::integral_constant<int, 2> rt_pass;
+  const std::integral_constant<int, 3> exact_pass;
+  auto set_exact = [&]() {
+    rx = pair_sum(r_part);
+    tx = pair_sum(t_part);
+  };
   auto set_centre = [&]() {
     const float sp = pair_sum(c_p), spg = pair_sum(c_pg), spd = pair_sum(c_pd), spgd = pair_sum(c_pgd),
                 spw = pair_sum(c_pw);
@@ -222,28 +269,40 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
     };
     // Tile kt from the set c*; the next tile's copies go to the set n* (read in the previous step, which
     // every wave has finished at the barrier).
-    auto step = [&](int kt, const char* cK, const char* cV, const char* cgK, const char* cgV, char* nK, char* nV,
-                    char* ngK, char* ngV) {
+    auto step = [&](auto pass_tag, int kt, const char* cK, const char* cV, const char* cgK, const char* cgV, char* nK,
+                    char* nV, char* ngK, char* ngV) __attribute__((always_inline)) {
       wait_vm_all();
       __syncthreads();
       if (kt + 1 < nkt) issue(kt + 1, nK, nV, ngK, ngV);
-      compute(full_pass, kt, cK, cV, cgK, cgV);
+      compute(pass_tag, kt, cK, cV, cgK, cgV);
       __builtin_amdgcn_sched_barrier(0);  // keep the two unrolled steps apart (register pressure)
+    };
+    // every key tile once, from tile 0 already issued
+    auto sweep = [&](auto pass_tag) __attribute__((always_inline)) {
+      int kt = 0;
+      for (; kt + 1 < nkt; kt += 2) {
+        step(pass_tag, kt, sK0, sV0, sgK0, sgV0, sK1, sV1, sgK1, sgV1);
+        step(pass_tag, kt + 1, sK1, sV1, sgK1, sgV1, sK0, sV0, sgK0, sgV0);
+      }
+      if (kt < nkt) step(pass_tag, kt, sK0, sV0, sgK0, sgV0, sK1, sV1, sgK1, sgV1);
     };
     if (nkt > 0) {
       issue(0, sK0, sV0, sgK0, sgV0);
-      if constexpr (sizeof(T) == 2) {
-        wait_vm_all();
-        __syncthreads();
-        compute(pre_pass, 0, sK0, sV0, sgK0, sgV0);
-        set_centre();
+      if (two_pass) {
+        sweep(rt_pass);
+        set_exact();
+        __syncthreads();  // every wave is done with the last tile's buffers
+        issue(0, sK0, sV0, sgK0, sgV0);
+        sweep(exact_pass);
+      } else {
+        if constexpr (sizeof(T) == 2) {
+          wait_vm_all();
+          __syncthreads();
+          compute(pre_pass, 0, sK0, sV0, sgK0, sgV0);
+          set_centre();
+        }
+        sweep(full_pass);
       }
-      int kt = 0;
-      for (; kt + 1 < nkt; kt += 2) {
-        step(kt, sK0, sV0, sgK0, sgV0, sK1, sV1, sgK1, sgV1);
-        step(kt + 1, sK1, sV1, sgK1, sgV1, sK0, sV0, sgK0, sgV0);
-      }
-      if (kt < nkt) step(kt, sK0, sV0, sgK0, sgV0, sK1, sV1, sgK1, sgV1);
     }
   } else {
     TileStage<T, BN, DP, NT> gsK, gsV, gsgK, gsgV;
@@ -253,26 +312,39 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
       if (has_gk) gsgK.load(GK, p.gk.sr, k0, s.M, s.D, s.vec);
       if (has_gv) gsgV.load(GV, p.gv.sr, k0, s.M, s.D, s.vec);
     };
+    // every key tile once, from tile 0 already prefetched
+    auto sweep = [&](auto pass_tag) __attribute__((always_inline)) {
+      for (int kt = 0; kt < nkt; ++kt) {
+        __syncthreads();
+        gsK.store((T*)sK0, PITCH);
+        gsV.store((T*)sV0, PITCH);
+        if (has_gk) gsgK.store((T*)sgK0, PITCH);
+        if (has_gv) gsgV.store((T*)sgV0, PITCH);
+        __syncthreads();
+        if (kt + 1 < nkt) prefetch((kt + 1) * BN);
+        compute(pass_tag, kt, sK0, sV0, sgK0, sgV0);
+      }
+    };
     if (nkt > 0) prefetch(0);
-    if (sizeof(T) == 2 && nkt > 0) {
-      // centre pre-pass over tile 0 (the loop stages the same registers again)
-      gsK.store((T*)sK0, PITCH);
-      gsV.store((T*)sV0, PITCH);
-      if (has_gk) gsgK.store((T*)sgK0, PITCH);
-      if (has_gv) gsgV.store((T*)sgV0, PITCH);
-      __syncthreads();
-      compute(pre_pass, 0, sK0, sV0, sgK0, sgV0);
-      set_centre();
-    }
-    for (int kt = 0; kt < nkt; ++kt) {
-      __syncthreads();
-      gsK.store((T*)sK0, PITCH);
-      gsV.store((T*)sV0, PITCH);
-      if (has_gk) gsgK.store((T*)sgK0, PITCH);
-      if (has_gv) gsgV.store((T*)sgV0, PITCH);
-      __syncthreads();
-      if (kt + 1 < nkt) prefetch((kt + 1) * BN);
-      compute(full_pass, kt, sK0, sV0, sgK0, sgV0);
+    if (two_pass) {
+      if (nkt > 0) {
+        sweep(rt_pass);
+        set_exact();
+        prefetch(0);
+        sweep(exact_pass);
+      }
+    } else {
+      if (sizeof(T) == 2 && nkt > 0) {
+        // centre pre-pass over tile 0 (the loop stages the same registers again)
+        gsK.store((T*)sK0, PITCH);
+        gsV.store((T*)sV0, PITCH);
+        if (has_gk) gsgK.store((T*)sgK0, PITCH);
+        if (has_gv) gsgV.store((T*)sgV0, PITCH);
+        __syncthreads();
+        compute(pre_pass, 0, sK0, sV0, sgK0, sgV0);
+        set_centre();
+      }
+      sweep(full_pass);
     }
   }
 
@@ -317,15 +389,16 @@ __global__ __launch_bounds__(256) void bwdbwd_cols_kernel(const BwdBwdParams p) 
   constexpr int NDT = DP / 32, NKC = DP / KC, NPC = 32 / KC, NSQ = BM / 32;
   constexpr int TB = DMA ? BM * DP * 2 : BM * PITCH * (int)sizeof(T);  // bytes per tile
   constexpr int TB2 = DMA ? TB : 16;                                    // second set (DMA only)
-  constexpr int RB2 = DMA ? 4 * BM : 4;
+  constexpr int RB = 4 * BM + 4;  // + whether the tile holds a row flagged peaked
+  constexpr int RB2 = DMA ? RB : 4;
   __shared__ __attribute__((aligned(1024))) char sQ0[TB];
   __shared__ __attribute__((aligned(1024))) char sdO0[TB];
   __shared__ __attribute__((aligned(1024))) char sgQ0[TB];
   __shared__ __attribute__((aligned(1024))) char sQ1[TB2];
   __shared__ __attribute__((aligned(1024))) char sdO1[TB2];
   __shared__ __attribute__((aligned(1024))) char sgQ1[TB2];
-  // row terms [lse * log2(e) | delta | r | t] of a tile
-  __shared__ __attribute__((aligned(16))) float sRow0[4 * BM];
+  // row terms [lse * log2(e) | delta | r | t | peaked] of a tile
+  __shared__ __attribute__((aligned(16))) float sRow0[RB];
   __shared__ __attribute__((aligned(16))) float sRow1[RB2];
 
   const Shape& s = p.s;
@@ -400,11 +473,16 @@ __global__ __launch_bounds__(256) void bwdbwd_cols_kernel(const BwdBwdParams p) 
       sr[BM + tid] = r_z;
       sr[2 * BM + tid] = r_r;
       sr[3 * BM + tid] = r_t;
+      const bool pk = __any(lse_peaked(r_lse));  // the tile's rows are the lanes of wave 0
+      if (tid == 0) sr[4 * BM] = pk ? 1.f : 0.f;
     }
   };
 
-  // The query tile it held in (tQ, tO, tgQ) with its row terms in sr, as 32-query subtiles.
-  auto compute = [&](int it, const char* tQ, const char* tO, const char* tgQ, const float* sr) {
+  // The query tile it held in (tQ, tO, tgQ) with its row terms in sr, as 32-query subtiles. SPLIT: Gbar_dP,
+  // Gbar_S and dS enter the products as two 16-bit terms each.
+  auto tile = [&](auto split_tag, int it, const char* tQ, const char* tO, const char* tgQ,
+                  const float* sr) __attribute__((always_inline)) {
+    constexpr bool SPLIT = decltype(split_tag)::value;
     const int q0 = qbeg + it * BM;
     if (CAUSAL && kw0 > q0 + BM - 1) return;
 #pragma unroll
@@ -449,19 +527,53 @@ __global__ __launch_bounds__(256) void bwdbwd_cols_kernel(const BwdBwdParams p) 
         gs[r] = pv * e1 - r4[qd][e] * ds - t4[qd][e] * pv;
         dpz[r] = ds;
       }
+      if constexpr (SPLIT && sizeof(T) == 2) {
 #pragma unroll
-      for (int cc = 0; cc < NPC; ++cc) {
-        const F gdpf = acc_frag<T>(gdp, cc);
-        const F gsf = acc_frag<T>(gs, cc);
-        const F dsf = acc_frag<T>(dpz, cc);
+        for (int cc = 0; cc < NPC; ++cc) {
+          F gdph, gdpl, gsh, gsl, dsh, dsl;
+          split_frag<T>(gdp, cc, gdph, gdpl);
+          split_frag<T>(gs, cc, gsh, gsl);
+          split_frag<T>(dpz, cc, dsh, dsl);
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-          accV[dt] = MM::mma(gdpf, rowsf(tO, 32 * sq, cc, dt * 32), accV[dt]);
-          accK[dt] = MM::mma(gsf, rowsf(tQ, 32 * sq, cc, dt * 32), accK[dt]);
-          if (has_gq) accK[dt] = MM::mma(dsf, rowsf(tgQ, 32 * sq, cc, dt * 32), accK[dt]);
+          for (int dt = 0; dt < NDT; ++dt) {
+            const F ro = rowsf(tO, 32 * sq, cc, dt * 32);
+            accV[dt] = MM::mma(gdph, ro, accV[dt]);
+            accV[dt] = MM::mma(gdpl, ro, accV[dt]);
+            const F rq = rowsf(tQ, 32 * sq, cc, dt * 32);
+            accK[dt] = MM::mma(gsh, rq, accK[dt]);
+            accK[dt] = MM::mma(gsl, rq, accK[dt]);
+            if (has_gq) {
+              const F rg = rowsf(tgQ, 32 * sq, cc, dt * 32);
+              accK[dt] = MM::mma(dsh, rg, accK[dt]);
+              accK[dt] = MM::mma(dsl, rg, accK[dt]);
+            }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int cc = 0; cc < NPC; ++cc) {
+          const F gdpf = acc_frag<T>(gdp, cc);
+          const F gsf = acc_frag<T>(gs, cc);
+          const F dsf = acc_frag<T>(dpz, cc);
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) {
+            accV[dt] = MM::mma(gdpf, rowsf(tO, 32 * sq, cc, dt * 32), accV[dt]);
+            accK[dt] = MM::mma(gsf, rowsf(tQ, 32 * sq, cc, dt * 32), accK[dt]);
+            if (has_gq) accK[dt] = MM::mma(dsf, rowsf(tgQ, 32 * sq, cc, dt * 32), accK[dt]);
+          }
         }
       }
     }
+  };
+  const std::integral_constant<bool, true> with_split;
+  const std::integral_constant<bool, false> no_split;
+  auto compute = [&](int it, const char* tQ, const char* tO, const char* tgQ,
+                     const float* sr) __attribute__((always_inline)) {
+    // uniform: every thread reads the same flag
+    if (sizeof(T) == 2 && __builtin_amdgcn_readfirstlane(__float_as_uint(sr[4 * BM])) != 0u)
+      tile(with_split, it, tQ, tO, tgQ, sr);
+    else
+      tile(no_split, it, tQ, tO, tgQ, sr);
   };
 
   if constexpr (DMA) {
@@ -565,11 +677,14 @@ struct RowsLauncher {
     if (nblk == 0) return hipSuccess;
     if constexpr (sizeof(T) == 2 && (DP == 64 || DP == 128)) {
       if (dma_tiles_ok<T, DP>(p, p.s.M, {&p.k, &p.v, &p.gk, &p.gv})) {
-        hipLaunchKernelGGL((bwdbwd_rows_kernel<T, DP, CAUSAL, true>), dim3((unsigned)nblk), dim3(256), 0, st, p);
+        hipLaunchKernelGGL((bwdbwd_rows_kernel<T, DP, CAUSAL, true, false>), dim3((unsigned)nblk), dim3(256), 0, st, p);
+        hipLaunchKernelGGL((bwdbwd_rows_kernel<T, DP, CAUSAL, true, true>), dim3((unsigned)nblk), dim3(256), 0, st, p);
         return hipGetLastError();
       }
     }
-    hipLaunchKernelGGL((bwdbwd_rows_kernel<T, DP, CAUSAL, false>), dim3((unsigned)nblk), dim3(256), 0, st, p);
+    hipLaunchKernelGGL((bwdbwd_rows_kernel<T, DP, CAUSAL, false, false>), dim3((unsigned)nblk), dim3(256), 0, st, p);
+    if constexpr (sizeof(T) == 2)
+      hipLaunchKernelGGL((bwdbwd_rows_kernel<T, DP, CAUSAL, false, true>), dim3((unsigned)nblk), dim3(256), 0, st, p);
     return hipGetLastError();
   }
 };

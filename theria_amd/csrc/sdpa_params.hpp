@@ -56,6 +56,9 @@ struct DqParams {
   const float* lse;
   float* delta;
   MutView dq;
+  // optional, with a row-term pass (blocks taking it): lse + ln(sum_j P_ij), the row's exact normaliser for P
+  // rebuilt from lse, flagged peaked from the row's exact largest probability (above 1/4)
+  float* lse_out;
 };
 
 // dK / dV pass of the backward (dv_only: no V, dK not computed).
