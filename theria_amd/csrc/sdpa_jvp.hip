@@ -260,6 +260,205 @@ __global__ __launch_bounds__(256) void jvp_kernel(const JvpParams p) {
   }
 }
 
+// 16-bit inputs at head dim 64 with LDS-DMA tiles: the same JVP with the keys of a query block split between
+// two groups of four waves (eight-wave workgroups), so that a SIMD holds two waves at 256 registers each
+// where jvp_kernel holds one at ~380 (config 4: B H T / 32 = 1024 query waves for 1024 SIMDs; 27.1 -> 23.0 us
+// there, same box). Each group streams its own half of the key tiles (64 keys per tile, 128 KB of LDS in
+// all) through its own double-buffered tiles; both groups meet at the same barrier every step (a group
+// whose half is shorter idles through the last step). The float32 partial sums of group 1 (accumulators,
+// row sums) pass to group 0 through LDS at the end.
+template <typename T, bool CAUSAL, bool HAS_O>
+__global__ __launch_bounds__(512, 2) void jvp_ksplit_kernel(const JvpParams p) {
+  using MM = Mfma<T>;
+  using F = typename MM::frag_t;
+  static_assert(sizeof(T) == 2, "16-bit inputs only");
+  constexpr int DP = 64, NW = 4, BM = 32 * NW, BN = 64, NST = BN / 32;
+  constexpr int NDT = DP / 32, NKC = DP / MM::KC, NPC = 32 / MM::KC;
+  constexpr int TB = BN * DP * 2;  // bytes per tile
+  using Dma = SwzDma<NW, DP>;
+  constexpr int NSLAB = BN / Dma::SLAB_ROWS;
+  static_assert(NSLAB * Dma::SLAB_ROWS == BN, "key tiles must be whole DMA slabs");
+  // [group][set][K, V, tK, tV]; reused for the partial sums after the key loop
+  __shared__ __attribute__((aligned(1024))) char smem[2 * 2 * 4 * TB];
+  static_assert(sizeof(smem) >= 4 * 64 * 34 * 4, "the combine rounds fit in the tile memory");
+
+  const Shape& s = p.s;
+  const int lane = threadIdx.x & 63, li = lane & 31, g = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave >> 2, wig = wave & 3;  // key group, wave in group
+  const int nqb = (s.T + BM - 1) / BM;
+  const int bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int bh = bid / nqb;
+  int qb = bid - bh * nqb;
+  if (CAUSAL) qb = nqb - 1 - qb;
+  const int b = bh / s.H, h = bh - b * s.H;
+  const T* Q = (const T*)p.q.p + b * p.q.sb + h * p.q.sh;
+  const T* K = (const T*)p.k.p + b * p.k.sb + h * p.k.sh;
+  const T* V = (const T*)p.v.p + b * p.v.sb + h * p.v.sh;
+  const bool has_tq = p.tq.p != nullptr, has_tk = p.tk.p != nullptr, has_tv = p.tv.p != nullptr;
+  const T* TQ = has_tq ? (const T*)p.tq.p + b * p.tq.sb + h * p.tq.sh : nullptr;
+  const T* TK = has_tk ? (const T*)p.tk.p + b * p.tk.sb + h * p.tk.sh : nullptr;
+  const T* TV = has_tv ? (const T*)p.tv.p + b * p.tv.sb + h * p.tv.sh : nullptr;
+  const int q0w = qb * BM + wig * 32;
+  const int myq = q0w + li;
+  const bool qvalid = myq < s.T;
+  const int64_t row_id = (int64_t)bh * s.T + myq;
+
+  F qf[NKC], tqf[NKC];
+#pragma unroll
+  for (int c = 0; c < NKC; ++c) {
+    qf[c] = gload_frag<T>(Q, p.q.sr, myq, s.T, c, s.D, s.vec);
+    tqf[c] = has_tq ? gload_frag<T>(TQ, p.tq.sr, myq, s.T, c, s.D, s.vec) : F{};
+  }
+  f32x16_t accA[NDT], accC[NDT], accO[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) {
+    accA[dt] = zero16();
+    accC[dt] = zero16();
+    accO[dt] = zero16();
+  }
+  const float c2 = s.scale * kLog2e;
+  const float lse2 = qvalid ? p.lse[row_id] * kLog2e : THERIA_INF;
+  const float moff = lse2 == -THERIA_INF ? THERIA_INF : lse2;  // a row without visible keys has P = 0
+  float cpart = 0.f, lpart = 0.f;
+
+  int kend = s.M;
+  if (CAUSAL) kend = min(s.M, qb * BM + BM);
+  const int nkt = (kend + BN - 1) / BN;
+  const int half = (nkt + 1) / 2;
+  const int kt0 = grp * half, kt1 = min(nkt, kt0 + half);  // this group's tiles [kt0, kt1)
+
+  // The key tile kt held in (tK, tV, ttK, ttV): as jvp_kernel, 32-key subtiles one after the other.
+  auto compute = [&](int kt, const char* tK, const char* tV, const char* ttK, const char* ttV) {
+#pragma unroll
+    for (int st = 0; st < NST; ++st) {
+      const int k0 = kt * BN + 32 * st;
+      if (CAUSAL && k0 > q0w + 31) continue;
+      f32x16_t sc = zero16(), gm = zero16();
+#pragma unroll
+      for (int c = 0; c < NKC; ++c) {
+        const F kfr = swz_cols<T, DP>(tK, 32 * st + li, c);
+        sc = MM::mma(kfr, qf[c], sc);
+        if (has_tq) gm = MM::mma(kfr, tqf[c], gm);
+        if (has_tk) gm = MM::mma(swz_cols<T, DP>(ttK, 32 * st + li, c), qf[c], gm);
+      }
+      const bool need_mask = (k0 + 32 > s.M) || (CAUSAL && k0 + 31 > q0w);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float pv = fast_exp2(fmaf(sc[r], c2, -moff));
+        if (need_mask) {
+          const int key = k0 + acc_row(r, g);
+          if (key >= s.M || (CAUSAL && key > myq)) pv = 0.f;
+        }
+        sc[r] = pv;
+        lpart += pv;
+        const float pg = pv * gm[r];
+        gm[r] = pg;
+        cpart += pg;
+      }
+#pragma unroll
+      for (int cc = 0; cc < NPC; ++cc) {
+        F pf, pf_lo, pgf, pgf_lo;
+        split_frag<T>(sc, cc, pf, pf_lo);
+        split_frag<T>(gm, cc, pgf, pgf_lo);
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+          const F vfr = swz_rows<T, DP>(tV, 32 * st, cc, dt * 32);
+          accA[dt] = MM::mma(vfr, pgf, accA[dt]);
+          accA[dt] = MM::mma(vfr, pgf_lo, accA[dt]);
+          accO[dt] = MM::mma(vfr, pf, accO[dt]);
+          accO[dt] = MM::mma(vfr, pf_lo, accO[dt]);
+          if (has_tv) accC[dt] = MM::mma(swz_rows<T, DP>(ttV, 32 * st, cc, dt * 32), pf, accC[dt]);
+        }
+      }
+    }
+  };
+
+  const Dma dma(wig, lane);
+  // Byte offsets fit in 32 bits: the host only selects this path when each (batch, head) slab of K, V, tK
+  // and tV spans less than 2^31 bytes.
+  const uint32_t krs = (uint32_t)p.k.sr * 2, vrs = (uint32_t)p.v.sr * 2;
+  const uint32_t tkrs = has_tk ? (uint32_t)p.tk.sr * 2 : 0u, tvrs = has_tv ? (uint32_t)p.tv.sr * 2 : 0u;
+  const rsrc_t krsrc = make_rsrc(K, (uint32_t)slab_span(s.M, krs, 2 * DP)),
+               vrsrc = make_rsrc(V, (uint32_t)slab_span(s.M, vrs, 2 * DP));
+  const rsrc_t tkrsrc = make_rsrc(has_tk ? (const void*)TK : (const void*)K, (uint32_t)slab_span(s.M, tkrs, 2 * DP));
+  const rsrc_t tvrsrc = make_rsrc(has_tv ? (const void*)TV : (const void*)V, (uint32_t)slab_span(s.M, tvrs, 2 * DP));
+  auto tile = [&](int set, int a) { return smem + ((grp * 2 + set) * 4 + a) * TB; };  // a: K, V, tK, tV
+  auto issue = [&](int kt, int set) {
+    const int k0 = kt * BN;
+    dma.template issue_clamped<NSLAB>(krsrc, krs, k0, s.M, tile(set, 0));
+    dma.template issue_clamped<NSLAB>(vrsrc, vrs, k0, s.M, tile(set, 1));
+    if (has_tk) dma.template issue_clamped<NSLAB>(tkrsrc, tkrs, k0, s.M, tile(set, 2));
+    if (has_tv) dma.template issue_clamped<NSLAB>(tvrsrc, tvrs, k0, s.M, tile(set, 3));
+  };
+  // Step i: tile kt0 + i of this group (if it has one) from set i & 1; the next one's copies go to the other
+  // set, read in step i - 1, which every wave has finished at the barrier.
+  if (kt0 < kt1) issue(kt0, 0);
+  for (int i = 0; i < half; ++i) {
+    const int kt = kt0 + i;
+    wait_vm_all();
+    __syncthreads();
+    if (kt + 1 < kt1) issue(kt + 1, (i + 1) & 1);
+    if (kt < kt1) compute(kt, tile(i & 1, 0), tile(i & 1, 1), tile(i & 1, 2), tile(i & 1, 3));
+  }
+
+  // Group 1's partial sums to group 0, 32 floats per lane per round (element e of lane l of wave w at
+  // e * 256 + w * 64 + l: consecutive lanes, consecutive words).
+  float* buf = reinterpret_cast<float*>(smem);
+  auto pass_over = [&](f32x16_t (&acc)[NDT]) {
+    __syncthreads();  // the previous readers (or the last tile's) are done
+    if (grp == 1) {
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) buf[(dt * 16 + r) * 256 + wig * 64 + lane] = acc[dt][r];
+    }
+    __syncthreads();
+    if (grp == 0) {
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[dt][r] += buf[(dt * 16 + r) * 256 + wig * 64 + lane];
+    }
+  };
+  pass_over(accA);
+  pass_over(accO);
+  if (has_tv) pass_over(accC);
+  __syncthreads();
+  if (grp == 1) {
+    buf[wig * 64 + lane] = lpart;
+    buf[256 + wig * 64 + lane] = cpart;
+  }
+  __syncthreads();
+  if (grp == 1) return;
+  lpart += buf[wig * 64 + lane];
+  cpart += buf[256 + wig * 64 + lane];
+
+  // Epilogue as jvp_kernel's (O rebuilt from the same P; normalize: P divided by its own row sum).
+  float inv = 1.f;
+  if (p.normalize) {
+    const float L = pair_sum(lpart);
+    inv = L > 0.f ? 1.f / L : 0.f;
+  }
+  const float cval = pair_sum(cpart) * s.scale * inv;
+  if (qvalid) {
+    T* TO = (T*)p.tout.p + b * p.tout.sb + h * p.tout.sh;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const int d0 = dt * 32 + 8 * qd + 4 * g;
+        float r4[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float ov = accO[dt][4 * qd + e] * inv;
+          r4[e] = inv * (s.scale * accA[dt][4 * qd + e] + accC[dt][4 * qd + e]) - cval * ov;
+        }
+        store4<T>(TO, p.tout.sr, myq, d0, s.D, r4[0], r4[1], r4[2], r4[3], s.vec);
+      }
+  }
+}
+
 template <bool HAS_O>
 struct JvpLauncher {
   template <typename T, int DP, bool CAUSAL>
@@ -273,7 +472,10 @@ struct JvpLauncher {
       for (const View* v : {&p.k, &p.v, &p.tk, &p.tv})
         if (v->p && !slab_fits_dma(p.s.M, v->sr, p.s.D)) ok = false;
       if (ok) {
-        hipLaunchKernelGGL((jvp_kernel<T, DP, CAUSAL, HAS_O, true>), dim3((unsigned)nblk), dim3(256), 0, st, p);
+        if constexpr (DP == 64)
+          hipLaunchKernelGGL((jvp_ksplit_kernel<T, CAUSAL, HAS_O>), dim3((unsigned)nblk), dim3(512), 0, st, p);
+        else
+          hipLaunchKernelGGL((jvp_kernel<T, DP, CAUSAL, HAS_O, true>), dim3((unsigned)nblk), dim3(256), 0, st, p);
         return hipGetLastError();
       }
     }
