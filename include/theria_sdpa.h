@@ -152,7 +152,8 @@ int theria_sdpa_jvp(const theria_sdpa_problem_t* p, const theria_tensor_t* q, co
  * with cotangents (gq, gk, gv) of (dQ, dK, dV). Outputs out_gq, out_gk, out_gv, out_gdout.
  * The reference has no kernel for this: its HVP is a finite difference of the VJP
  * (theria/attention/hvp_utils.py:30-49) or autograd-in-backward (theria/autograd/sdpa_custom_function.py:32-53).
- * delta is the row term written by theria_sdpa_bwd. Any cotangent may have data == NULL (zero).
+ * delta is the row term written by theria_sdpa_bwd (float32 inputs; 16-bit inputs do not read it, and it may
+ * be NULL there). Any cotangent may have data == NULL (zero).
  * For 16-bit inputs a pass over the keys recomputes, into the workspace, the row normaliser
  * lse + ln(sum_j P_ij) (a 16-bit forward's lse comes from rounded probabilities, so P rebuilt from it sums to
  * one only within ~2^-9) and the row term sum_j P_ij dP_ij / sum_j P_ij in float32 (delta from the 16-bit O

@@ -292,6 +292,7 @@ def jvp(q, k, v, o, lse, tq, tk, tv, scale: float, causal: bool, normalize: bool
 
 def bwd_bwd(q, k, v, o, do, lse, delta, gq, gk, gv, scale: float, causal: bool, noalloc: bool = False):
     """(G_Q, G_K, G_V, G_dO): VJP of the backward map with cotangents (gq, gk, gv) (None = zero).
+    delta (the backward's row term) may be None for 16-bit inputs, which recompute it.
 
     noalloc: run theria_sdpa_bwd_bwd_noalloc, whose row workspace is the library's static device array
     (4 * B * H * T up to 4 * 2^20), instead of a workspace allocated here."""
@@ -306,7 +307,11 @@ def bwd_bwd(q, k, v, o, do, lse, delta, gq, gk, gv, scale: float, causal: bool, 
     if o is not None:
         o = _rowmajor(o) if o.dtype == q.dtype else None
     lse = lse.contiguous()
-    delta = delta.contiguous()
+    if delta is None:
+        if q.dtype == torch.float32:
+            raise AssertionError("bwd_bwd: delta is required for float32 inputs")
+    else:
+        delta = delta.contiguous()
     dev = q.device
     out_q = torch.empty((B, H, T, D), dtype=q.dtype, device=dev)
     out_k = torch.empty((B, H, M, D), dtype=q.dtype, device=dev)

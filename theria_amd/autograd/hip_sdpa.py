@@ -181,17 +181,19 @@ def hip_sdpa_hvp(q, k, v, vq, vk, vv, *, weight=None, target=None, causal: bool 
     with torch.no_grad():
         o, lse, _, _ = _ops.fwd(q, k, v, float(scale), bool(causal))
         if target is not None:
-            dout = (o.float() - target.float()).to(o.dtype)
+            # the float32 difference rounded once to o's dtype (one kernel when the dtypes agree)
+            dout = o - target if target.dtype == o.dtype else (o.float() - target.float()).to(o.dtype)
         elif weight is not None:
             dout = weight.to(o.dtype)
         else:
             dout = torch.ones_like(o)
-        delta = (dout.float() * o.float()).sum(-1)
+        # 16-bit inputs: the double backward forms its own row term
+        delta = (dout.float() * o.float()).sum(-1) if o.dtype == torch.float32 else None
         hq, hk, hv, g_do = _ops.bwd_bwd(q, k, v, o, dout, lse, delta, vq, vk, vv, float(scale), bool(causal))
         if target is None:
             return hq, hk, hv
         jq, jk, jv, _ = _ops.bwd(q, k, v, o, lse, g_do.to(o.dtype), float(scale), bool(causal))
-        return hq + jq, hk + jk, hv + jv
+        return hq.add_(jq), hk.add_(jk), hv.add_(jv)
 
 
 __all__ = ["SDPAOp", "SDPABackwardOp", "hip_sdpa", "hip_sdpa_with_lse", "hip_sdpa_hvp"]

@@ -401,7 +401,8 @@ static int run_bwd_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q,
   c.kview(out_gv, "out_gv", true);
   c.qview(out_gdout, "out_gdout", true);
   c.need(lse != nullptr || !c.q_rows, "lse is required");
-  c.need(delta != nullptr || !c.q_rows, "delta is required");
+  // 16-bit inputs recompute the row term (below) and do not read delta
+  c.need(delta != nullptr || !c.q_rows || s.dtype != THERIA_DTYPE_F32, "delta is required (float32 inputs)");
   c.need(noalloc || row_ws != nullptr || !c.q_rows, "row_ws is required");
   if (!c.err.empty()) return fail(THERIA_ERR_CONTRACT, c.err);
   s.vec = c.vec;
