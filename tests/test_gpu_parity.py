@@ -265,6 +265,30 @@ def test_double_backward_single_visible_key_row(dt, hip_device):
     assert row0 <= 1e-3, f"G_Q of the single-key row: {row0}"
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_double_backward_16bit_ignores_delta(dt, hip_device):
+    """16-bit inputs: the double backward forms its own row term and row normaliser (a pass over the keys),
+    so the delta argument is not read: None, the backward's delta and a wrong delta give the same bits."""
+    B, H, T, M, D = 1, 2, 200, 180, 64
+    q, _ = make((B, H, T, D), dt, hip_device, 31)
+    k, _ = make((B, H, M, D), dt, hip_device, 32)
+    v, _ = make((B, H, M, D), dt, hip_device, 33)
+    do, _ = make((B, H, T, D), dt, hip_device, 34)
+    tq, tk, tv = (make(t.shape, dt, hip_device, 35 + i)[0] for i, t in enumerate((q, k, v)))
+    s = 1 / math.sqrt(D)
+    print(f"[16-bit bwd_bwd without delta] {dt}", flush=True)
+    o, lse, _, _ = _ops.fwd(q, k, v, s, False)
+    delta = _ops.bwd(q, k, v, o, lse, do, s, False)[3]
+    ref = _ops.bwd_bwd(q, k, v, o, do, lse, delta, tq, tk, tv, s, False)
+    for d in (None, delta + 5.0):
+        got = _ops.bwd_bwd(q, k, v, o, do, lse, d, tq, tk, tv, s, False)
+        for name, a, b in zip(("G_Q", "G_K", "G_V", "G_dO"), got, ref):
+            assert torch.equal(a, b), f"{name} depends on delta ({dt})"
+    with pytest.raises(AssertionError, match="delta"):
+        qf, kf, vf = q.float(), k.float(), v.float()
+        _ops.bwd_bwd(qf, kf, vf, o.float(), do.float(), lse, None, tq.float(), None, None, s, False)
+
+
 # bfloat16 causal cases whose G_Q on the first rows (two to ten visible keys) missed the bar by up to 0.044
 # while the rows kernel formed G_Q from uncentred products; (case, seed) as a random sweep drew them.
 CENTRED_GQ_CASES = [
