@@ -17,9 +17,10 @@
 //
 // rows kernel: lane per query (transposed score tiles, as in the forward). One pass over key tiles (64
 //   keys as two 32-key subtiles for 16-bit inputs at head dim <= 64, else 32) accumulates the four D-wide products of the G_Q expression plus r and t, writes G_Q, r, t.
-//   16-bit workgroups holding a row flagged peaked in lse instead make two passes: r and t first, then
-//   Gbar_S = P o ((Gam - r)(dP - z) + W - t) formed in float32 and, with dS, entered as two 16-bit terms
-//   (hi + lo), so that G_Q = s (Gbar_S K + dS gK) is no longer a small difference of large products.
+//   16-bit workgroups holding a row flagged peaked in lse are redone by a second launch: with the exact
+//   r and t the first launch wrote, Gbar_S = P o ((Gam - r)(dP - z) + W - t) is formed in float32 and, with
+//   dS, entered as two 16-bit terms (hi + lo), so that G_Q = s (Gbar_S K + dS gK) is no longer a small
+//   difference of large products.
 // cols kernel: lane per key (as in the backward). One pass over query tiles (64 queries as two 32-query
 //   subtiles for 16-bit inputs at head dim <= 64, else 32) with r, t, z, lse per row staged in LDS
 //   accumulates G_V and G_K in registers. 16-bit query tiles holding a row flagged peaked enter
@@ -38,7 +39,8 @@ namespace theria {
 // tile with the next tile's copies in flight; otherwise they pass through registers into padded LDS rows
 // (two barriers per tile).
 // EXACT: the second launch of 16-bit problems, which redoes only the workgroups holding a row flagged peaked in
-// lse in the two-pass form (overwriting G_Q, r, t); apart, the first launch keeps its registers and schedule.
+// lse in the exact form (overwriting G_Q; r and t are the first launch's); apart, the first launch keeps its
+// registers and schedule.
 template <typename T, int DP, bool CAUSAL, bool DMA, bool EXACT>
 __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) {
   using MM = Mfma<T>;
@@ -80,10 +82,10 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
   const int myq = q0w + li;
   const bool qvalid = myq < s.T;
   const int64_t row_id = (int64_t)bh * s.T + myq;
-  // 16-bit, second launch: the workgroups holding a row flagged peaked in lse, in the two-pass form (uniform)
-  static_assert(!EXACT || sizeof(T) == 2, "the two-pass form is for 16-bit inputs");
-  const bool two_pass = EXACT && __syncthreads_or(qvalid && lse_peaked(p.lse[row_id]));
-  if (EXACT && !two_pass) return;
+  // 16-bit, second launch: the workgroups holding a row flagged peaked in lse, in the exact form (uniform)
+  static_assert(!EXACT || sizeof(T) == 2, "the exact form is for 16-bit inputs");
+  const bool exact = EXACT && __syncthreads_or(qvalid && lse_peaked(p.lse[row_id]));
+  if (EXACT && !exact) return;
 
   F qf[NKC], dof[NKC], gqf[NKC];
 #pragma unroll
@@ -113,7 +115,7 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
   // on rows with few visible keys, where G_Q is a small difference of large terms, the products then carry
   // small centred values instead (one visible key gives G_Q = 0 exactly).
   float t_frag = 0.f, cr = 0.f, ct = 0.f;
-  float rx = 0.f, tx = 0.f;  // exact row terms of the two-pass form
+  float rx = 0.f, tx = 0.f;  // exact row terms for the second launch
   float c_p = 0.f, c_pg = 0.f, c_pgd = 0.f, c_pd = 0.f, c_pw = 0.f;
 
   int kend = s.M;
@@ -135,8 +137,8 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
   };
 
   // The key tile kt held in (tK, tV, tgK, tgV), as 32-key subtiles.
-  // PASS: 0 centre pre-pass (sums for c only), 1 the common pass, 2 exact row terms r, t only, 3 the exact
-  // pass (Gbar_S from r, t; 16-bit only).
+  // PASS: 0 centre pre-pass (sums for c only), 1 the common pass, 3 the exact pass (Gbar_S from the row
+  // terms r, t of the first launch; 16-bit only).
   auto compute = [&](auto pass_tag, int kt, const char* tK, const char* tV, const char* tgK,
                      const char* tgV) __attribute__((always_inline)) {
     constexpr int PASS = decltype(pass_tag)::value;
@@ -176,9 +178,6 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
           c_pd = fmaf(pv, dpz[r], c_pd);
           c_pgd = fmaf(pv * gam, dpz[r], c_pgd);
           c_pw = fmaf(pv, w[r], c_pw);
-        } else if constexpr (PASS == 2) {
-          r_part = fmaf(pv, gam, r_part);
-          t_part += pe1;
         } else if constexpr (PASS == 3) {
           gm[r] = pv * (fmaf(gam - rx, dpz[r], w[r]) - tx);  // Gbar_S
           dpz[r] = pv * dpz[r];                              // dS
@@ -190,7 +189,7 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
           dpz[r] = pv * dpz[r];  // dS
         }
       }
-      if constexpr (PRE || PASS == 2) continue;
+      if constexpr (PRE) continue;
       if constexpr (PASS == 3 && sizeof(T) == 2) {
 #pragma unroll
         for (int cc = 0; cc < NPC; ++cc) {
@@ -231,12 +230,11 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
 
   const std::integral_constant<int, 0> pre_pass;
   const std::integral_constant<int, 1> full_pass;
-  const std::integral_constant<int, 2> rt_pass;
   const std::integral_constant<int, 3> exact_pass;
-  auto set_exact = [&]() {
-    rx = pair_sum(r_part);
-    tx = pair_sum(t_part);
-  };
+  if (exact) {  // the first launch's exact float32 row terms (same stream, so already written)
+    rx = qvalid ? p.r_row[row_id] : 0.f;
+    tx = qvalid ? p.t_row[row_id] : 0.f;
+  }
   auto set_centre = [&]() {
     const float sp = pair_sum(c_p), spg = pair_sum(c_pg), spd = pair_sum(c_pd), spgd = pair_sum(c_pgd),
                 spw = pair_sum(c_pw);
@@ -288,11 +286,7 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
     };
     if (nkt > 0) {
       issue(0, sK0, sV0, sgK0, sgV0);
-      if (two_pass) {
-        sweep(rt_pass);
-        set_exact();
-        __syncthreads();  // every wave is done with the last tile's buffers
-        issue(0, sK0, sV0, sgK0, sgV0);
+      if (exact) {
         sweep(exact_pass);
       } else {
         if constexpr (sizeof(T) == 2) {
@@ -326,13 +320,8 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
       }
     };
     if (nkt > 0) prefetch(0);
-    if (two_pass) {
-      if (nkt > 0) {
-        sweep(rt_pass);
-        set_exact();
-        prefetch(0);
-        sweep(exact_pass);
-      }
+    if (exact) {
+      if (nkt > 0) sweep(exact_pass);
     } else {
       if (sizeof(T) == 2 && nkt > 0) {
         // centre pre-pass over tile 0 (the loop stages the same registers again)
@@ -368,7 +357,7 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
           store4<T>(OG, p.out_gq.sr, myq, d0, s.D, r4[0], r4[1], r4[2], r4[3], s.vec);
         }
       }
-    if (g == 0) {
+    if (g == 0 && !EXACT) {
       p.r_row[row_id] = rr;
       p.t_row[row_id] = tt;
     }
