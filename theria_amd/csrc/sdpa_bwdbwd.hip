@@ -556,13 +556,43 @@ __global__ __launch_bounds__(256) void bwdbwd_cols_kernel(const BwdBwdParams p) 
   };
   const std::integral_constant<bool, true> with_split;
   const std::integral_constant<bool, false> no_split;
+  bool pk_any = false;  // uniform: a tile holding a peaked row was skipped (16-bit)
   auto compute = [&](int it, const char* tQ, const char* tO, const char* tgQ,
                      const float* sr) __attribute__((always_inline)) {
     // uniform: every thread reads the same flag
-    if (sizeof(T) == 2 && __builtin_amdgcn_readfirstlane(__float_as_uint(sr[4 * BM])) != 0u)
-      tile(with_split, it, tQ, tO, tgQ, sr);
-    else
-      tile(no_split, it, tQ, tO, tgQ, sr);
+    const bool pk = sizeof(T) == 2 && __builtin_amdgcn_readfirstlane(__float_as_uint(sr[4 * BM])) != 0u;
+    pk_any |= pk;  // run after the loop, so the loop's schedule holds only the one-term products
+    if (!pk) tile(no_split, it, tQ, tO, tgQ, sr);
+  };
+  // The tiles holding a peaked row, found 64 at a time from the lse flags and run one after the other with
+  // the split products, from stage(it) (loads tile it into sQ0, sdO0, sgQ0 and its row terms into sRow0).
+  auto peaked_tiles = [&](auto stage) __attribute__((always_inline)) {
+    __shared__ int sPk[64];
+    for (int t0 = 0; t0 < nqt; t0 += 64) {
+      const int nt = min(64, nqt - t0);
+      __syncthreads();  // every thread is done with the previous flags and tile buffers
+      if (tid < 64) sPk[tid] = 0;
+      __syncthreads();
+      constexpr int RPT = (64 * BM + NT - 1) / NT;
+      const int r0 = qbeg + t0 * BM, r1 = min(s.T, qbeg + (t0 + nt) * BM);
+      float lv[RPT];
+#pragma unroll
+      for (int j = 0; j < RPT; ++j) {
+        const int r = r0 + tid + NT * j;
+        lv[j] = r < r1 ? p.lse[rowbase + r] : THERIA_INF;  // rows past the end: no flag
+      }
+#pragma unroll
+      for (int j = 0; j < RPT; ++j)
+        if (lse_peaked(lv[j])) sPk[(tid + NT * j) / BM] = 1;
+      __syncthreads();
+      for (int i = 0; i < nt; ++i) {
+        if (!sPk[i]) continue;  // uniform: every thread reads the same flag
+        stage(t0 + i);
+        __syncthreads();
+        tile(with_split, t0 + i, sQ0, sdO0, sgQ0, sRow0);
+        __syncthreads();  // the tile buffers are free again
+      }
+    }
   };
 
   if constexpr (DMA) {
@@ -608,6 +638,13 @@ __global__ __launch_bounds__(256) void bwdbwd_cols_kernel(const BwdBwdParams p) 
       }
       if (it < nqt) step(it, sQ0, sdO0, sgQ0, sRow0, sQ1, sdO1, sgQ1, sRow1);
     }
+    if (pk_any)
+      peaked_tiles([&](int it) __attribute__((always_inline)) {
+        issue(it, sQ0, sdO0, sgQ0);
+        load_rows(it);
+        wait_vm_all();
+        store_rows(sRow0);
+      });
   } else {
     TileStage<T, BM, DP, NT> gsQ, gsO, gsgQ;
     auto prefetch = [&](int it) {
@@ -628,6 +665,14 @@ __global__ __launch_bounds__(256) void bwdbwd_cols_kernel(const BwdBwdParams p) 
       if (it + 1 < nqt) prefetch(it + 1);
       compute(it, sQ0, sdO0, sgQ0, sRow0);
     }
+    if (pk_any)
+      peaked_tiles([&](int it) __attribute__((always_inline)) {
+        prefetch(it);
+        gsQ.store((T*)sQ0, PITCH);
+        gsO.store((T*)sdO0, PITCH);
+        if (has_gq) gsgQ.store((T*)sgQ0, PITCH);
+        store_rows(sRow0);
+      });
   }
 
   T* OV = (T*)p.out_gv.p + b * p.out_gv.sb + h * p.out_gv.sh;
