@@ -42,7 +42,7 @@ namespace theria {
 // lse in the exact form (overwriting G_Q; r and t are the first launch's); apart, the first launch keeps its
 // registers and schedule.
 template <typename T, int DP, bool CAUSAL, bool DMA, bool EXACT>
-__global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) {
+__device__ __attribute__((always_inline)) inline void rows_block(const BwdBwdParams& p, const int bid) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
   constexpr int KC = MM::KC;
@@ -65,7 +65,6 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
   const Shape& s = p.s;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, li = lane & 31, g = lane >> 5;
   const int nqb = (s.T + BM - 1) / BM;
-  const int bid = xcd_remap(blockIdx.x, gridDim.x);
   const int bh = bid / nqb;
   int qb = bid - bh * nqb;
   if (CAUSAL) qb = nqb - 1 - qb;
@@ -364,10 +363,15 @@ __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) 
   }
 }
 
+template <typename T, int DP, bool CAUSAL, bool DMA, bool EXACT>
+__global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) {
+  rows_block<T, DP, CAUSAL, DMA, EXACT>(p, xcd_remap(blockIdx.x, gridDim.x));
+}
+
 // DMA: as in the rows kernel, for the Q, dO, gQ tiles (the row terms are loaded two tiles ahead by the
 // first BM threads and written beside them one tile ahead).
 template <typename T, int DP, bool CAUSAL, bool DMA>
-__global__ __launch_bounds__(256) void bwdbwd_cols_kernel(const BwdBwdParams p) {
+__device__ __attribute__((always_inline)) inline void cols_block(const BwdBwdParams& p, const int bid) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
   constexpr int KC = MM::KC;
@@ -394,7 +398,6 @@ __global__ __launch_bounds__(256) void bwdbwd_cols_kernel(const BwdBwdParams p) 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6, li = lane & 31, g = lane >> 5;
   const int nkb = (s.M + BN - 1) / BN;
-  const int bid = xcd_remap(blockIdx.x, gridDim.x);
   const int bh = bid / nkb;
   const int kb = bid - bh * nkb;
   const int b = bh / s.H, h = bh - b * s.H;
@@ -693,6 +696,25 @@ __global__ __launch_bounds__(256) void bwdbwd_cols_kernel(const BwdBwdParams p) 
   }
 }
 
+template <typename T, int DP, bool CAUSAL, bool DMA>
+__global__ __launch_bounds__(256) void bwdbwd_cols_kernel(const BwdBwdParams p) {
+  cols_block<T, DP, CAUSAL, DMA>(p, xcd_remap(blockIdx.x, gridDim.x));
+}
+
+// 16-bit: the column blocks, then the rows kernel's second (exact) launch as further workgroups of the same
+// grid. Those read only what the first rows launch wrote (r, t) and write only G_Q, so they are independent of
+// the column blocks; as the grid's last workgroups they run where column blocks have finished, instead of
+// as a launch of their own whose few busy workgroups would leave the GPU idle.
+template <typename T, int DP, bool CAUSAL, bool DMA>
+__global__ __launch_bounds__(256) void bwdbwd_cols_exact_kernel(const BwdBwdParams p) {
+  const int ncols = ((p.s.M + 127) / 128) * p.s.B * p.s.H;
+  const int bid = blockIdx.x;  // uniform
+  if (bid < ncols)
+    cols_block<T, DP, CAUSAL, DMA>(p, xcd_remap(bid, ncols));
+  else
+    rows_block<T, DP, CAUSAL, DMA, true>(p, xcd_remap(bid - ncols, (int)gridDim.x - ncols));
+}
+
 // The LDS-DMA tile path applies: 16-bit inputs, head dim exactly DP (64 or 128), 16-byte-aligned views,
 // and every (batch, head) slab of the streamed tensors (rows x row stride) below 2^31 bytes.
 template <typename T, int DP>
@@ -703,38 +725,69 @@ static bool dma_tiles_ok(const BwdBwdParams& p, int64_t rows, std::initializer_l
   return true;
 }
 
+template <typename T, int DP>
+static bool rows_dma(const BwdBwdParams& p) {
+  return dma_tiles_ok<T, DP>(p, p.s.M, {&p.k, &p.v, &p.gk, &p.gv});
+}
+template <typename T, int DP>
+static bool cols_dma(const BwdBwdParams& p) {
+  return dma_tiles_ok<T, DP>(p, p.s.T, {&p.q, &p.dout, &p.gq});
+}
+// 16-bit: the rows kernel's exact launch rides in the column grid when both take the same tile path.
+template <typename T, int DP>
+static bool exact_in_cols(const BwdBwdParams& p) {
+  return sizeof(T) == 2 && rows_dma<T, DP>(p) == cols_dma<T, DP>(p);
+}
+
 struct RowsLauncher {
   template <typename T, int DP, bool CAUSAL>
   static hipError_t run(const BwdBwdParams& p, hipStream_t st) {
     const int nqb = (p.s.T + 127) / 128;
     const int64_t nblk = (int64_t)nqb * p.s.B * p.s.H;
     if (nblk == 0) return hipSuccess;
+    const bool with_cols = exact_in_cols<T, DP>(p);
     if constexpr (sizeof(T) == 2 && (DP == 64 || DP == 128)) {
-      if (dma_tiles_ok<T, DP>(p, p.s.M, {&p.k, &p.v, &p.gk, &p.gv})) {
+      if (rows_dma<T, DP>(p)) {
         hipLaunchKernelGGL((bwdbwd_rows_kernel<T, DP, CAUSAL, true, false>), dim3((unsigned)nblk), dim3(256), 0, st, p);
-        hipLaunchKernelGGL((bwdbwd_rows_kernel<T, DP, CAUSAL, true, true>), dim3((unsigned)nblk), dim3(256), 0, st, p);
+        if (!with_cols)
+          hipLaunchKernelGGL((bwdbwd_rows_kernel<T, DP, CAUSAL, true, true>), dim3((unsigned)nblk), dim3(256), 0, st, p);
         return hipGetLastError();
       }
     }
     hipLaunchKernelGGL((bwdbwd_rows_kernel<T, DP, CAUSAL, false, false>), dim3((unsigned)nblk), dim3(256), 0, st, p);
     if constexpr (sizeof(T) == 2)
-      hipLaunchKernelGGL((bwdbwd_rows_kernel<T, DP, CAUSAL, false, true>), dim3((unsigned)nblk), dim3(256), 0, st, p);
+      if (!with_cols)
+        hipLaunchKernelGGL((bwdbwd_rows_kernel<T, DP, CAUSAL, false, true>), dim3((unsigned)nblk), dim3(256), 0, st, p);
     return hipGetLastError();
   }
 };
 
+// Runs after RowsLauncher on the same stream (the exact row blocks read the first rows launch's r and t).
 struct ColsLauncher {
   template <typename T, int DP, bool CAUSAL>
   static hipError_t run(const BwdBwdParams& p, hipStream_t st) {
-    const int nkb = (p.s.M + 127) / 128;
-    const int64_t nblk = (int64_t)nkb * p.s.B * p.s.H;
-    if (nblk == 0) return hipSuccess;
-    if constexpr (sizeof(T) == 2 && (DP == 64 || DP == 128)) {
-      if (dma_tiles_ok<T, DP>(p, p.s.T, {&p.q, &p.dout, &p.gq})) {
-        hipLaunchKernelGGL((bwdbwd_cols_kernel<T, DP, CAUSAL, true>), dim3((unsigned)nblk), dim3(256), 0, st, p);
+    const int64_t nblk = (int64_t)((p.s.M + 127) / 128) * p.s.B * p.s.H;
+    const int64_t nrow = (int64_t)((p.s.T + 127) / 128) * p.s.B * p.s.H;
+    const bool dma = (sizeof(T) == 2 && (DP == 64 || DP == 128)) && cols_dma<T, DP>(p);
+    if constexpr (sizeof(T) == 2) {
+      if (exact_in_cols<T, DP>(p)) {
+        if (nblk + nrow == 0) return hipSuccess;
+        const dim3 grid((unsigned)(nblk + nrow));
+        if constexpr (DP == 64 || DP == 128)
+          if (dma) {
+            hipLaunchKernelGGL((bwdbwd_cols_exact_kernel<T, DP, CAUSAL, true>), grid, dim3(256), 0, st, p);
+            return hipGetLastError();
+          }
+        hipLaunchKernelGGL((bwdbwd_cols_exact_kernel<T, DP, CAUSAL, false>), grid, dim3(256), 0, st, p);
         return hipGetLastError();
       }
     }
+    if (nblk == 0) return hipSuccess;
+    if constexpr (sizeof(T) == 2 && (DP == 64 || DP == 128))
+      if (dma) {
+        hipLaunchKernelGGL((bwdbwd_cols_kernel<T, DP, CAUSAL, true>), dim3((unsigned)nblk), dim3(256), 0, st, p);
+        return hipGetLastError();
+      }
     hipLaunchKernelGGL((bwdbwd_cols_kernel<T, DP, CAUSAL, false>), dim3((unsigned)nblk), dim3(256), 0, st, p);
     return hipGetLastError();
   }
