@@ -17,14 +17,15 @@
 //
 // rows kernel: lane per query (transposed score tiles, as in the forward). One pass over key tiles (64
 //   keys as two 32-key subtiles for 16-bit inputs at head dim <= 64, else 32) accumulates the four D-wide products of the G_Q expression plus r and t, writes G_Q, r, t.
-//   16-bit workgroups holding a row flagged peaked in lse are redone by a second launch: with the exact
-//   r and t the first launch wrote, Gbar_S = P o ((Gam - r)(dP - z) + W - t) is formed in float32 and, with
-//   dS, entered as two 16-bit terms (hi + lo), so that G_Q = s (Gbar_S K + dS gK) is no longer a small
-//   difference of large products.
+//   16-bit workgroups holding a row flagged peaked in lse are redone after it (as extra workgroups of the
+//   cols kernel's grid): with the exact r and t the first launch wrote, Gbar_S = P o ((Gam - r)(dP - z) + W - t)
+//   is formed in float32 and, with dS, entered as two 16-bit terms (hi + lo), so that
+//   G_Q = s (Gbar_S K + dS gK) is no longer a small difference of large products.
 // cols kernel: lane per key (as in the backward). One pass over query tiles (64 queries as two 32-query
 //   subtiles for 16-bit inputs at head dim <= 64, else 32) with r, t, z, lse per row staged in LDS
-//   accumulates G_V and G_K in registers. 16-bit query tiles holding a row flagged peaked enter
-//   Gbar_dP, Gbar_S and dS as two 16-bit terms each (their sums over many queries are small there).
+//   accumulates G_V and G_K in registers. 16-bit query tiles holding a row flagged peaked are skipped by
+//   that pass and run after it with Gbar_dP, Gbar_S and dS entered as two 16-bit terms each (their sums over
+//   many queries are small there).
 #include <initializer_list>
 #include <type_traits>
 
@@ -38,11 +39,11 @@ namespace theria {
 // then filled by LDS DMA into two sets of unpadded, XOR-swizzled buffers (sdpa_lds.hpp), one barrier per
 // tile with the next tile's copies in flight; otherwise they pass through registers into padded LDS rows
 // (two barriers per tile).
-// EXACT: the second launch of 16-bit problems, which redoes only the workgroups holding a row flagged peaked in
+// EXACT: the second pass of 16-bit problems, which redoes only the workgroups holding a row flagged peaked in
 // lse in the exact form (overwriting G_Q; r and t are the first launch's); apart, the first launch keeps its
 // registers and schedule.
 template <typename T, int DP, bool CAUSAL, bool DMA, bool EXACT>
-__device__ __attribute__((always_inline)) inline void rows_block(const BwdBwdParams& p, const int bid) {
+__device__ __attribute__((always_inline)) inline void rows_block(const BwdBwdParams& p, const int blk, const int nblk) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
   constexpr int KC = MM::KC;
@@ -65,6 +66,7 @@ __device__ __attribute__((always_inline)) inline void rows_block(const BwdBwdPar
   const Shape& s = p.s;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, li = lane & 31, g = lane >> 5;
   const int nqb = (s.T + BM - 1) / BM;
+  const int bid = xcd_remap(blk, nblk);
   const int bh = bid / nqb;
   int qb = bid - bh * nqb;
   if (CAUSAL) qb = nqb - 1 - qb;
@@ -365,13 +367,13 @@ __device__ __attribute__((always_inline)) inline void rows_block(const BwdBwdPar
 
 template <typename T, int DP, bool CAUSAL, bool DMA, bool EXACT>
 __global__ __launch_bounds__(256) void bwdbwd_rows_kernel(const BwdBwdParams p) {
-  rows_block<T, DP, CAUSAL, DMA, EXACT>(p, xcd_remap(blockIdx.x, gridDim.x));
+  rows_block<T, DP, CAUSAL, DMA, EXACT>(p, blockIdx.x, gridDim.x);
 }
 
 // DMA: as in the rows kernel, for the Q, dO, gQ tiles (the row terms are loaded two tiles ahead by the
 // first BM threads and written beside them one tile ahead).
 template <typename T, int DP, bool CAUSAL, bool DMA>
-__device__ __attribute__((always_inline)) inline void cols_block(const BwdBwdParams& p, const int bid) {
+__device__ __attribute__((always_inline)) inline void cols_block(const BwdBwdParams& p, const int blk, const int nblk) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
   constexpr int KC = MM::KC;
@@ -398,6 +400,7 @@ __device__ __attribute__((always_inline)) inline void cols_block(const BwdBwdPar
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6, li = lane & 31, g = lane >> 5;
   const int nkb = (s.M + BN - 1) / BN;
+  const int bid = xcd_remap(blk, nblk);
   const int bh = bid / nkb;
   const int kb = bid - bh * nkb;
   const int b = bh / s.H, h = bh - b * s.H;
@@ -698,7 +701,7 @@ __device__ __attribute__((always_inline)) inline void cols_block(const BwdBwdPar
 
 template <typename T, int DP, bool CAUSAL, bool DMA>
 __global__ __launch_bounds__(256) void bwdbwd_cols_kernel(const BwdBwdParams p) {
-  cols_block<T, DP, CAUSAL, DMA>(p, xcd_remap(blockIdx.x, gridDim.x));
+  cols_block<T, DP, CAUSAL, DMA>(p, blockIdx.x, gridDim.x);
 }
 
 // 16-bit: the column blocks, then the rows kernel's second (exact) launch as further workgroups of the same
@@ -708,11 +711,21 @@ __global__ __launch_bounds__(256) void bwdbwd_cols_kernel(const BwdBwdParams p) 
 template <typename T, int DP, bool CAUSAL, bool DMA>
 __global__ __launch_bounds__(256) void bwdbwd_cols_exact_kernel(const BwdBwdParams p) {
   const int ncols = ((p.s.M + 127) / 128) * p.s.B * p.s.H;
+  const int nrows = (int)gridDim.x - ncols;
   const int bid = blockIdx.x;  // uniform
-  if (bid < ncols)
-    cols_block<T, DP, CAUSAL, DMA>(p, xcd_remap(bid, ncols));
-  else
-    rows_block<T, DP, CAUSAL, DMA, true>(p, xcd_remap(bid - ncols, (int)gridDim.x - ncols));
+  if constexpr (CAUSAL) {
+    // row blocks first: most exit at once (no flagged row), and the few heavy ones start beside the
+    // column blocks instead of after the longest of them
+    if (bid < nrows)
+      rows_block<T, DP, CAUSAL, DMA, true>(p, bid, nrows);
+    else
+      cols_block<T, DP, CAUSAL, DMA>(p, bid - nrows, ncols);
+  } else {
+    if (bid < ncols)
+      cols_block<T, DP, CAUSAL, DMA>(p, bid, ncols);
+    else
+      rows_block<T, DP, CAUSAL, DMA, true>(p, bid - ncols, nrows);
+  }
 }
 
 // The LDS-DMA tile path applies: 16-bit inputs, head dim exactly DP (64 or 128), 16-byte-aligned views,
