@@ -158,9 +158,9 @@ int theria_sdpa_jvp(const theria_sdpa_problem_t* p, const theria_tensor_t* q, co
  * lse + ln(sum_j P_ij) (a 16-bit forward's lse comes from rounded probabilities, so P rebuilt from it sums to
  * one only within ~2^-9) and the row term sum_j P_ij dP_ij / sum_j P_ij in float32 (delta from the 16-bit O
  * differs from it by the rounding of O); the second-order terms amplify both where they cancel. delta is
- * then not read. Query blocks holding a row flagged peaked in lse are redone by a second row launch that
- * forms G_Q's score-gradient in float32 from the first launch's row terms; those blocks and tiles enter the
- * G_Q, G_K, G_V products as two 16-bit terms.
+ * then not read. Query blocks holding a row flagged peaked in lse are redone by a second row pass (run as
+ * part of the column kernel's grid) that forms G_Q's score-gradient in float32 from the first pass's row
+ * terms; those blocks and tiles enter the G_Q, G_K, G_V products as two 16-bit terms.
  * row_ws is a caller-owned float32 workspace of 4*batch*heads*tq elements.
  */
 int theria_sdpa_bwd_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
