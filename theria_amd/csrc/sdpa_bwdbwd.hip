@@ -704,28 +704,21 @@ __global__ __launch_bounds__(256) void bwdbwd_cols_kernel(const BwdBwdParams p) 
   cols_block<T, DP, CAUSAL, DMA>(p, blockIdx.x, gridDim.x);
 }
 
-// 16-bit: the column blocks, then the rows kernel's second (exact) launch as further workgroups of the same
-// grid. Those read only what the first rows launch wrote (r, t) and write only G_Q, so they are independent of
-// the column blocks; as the grid's last workgroups they run where column blocks have finished, instead of
-// as a launch of their own whose few busy workgroups would leave the GPU idle.
+// 16-bit: the rows kernel's second (exact) launch and the column blocks as one grid. The exact row blocks
+// read only what the first rows launch wrote (r, t) and write only G_Q, so they are independent of the
+// column blocks; in one grid they run beside them, instead of as a launch of their own whose few busy
+// workgroups would leave the GPU idle.
 template <typename T, int DP, bool CAUSAL, bool DMA>
 __global__ __launch_bounds__(256) void bwdbwd_cols_exact_kernel(const BwdBwdParams p) {
   const int ncols = ((p.s.M + 127) / 128) * p.s.B * p.s.H;
   const int nrows = (int)gridDim.x - ncols;
   const int bid = blockIdx.x;  // uniform
-  if constexpr (CAUSAL) {
-    // row blocks first: most exit at once (no flagged row), and the few heavy ones start beside the
-    // column blocks instead of after the longest of them
-    if (bid < nrows)
-      rows_block<T, DP, CAUSAL, DMA, true>(p, bid, nrows);
-    else
-      cols_block<T, DP, CAUSAL, DMA>(p, bid - nrows, ncols);
-  } else {
-    if (bid < ncols)
-      cols_block<T, DP, CAUSAL, DMA>(p, bid, ncols);
-    else
-      rows_block<T, DP, CAUSAL, DMA, true>(p, bid - ncols, nrows);
-  }
+  // Row blocks first: most exit at once (no flagged row), and the few heavy ones (a single peaked row
+  // makes its block sweep every key) start beside the column blocks instead of after all of them.
+  if (bid < nrows)
+    rows_block<T, DP, CAUSAL, DMA, true>(p, bid, nrows);
+  else
+    cols_block<T, DP, CAUSAL, DMA>(p, bid - nrows, ncols);
 }
 
 // The LDS-DMA tile path applies: 16-bit inputs, head dim exactly DP (64 or 128), 16-byte-aligned views,
