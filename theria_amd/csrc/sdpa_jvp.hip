@@ -23,6 +23,7 @@
 // (P o G) V, P tv and (if needed) P V accumulate lane-per-query as V^T (.)^T, with V^T / tv^T
 // fragments from the LDS transpose read. A single pass: c_i is folded in at the end.
 #include <initializer_list>
+#include <type_traits>
 
 #include "dispatch.hpp"
 #include "sdpa_common.hpp"
@@ -318,9 +319,14 @@ __global__ __launch_bounds__(512, 2) void jvp_ksplit_kernel(const JvpParams p) {
     accO[dt] = zero16();
   }
   const float c2 = s.scale * kLog2e;
-  const float lse2 = qvalid ? p.lse[row_id] * kLog2e : THERIA_INF;
+  const float lse_raw = qvalid ? p.lse[row_id] : THERIA_INF;
+  const float lse2 = lse_raw * kLog2e;
   const float moff = lse2 == -THERIA_INF ? THERIA_INF : lse2;  // a row without visible keys has P = 0
   float cpart = 0.f, lpart = 0.f;
+  // The two-term products only in waves holding a row flagged peaked in lse (a dominant probability, which
+  // rows with few visible keys have): there (P o G) V and c o O cancel. Elsewhere the rounding of P o G and
+  // P spreads over many keys and one 16-bit term each suffices (uniform per wave).
+  const bool split = __any(lse_peaked(lse_raw));
 
   int kend = s.M;
   if (CAUSAL) kend = min(s.M, qb * BM + BM);
@@ -329,7 +335,9 @@ __global__ __launch_bounds__(512, 2) void jvp_ksplit_kernel(const JvpParams p) {
   const int kt0 = grp * half, kt1 = min(nkt, kt0 + half);  // this group's tiles [kt0, kt1)
 
   // The key tile kt held in (tK, tV, ttK, ttV): as jvp_kernel, 32-key subtiles one after the other.
-  auto compute = [&](int kt, const char* tK, const char* tV, const char* ttK, const char* ttV) {
+  auto compute = [&](auto split_tag, int kt, const char* tK, const char* tV, const char* ttK,
+                     const char* ttV) __attribute__((always_inline)) {
+    constexpr bool SPLIT = decltype(split_tag)::value;
 #pragma unroll
     for (int st = 0; st < NST; ++st) {
       const int k0 = kt * BN + 32 * st;
@@ -356,19 +364,33 @@ __global__ __launch_bounds__(512, 2) void jvp_ksplit_kernel(const JvpParams p) {
         gm[r] = pg;
         cpart += pg;
       }
+      if constexpr (SPLIT) {
 #pragma unroll
-      for (int cc = 0; cc < NPC; ++cc) {
-        F pf, pf_lo, pgf, pgf_lo;
-        split_frag<T>(sc, cc, pf, pf_lo);
-        split_frag<T>(gm, cc, pgf, pgf_lo);
+        for (int cc = 0; cc < NPC; ++cc) {
+          F pf, pf_lo, pgf, pgf_lo;
+          split_frag<T>(sc, cc, pf, pf_lo);
+          split_frag<T>(gm, cc, pgf, pgf_lo);
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-          const F vfr = swz_rows<T, DP>(tV, 32 * st, cc, dt * 32);
-          accA[dt] = MM::mma(vfr, pgf, accA[dt]);
-          accA[dt] = MM::mma(vfr, pgf_lo, accA[dt]);
-          accO[dt] = MM::mma(vfr, pf, accO[dt]);
-          accO[dt] = MM::mma(vfr, pf_lo, accO[dt]);
-          if (has_tv) accC[dt] = MM::mma(swz_rows<T, DP>(ttV, 32 * st, cc, dt * 32), pf, accC[dt]);
+          for (int dt = 0; dt < NDT; ++dt) {
+            const F vfr = swz_rows<T, DP>(tV, 32 * st, cc, dt * 32);
+            accA[dt] = MM::mma(vfr, pgf, accA[dt]);
+            accA[dt] = MM::mma(vfr, pgf_lo, accA[dt]);
+            accO[dt] = MM::mma(vfr, pf, accO[dt]);
+            accO[dt] = MM::mma(vfr, pf_lo, accO[dt]);
+            if (has_tv) accC[dt] = MM::mma(swz_rows<T, DP>(ttV, 32 * st, cc, dt * 32), pf, accC[dt]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int cc = 0; cc < NPC; ++cc) {
+          const F pf = acc_frag<T>(sc, cc), pgf = acc_frag<T>(gm, cc);
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) {
+            const F vfr = swz_rows<T, DP>(tV, 32 * st, cc, dt * 32);
+            accA[dt] = MM::mma(vfr, pgf, accA[dt]);
+            accO[dt] = MM::mma(vfr, pf, accO[dt]);
+            if (has_tv) accC[dt] = MM::mma(swz_rows<T, DP>(ttV, 32 * st, cc, dt * 32), pf, accC[dt]);
+          }
         }
       }
     }
@@ -393,14 +415,21 @@ __global__ __launch_bounds__(512, 2) void jvp_ksplit_kernel(const JvpParams p) {
   };
   // Step i: tile kt0 + i of this group (if it has one) from set i & 1; the next one's copies go to the other
   // set, read in step i - 1, which every wave has finished at the barrier.
+  auto sweep = [&](auto split_tag) __attribute__((always_inline)) {
+    for (int i = 0; i < half; ++i) {
+      const int kt = kt0 + i;
+      wait_vm_all();
+      __syncthreads();
+      if (kt + 1 < kt1) issue(kt + 1, (i + 1) & 1);
+      if (kt < kt1) compute(split_tag, kt, tile(i & 1, 0), tile(i & 1, 1), tile(i & 1, 2), tile(i & 1, 3));
+    }
+  };
   if (kt0 < kt1) issue(kt0, 0);
-  for (int i = 0; i < half; ++i) {
-    const int kt = kt0 + i;
-    wait_vm_all();
-    __syncthreads();
-    if (kt + 1 < kt1) issue(kt + 1, (i + 1) & 1);
-    if (kt < kt1) compute(kt, tile(i & 1, 0), tile(i & 1, 1), tile(i & 1, 2), tile(i & 1, 3));
-  }
+  // The waves of a workgroup may take different copies of the loop: both meet the same barriers.
+  if (split)
+    sweep(std::integral_constant<bool, true>{});
+  else
+    sweep(std::integral_constant<bool, false>{});
 
   // Group 1's partial sums to group 0, 32 floats per lane per round (element e of lane l of wave w at
   // e * 256 + w * 64 + l: consecutive lanes, consecutive words).
