@@ -328,3 +328,29 @@ def test_kernel_only_hvp_matches_oracle_and_autograd(dt, causal, hip_device):
     ag = torch.autograd.grad(sum((a.float() * b.float()).sum() for a, b in zip(g, uv)), (qg, kg, vg))
     for part, a, b in zip("qkv", hip_sdpa_hvp(q, k, v, *uv, target=t_, causal=causal), ag):
         close(a, b.detach().double().cpu(), dt, f"hvp vs autograd {part}")
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_kernel_only_hvp_with_peaked_rows(dt, D, causal, hip_device):
+    """hip_sdpa_hvp of 0.5 ||O - T||^2 against the float64 oracle on inputs with rows whose probability sits
+    on one key: the 16-bit double backward's exact row pass and split column products run there."""
+    from theria_amd.autograd.hip_sdpa import hip_sdpa_hvp
+
+    dev = hip_device
+    print(f"kernel-only HVP, peaked rows, {dt} D{D} causal={causal}", flush=True)
+    B, H, T, M = 2, 2, 160, 192
+    g = torch.Generator().manual_seed(211)
+    qh, kh = torch.randn(B, H, T, D, generator=g), torch.randn(B, H, M, D, generator=g)
+    for r in (5, 77, 150):
+        qh[:, :, r] = kh[:, :, r]  # score ~ sqrt(D) on key r against N(0, 1) elsewhere
+    q, k = qh.to(dt).to(dev), kh.to(dt).to(dev)
+    qc, kc = q.double().cpu(), k.double().cpu()
+    v, vc = make((B, H, M, D), dt, dev, 212)
+    t_, tc = make((B, H, T, D), dt, dev, 213)
+    u = [make(x.shape, dt, dev, 214 + i, std=0.1) for i, x in enumerate((q, k, v))]
+    uv, uc = [x[0] for x in u], [x[1] for x in u]
+    ref = O.hvp_quadratic(qc, kc, vc, tc, *uc, causal=causal)
+    for part, a, b in zip("qkv", hip_sdpa_hvp(q, k, v, *uv, target=t_, causal=causal), ref):
+        close(a, b, dt, f"hvp {part}")
