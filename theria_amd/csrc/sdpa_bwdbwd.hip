@@ -83,9 +83,19 @@ __device__ __attribute__((always_inline)) inline void rows_block(const BwdBwdPar
   const int myq = q0w + li;
   const bool qvalid = myq < s.T;
   const int64_t row_id = (int64_t)bh * s.T + myq;
-  // 16-bit, second launch: the workgroups holding a row flagged peaked in lse, in the exact form (uniform)
+  int kend = s.M;
+  if (CAUSAL) kend = min(s.M, qb * BM + BM);
+  const int nkt = (kend + BN - 1) / BN;
+  // 16-bit workgroups holding a row flagged peaked in lse take the exact form (uniform). Causal ones with at
+  // most half the longest workgroup's key tiles run both of its passes in the first launch, inside that
+  // launch's slack (every head's first query block holds such rows); the others are the second pass's.
   static_assert(!EXACT || sizeof(T) == 2, "the exact form is for 16-bit inputs");
-  const bool exact = EXACT && __syncthreads_or(qvalid && lse_peaked(p.lse[row_id]));
+  constexpr bool LIGHT_OK = CAUSAL && sizeof(T) == 2 && DP <= 64;  // at 128 the second sweep spills
+  const bool light = LIGHT_OK && 2 * nkt <= (s.M + BN - 1) / BN;
+  bool flagged = false;
+  if (EXACT || (LIGHT_OK && light)) flagged = __syncthreads_or(qvalid && lse_peaked(p.lse[row_id]));
+  const bool exact = EXACT && flagged && !light;
+  const bool two_pass = !EXACT && LIGHT_OK && flagged && light;
   if (EXACT && !exact) return;
 
   F qf[NKC], dof[NKC], gqf[NKC];
@@ -116,12 +126,8 @@ __device__ __attribute__((always_inline)) inline void rows_block(const BwdBwdPar
   // on rows with few visible keys, where G_Q is a small difference of large terms, the products then carry
   // small centred values instead (one visible key gives G_Q = 0 exactly).
   float t_frag = 0.f, cr = 0.f, ct = 0.f;
-  float rx = 0.f, tx = 0.f;  // exact row terms for the second launch
+  float rx = 0.f, tx = 0.f;  // exact row terms of the exact form
   float c_p = 0.f, c_pg = 0.f, c_pgd = 0.f, c_pd = 0.f, c_pw = 0.f;
-
-  int kend = s.M;
-  if (CAUSAL) kend = min(s.M, qb * BM + BM);
-  const int nkt = (kend + BN - 1) / BN;
 
   // Fragment reads: "cols" (k along a tile row, KLIN) and "rows" (k down the tile rows, KACC).
   auto colsf = [&](const char* t, int row, int c) -> F {
@@ -236,6 +242,11 @@ __device__ __attribute__((always_inline)) inline void rows_block(const BwdBwdPar
     rx = qvalid ? p.r_row[row_id] : 0.f;
     tx = qvalid ? p.t_row[row_id] : 0.f;
   }
+  // r = sum_j P Gam, t = sum_j P (Gam (dP - z) + W) from the pre-pass sums over all keys
+  auto set_exact_terms = [&]() {
+    rx = pair_sum(c_pg);
+    tx = pair_sum(c_pgd) + pair_sum(c_pw);
+  };
   auto set_centre = [&]() {
     const float sp = pair_sum(c_p), spg = pair_sum(c_pg), spd = pair_sum(c_pd), spgd = pair_sum(c_pgd),
                 spw = pair_sum(c_pw);
@@ -289,6 +300,12 @@ __device__ __attribute__((always_inline)) inline void rows_block(const BwdBwdPar
       issue(0, sK0, sV0, sgK0, sgV0);
       if (exact) {
         sweep(exact_pass);
+      } else if (two_pass) {
+        sweep(pre_pass);  // r and t of every row from all its keys
+        set_exact_terms();
+        __syncthreads();  // every wave is done with the last tile's buffers
+        issue(0, sK0, sV0, sgK0, sgV0);
+        sweep(exact_pass);
       } else {
         if constexpr (sizeof(T) == 2) {
           wait_vm_all();
@@ -323,6 +340,13 @@ __device__ __attribute__((always_inline)) inline void rows_block(const BwdBwdPar
     if (nkt > 0) prefetch(0);
     if (exact) {
       if (nkt > 0) sweep(exact_pass);
+    } else if (two_pass) {
+      if (nkt > 0) {
+        sweep(pre_pass);  // r and t of every row from all its keys
+        set_exact_terms();
+        prefetch(0);
+        sweep(exact_pass);
+      }
     } else {
       if (sizeof(T) == 2 && nkt > 0) {
         // centre pre-pass over tile 0 (the loop stages the same registers again)
@@ -338,7 +362,7 @@ __device__ __attribute__((always_inline)) inline void rows_block(const BwdBwdPar
     }
   }
 
-  const float rr = pair_sum(r_part), tt = pair_sum(t_part);
+  const float rr = two_pass ? rx : pair_sum(r_part), tt = two_pass ? tx : pair_sum(t_part);
   const float tg = sizeof(T) == 2 ? pair_sum(t_frag) : tt;  // t_c as G_Q uses it; the cols kernel takes tt
   const float rg = rr - cr;                                   // r - cr (cr = 0 for float32)
   if (qvalid) {
