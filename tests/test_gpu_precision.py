@@ -75,6 +75,7 @@ PEAKED = [
     (torch.bfloat16, 1, 2, 300, 300, 64, False, 3.0),
     (torch.float32, 1, 1, 150, 170, 32, True, 3.0),
     (torch.bfloat16, 1, 1, 150, 90, 32, False, 3.0),
+    (torch.bfloat16, 1, 2, 200, 200, 32, True, 3.0),
 ]
 
 
