@@ -69,7 +69,7 @@ __device__ __attribute__((always_inline)) inline void rows_block(const BwdBwdPar
   const int bid = xcd_remap(blk, nblk);
   const int bh = bid / nqb;
   int qb = bid - bh * nqb;
-  if (CAUSAL) qb = nqb - 1 - qb;
+  if (CAUSAL && !EXACT) qb = nqb - 1 - qb;  // longest first (the exact pass: query order, see the cols grid)
   const int b = bh / s.H, h = bh - b * s.H;
   const T* Q = (const T*)p.q.p + b * p.q.sb + h * p.q.sh;
   const T* K = (const T*)p.k.p + b * p.k.sb + h * p.k.sh;
@@ -737,8 +737,11 @@ __global__ __launch_bounds__(256) void bwdbwd_cols_exact_kernel(const BwdBwdPara
   const int ncols = ((p.s.M + 127) / 128) * p.s.B * p.s.H;
   const int nrows = (int)gridDim.x - ncols;
   const int bid = blockIdx.x;  // uniform
-  // Row blocks first: most exit at once (no flagged row), and the few heavy ones (a single peaked row
-  // makes its block sweep every key) start beside the column blocks instead of after all of them.
+  // Row blocks first: most exit at once (no flagged row), and the few heavy ones (a single peaked row makes
+  // its block sweep every key) start at once. A workgroup waits for the CU of its own place in the grid,
+  // so the column block placed like a heavy row block starts when that one ends; for causal problems the
+  // row blocks run in query order (no heavy-first reversal), which pairs query block i with key block i,
+  // whose lengths (i + 1 and n - i key tiles) add up to about the longest column block's.
   if (bid < nrows)
     rows_block<T, DP, CAUSAL, DMA, true>(p, bid, nrows);
   else
