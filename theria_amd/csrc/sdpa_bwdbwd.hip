@@ -144,8 +144,8 @@ __device__ __attribute__((always_inline)) inline void rows_block(const BwdBwdPar
   };
 
   // The key tile kt held in (tK, tV, tgK, tgV), as 32-key subtiles.
-  // PASS: 0 centre pre-pass (sums for c only), 1 the common pass, 3 the exact pass (Gbar_S from the row
-  // terms r, t of the first launch; 16-bit only).
+  // PASS: 0 the pre-pass (sums only: for the centres over the first tile, or for r and t over every tile),
+  // 1 the common pass, 3 the exact pass (Gbar_S from exact row terms r, t; 16-bit only).
   auto compute = [&](auto pass_tag, int kt, const char* tK, const char* tV, const char* tgK,
                      const char* tgV) __attribute__((always_inline)) {
     constexpr int PASS = decltype(pass_tag)::value;
