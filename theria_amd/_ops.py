@@ -129,6 +129,14 @@ def check_inputs(q, k, v, what: str = "theria_amd SDPA", require_v: bool = True)
         raise AssertionError(f"{what}: sizes exceed the 32-bit row index range")
 
 
+def _out_like(t: torch.Tensor, shape, ref: torch.Tensor, name: str) -> torch.Tensor:
+    """A caller-given output: the shape, dtype and device the entry point writes, last dimension contiguous."""
+    if tuple(t.shape) != tuple(shape) or t.dtype != ref.dtype or t.device != ref.device or t.stride(-1) != 1:
+        raise AssertionError(f"{name} must be a {ref.dtype} tensor of shape {tuple(shape)} on {ref.device} "
+                             f"with a contiguous last dimension")
+    return t
+
+
 def _like_rows(t: torch.Tensor | None, ref: torch.Tensor, rows: int, name: str) -> torch.Tensor | None:
     """Cast a (B,H,rows,D) operand to the compute dtype and check its shape."""
     if t is None:
@@ -182,9 +190,9 @@ def _fwd(q, k, v, scale, causal, out_fp32, want_m, want_l):
     return o, lse, m, l
 
 
-def bwd(q, k, v, o, lse, do, scale: float, causal: bool, need_dq: bool = True, need_dk: bool = True):
+def bwd(q, k, v, o, lse, do, scale: float, causal: bool, need_dq: bool = True, need_dk: bool = True, out=None):
     """dQ, dK, dV (input dtype) and the row term delta = rowsum(dO * O) (float32; formed exactly on query
-    blocks that hold a row flagged peaked in lse)."""
+    blocks that hold a row flagged peaked in lse). out: (dq, dk, dv) tensors to write instead of new ones."""
     check_inputs(q, k, v)
     q, k, v = _rowmajor(q), _rowmajor(k), _rowmajor(v)
     B, H, T, D = q.shape
@@ -199,9 +207,12 @@ def bwd(q, k, v, o, lse, do, scale: float, causal: bool, need_dq: bool = True, n
     lse = lse.contiguous()
     dev = q.device
     delta = torch.empty((B, H, T), dtype=torch.float32, device=dev)
-    dq = torch.empty((B, H, T, D), dtype=q.dtype, device=dev) if need_dq else None
-    dk = torch.empty((B, H, M, D), dtype=q.dtype, device=dev) if need_dk else None
-    dv = torch.empty((B, H, M, D), dtype=q.dtype, device=dev)
+    if out is not None:
+        dq, dk, dv = (_out_like(t, (B, H, n, D), q, name) for t, n, name in zip(out, (T, M, M), ("dq", "dk", "dv")))
+    else:
+        dq = torch.empty((B, H, T, D), dtype=q.dtype, device=dev) if need_dq else None
+        dk = torch.empty((B, H, M, D), dtype=q.dtype, device=dev) if need_dk else None
+        dv = torch.empty((B, H, M, D), dtype=q.dtype, device=dev)
     prob = _problem(q, k, scale, causal)
     with _OnDevice(dev):
         bwd_dq(prob, q, k, v, o, o_f32, do, lse, delta, dq)
@@ -290,7 +301,7 @@ def jvp(q, k, v, o, lse, tq, tk, tv, scale: float, causal: bool, normalize: bool
     return out
 
 
-def bwd_bwd(q, k, v, o, do, lse, delta, gq, gk, gv, scale: float, causal: bool, noalloc: bool = False):
+def bwd_bwd(q, k, v, o, do, lse, delta, gq, gk, gv, scale: float, causal: bool, noalloc: bool = False, out=None):
     """(G_Q, G_K, G_V, G_dO): VJP of the backward map with cotangents (gq, gk, gv) (None = zero).
     delta (the backward's row term) may be None for 16-bit inputs, which recompute it.
 
@@ -313,9 +324,13 @@ def bwd_bwd(q, k, v, o, do, lse, delta, gq, gk, gv, scale: float, causal: bool, 
     else:
         delta = delta.contiguous()
     dev = q.device
-    out_q = torch.empty((B, H, T, D), dtype=q.dtype, device=dev)
-    out_k = torch.empty((B, H, M, D), dtype=q.dtype, device=dev)
-    out_v = torch.empty((B, H, M, D), dtype=q.dtype, device=dev)
+    if out is not None:  # (G_Q, G_K, G_V) written to the given tensors
+        out_q, out_k, out_v = (_out_like(t, (B, H, n, D), q, name)
+                               for t, n, name in zip(out, (T, M, M), ("out_gq", "out_gk", "out_gv")))
+    else:
+        out_q = torch.empty((B, H, T, D), dtype=q.dtype, device=dev)
+        out_k = torch.empty((B, H, M, D), dtype=q.dtype, device=dev)
+        out_v = torch.empty((B, H, M, D), dtype=q.dtype, device=dev)
     out_do = torch.empty((B, H, T, D), dtype=q.dtype, device=dev)
     lib = _lib.load()
     prob = _problem(q, k, scale, causal)

@@ -189,11 +189,19 @@ def hip_sdpa_hvp(q, k, v, vq, vk, vv, *, weight=None, target=None, causal: bool 
             dout = torch.ones_like(o)
         # 16-bit inputs: the double backward forms its own row term
         delta = (dout.float() * o.float()).sum(-1) if o.dtype == torch.float32 else None
-        hq, hk, hv, g_do = _ops.bwd_bwd(q, k, v, o, dout, lse, delta, vq, vk, vv, float(scale), bool(causal))
         if target is None:
-            return hq, hk, hv
-        jq, jk, jv, _ = _ops.bwd(q, k, v, o, lse, g_do.to(o.dtype), float(scale), bool(causal))
-        return hq.add_(jq), hk.add_(jk), hv.add_(jv)
+            return _ops.bwd_bwd(q, k, v, o, dout, lse, delta, vq, vk, vv, float(scale), bool(causal))[:3]
+        # both results as views of one flat buffer each, so that their sum is one full-grid launch
+        B, H, T, D = q.shape
+        M = k.shape[2]
+        sizes = (B * H * T * D, B * H * M * D, B * H * M * D)
+        shapes = ((B, H, T, D), (B, H, M, D), (B, H, M, D))
+        flat_h, flat_j = (torch.empty(sum(sizes), dtype=q.dtype, device=q.device) for _ in range(2))
+        hs, js = ([f.view(sh) for f, sh in zip(buf.split(sizes), shapes)] for buf in (flat_h, flat_j))
+        g_do = _ops.bwd_bwd(q, k, v, o, dout, lse, delta, vq, vk, vv, float(scale), bool(causal), out=hs)[3]
+        _ops.bwd(q, k, v, o, lse, g_do.to(o.dtype), float(scale), bool(causal), out=js)
+        flat_h.add_(flat_j)
+        return tuple(hs)
 
 
 __all__ = ["SDPAOp", "SDPABackwardOp", "hip_sdpa", "hip_sdpa_with_lse", "hip_sdpa_hvp"]
