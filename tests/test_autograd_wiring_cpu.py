@@ -128,3 +128,17 @@ def test_gradient_of_dout_path_is_not_double_counted(kernels):
         return torch.autograd.grad(sum(x.pow(2).sum() for x in g), qkv, create_graph=True)
 
     _close(second(_hip(False), a), second(_ref(False), b))
+
+
+def test_caller_given_outputs_are_checked():
+    """bwd / bwd_bwd write into caller-given outputs only of the exact shape, dtype and row layout."""
+    ref = torch.zeros(2, 3, 5, 8, dtype=torch.bfloat16)
+    good = torch.empty(2, 3, 7, 8, dtype=torch.bfloat16)
+    assert _ops._out_like(good, (2, 3, 7, 8), ref, "dk") is good
+    strided_rows = torch.empty(2, 3, 7, 16, dtype=torch.bfloat16)[..., :8]  # row stride 16, last dim contiguous
+    assert _ops._out_like(strided_rows, (2, 3, 7, 8), ref, "dk") is strided_rows
+    for bad in (torch.empty(2, 3, 6, 8, dtype=torch.bfloat16),          # wrong rows
+                torch.empty(2, 3, 7, 8, dtype=torch.float32),           # wrong dtype
+                torch.empty(2, 3, 8, 7, dtype=torch.bfloat16).transpose(-1, -2)):  # last dim strided
+        with pytest.raises(AssertionError):
+            _ops._out_like(bad, (2, 3, 7, 8), ref, "dk")
