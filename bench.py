@@ -66,8 +66,9 @@ def _rand(shape, dtype, dev, seed, std=1.0):
 
 
 def _step_fns(q, k, v, do, scale, causal):
-    """One fwd + bwd step as the autograd operator runs it: the forward saves lse, the row maxima m and the
-    rounding residual of O; the dQ kernel forms the row term from O and its residual, then dK/dV."""
+    """One fwd + bwd step as the autograd operator runs it: the forward writes O and lse; the dQ kernel forms
+    the row term (dO . O, or its exact form on query blocks holding a row flagged peaked in lse) and dQ;
+    then the dK/dV kernel reads that row term."""
     import torch
 
     from theria_amd import _ops

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define THERIA_SDPA_ABI_VERSION 7
+#define THERIA_SDPA_ABI_VERSION 8
 
 enum theria_dtype { THERIA_DTYPE_F32 = 0, THERIA_DTYPE_F16 = 1, THERIA_DTYPE_BF16 = 2 };
 enum theria_status { THERIA_OK = 0, THERIA_ERR_CONTRACT = 1, THERIA_ERR_HIP = 2 };
@@ -75,8 +75,11 @@ int theria_sdpa_fwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q, co
  * Replaces sdpa_bwd_dq / sdpa_bwd_dk / sdpa_bwd_dv and their kernels
  * (theria/attention/triton_sdpa_backward.py:106-266, 269-462, 505-696) and the backward of
  * TritonFusedSDPAFunction (triton_qk.py:379-387). The row term z_i = sum_j dP_ij P_ij of the
- * reference (triton_sdpa_backward.py:312-353, 543-585) is computed once as delta_i = dO_i . O_i and
- * written to delta_out (B,H,tq) float32. dout has the input dtype; o may be float32 (o_is_f32).
+ * reference (triton_sdpa_backward.py:312-353, 543-585) is computed once per row and written to delta_out
+ * (B,H,tq) float32: as delta_i = dO_i . O_i for 16-bit inputs (see below for peaked rows), and for float32
+ * inputs as sum_j P_ij dP_ij / sum_j P_ij in a pass over the keys with the same P and dP the gradient uses
+ * (on a row whose probability sits on one key, dP - z is then a difference of consistently rounded values;
+ * dO . O with the forward's O leaves ~2e-5 in dQ there). dout has the input dtype; o may be float32 (o_is_f32).
  * dq / dk may have data == NULL to skip that output. Deterministic (no atomics, no workspace).
  * theria_sdpa_bwd = theria_sdpa_bwd_dq followed by theria_sdpa_bwd_dkdv on the same stream.
  *
@@ -152,8 +155,13 @@ int theria_sdpa_jvp(const theria_sdpa_problem_t* p, const theria_tensor_t* q, co
  * with cotangents (gq, gk, gv) of (dQ, dK, dV). Outputs out_gq, out_gk, out_gv, out_gdout.
  * The reference has no kernel for this: its HVP is a finite difference of the VJP
  * (theria/attention/hvp_utils.py:30-49) or autograd-in-backward (theria/autograd/sdpa_custom_function.py:32-53).
- * delta is the row term written by theria_sdpa_bwd (float32 inputs; 16-bit inputs do not read it, and it may
- * be NULL there). Any cotangent may have data == NULL (zero).
+ * delta (the row term written by theria_sdpa_bwd) is not read and may be NULL: a pass over the keys recomputes
+ * the row term into the workspace. Any cotangent may have data == NULL (zero).
+ * For float32 inputs that pass also forms each row's own statistics from its float32 scores, m2 = max_j fl(S c)
+ * and L2 = log2 sum_j exp2(fl(S c) - m2) with c = scale log2(e), and the row and column kernels rebuild
+ * P = exp2((fl(S c) - m2) - L2) with dP formed as in that pass (lse is read only by the G_dO pass): on rows
+ * whose probability sits on one key the second-order terms are differences (dP - z, Gam - r, E1 - t) that
+ * P from a rounded lse would leave at ~1e-5.
  * For 16-bit inputs a pass over the keys recomputes, into the workspace, the row normaliser
  * lse + ln(sum_j P_ij) (a 16-bit forward's lse comes from rounded probabilities, so P rebuilt from it sums to
  * one only within ~2^-9) and the row term sum_j P_ij dP_ij / sum_j P_ij in float32 (delta from the 16-bit O
@@ -161,7 +169,7 @@ int theria_sdpa_jvp(const theria_sdpa_problem_t* p, const theria_tensor_t* q, co
  * then not read. Query blocks holding a row flagged peaked in lse are redone by a second row pass (run as
  * part of the column kernel's grid) that forms G_Q's score-gradient in float32 from the first pass's row
  * terms; those blocks and tiles enter the G_Q, G_K, G_V products as two 16-bit terms.
- * row_ws is a caller-owned float32 workspace of 4*batch*heads*tq elements.
+ * row_ws is a caller-owned float32 workspace of 5*batch*heads*tq elements.
  */
 int theria_sdpa_bwd_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
                         const theria_tensor_t* v, const theria_tensor_t* o, const theria_tensor_t* dout,
@@ -172,9 +180,9 @@ int theria_sdpa_bwd_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q
 /*
  * theria_sdpa_bwd_bwd without a workspace argument and without any allocation. It has no counterpart in the
  * reference: it is for callers that cannot allocate (code under HIP graph capture, tight serving loops,
- * harnesses that forbid hipMalloc). The row workspace is a static device array of 4 * 2^20 floats (16 MiB)
- * that each GPU the library runs on holds until the process ends, so 4 * batch * heads * tq must not exceed
- * 4 * 2^20 (a larger problem is rejected with THERIA_ERR_CONTRACT). Every call on one GPU shares that GPU's
+ * harnesses that forbid hipMalloc). The row workspace is a static device array of 5 * 2^20 floats (20 MiB)
+ * that each GPU the library runs on holds until the process ends, so 5 * batch * heads * tq must not exceed
+ * 5 * 2^20 (a larger problem is rejected with THERIA_ERR_CONTRACT). Every call on one GPU shares that GPU's
  * array: calls that overlap on one GPU (other streams, other threads) race and must be serialised by the
  * caller. Results equal theria_sdpa_bwd_bwd's bit for bit.
  */

@@ -3,7 +3,7 @@ the reference-named entry points, and the second-order boundary (GPU).
 
 Config 4: B8 H8 S512 D64 in float32 and bfloat16; primals ~ N(0,1), tangents ~ N(0, 0.1^2);
 HVP of 0.5 ||O - T||^2 with T, v ~ N(0,1) via double backward through the explicit kernels.
-Bars: float32 1e-5 abs/rel, bfloat16/float16 2e-2 abs.
+Bars (tests/bars.py): float32 1e-5 abs/rel, bfloat16/float16 2e-2 abs plus one output rounding unit relative.
 """
 
 import math
@@ -11,6 +11,7 @@ import math
 import pytest
 import torch
 
+import bars
 from oracle import sdpa_oracle as O
 from theria_amd.attention import (
     TritonFusedSDPAFunction,
@@ -27,17 +28,11 @@ from theria_amd.attention.hvp_utils import hvp_fd_vjp
 pytestmark = pytest.mark.gpu
 
 
-def tol(dtype):
-    """float32: 1e-5 abs/rel. 16-bit: the reference's GPU-test bound rtol = atol = 2e-2
-    (tests/test_triton_fused_forward.py:27, test_triton_sdpa_dq.py:42): outputs are rounded to the input
-    dtype, and half a bfloat16 ulp already exceeds 2e-2 for |x| >= 8, so a pure absolute bound cannot hold."""
-    return dict(rtol=1e-5, atol=1e-5) if dtype == torch.float32 else dict(rtol=2e-2, atol=2e-2)
+tol = bars.tol
 
 
 def close(gpu, ref, dtype, what):
-    a = gpu.detach().double().cpu()
-    assert torch.isfinite(a).all(), f"{what}: non-finite"
-    torch.testing.assert_close(a, ref.double(), **tol(dtype), msg=lambda m: f"{what}: {m}")
+    bars.close(gpu, ref, what=what, **tol(dtype))
 
 
 def make(shape, dtype, dev, seed, std=1.0, grad=False):
@@ -144,8 +139,13 @@ def test_third_order_matches_oracle(causal, hip_device):
     got = _third_order(lambda a, b, c: hip_sdpa(a, b, c, causal=causal), q, k, v)
     ref = _third_order(lambda a, b, c: O.autograd_attention(a, b, c, causal=causal),
                        *(t.clone().requires_grad_(True) for t in (qc, kc, vc)))
-    for name, a, b in zip(("q", "k", "v"), got, ref):
-        torch.testing.assert_close(a.double().cpu(), b, rtol=1e-4, atol=1e-4, msg=lambda m: f"d3/d{name}: {m}")
+    # the same derivative of textbook attention in float32 (theria's pure-PyTorch path): its error against float64
+    # sets the bar where float32 arithmetic itself cannot reach 1e-5 (third derivatives sum many large products)
+    ref32 = _third_order(lambda a, b, c: O.autograd_attention(a, b, c, causal=causal),
+                         *(t.float().clone().requires_grad_(True) for t in (qc, kc, vc)))
+    for name, a, b, c in zip(("q", "k", "v"), got, ref, ref32):
+        err32 = float((c.double() - b).abs().max())
+        bars.close(a, b, rtol=1e-5, atol=max(1e-5, 2 * err32), what=f"d3/d{name} (float32 reference error {err32:.2e})")
 
 
 def test_autograd_functional_hvp(hip_device):
@@ -159,7 +159,7 @@ def test_autograd_functional_hvp(hip_device):
     _, h = torch.autograd.functional.hvp(lambda a, b, c: (hip_sdpa(a, b, c) * w).sum(), (q, k, v),
                                          tuple(x[0] for x in u))
     for name, a, b in zip(("q", "k", "v"), h, O.hvp_weighted_sum(qc, kc, vc, wc, *(x[1] for x in u))):
-        torch.testing.assert_close(a.double().cpu(), b, rtol=1e-4, atol=1e-4, msg=lambda m: f"hvp {name}: {m}")
+        close(a, b, torch.float32, f"hvp {name}")
 
 
 def test_second_order_probe_sees_attention_curvature(hip_device):
@@ -287,7 +287,7 @@ def test_value_head_dim_differs(D, Dv, causal, hip_device):
         close(a, b, torch.float32, name)
     h = torch.autograd.grad(sum((a * b[0]).sum() for a, b in zip(g, u)), (q, k, v))
     for name, a, b in zip(("q", "k", "v"), h, O.hvp_weighted_sum(qc, kc, vc, wc, *(x[1] for x in u), causal=causal)):
-        torch.testing.assert_close(a.double().cpu(), b, rtol=1e-4, atol=1e-4, msg=lambda m: f"hvp {name}: {m}")
+        close(a, b, torch.float32, f"hvp {name}")
     _, jv = torch.func.jvp(lambda a, b, c: hip_sdpa(a, b, c, causal=causal), (q.detach(), k.detach(), v.detach()),
                            tuple(x[0] for x in u))
     close(jv, O.jvp(qc, kc, vc, *(x[1] for x in u), causal=causal), torch.float32, "jvp")

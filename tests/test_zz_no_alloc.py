@@ -34,7 +34,7 @@ def test_noalloc_double_backward_equals_the_workspace_entry_point(dt, hip_device
 
 
 def test_noalloc_rejects_problems_beyond_the_static_scratch(hip_device):
-    """4 * B * H * T > 4 * 2^20 is refused before any launch (a contract error, not a fault)."""
+    """5 * B * H * T > 5 * 2^20 is refused before any launch (a contract error, not a fault)."""
     B, H, T, M, D = 1, 1, (1 << 20) + 1, 8, 8
     q = torch.zeros(B, H, T, D, dtype=torch.bfloat16, device=hip_device)
     k = torch.zeros(B, H, M, D, dtype=torch.bfloat16, device=hip_device)

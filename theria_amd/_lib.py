@@ -16,7 +16,7 @@ import torch  # noqa: F401  (must be imported first: it loads the HIP runtime th
 
 # THERIA_SDPA_LIB overrides the in-tree build (e.g. a library installed elsewhere).
 LIB_PATH = Path(os.environ.get("THERIA_SDPA_LIB") or Path(__file__).resolve().parent / "lib" / "libtheria_sdpa.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 OK, ERR_CONTRACT, ERR_HIP = 0, 1, 2

@@ -303,10 +303,10 @@ def jvp(q, k, v, o, lse, tq, tk, tv, scale: float, causal: bool, normalize: bool
 
 def bwd_bwd(q, k, v, o, do, lse, delta, gq, gk, gv, scale: float, causal: bool, noalloc: bool = False, out=None):
     """(G_Q, G_K, G_V, G_dO): VJP of the backward map with cotangents (gq, gk, gv) (None = zero).
-    delta (the backward's row term) may be None for 16-bit inputs, which recompute it.
+    delta (the backward's row term) is not read: the library recomputes the row term; it may be None.
 
     noalloc: run theria_sdpa_bwd_bwd_noalloc, whose row workspace is the library's static device array
-    (4 * B * H * T up to 4 * 2^20), instead of a workspace allocated here."""
+    (5 * B * H * T up to 5 * 2^20), instead of a workspace allocated here."""
     check_inputs(q, k, v)
     q, k, v = _rowmajor(q), _rowmajor(k), _rowmajor(v)
     B, H, T, D = q.shape
@@ -318,10 +318,7 @@ def bwd_bwd(q, k, v, o, do, lse, delta, gq, gk, gv, scale: float, causal: bool, 
     if o is not None:
         o = _rowmajor(o) if o.dtype == q.dtype else None
     lse = lse.contiguous()
-    if delta is None:
-        if q.dtype == torch.float32:
-            raise AssertionError("bwd_bwd: delta is required for float32 inputs")
-    else:
+    if delta is not None:
         delta = delta.contiguous()
     dev = q.device
     if out is not None:  # (G_Q, G_K, G_V) written to the given tensors
@@ -340,7 +337,7 @@ def bwd_bwd(q, k, v, o, do, lse, delta, gq, gk, gv, scale: float, causal: bool, 
         if noalloc:
             rc = lib.theria_sdpa_bwd_bwd_noalloc(*args, _stream(dev))
         else:
-            ws = torch.empty((4 * B * H * T,), dtype=torch.float32, device=dev)
+            ws = torch.empty((5 * B * H * T,), dtype=torch.float32, device=dev)
             rc = lib.theria_sdpa_bwd_bwd(*args, _fp(ws), _stream(dev))
     _lib.check(rc, "theria_sdpa_bwd_bwd_noalloc" if noalloc else "theria_sdpa_bwd_bwd")
     return out_q, out_k, out_v, out_do

@@ -59,42 +59,43 @@ def _assert_jvp_contract(q, k, v, dq, dk, dv, m, l):
         raise AssertionError("frozen-stats JVP requires l > 0 (forward sumexp stats)")
 
 
-def _lse(m, l):
-    return _ops.lse_from_stats(m, l)
+def _lse(m, l, q):
+    # the peaked-row flag bits are read by the 16-bit kernels only; a float32 lse stays exactly m + log l
+    return _ops.lse_from_stats(m, l, peaked_bits=q.dtype != torch.float32)
 
 
 def sdpa_bwd_dq(q, k, v, dout, m, l, scale):
     """dQ = scale dS K with P rebuilt from (m, l)."""
     _assert_backward_contract(q, k, v, dout, m, l, require_v=True)
-    dq, _, _ = _ops.bwd_from_stats(q, k, v, dout, _lse(m, l), scale, False, True, False, False)
+    dq, _, _ = _ops.bwd_from_stats(q, k, v, dout, _lse(m, l, q), scale, False, True, False, False)
     return dq
 
 
 def sdpa_bwd_dk(q, k, v, dout, m, l, scale):
     """dK = scale dS^T Q with P rebuilt from (m, l)."""
     _assert_backward_contract(q, k, v, dout, m, l, require_v=True)
-    _, dk, _ = _ops.bwd_from_stats(q, k, v, dout, _lse(m, l), scale, False, False, True, False)
+    _, dk, _ = _ops.bwd_from_stats(q, k, v, dout, _lse(m, l, q), scale, False, False, True, False)
     return dk
 
 
 def sdpa_bwd_dv(q, k, dout, m, l, scale):
     """dV = P^T dO with P rebuilt from (m, l); needs no v (triton_sdpa_backward.py:194)."""
     _assert_backward_contract(q, k, None, dout, m, l, require_v=False)
-    _, _, dv = _ops.bwd_from_stats(q, k, None, dout, _lse(m, l), scale, False, False, False, True)
+    _, _, dv = _ops.bwd_from_stats(q, k, None, dout, _lse(m, l, q), scale, False, False, False, True)
     return dv
 
 
 def sdpa_bwd(q, k, v, dout, m, l, scale):
     """All three gradients in one backward pass: (dq, dk, dv)."""
     _assert_backward_contract(q, k, v, dout, m, l, require_v=True)
-    return _ops.bwd_from_stats(q, k, v, dout, _lse(m, l), scale, False, True, True, True)
+    return _ops.bwd_from_stats(q, k, v, dout, _lse(m, l, q), scale, False, True, True, True)
 
 
 def sdpa_jvp(q, k, v, dq, dk, dv, m, l, scale):
     """Frozen-stats JVP (docs/phase9.md:30-39): dO = P o (dS - rowsum(dS o P)) V + P dv, with
     P = exp(S - m) / l held exactly as given (triton_sdpa_backward.py:488-503)."""
     _assert_jvp_contract(q, k, v, dq, dk, dv, m, l)
-    return _ops.jvp(q, k, v, None, _lse(m, l), dq, dk, dv, scale, False, normalize=False)
+    return _ops.jvp(q, k, v, None, _lse(m, l, q), dq, dk, dv, scale, False, normalize=False)
 
 
 __all__ = ["sdpa_bwd_dq", "sdpa_bwd_dk", "sdpa_bwd_dv", "sdpa_bwd", "sdpa_jvp"]

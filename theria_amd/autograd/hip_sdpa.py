@@ -187,8 +187,7 @@ def hip_sdpa_hvp(q, k, v, vq, vk, vv, *, weight=None, target=None, causal: bool 
             dout = weight.to(o.dtype)
         else:
             dout = torch.ones_like(o)
-        # 16-bit inputs: the double backward forms its own row term
-        delta = (dout.float() * o.float()).sum(-1) if o.dtype == torch.float32 else None
+        delta = None  # the double backward forms its own row term
         if target is None:
             return _ops.bwd_bwd(q, k, v, o, dout, lse, delta, vq, vk, vv, float(scale), bool(causal))[:3]
         # both results as views of one flat buffer each, so that their sum is one full-grid launch

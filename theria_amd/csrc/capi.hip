@@ -122,12 +122,13 @@ int device_cu_count() {
 
 }  // namespace theria
 
-// Static row workspace of theria_sdpa_bwd_bwd_noalloc: kScratchFloats floats (16 MiB) on every device the
+// Static row workspace of theria_sdpa_bwd_bwd_noalloc: kScratchFloats floats (20 MiB) on every device the
 // library runs on, held until the process ends. Its name is only a host-side stand-in; the device address is
 // looked up once per device (with that device current) and kept in g_scratch_ptr. The kernels overwrite
-// every element they later read (r, t, the row term and the normaliser), so nothing is cleared; two calls that overlap on
-// one device race on it.
-constexpr int64_t kScratchFloats = int64_t(4) << 20;
+// every element they later read (r, t, the row term and the row statistics), so nothing is cleared; two calls that
+// overlap on one device race on it.
+constexpr int64_t kWsRows = 5;  // row workspace: kWsRows * batch * heads * tq floats
+constexpr int64_t kScratchFloats = kWsRows << 20;
 static __device__ __align__(256) float scratch[kScratchFloats];
 
 namespace {
@@ -190,7 +191,8 @@ THERIA_API int theria_sdpa_fwd(const theria_sdpa_problem_t* p, const theria_tens
 static int run_dq(const theria::Shape& s, const theria_tensor_t* q, const theria_tensor_t* k,
                   const theria_tensor_t* v, const theria_tensor_t* o, bool o_f32, int row_term,
                   const theria_tensor_t* dout, const float* lse, float* delta,
-                  const theria_tensor_t* dq, hipStream_t st, const char* what, float* lse_out = nullptr) {
+                  const theria_tensor_t* dq, hipStream_t st, const char* what, float* lse_out = nullptr,
+                  float* l2_out = nullptr) {
   theria::DqParams dp{};
   dp.s = s;
   dp.q = cv(q);
@@ -204,6 +206,7 @@ static int run_dq(const theria::Shape& s, const theria_tensor_t* q, const theria
   dp.delta = delta;
   dp.dq = mv(dq);
   dp.lse_out = lse_out;
+  dp.l2_out = l2_out;
   return hip_status(theria::launch_bwd_dq(dp, st), what);
 }
 
@@ -401,8 +404,8 @@ static int run_bwd_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q,
   c.kview(out_gv, "out_gv", true);
   c.qview(out_gdout, "out_gdout", true);
   c.need(lse != nullptr || !c.q_rows, "lse is required");
-  // 16-bit inputs recompute the row term (below) and do not read delta
-  c.need(delta != nullptr || !c.q_rows || s.dtype != THERIA_DTYPE_F32, "delta is required (float32 inputs)");
+  // the row term is recomputed (below); delta is not read
+  (void)delta;
   c.need(noalloc || row_ws != nullptr || !c.q_rows, "row_ws is required");
   if (!c.err.empty()) return fail(THERIA_ERR_CONTRACT, c.err);
   s.vec = c.vec;
@@ -410,9 +413,9 @@ static int run_bwd_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q,
   const hipStream_t st = (hipStream_t)stream;
   const int64_t nrows = (int64_t)s.B * s.H * s.T;
   if (noalloc) {
-    if (4 * nrows > kScratchFloats)
-      return fail(THERIA_ERR_CONTRACT, "theria_sdpa_bwd_bwd_noalloc: 4 * batch * heads * tq = " +
-                                           std::to_string(4 * nrows) + " floats exceeds the static scratch of " +
+    if (kWsRows * nrows > kScratchFloats)
+      return fail(THERIA_ERR_CONTRACT, "theria_sdpa_bwd_bwd_noalloc: 5 * batch * heads * tq = " +
+                                           std::to_string(kWsRows * nrows) + " floats exceeds the static scratch of " +
                                            std::to_string(kScratchFloats) + " (use theria_sdpa_bwd_bwd with row_ws)");
     const int rc = scratch_on_current_device(&row_ws);
     if (rc != THERIA_OK) return rc;
@@ -427,9 +430,27 @@ static int run_bwd_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q,
   bp.gk = cv(gk);
   bp.gv = cv(gv);
   bp.lse = lse;
-  bp.delta = delta;
+  bp.row_l2 = nullptr;
   bp.r_row = row_ws;
   bp.t_row = row_ws + nrows;
+  if (s.dtype == THERIA_DTYPE_F32 && s.T > 0) {
+    // float32: a pass over the keys forms each row's own statistics from its float32 scores, m2 = max_j fl(S c),
+    // L2 = log2 sum_j exp2(fl(S c) - m2) (c = scale log2 e), and the row term z = sum_j P dP / sum_j P with dP
+    // formed from zero. The row and column kernels rebuild P = exp2((fl(S c) - m2) - L2) and dP the same way,
+    // so on a row whose probability sits on one key that key's P is exactly 2^-L2 and dP - z, Gam - r, E1 - t
+    // are differences of consistently rounded values. P from the forward's lse instead carries the rounding
+    // of lse and of S against it (~2e-6 relative at |lse| ~ 30), which those differences amplify: G_Q, G_K, G_V
+    // then miss 1e-5 on such rows.
+    float* z = row_ws + 2 * nrows;
+    float* m2 = row_ws + 3 * nrows;
+    float* l2 = row_ws + 4 * nrows;
+    const int rc = run_dq(s, q, k, v, nullptr, false, theria::kRowOwnStats, dout, lse, z, nullptr, st,
+                          "theria_sdpa_bwd_bwd (row statistics)", m2, l2);
+    if (rc != THERIA_OK) return rc;
+    bp.delta = z;
+    bp.lse = m2;
+    bp.row_l2 = l2;
+  }
   if (s.dtype != THERIA_DTYPE_F32 && s.T > 0) {
     // 16-bit inputs: a 16-bit forward's lse comes from rounded probabilities, so P rebuilt from it sums to one
     // only within ~2^-9, and on peaked rows the second-order terms (Gam - r, dP - z, E1 - t) are differences

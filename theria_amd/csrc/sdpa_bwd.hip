@@ -11,7 +11,8 @@
 // dP^T = V dO^T with Q and dO in registers as B operands and K / V rows from LDS, seeds dP with
 // -delta so the MFMA yields dP - delta directly, rebuilds P = exp2(S scale log2e - lse log2e), and
 // accumulates dQ^T += K^T dS^T with K^T from the LDS transpose read and dS^T straight from the
-// accumulator tile. It also computes delta from O and dO at the start and writes it for dkdv_kernel.
+// accumulator tile. It also computes delta (16-bit: from O and dO at the start; float32, and 16-bit blocks
+// holding a peaked row: sum_j P dP / sum_j P in a pass over the keys) and writes it for dkdv_kernel.
 // dkdv_kernel (second): lane per key. Each wave owns KT tiles of 32 keys (K and V fragments in
 // registers as B operands) and walks the query rows in tiles of 64 staged in LDS; S = Q K^T and
 // dP = dO V^T land with one key per lane, so P and dS are directly the A operands of
@@ -84,14 +85,14 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DQ_MINW : 1)) void dq_kernel(const
     lse2[j] = lse == -THERIA_INF ? THERIA_INF : lse * kLog2e;  // a row without visible keys has P = 0
     peaked |= qvalid && lse_peaked(lse);
     del[j] = 0.f;
-    if (p.row_term == kRowFromO) {
+    if (sizeof(T) == 2 && p.row_term == kRowFromO) {
       // delta = dO . O over this lane's half of the head dim (the dO fragment's columns), then the pair
       float part = 0.f;
       if (qvalid) {
 #pragma unroll
         for (int c = 0; c < NKC; ++c) {
           const F od = of[j][c];
-          if constexpr (sizeof(T) == 2) {
+          if constexpr (sizeof(T) == 2) {  // (float32 forms the row term in the pass below)
             const int col = c * 16 + 8 * g;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
@@ -102,9 +103,6 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DQ_MINW : 1)) void dq_kernel(const
                 part += ov * (float)od[e];
               }
             }
-          } else {
-            const int col = 2 * c + g;
-            if (col < s.D) part += ((const float*)p.o.p + b * p.o.sb + h * p.o.sh)[(int64_t)myq * p.o.sr + col] * od;
           }
         }
       }
@@ -114,7 +112,6 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DQ_MINW : 1)) void dq_kernel(const
       del[j] = qvalid ? p.delta[rowbase + myq] : 0.f;
     }
   }
-  if (!p.dq.p && p.row_term < kRowFrozen) return;  // only dO . O was requested (uniform over the grid)
   const float c2 = s.scale * kLog2e;
 
   int kend = s.M;
@@ -123,13 +120,25 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DQ_MINW : 1)) void dq_kernel(const
 
   // The row term from a pass over the key tiles: always for the frozen / normalised forms, and (16-bit) for a
   // workgroup holding a peaked row in place of dO . O, whose 16-bit P rounding in the forward's PV product
-  // a peaked row does not average out. The dK/dV kernel reads the same delta.
-  bool exact_row_term = p.row_term >= kRowFrozen;
+  // a peaked row does not average out. The dK/dV kernel reads the same delta, so this pass runs whether or
+  // not dQ is wanted.
+  // Float32 always takes the pass in place of dO . O (the reference's own row term, z = sum_j dP_ij P_ij,
+  // theria/attention/triton_sdpa_backward.py:312-353): on a row whose probability sits on one key dP - z ~ 0
+  // there, and z from the forward's O would leave the roundings of O and of dP against it (~2e-5 in dQ where
+  // the bar is 1e-5); from the same P and dP the difference keeps only z's own rounding.
+  bool exact_row_term = p.row_term >= kRowFrozen || (sizeof(T) == 4 && p.row_term == kRowFromO);
   if (sizeof(T) == 2 && p.row_term == kRowFromO) exact_row_term = __syncthreads_or(__any(peaked));
+  if (!p.dq.p && !exact_row_term) return;  // only dO . O or the given row term was needed (uniform)
   if (exact_row_term) {
-    float a_part[QT], l_part[QT], p_mx[QT];
+    // own: float32 row statistics from these scores alone (kRowOwnStats), with a running max m_run of
+    // fl(S c2) over this lane's keys (the partial sums are rescaled when it grows)
+    const bool own = sizeof(T) == 4 && p.row_term == kRowOwnStats;
+    float a_part[QT], l_part[QT], p_mx[QT], m_run[QT];
 #pragma unroll
-    for (int j = 0; j < QT; ++j) a_part[j] = l_part[j] = p_mx[j] = 0.f;
+    for (int j = 0; j < QT; ++j) {
+      a_part[j] = l_part[j] = p_mx[j] = 0.f;
+      m_run[j] = -THERIA_INF;
+    }
     TileStage<T, BN, DP, NT> pK, pV;
     for (int kt = 0; kt < nkt; ++kt) {
       const int k0 = kt * BN;
@@ -156,6 +165,28 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DQ_MINW : 1)) void dq_kernel(const
 #pragma unroll
       for (int j = 0; j < QT; ++j) {
         const int lim = CAUSAL ? min(s.M, q0w + 32 * j + li + 1) : s.M;  // first key this query cannot see
+        if (own) {
+          float t[16];
+          float mt = m_run[j];
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            t[r] = k0 + acc_row(r, g) < lim ? mul_rn(sc[j][r], c2) : -THERIA_INF;
+            mt = fmaxf(mt, t[r]);
+          }
+          if (mt > m_run[j]) {  // m_run = -inf: the partial sums are still 0
+            const float f = fast_exp2(m_run[j] - mt);
+            a_part[j] *= f;
+            l_part[j] *= f;
+            m_run[j] = mt;
+          }
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float pv = t[r] > -THERIA_INF ? fast_exp2(t[r] - m_run[j]) : 0.f;  // (m_run finite then)
+            a_part[j] = fmaf(pv, dpp[j][r], a_part[j]);
+            l_part[j] += pv;
+          }
+          continue;
+        }
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const float pv = k0 + acc_row(r, g) < lim ? fast_exp2(fmaf(sc[j][r], c2, -lse2[j])) : 0.f;
@@ -167,12 +198,22 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DQ_MINW : 1)) void dq_kernel(const
     }
 #pragma unroll
     for (int j = 0; j < QT; ++j) {
+      float mm = -THERIA_INF;
+      if (own) {  // both halves of the row onto the common max
+        mm = pair_max(m_run[j]);
+        const float f = m_run[j] > -THERIA_INF ? fast_exp2(m_run[j] - mm) : 0.f;
+        a_part[j] *= f;
+        l_part[j] *= f;
+      }
       const float a = pair_sum(a_part[j]), l = pair_sum(l_part[j]), pm = pair_max(p_mx[j]);
       del[j] = p.row_term == kRowFrozen ? a : (l > 0.f ? a / l : 0.f);
       const int myq = q0w + 32 * j + li;
       if (myq < s.T && g == 0) {
         p.delta[rowbase + myq] = del[j];
-        if (p.lse_out) {  // flagged from the exact largest probability
+        if (own) {
+          p.lse_out[rowbase + myq] = l > 0.f ? mm : THERIA_INF;
+          p.l2_out[rowbase + myq] = l > 0.f ? __builtin_log2f(l) : 0.f;
+        } else if (p.lse_out) {  // flagged from the exact largest probability
           const float lin = p.lse[rowbase + myq];
           p.lse_out[rowbase + myq] = l > 0.f ? lse_with_flag(lin + __builtin_log2f(l) * kLn2, pm > kPeakedFrac * l) : lin;
         }
@@ -208,12 +249,16 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DQ_MINW : 1)) void dq_kernel(const
     }
     if (CAUSAL && k0 > q0w + 32 * QT - 1) continue;
 
+    // dP starts from -delta, so the MFMA yields dP - delta; float32 forms dP from zero and subtracts after, so
+    // that dP rounds exactly as in the row-term pass and dP - delta keeps only delta's own rounding (a row whose
+    // probability sits on one key has dP - delta ~ 0 there, and independent roundings of dP would remain).
+    constexpr bool SEED = sizeof(T) == 2;
     f32x16_t sc[QT], dp[QT];
 #pragma unroll
     for (int j = 0; j < QT; ++j) {
       sc[j] = zero16();
 #pragma unroll
-      for (int r = 0; r < 16; ++r) dp[j][r] = -del[j];
+      for (int r = 0; r < 16; ++r) dp[j][r] = SEED ? -del[j] : 0.f;
     }
 #pragma unroll
     for (int c = 0; c < NKC; ++c) {
@@ -238,7 +283,8 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DQ_MINW : 1)) void dq_kernel(const
 #pragma unroll
     for (int j = 0; j < QT; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sc[j][r] = fast_exp2(fmaf(sc[j][r], c2, -lse2[j])) * dp[j][r];  // dS^T
+      for (int r = 0; r < 16; ++r)
+        sc[j][r] = fast_exp2(fmaf(sc[j][r], c2, -lse2[j])) * (SEED ? dp[j][r] : dp[j][r] - del[j]);  // dS^T
 #pragma unroll
     for (int cc = 0; cc < NPC; ++cc) {
       F dsf[QT], dsl[QT];

@@ -11,8 +11,9 @@
 //  * Q and dO tiles reach LDS by DMA (sdpa_lds.hpp) into double buffers with one barrier per tile;
 //    the row terms -lse / scale and -delta of the next tile are loaded by the first 64 threads during
 //    the current tile and written beside them, with a flag for a tile holding a peaked row (largest
-//    probability above 1/16): such a tile forms P and dS as two 16-bit terms (hi + lo) and runs its
-//    subtiles one after the other.
+//    probability above 1/4, flagged in lse): the tile loop skips such tiles, and a workgroup that skipped
+//    any runs them after the loop (found from the lse flags) from exact float32 scores, with P and dS as
+//    two 16-bit terms (hi + lo), into the same dK / dV accumulators.
 //  * Scores are S = Q K^T with this lane's key in the column, so dV += P^T dO and dK += dS^T Q take
 //    P and dS straight from the accumulators (KACC order) and dO^T / Q^T from LDS transpose reads.
 //  * Phase order per 64-row half of a tile, i.e. two 32-query subtiles (scheduling barriers keep it):

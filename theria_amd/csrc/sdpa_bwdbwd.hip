@@ -116,6 +116,12 @@ __device__ __attribute__((always_inline)) inline void rows_block(const BwdBwdPar
   const float c2 = s.scale * kLog2e;
   const float lse2 = qvalid ? p.lse[row_id] * kLog2e : THERIA_INF;
   const float moff = lse2 == -THERIA_INF ? THERIA_INF : lse2;
+  // float32: P = exp2((fl(S c2) - m2) - L2) from the row's own statistics, and dP formed from zero, both as in
+  // the row-term pass that wrote m2, L2 and z (so the largest score gives exactly 2^-L2, and dP - z keeps only
+  // z's own rounding)
+  constexpr bool OWN = sizeof(T) == 4;
+  const float m2 = OWN && qvalid ? p.lse[row_id] : THERIA_INF;
+  const float l2 = OWN && qvalid ? p.row_l2[row_id] : 0.f;
   const float z = qvalid ? p.delta[row_id] : 0.f;
   float r_part = 0.f, t_part = 0.f;
   // 16-bit inputs: Gbar_S = P o ((Gam - r)(dP - z) + W - t), and for any row constants cr, ct
@@ -158,7 +164,7 @@ __device__ __attribute__((always_inline)) inline void rows_block(const BwdBwdPar
 
       f32x16_t sc = zero16(), gm = zero16(), w = zero16(), dpz;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) dpz[r] = -z;
+      for (int r = 0; r < 16; ++r) dpz[r] = OWN ? 0.f : -z;
 #pragma unroll
       for (int c = 0; c < NKC; ++c) {
         const F kfr = colsf(tK, 32 * st + li, c);
@@ -171,7 +177,8 @@ __device__ __attribute__((always_inline)) inline void rows_block(const BwdBwdPar
       const bool need_mask = (k0s + 32 > s.M) || (CAUSAL && k0s + 31 > q0w);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        float pv = fast_exp2(fmaf(sc[r], c2, -moff));
+        if constexpr (OWN) dpz[r] -= z;
+        float pv = OWN ? own_prob(sc[r], c2, m2, l2) : fast_exp2(fmaf(sc[r], c2, -moff));
         if (need_mask) {
           const int key = k0s + acc_row(r, g);
           if (key >= s.M || (CAUSAL && key > myq)) pv = 0.f;
@@ -408,7 +415,11 @@ __device__ __attribute__((always_inline)) inline void cols_block(const BwdBwdPar
   constexpr int NDT = DP / 32, NKC = DP / KC, NPC = 32 / KC, NSQ = BM / 32;
   constexpr int TB = DMA ? BM * DP * 2 : BM * PITCH * (int)sizeof(T);  // bytes per tile
   constexpr int TB2 = DMA ? TB : 16;                                    // second set (DMA only)
-  constexpr int RB = 4 * BM + 4;  // + whether the tile holds a row flagged peaked
+  // float32 (OWN): P = exp2((fl(S c2) - m2) - L2) with the rows' own m2 (in lse) and L2 (row_l2), and dP formed
+  // from zero, as in the row-term pass that wrote them
+  constexpr bool OWN = sizeof(T) == 4;
+  constexpr int FLAG = OWN ? 5 * BM : 4 * BM;  // row terms, then whether the tile holds a row flagged peaked
+  constexpr int RB = FLAG + 4;
   constexpr int RB2 = DMA ? RB : 4;
   __shared__ __attribute__((aligned(1024))) char sQ0[TB];
   __shared__ __attribute__((aligned(1024))) char sdO0[TB];
@@ -416,7 +427,7 @@ __device__ __attribute__((always_inline)) inline void cols_block(const BwdBwdPar
   __shared__ __attribute__((aligned(1024))) char sQ1[TB2];
   __shared__ __attribute__((aligned(1024))) char sdO1[TB2];
   __shared__ __attribute__((aligned(1024))) char sgQ1[TB2];
-  // row terms [lse * log2(e) | delta | r | t | peaked] of a tile
+  // row terms [lse * log2(e) (float32: m2) | delta | r | t | (float32: L2) | peaked] of a tile
   __shared__ __attribute__((aligned(16))) float sRow0[RB];
   __shared__ __attribute__((aligned(16))) float sRow1[RB2];
 
@@ -475,7 +486,7 @@ __device__ __attribute__((always_inline)) inline void cols_block(const BwdBwdPar
 
   // Row terms of a tile for thread tid < BM, held raw (rows past the end: lse = +inf) and converted when
   // stored: lse * log2(e) (+inf for rows past the end or without visible keys, so P = 0), delta, r, t.
-  float r_lse = THERIA_INF, r_z = 0.f, r_r = 0.f, r_t = 0.f;
+  float r_lse = THERIA_INF, r_z = 0.f, r_r = 0.f, r_t = 0.f, r_l2 = 0.f;
   auto load_rows = [&](int it) {
     if (tid < BM && it < nqt) {
       const int qq = qbeg + it * BM + tid;
@@ -484,16 +495,19 @@ __device__ __attribute__((always_inline)) inline void cols_block(const BwdBwdPar
       r_z = ok ? p.delta[rowbase + qq] : 0.f;
       r_r = ok ? p.r_row[rowbase + qq] : 0.f;
       r_t = ok ? p.t_row[rowbase + qq] : 0.f;
+      if constexpr (OWN) r_l2 = ok ? p.row_l2[rowbase + qq] : 0.f;
     }
   };
   auto store_rows = [&](float* sr) {
     if (tid < BM) {
-      sr[tid] = __builtin_isinf(r_lse) ? THERIA_INF : r_lse * kLog2e;
+      // float32: m2 as it is (+inf for a row without visible keys or past the end, so P = 0)
+      sr[tid] = OWN ? r_lse : (__builtin_isinf(r_lse) ? THERIA_INF : r_lse * kLog2e);
       sr[BM + tid] = r_z;
       sr[2 * BM + tid] = r_r;
       sr[3 * BM + tid] = r_t;
-      const bool pk = __any(lse_peaked(r_lse));  // the tile's rows are the lanes of wave 0
-      if (tid == 0) sr[4 * BM] = pk ? 1.f : 0.f;
+      if constexpr (OWN) sr[4 * BM + tid] = r_l2;
+      const bool pk = !OWN && __any(lse_peaked(r_lse));  // the tile's rows are the lanes of wave 0
+      if (tid == 0) sr[FLAG] = pk ? 1.f : 0.f;
     }
   };
 
@@ -510,7 +524,7 @@ __device__ __attribute__((always_inline)) inline void cols_block(const BwdBwdPar
       if (CAUSAL && kw0 > q0s + 31) continue;
 
       f32x16_t sc = zero16(), gm = zero16(), w = zero16(), dpz;
-      f32x4_t l4[4], z4[4], r4[4], t4[4];
+      f32x4_t l4[4], z4[4], r4[4], t4[4], lo4[4];
 #pragma unroll
       for (int qd = 0; qd < 4; ++qd) {
         const int o = 32 * sq + 8 * qd + 4 * g;
@@ -518,8 +532,9 @@ __device__ __attribute__((always_inline)) inline void cols_block(const BwdBwdPar
         z4[qd] = *reinterpret_cast<const f32x4_t*>(sr + BM + o);
         r4[qd] = *reinterpret_cast<const f32x4_t*>(sr + 2 * BM + o);
         t4[qd] = *reinterpret_cast<const f32x4_t*>(sr + 3 * BM + o);
+        if constexpr (OWN) lo4[qd] = *reinterpret_cast<const f32x4_t*>(sr + 4 * BM + o);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) dpz[4 * qd + e] = -z4[qd][e];
+        for (int e = 0; e < 4; ++e) dpz[4 * qd + e] = OWN ? 0.f : -z4[qd][e];
       }
 #pragma unroll
       for (int c = 0; c < NKC; ++c) {
@@ -536,7 +551,8 @@ __device__ __attribute__((always_inline)) inline void cols_block(const BwdBwdPar
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int qd = r >> 2, e = r & 3;
-        float pv = fast_exp2(fmaf(sc[r], c2, -l4[qd][e]));
+        if constexpr (OWN) dpz[r] -= z4[qd][e];
+        float pv = OWN ? own_prob(sc[r], c2, l4[qd][e], lo4[qd][e]) : fast_exp2(fmaf(sc[r], c2, -l4[qd][e]));
         if (!kvalid) pv = 0.f;
         if (diag && mykey > q0s + acc_row(r, g)) pv = 0.f;
         const float gam = s.scale * gm[r];
@@ -590,7 +606,7 @@ __device__ __attribute__((always_inline)) inline void cols_block(const BwdBwdPar
   auto compute = [&](int it, const char* tQ, const char* tO, const char* tgQ,
                      const float* sr) __attribute__((always_inline)) {
     // uniform: every thread reads the same flag
-    const bool pk = sizeof(T) == 2 && __builtin_amdgcn_readfirstlane(__float_as_uint(sr[4 * BM])) != 0u;
+    const bool pk = sizeof(T) == 2 && __builtin_amdgcn_readfirstlane(__float_as_uint(sr[FLAG])) != 0u;
     pk_any |= pk;  // run after the loop, so the loop's schedule holds only the one-term products
     if (!pk) tile(no_split, it, tQ, tO, tgQ, sr);
   };

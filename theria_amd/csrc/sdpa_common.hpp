@@ -97,6 +97,19 @@ __device__ __forceinline__ float pair_sum(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// a * b rounded once and never fused into a following add: the float32 kernels form x = fl(S c) - m2 from
+// the same fl(S c) that the row max m2 was taken over, so the row's largest score gives x = 0 exactly.
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+
+// float32 probability from the row's own statistics (kRowOwnStats): exp2((fl(S c) - m2) - L2). m2 = +inf
+// (a row without visible keys, or past the end) gives 0.
+__device__ __forceinline__ float own_prob(float s_raw, float c2, float m2, float l2) {
+  return fast_exp2((mul_rn(s_raw, c2) - m2) - l2);
+}
+
 // Peaked rows. With 16-bit inputs the lowest mantissa bit of each lse the forward writes marks a row whose
 // largest probability may exceed 1/4 (kPeakedFrac); the backward kernels read it to take their exact path
 // there (two-term 16-bit operands, the row term from a pass over the keys). Setting the bit moves lse by at

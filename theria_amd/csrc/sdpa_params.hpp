@@ -45,6 +45,9 @@ enum RowTerm : int {
   kRowGiven = 1,    // read from delta
   kRowFrozen = 2,   // sum_j P_ij dP_ij with P = exp(S - lse) exactly as given (frozen statistics)
   kRowNormalized = 3,  // sum_j P_ij dP_ij / sum_j P_ij: the exact softmax's row term for this lse
+  kRowOwnStats = 4,    // float32: the row's own statistics from this kernel's scores, ignoring lse: m2 = max_j
+                       // fl(S_ij scale log2 e) (to lse_out), L2 = log2 sum_j exp2(fl(S_ij scale log2 e) - m2) (to
+                       // l2_out) and sum_j P_ij dP_ij / sum_j P_ij (to delta), with dP formed from zero
 };
 
 // dQ pass of the backward (dq.p may be null: the row term only). 16-bit inputs: peaked rows are flagged in lse.
@@ -57,8 +60,10 @@ struct DqParams {
   float* delta;
   MutView dq;
   // optional, with a row-term pass (blocks taking it): lse + ln(sum_j P_ij), the row's exact normaliser for P
-  // rebuilt from lse, flagged peaked from the row's exact largest probability (above 1/4)
+  // rebuilt from lse, flagged peaked from the row's exact largest probability (above 1/4); with kRowOwnStats
+  // the row max m2 (+inf for a row without visible keys)
   float* lse_out;
+  float* l2_out;  // kRowOwnStats: L2 (0 for a row without visible keys)
 };
 
 // dK / dV pass of the backward (dv_only: no V, dK not computed).
@@ -81,10 +86,13 @@ struct JvpParams {
   bool normalize;
 };
 
+// lse: 16-bit inputs, the row normaliser (natural log, peaked rows flagged); float32 inputs, the row max m2 of
+// fl(S scale log2 e) with row_l2 = L2, so that P = exp2((fl(S scale log2 e) - m2) - L2) (kRowOwnStats).
 struct BwdBwdParams {
   Shape s;
   View q, k, v, dout, gq, gk, gv;
   const float* lse;
+  const float* row_l2;  // float32 inputs only
   const float* delta;
   float* r_row;
   float* t_row;
