@@ -329,11 +329,12 @@ def extras_c4():
         qg, kg, vg = (t.clone().requires_grad_(True) for t in (q, k, v))
 
         def hvp():
+            # H v = d/dx <grad L, v>: the gradient taken with create_graph, then its vector-Jacobian product with v
+            # (grad_outputs), the loss formed in the input dtype as hip_sdpa_hvp forms dO = O - T
             o2 = hip_sdpa(qg, kg, vg)
-            loss = 0.5 * ((o2.float() - T_.float()) ** 2).sum()
+            loss = 0.5 * ((o2 - T_) ** 2).sum()
             g = torch.autograd.grad(loss, (qg, kg, vg), create_graph=True)
-            dot = sum((a.float() * b.float()).sum() for a, b in zip(g, (vq, vk, vv)))
-            return torch.autograd.grad(dot, (qg, kg, vg))
+            return torch.autograd.grad(g, (qg, kg, vg), grad_outputs=(vq, vk, vv))
 
         out[f"hvp_ms_{name}"] = round(_time(hvp, 10), 4)
         # the same HVP from the kernels directly (forward, double backward, backward of J v; no autograd graph)

@@ -112,3 +112,14 @@ def test_score_kernels_reject_causal():
     assert lib.theria_qk_scores(ctypes.byref(prob), None, None, None, 1, None) == _lib.ERR_CONTRACT
     assert "causal" in lib.theria_last_error().decode()
     assert lib.theria_qk_softmax(ctypes.byref(prob), None, None, None, None) == _lib.ERR_CONTRACT
+
+
+def test_torch_binding_loads_and_matches_the_abi():
+    """The tensor-level binding of the hot entry points (theria_amd/_theria_host) imports without a GPU and is
+    linked to the library of this ABI version."""
+    from theria_amd import _lib, _ops
+
+    host = _ops._host()
+    assert host.abi_version() == _lib.ABI_VERSION
+    for name in ("fwd", "bwd", "jvp", "bwd_bwd"):
+        assert callable(getattr(host, name))

@@ -465,3 +465,33 @@ def test_large_grids_ragged(S, H, causal, hip_device):
                               O.backward(qc[sl], kc[sl], vc[sl], doc[sl], s, causal)):
             close(a, r, dt, f"{name}[{b},{h}]")
     torch.testing.assert_close(dv.double().sum(2), do.double().sum(2), rtol=0, atol=0.5)
+
+
+def test_caller_given_outputs_are_checked(hip_device):
+    """bwd / bwd_bwd write into caller-given outputs only of the exact shape, dtype and row layout (the torch
+    binding checks them before any launch), and results written there equal fresh ones."""
+    dt, B, H, T, M, D = torch.bfloat16, 1, 2, 70, 90, 64
+    q, k, v, do, gq, gk, gv = (make(sh, dt, hip_device, 200 + i)[0] for i, sh in
+                               enumerate([(B, H, T, D), (B, H, M, D), (B, H, M, D), (B, H, T, D), (B, H, T, D),
+                                          (B, H, M, D), (B, H, M, D)]))
+    s = 1 / math.sqrt(D)
+    print("[caller-given outputs]", flush=True)
+    o, lse, _, _ = _ops.fwd(q, k, v, s, False)
+    ref = _ops.bwd(q, k, v, o, lse, do, s, False)
+    # a row-strided output (row stride 2 D, last dimension contiguous) is accepted
+    dk_strided = torch.empty(B, H, M, 2 * D, dtype=dt, device=hip_device)[..., :D]
+    outs = (torch.empty_like(q), dk_strided, torch.empty_like(v))
+    got = _ops.bwd(q, k, v, o, lse, do, s, False, out=outs)
+    for name, a, b in zip(("dQ", "dK", "dV"), got[:3], ref[:3]):
+        assert torch.equal(a, b), f"{name} written to a caller-given output differs"
+    assert got[1].data_ptr() == dk_strided.data_ptr()
+    for bad in (torch.empty(B, H, M - 1, D, dtype=dt, device=hip_device),            # wrong rows
+                torch.empty(B, H, M, D, dtype=torch.float32, device=hip_device),    # wrong dtype
+                torch.empty(B, H, D, M, dtype=dt, device=hip_device).transpose(-1, -2)):  # last dim strided
+        with pytest.raises(AssertionError):
+            _ops.bwd(q, k, v, o, lse, do, s, False, out=(torch.empty_like(q), bad, torch.empty_like(v)))
+        with pytest.raises(AssertionError):
+            _ops.bwd_bwd(q, k, v, o, do, lse, None, gq, gk, gv, s, False,
+                         out=(torch.empty_like(q), bad, torch.empty_like(v)))
+    with pytest.raises(AssertionError, match="dout"):
+        _ops.bwd(q, k, v, o, lse, do[:, :, :-1], s, False)

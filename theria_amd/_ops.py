@@ -91,6 +91,27 @@ class _OnDevice:
         return False
 
 
+_HOST = None
+
+
+def _host():
+    """The torch binding of the hot entry points (theria_amd/csrc/host/theria_host.cpp), loaded once after the
+    C ABI library. There is no fallback: a missing binding raises, as a missing library does."""
+    global _HOST
+    if _HOST is None:
+        _lib.load()
+        try:
+            from . import _theria_host as host
+        except ImportError as e:
+            raise RuntimeError("theria_amd: the torch binding _theria_host is not built. Run `python -m "
+                               "theria_amd.build` (needs hipcc and g++) before using the HIP SDPA operators.") from e
+        if host.abi_version() != _lib.ABI_VERSION:
+            raise RuntimeError(f"theria_amd: _theria_host is linked to ABI {host.abi_version()}, expected "
+                               f"{_lib.ABI_VERSION}; rebuild it")
+        _HOST = host
+    return _HOST
+
+
 def _problem(q: torch.Tensor, k: torch.Tensor, scale: float, causal: bool) -> _lib.Problem:
     B, H, T, D = q.shape
     return _lib.Problem(_DTYPE_CODE[q.dtype], B, H, T, k.shape[2], D, float(scale), 1 if causal else 0)
@@ -129,14 +150,6 @@ def check_inputs(q, k, v, what: str = "theria_amd SDPA", require_v: bool = True)
         raise AssertionError(f"{what}: sizes exceed the 32-bit row index range")
 
 
-def _out_like(t: torch.Tensor, shape, ref: torch.Tensor, name: str) -> torch.Tensor:
-    """A caller-given output: the shape, dtype and device the entry point writes, last dimension contiguous."""
-    if tuple(t.shape) != tuple(shape) or t.dtype != ref.dtype or t.device != ref.device or t.stride(-1) != 1:
-        raise AssertionError(f"{name} must be a {ref.dtype} tensor of shape {tuple(shape)} on {ref.device} "
-                             f"with a contiguous last dimension")
-    return t
-
-
 def _like_rows(t: torch.Tensor | None, ref: torch.Tensor, rows: int, name: str) -> torch.Tensor | None:
     """Cast a (B,H,rows,D) operand to the compute dtype and check its shape."""
     if t is None:
@@ -151,11 +164,14 @@ def _like_rows(t: torch.Tensor | None, ref: torch.Tensor, rows: int, name: str) 
     return _rowmajor(t)
 
 
-def fwd(q, k, v, scale: float, causal: bool, out_fp32: bool = False, stats: bool = False):
+def fwd(q, k, v, scale: float, causal: bool, out_fp32: bool = False, stats: bool = False, checked: bool = True):
     """O, lse (and the reference's m, l when stats=True). O is float32 when out_fp32. With 16-bit inputs the
     lowest mantissa bit of lse flags the peaked rows (largest probability above 1/4), which the backward
-    takes on its exact path."""
-    return _fwd(q, k, v, scale, causal, out_fp32, stats, stats)
+    takes on its exact path. checked=False skips the Python-side input checks (for callers that made them);
+    shapes are still checked by the binding and the C ABI."""
+    if checked:
+        check_inputs(q, k, v)
+    return _host().fwd(q, k, v, float(scale), bool(causal), bool(out_fp32), bool(stats))
 
 
 def lse_from_stats(m, l, peaked_bits: bool = True):
@@ -170,54 +186,15 @@ def lse_from_stats(m, l, peaked_bits: bool = True):
     return lse
 
 
-def _fwd(q, k, v, scale, causal, out_fp32, want_m, want_l):
-    check_inputs(q, k, v)
-    q, k, v = _rowmajor(q), _rowmajor(k), _rowmajor(v)
-    B, H, T, D = q.shape
-    dev = q.device
-    o = torch.empty((B, H, T, D), dtype=torch.float32 if out_fp32 else q.dtype, device=dev)
-    lse = torch.empty((B, H, T), dtype=torch.float32, device=dev)
-    m = torch.empty_like(lse) if want_m else None
-    l = torch.empty_like(lse) if want_l else None
-    lib = _lib.load()
-    prob = _problem(q, k, scale, causal)
-    with _OnDevice(dev):
-        rc = lib.theria_sdpa_fwd(
-            ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(o), 1 if out_fp32 else 0, _fp(lse), _fp(m), _fp(l),
-            _stream(dev),
-        )
-    _lib.check(rc, "theria_sdpa_fwd")
-    return o, lse, m, l
-
-
-def bwd(q, k, v, o, lse, do, scale: float, causal: bool, need_dq: bool = True, need_dk: bool = True, out=None):
-    """dQ, dK, dV (input dtype) and the row term delta = rowsum(dO * O) (float32; formed exactly on query
-    blocks that hold a row flagged peaked in lse). out: (dq, dk, dv) tensors to write instead of new ones."""
-    check_inputs(q, k, v)
-    q, k, v = _rowmajor(q), _rowmajor(k), _rowmajor(v)
-    B, H, T, D = q.shape
-    M = k.shape[2]
-    do = _like_rows(do, q, T, "dout")
-    o = _rowmajor(o)
-    if tuple(o.shape) != (B, H, T, D):
-        raise AssertionError("o must have shape (B,H,T,D)")
-    o_f32 = o.dtype == torch.float32 and q.dtype != torch.float32
-    if not o_f32 and o.dtype != q.dtype:
-        o = o.to(q.dtype)
-    lse = lse.contiguous()
-    dev = q.device
-    delta = torch.empty((B, H, T), dtype=torch.float32, device=dev)
-    if out is not None:
-        dq, dk, dv = (_out_like(t, (B, H, n, D), q, name) for t, n, name in zip(out, (T, M, M), ("dq", "dk", "dv")))
-    else:
-        dq = torch.empty((B, H, T, D), dtype=q.dtype, device=dev) if need_dq else None
-        dk = torch.empty((B, H, M, D), dtype=q.dtype, device=dev) if need_dk else None
-        dv = torch.empty((B, H, M, D), dtype=q.dtype, device=dev)
-    prob = _problem(q, k, scale, causal)
-    with _OnDevice(dev):
-        bwd_dq(prob, q, k, v, o, o_f32, do, lse, delta, dq)
-        bwd_dkdv(prob, q, k, v, do, lse, delta, dk, dv)
-    return dq, dk, dv, delta
+def bwd(q, k, v, o, lse, do, scale: float, causal: bool, need_dq: bool = True, need_dk: bool = True, out=None,
+        checked: bool = True):
+    """dQ, dK, dV (input dtype) and the row term delta (float32: dO . O for 16-bit inputs, formed exactly on query
+    blocks that hold a row flagged peaked in lse; sum_j P dP / sum_j P for float32). out: (dq, dk, dv) tensors to
+    write instead of new ones. checked=False skips the Python-side input checks."""
+    if checked:
+        check_inputs(q, k, v)
+    return _host().bwd(q, k, v, o, lse, do, float(scale), bool(causal), bool(need_dq), bool(need_dk),
+                       None if out is None else list(out))
 
 
 # The two backward kernels (theria_sdpa_bwd = bwd_dq then bwd_dkdv), on the current stream of the
@@ -270,77 +247,29 @@ def bwd_from_stats(q, k, v, do, lse, scale: float, causal: bool, need_dq: bool, 
     return dq, dk, (dv if need_dv else None)
 
 
-def jvp(q, k, v, o, lse, tq, tk, tv, scale: float, causal: bool, normalize: bool = True):
+def jvp(q, k, v, o, lse, tq, tk, tv, scale: float, causal: bool, normalize: bool = True, checked: bool = True):
     """Tangent of O along (tq, tk, tv) with P rebuilt from lse; o=None rebuilds O inside the kernel.
 
     normalize=True: the JVP of the exact softmax (P divided by its row sum), for the operator's own lse.
-    normalize=False: the reference's frozen-stats JVP, P = exp(S - lse) held as given (o is then not read)."""
-    check_inputs(q, k, v)
-    q, k, v = _rowmajor(q), _rowmajor(k), _rowmajor(v)
-    B, H, T, D = q.shape
-    M = k.shape[2]
-    tq = _like_rows(tq, q, T, "tq")
-    tk = _like_rows(tk, q, M, "tk")
-    tv = _like_rows(tv, q, M, "tv")
-    if o is not None:
-        if o.dtype != q.dtype:
-            o = None  # a float32 O of a low-precision op: rebuild it at full precision instead
-        else:
-            o = _rowmajor(o)
-    lse = lse.contiguous()
-    dev = q.device
-    out = torch.empty((B, H, T, D), dtype=q.dtype, device=dev)
-    lib = _lib.load()
-    prob = _problem(q, k, scale, causal)
-    with _OnDevice(dev):
-        rc = lib.theria_sdpa_jvp(
-            ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(o), _fp(lse), _tv(tq), _tv(tk), _tv(tv), _tv(out),
-            1 if normalize else 0, _stream(dev),
-        )
-    _lib.check(rc, "theria_sdpa_jvp")
-    return out
+    normalize=False: the reference's frozen-stats JVP, P = exp(S - lse) held as given (o is then not read).
+    checked=False skips the Python-side input checks."""
+    if checked:
+        check_inputs(q, k, v)
+    return _host().jvp(q, k, v, o, lse, tq, tk, tv, float(scale), bool(causal), bool(normalize))
 
 
-def bwd_bwd(q, k, v, o, do, lse, delta, gq, gk, gv, scale: float, causal: bool, noalloc: bool = False, out=None):
+def bwd_bwd(q, k, v, o, do, lse, delta, gq, gk, gv, scale: float, causal: bool, noalloc: bool = False, out=None,
+            checked: bool = True):
     """(G_Q, G_K, G_V, G_dO): VJP of the backward map with cotangents (gq, gk, gv) (None = zero).
     delta (the backward's row term) is not read: the library recomputes the row term; it may be None.
 
     noalloc: run theria_sdpa_bwd_bwd_noalloc, whose row workspace is the library's static device array
-    (5 * B * H * T up to 5 * 2^20), instead of a workspace allocated here."""
-    check_inputs(q, k, v)
-    q, k, v = _rowmajor(q), _rowmajor(k), _rowmajor(v)
-    B, H, T, D = q.shape
-    M = k.shape[2]
-    do = _like_rows(do, q, T, "dout")
-    gq = _like_rows(gq, q, T, "gq")
-    gk = _like_rows(gk, q, M, "gk")
-    gv = _like_rows(gv, q, M, "gv")
-    if o is not None:
-        o = _rowmajor(o) if o.dtype == q.dtype else None
-    lse = lse.contiguous()
-    if delta is not None:
-        delta = delta.contiguous()
-    dev = q.device
-    if out is not None:  # (G_Q, G_K, G_V) written to the given tensors
-        out_q, out_k, out_v = (_out_like(t, (B, H, n, D), q, name)
-                               for t, n, name in zip(out, (T, M, M), ("out_gq", "out_gk", "out_gv")))
-    else:
-        out_q = torch.empty((B, H, T, D), dtype=q.dtype, device=dev)
-        out_k = torch.empty((B, H, M, D), dtype=q.dtype, device=dev)
-        out_v = torch.empty((B, H, M, D), dtype=q.dtype, device=dev)
-    out_do = torch.empty((B, H, T, D), dtype=q.dtype, device=dev)
-    lib = _lib.load()
-    prob = _problem(q, k, scale, causal)
-    args = (ctypes.byref(prob), _tv(q), _tv(k), _tv(v), _tv(o), _tv(do), _fp(lse), _fp(delta), _tv(gq), _tv(gk),
-            _tv(gv), _tv(out_q), _tv(out_k), _tv(out_v), _tv(out_do))
-    with _OnDevice(dev):
-        if noalloc:
-            rc = lib.theria_sdpa_bwd_bwd_noalloc(*args, _stream(dev))
-        else:
-            ws = torch.empty((5 * B * H * T,), dtype=torch.float32, device=dev)
-            rc = lib.theria_sdpa_bwd_bwd(*args, _fp(ws), _stream(dev))
-    _lib.check(rc, "theria_sdpa_bwd_bwd_noalloc" if noalloc else "theria_sdpa_bwd_bwd")
-    return out_q, out_k, out_v, out_do
+    (5 * B * H * T up to 5 * 2^20), instead of a workspace allocated here. out: (G_Q, G_K, G_V) written to the
+    given tensors. checked=False skips the Python-side input checks."""
+    if checked:
+        check_inputs(q, k, v)
+    return _host().bwd_bwd(q, k, v, o, do, lse, gq, gk, gv, float(scale), bool(causal), bool(noalloc),
+                           None if out is None else list(out))
 
 
 def qk_scores(q, k, out_f32: bool = True):

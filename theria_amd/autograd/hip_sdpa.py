@@ -72,21 +72,22 @@ class SDPABackwardOp(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, o, lse, dout, scale, causal):
-        dq, dk, dv, delta = _ops.bwd(q, k, v, o, lse, dout, scale, causal)
-        ctx.save_for_backward(q, k, v, o, lse, dout, delta)
+        dq, dk, dv, _ = _ops.bwd(q, k, v, o, lse, dout, scale, causal, checked=False)
+        ctx.save_for_backward(q, k, v, o, lse, dout)
         ctx.scale = scale
         ctx.causal = causal
         return dq, dk, dv
 
     @staticmethod
     def backward(ctx, gq, gk, gv):
-        q, k, v, o, lse, dout, delta = ctx.saved_tensors
+        q, k, v, o, lse, dout = ctx.saved_tensors
         if gq is None and gk is None and gv is None:
             return None, None, None, None, None, None, None, None
         if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (q, k, v, dout, gq, gk, gv)):
             g_q, g_k, g_v, g_do = _differentiable_double_backward(q, k, v, dout, gq, gk, gv, ctx.scale, ctx.causal)
             return g_q, g_k, g_v, None, None, g_do, None, None
-        g_q, g_k, g_v, g_do = _ops.bwd_bwd(q, k, v, o, dout, lse, delta, gq, gk, gv, ctx.scale, ctx.causal)
+        g_q, g_k, g_v, g_do = _ops.bwd_bwd(q, k, v, o, dout, lse, None, gq, gk, gv, ctx.scale, ctx.causal,
+                                           checked=False)
         return g_q, g_k, g_v, None, None, g_do.to(dout.dtype), None, None
 
 
@@ -118,7 +119,7 @@ class SDPAOp(torch.autograd.Function):
     @staticmethod
     def jvp(ctx, tq, tk, tv, _ts, _tc, _tf):
         q, k, v, o, lse = ctx.saved_tensors
-        to = _ops.jvp(q, k, v, o, lse, tq, tk, tv, ctx.scale, ctx.causal, normalize=True)
+        to = _ops.jvp(q, k, v, o, lse, tq, tk, tv, ctx.scale, ctx.causal, normalize=True, checked=False)
         if to.dtype != o.dtype:
             to = to.to(o.dtype)
         return to, None
@@ -187,9 +188,8 @@ def hip_sdpa_hvp(q, k, v, vq, vk, vv, *, weight=None, target=None, causal: bool 
             dout = weight.to(o.dtype)
         else:
             dout = torch.ones_like(o)
-        delta = None  # the double backward forms its own row term
         if target is None:
-            return _ops.bwd_bwd(q, k, v, o, dout, lse, delta, vq, vk, vv, float(scale), bool(causal))[:3]
+            return _ops.bwd_bwd(q, k, v, o, dout, lse, None, vq, vk, vv, float(scale), bool(causal), checked=False)[:3]
         # both results as views of one flat buffer each, so that their sum is one full-grid launch
         B, H, T, D = q.shape
         M = k.shape[2]
@@ -197,8 +197,9 @@ def hip_sdpa_hvp(q, k, v, vq, vk, vv, *, weight=None, target=None, causal: bool 
         shapes = ((B, H, T, D), (B, H, M, D), (B, H, M, D))
         flat_h, flat_j = (torch.empty(sum(sizes), dtype=q.dtype, device=q.device) for _ in range(2))
         hs, js = ([f.view(sh) for f, sh in zip(buf.split(sizes), shapes)] for buf in (flat_h, flat_j))
-        g_do = _ops.bwd_bwd(q, k, v, o, dout, lse, delta, vq, vk, vv, float(scale), bool(causal), out=hs)[3]
-        _ops.bwd(q, k, v, o, lse, g_do.to(o.dtype), float(scale), bool(causal), out=js)
+        g_do = _ops.bwd_bwd(q, k, v, o, dout, lse, None, vq, vk, vv, float(scale), bool(causal), out=hs,
+                            checked=False)[3]
+        _ops.bwd(q, k, v, o, lse, g_do.to(o.dtype), float(scale), bool(causal), out=js, checked=False)
         flat_h.add_(flat_j)
         return tuple(hs)
 

@@ -1,8 +1,10 @@
-"""Build libtheria_sdpa.so (the gfx950 HIP kernels + C ABI) in-tree.
+"""Build libtheria_sdpa.so (the gfx950 HIP kernels + C ABI) and its torch binding in-tree.
 
 Usage: ``python -m theria_amd.build`` (or ``theria_amd.build.build()``). Every ``csrc/*.hip`` file is
 compiled for gfx950 in parallel into ``_build/`` at the repository root and linked into
-``theria_amd/lib/libtheria_sdpa.so``. The library links against the HIP runtime by its soname
+``theria_amd/lib/libtheria_sdpa.so``. ``csrc/host/theria_host.cpp`` (host code only, g++) is compiled beside
+them and linked against that library into the Python module ``theria_amd/_theria_host*.so``, the tensor-level
+binding of the hot entry points that the autograd operator calls. The library links against the HIP runtime by its soname
 (libamdhip64.so.7), so inside a process that already imported torch it binds to the runtime torch
 loaded: one HIP runtime per process. Only the C ABI (``theria_*``) is exported: the host stubs of the
 kernel templates are weak symbols, and exported they would bind to another copy of this library loaded
@@ -63,19 +65,68 @@ def _compile(hipcc: str, src: Path) -> Path:
     return obj
 
 
+HOST_SRC = CSRC / "host" / "theria_host.cpp"
+
+
+def host_module_path() -> Path:
+    import sysconfig
+
+    return PKG_DIR / ("_theria_host" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def _torch_dirs():
+    import torch
+
+    root = Path(torch.__file__).resolve().parent
+    return root / "include", root / "lib", int(torch._C._GLIBCXX_USE_CXX11_ABI)
+
+
+def _compile_host() -> Path:
+    """The torch binding's object (host C++ only: torch, c10/hip and HIP runtime headers)."""
+    import sysconfig
+
+    inc, _, abi = _torch_dirs()
+    obj = BUILD_DIR / "theria_host.o"
+    cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-fvisibility=hidden", "-D__HIP_PLATFORM_AMD__",
+           f"-D_GLIBCXX_USE_CXX11_ABI={abi}", f"-I{inc}", f"-I{inc / 'torch' / 'csrc' / 'api' / 'include'}",
+           "-I/opt/rocm/include", f"-I{REPO_DIR / 'include'}", f"-I{sysconfig.get_paths()['include']}",
+           "-c", str(HOST_SRC), "-o", str(obj)]
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}")
+    return obj
+
+
+def _link_host(obj: Path) -> Path:
+    """Link the binding against libtheria_sdpa.so (found next to it through an $ORIGIN/lib run path)."""
+    _, lib, _ = _torch_dirs()
+    out = host_module_path()
+    tmp = out.with_suffix(".tmp")
+    cmd = ["g++", "-shared", "-fPIC", str(obj), "-o", str(tmp), f"-L{lib}", "-lc10", "-lc10_hip", "-ltorch",
+           "-ltorch_cpu", "-ltorch_python", f"-L{LIB_DIR}", "-ltheria_sdpa", "-Wl,-rpath,$ORIGIN/lib"]
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed: {' '.join(cmd)}\n{res.stdout}")
+    os.replace(tmp, out)
+    return out
+
+
 def build(verbose: bool = True, jobs: int | None = None) -> Path:
-    """Compile every kernel source and link the shared library. Always rebuilds."""
+    """Compile every kernel source and link the shared library, then the torch binding. Always rebuilds."""
     hipcc = _hipcc()
     BUILD_DIR.mkdir(parents=True, exist_ok=True)
     LIB_DIR.mkdir(parents=True, exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
-    jobs = jobs or min(len(sources), max(1, (os.cpu_count() or 4)))
+    jobs = jobs or min(len(sources) + 1, max(1, (os.cpu_count() or 4)))
     if verbose:
-        print(f"[theria_amd.build] compiling {len(sources)} sources for {ARCH} with {jobs} jobs", flush=True)
+        print(f"[theria_amd.build] compiling {len(sources)} sources for {ARCH} and the torch binding with {jobs} jobs",
+              flush=True)
     with _cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        host_obj = ex.submit(_compile_host)
         objs = list(ex.map(lambda s: _compile(hipcc, s), sources))
+        host_obj = host_obj.result()
     tmp = LIB_PATH.with_suffix(".so.tmp")
     vmap = BUILD_DIR / "exports.map"
     vmap.write_text(EXPORTS)
@@ -85,8 +136,9 @@ def build(verbose: bool = True, jobs: int | None = None) -> Path:
     if res.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{res.stdout}")
     os.replace(tmp, LIB_PATH)
+    host = _link_host(host_obj)
     if verbose:
-        print(f"[theria_amd.build] built {LIB_PATH}", flush=True)
+        print(f"[theria_amd.build] built {LIB_PATH} and {host.name}", flush=True)
     return LIB_PATH
 
 

@@ -1,140 +1,157 @@
 // Materialised score kernels behind the partial-fusion sdpa_custom backends on gfx950.
 //
-// qk_scores_kernel:  S = Q K^T (unscaled), written as a (B, H, T, M) tensor in float32 or in the input
-//                    dtype. Replaces _qk_kernel / _qk_kernel_fast (reference theria/attention/
-//                    triton_qk.py:24-64 and 402-453); the softmax and PV stay in PyTorch there too.
-// qk_softmax_kernel: P = softmax_row(scale Q K^T), written as a float32 (B, H, T, M) tensor. Replaces
-//                    _qk_softmax_kernel (triton_qk.py:128-194).
+// S = Q K^T (unscaled) as a (B, H, T, M) tensor in float32 or in the input dtype: replaces _qk_kernel /
+//   _qk_kernel_fast (reference theria/attention/triton_qk.py:24-64 and 402-453); the softmax and PV stay in
+//   PyTorch there too.
+// P = softmax_row(scale Q K^T) as a float32 (B, H, T, M) tensor: replaces _qk_softmax_kernel
+//   (triton_qk.py:128-194).
 //
-// Both compute the dot products with MFMA (32x32 output tiles per wave, fp32 accumulation: for float32
-// inputs v_mfma_f32_32x32x2_f32 forms exact float32 products and sums, the reference's "ieee" dot).
-// Operand fragments come straight from global memory (these backends exist for experiments; the fused
-// operator is the fast path). qk_softmax makes two passes over the keys: pass 1 with this lane's query
-// in the column (S^T = K Q^T) keeps an online row max and row sum per lane; pass 2 recomputes S with
-// the query in the row, so that each store instruction writes 32 consecutive keys of a row.
+// These kernels are bound by the write of the (B, H, T, M) output (1.07 GB in float32 at B4 H16 S2048), not by
+// the dot products, so the layout serves the stores:
+//  * one workgroup = 4 waves = 128 query rows of one (batch, head); each wave keeps its 32 queries' Q fragments
+//    in registers and the workgroup streams K in 64-key tiles through LDS (one global read of K per workgroup,
+//    register-prefetched one tile ahead);
+//  * scores are formed lane-per-query (S^T = K Q^T with MFMA, float32 accumulation: for float32 inputs
+//    v_mfma_f32_32x32x2_f32 forms exact float32 products and sums, the reference's "ieee" dot);
+//  * each wave writes its 32 x 32 subtiles of results into its own padded LDS buffer and reads them back
+//    row-major, 16 bytes per lane, so that one store instruction writes 8 rows x 32 consecutive keys (128 bytes
+//    each in float32) with non-temporal stores (the output is not read again by this kernel; K stays in L2).
+//    The buffer holds one subtile (4.5 KiB per wave), so five workgroups fit a CU's LDS and config 2's 4096
+//    waves are all resident at once;
+//  * P: a first pass over the key tiles keeps an online row max and sum per lane (the two lane halves of a
+//    query combined at the end), the second forms exp2(S scale log2 e - m) / l and stores it.
+#include <type_traits>
+
 #include "dispatch.hpp"
 #include "sdpa_common.hpp"
 
 namespace theria {
 
-template <typename T, int DP, bool OUT_F32>
-__global__ __launch_bounds__(256) void qk_scores_kernel(const ScoresParams p) {
+enum ScoreMode { kScoresF32 = 0, kScoresT = 1, kProbs = 2 };
+
+template <typename T, int DP, int MODE>
+__global__ __launch_bounds__(256) void scores_kernel(const ScoresParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
   constexpr int NKC = DP / MM::KC;
-  const Shape& s = p.s;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, li = lane & 31, g = lane >> 5;
-  const int nqb = (s.T + 63) / 64, nkb = (s.M + 63) / 64;
-  const int bid = blockIdx.x;
-  const int bh = bid / (nqb * nkb);
-  const int rem = bid - bh * nqb * nkb;
-  const int qb = rem / nkb, kb = rem - qb * nkb;
-  const int b = bh / s.H, h = bh - b * s.H;
-  const T* Q = (const T*)p.q.p + b * p.q.sb + h * p.q.sh;
-  const T* K = (const T*)p.k.p + b * p.k.sb + h * p.k.sh;
-  const int q0 = qb * 64 + (wave >> 1) * 32, k0 = kb * 64 + (wave & 1) * 32;
+  constexpr int NW = 4, NT = 64 * NW, BN = 64;
+  constexpr int PITCH = DP + 16 / (int)sizeof(T);  // K tile rows (padded)
+  constexpr int OP = 32 + 4;                        // output staging rows, in floats (padded against bank conflicts)
+  __shared__ __attribute__((aligned(16))) T sK[BN * PITCH];
+  __shared__ __attribute__((aligned(16))) float sO[NW][32 * OP];
 
-  f32x16_t acc = zero16();
-#pragma unroll
-  for (int c = 0; c < NKC; ++c) {
-    const F a = gload_frag<T>(Q, p.q.sr, q0 + li, s.T, c, s.D, s.vec);
-    const F bf = gload_frag<T>(K, p.k.sr, k0 + li, s.M, c, s.D, s.vec);
-    acc = MM::mma(a, bf, acc);
-  }
-  const int key = k0 + li;
-  if (key >= s.M) return;
-  const int64_t base = (int64_t)bh * s.T * s.M;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int row = q0 + acc_row(r, g);
-    if (row < s.T) {
-      if (OUT_F32)
-        ((float*)p.out)[base + (int64_t)row * s.M + key] = acc[r];
-      else
-        ((T*)p.out)[base + (int64_t)row * s.M + key] = (T)acc[r];
-    }
-  }
-}
-
-template <typename T, int DP>
-__global__ __launch_bounds__(256) void qk_softmax_kernel(const ScoresParams p) {
-  using MM = Mfma<T>;
-  using F = typename MM::frag_t;
-  constexpr int NKC = DP / MM::KC;
-  __shared__ __attribute__((aligned(16))) float sM[4][32];
-  __shared__ __attribute__((aligned(16))) float sL[4][32];
   const Shape& s = p.s;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, li = lane & 31, g = lane >> 5;
   const int nqb = (s.T + 127) / 128;
-  const int bh = blockIdx.x / nqb;
-  const int qb = blockIdx.x - bh * nqb;
+  const int bid = xcd_remap(blockIdx.x, gridDim.x);  // the query blocks of one head on one XCD (K shared in L2)
+  const int bh = bid / nqb;
+  const int qb = bid - bh * nqb;
   const int b = bh / s.H, h = bh - b * s.H;
   const T* Q = (const T*)p.q.p + b * p.q.sb + h * p.q.sh;
   const T* K = (const T*)p.k.p + b * p.k.sb + h * p.k.sh;
-  const int q0 = qb * 128 + wave * 32;
+  const int q0w = qb * 128 + wave * 32;
   const float c2 = s.scale * kLog2e;
 
   F qf[NKC];
 #pragma unroll
-  for (int c = 0; c < NKC; ++c) qf[c] = gload_frag<T>(Q, p.q.sr, q0 + li, s.T, c, s.D, s.vec);
+  for (int c = 0; c < NKC; ++c) qf[c] = gload_frag<T>(Q, p.q.sr, q0w + li, s.T, c, s.D, s.vec);
 
-  // pass 1: per-query max and sum of exp (this lane's query li, keys acc_row(r, g) of each tile)
-  float m = -THERIA_INF, l = 0.f;
-  for (int k0 = 0; k0 < s.M; k0 += 32) {
-    f32x16_t st = zero16();
+  const int nkt = (s.M + BN - 1) / BN;
+  TileStage<T, BN, DP, NT> stK;
+  // S^T of key tile kt for this wave's 32 queries: st[u] holds keys kt*BN + 32u + acc_row(r, g) of query li;
+  // keys past the end are -inf. Stages the tile (two barriers) and prefetches the next one.
+  auto tile_scores = [&](int kt, f32x16_t (&st)[2]) {
+    __syncthreads();  // every wave is done with the previous tile
+    stK.store(sK, PITCH);
+    __syncthreads();
+    if (kt + 1 < nkt) stK.load_any(K, p.k.sr, (kt + 1) * BN, s.M, s.D, s.vec);
 #pragma unroll
-    for (int c = 0; c < NKC; ++c) st = MM::mma(gload_frag<T>(K, p.k.sr, k0 + li, s.M, c, s.D, s.vec), qf[c], st);
-    float mx = -THERIA_INF;
+    for (int u = 0; u < 2; ++u) {
+      st[u] = zero16();
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      if (k0 + acc_row(r, g) >= s.M) st[r] = -THERIA_INF;
-      mx = fmaxf(mx, st[r]);
+      for (int c = 0; c < NKC; ++c) st[u] = MM::mma(lds_cols<T, KLIN>(sK, PITCH, 32 * u + li, 0, c), qf[c], st[u]);
+      if (kt * BN + 32 * u + 32 > s.M) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (kt * BN + 32 * u + acc_row(r, g) >= s.M) st[u][r] = -THERIA_INF;
+      }
     }
-    const float mnew = fmaxf(m, mx * c2);
-    if (mnew != -THERIA_INF) {
+  };
+
+  // softmax statistics of query li (log2 domain): max m and sum l of exp2(S c2 - m) over its keys
+  float mrow = 0.f, inv_l = 0.f;
+  if constexpr (MODE == kProbs) {
+    float m = -THERIA_INF, l = 0.f;
+    if (nkt > 0) stK.load_any(K, p.k.sr, 0, s.M, s.D, s.vec);
+    for (int kt = 0; kt < nkt; ++kt) {
+      f32x16_t st[2];
+      tile_scores(kt, st);
+      float mx = m;
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[u][r] * c2);
+      if (mx == -THERIA_INF) continue;  // no visible key yet (M = 0 never reaches here)
       float part = 0.f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) part += fast_exp2(fmaf(st[r], c2, -mnew));
-      l = l * fast_exp2(m - mnew) + part;
-      m = mnew;
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) part += fast_exp2(fmaf(st[u][r], c2, -mx));
+      l = l * fast_exp2(m - mx) + part;
+      m = mx;
     }
+    const float mt = pair_max(m);
+    const float lt = pair_sum(m == -THERIA_INF ? 0.f : l * fast_exp2(m - mt));
+    mrow = mt;
+    inv_l = lt > 0.f ? 1.f / lt : 0.f;
   }
-  // combine the two lane halves (each saw half of the keys of every tile)
-  const float mt = pair_max(m);
-  const float lt = pair_sum(m == -THERIA_INF ? 0.f : l * fast_exp2(m - mt));
-  if (g == 0) {
-    sM[wave][li] = mt;
-    sL[wave][li] = lt > 0.f ? 1.f / lt : 0.f;
-  }
-  __syncthreads();
 
-  // pass 2: P with the query in the row (register r <-> query acc_row(r, g)), 32 keys per store
-  const int64_t base = (int64_t)bh * s.T * s.M;
-  float mrow[16], irow[16];
+  using OutT = typename std::conditional<MODE == kScoresT, T, float>::type;
+  OutT* out = (OutT*)p.out + (int64_t)bh * s.T * s.M;
+  float* so = sO[wave];
+  // the output store: 8 lanes per row, 4 consecutive keys per lane (vector stores when the rows are aligned)
+  const bool vrows = (s.M % 4) == 0;
+  if (nkt > 0) stK.load_any(K, p.k.sr, 0, s.M, s.D, s.vec);
+  for (int kt = 0; kt < nkt; ++kt) {
+    f32x16_t st[2];
+    tile_scores(kt, st);
 #pragma unroll
-  for (int qd = 0; qd < 4; ++qd) {
-    const f32x4_t m4 = *reinterpret_cast<const f32x4_t*>(&sM[wave][8 * qd + 4 * g]);
-    const f32x4_t i4 = *reinterpret_cast<const f32x4_t*>(&sL[wave][8 * qd + 4 * g]);
+    for (int u = 0; u < 2; ++u) {
+      // this lane's values into the wave's buffer: row li (query), keys 8j + 4g .. + 3 of subtile u
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      mrow[4 * qd + e] = m4[e];
-      irow[4 * qd + e] = i4[e];
-    }
-  }
-  for (int k0 = 0; k0 < s.M; k0 += 32) {
-    f32x16_t st = zero16();
+      for (int j = 0; j < 4; ++j) {
+        f32x4_t v;
 #pragma unroll
-    for (int c = 0; c < NKC; ++c) st = MM::mma(qf[c], gload_frag<T>(K, p.k.sr, k0 + li, s.M, c, s.D, s.vec), st);
-    const int key = k0 + li;
-    if (key < s.M) {
+        for (int e = 0; e < 4; ++e) {
+          const float x = st[u][4 * j + e];
+          v[e] = MODE == kProbs ? (x == -THERIA_INF ? 0.f : fast_exp2(fmaf(x, c2, -mrow)) * inv_l) : x;
+        }
+        *reinterpret_cast<f32x4_t*>(so + li * OP + 8 * j + 4 * g) = v;
+      }
+      __builtin_amdgcn_wave_barrier();
+      const int col = 4 * (lane & 7);
+      const int key = kt * BN + 32 * u + col;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = q0 + acc_row(r, g);
-        if (row < s.T) {
-          const float pv = mrow[r] == -THERIA_INF ? 0.f : fast_exp2(fmaf(st[r], c2, -mrow[r])) * irow[r];
-          ((float*)p.out)[base + (int64_t)row * s.M + key] = pv;
+      for (int it = 0; it < 4; ++it) {
+        const int row = 8 * it + (lane >> 3);
+        const int q = q0w + row;
+        const f32x4_t v = *reinterpret_cast<const f32x4_t*>(so + row * OP + col);
+        if (q >= s.T || key >= s.M) continue;
+        OutT* dst = out + (int64_t)q * s.M + key;
+        if (vrows && key + 4 <= s.M) {
+          if constexpr (sizeof(OutT) == 4) {
+            __builtin_nontemporal_store(v, reinterpret_cast<f32x4_t*>(dst));
+          } else {
+            OutT w[4] = {(OutT)v[0], (OutT)v[1], (OutT)v[2], (OutT)v[3]};
+            __builtin_nontemporal_store(__builtin_bit_cast(i16x4_t, w), reinterpret_cast<i16x4_t*>(dst));
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (key + e < s.M) dst[e] = (OutT)v[e];
         }
       }
+      __builtin_amdgcn_wave_barrier();  // the buffer is rewritten by the next subtile
     }
   }
 }
@@ -145,19 +162,15 @@ struct ScoresLauncher {
     if constexpr (CAUSAL) {
       return hipErrorInvalidValue;  // the score backends have no mask
     } else {
-      const int64_t bh = (int64_t)p.s.B * p.s.H;
-      if (p.softmax) {
-        const int64_t nblk = (int64_t)((p.s.T + 127) / 128) * bh;
-        if (nblk == 0) return hipSuccess;
-        hipLaunchKernelGGL((qk_softmax_kernel<T, DP>), dim3((unsigned)nblk), dim3(256), 0, st, p);
-      } else {
-        const int64_t nblk = (int64_t)((p.s.T + 63) / 64) * ((p.s.M + 63) / 64) * bh;
-        if (nblk == 0) return hipSuccess;
-        if (p.out_f32)
-          hipLaunchKernelGGL((qk_scores_kernel<T, DP, true>), dim3((unsigned)nblk), dim3(256), 0, st, p);
-        else
-          hipLaunchKernelGGL((qk_scores_kernel<T, DP, false>), dim3((unsigned)nblk), dim3(256), 0, st, p);
-      }
+      const int64_t nblk = (int64_t)((p.s.T + 127) / 128) * p.s.B * p.s.H;
+      if (nblk == 0) return hipSuccess;
+      const dim3 grid((unsigned)nblk), block(256);
+      if (p.softmax)
+        hipLaunchKernelGGL((scores_kernel<T, DP, kProbs>), grid, block, 0, st, p);
+      else if (p.out_f32 || sizeof(T) == 4)
+        hipLaunchKernelGGL((scores_kernel<T, DP, kScoresF32>), grid, block, 0, st, p);
+      else
+        hipLaunchKernelGGL((scores_kernel<T, DP, kScoresT>), grid, block, 0, st, p);
       return hipGetLastError();
     }
   }
