@@ -250,42 +250,63 @@ def extras_c3():
     run = _step_fns(q, k, v, do, scale, True)
     ms = _time(run, 5, 2)
     useful = 14 * B * H * (S * (S + 1) / 2) * D  # unmasked elements only
-    fwd_t = _causal_tiles(S, 32, 64)  # forward at head dim 128: a wave's 32 queries x a 64-key tile
-    bwd_t = _causal_tiles(S, 32, 32)  # dQ, dK/dV: 32 queries x 32 keys per wave subtile
-    return {
+    counted = _kernel_tile_counts(q, k, v, do, scale, True)
+    n = S // 32
+    needed = B * H * n * (n + 1) // 2  # 32 x 32 (query, key) units holding an unmasked element (key <= query)
+    total = B * H * n * n
+    out = {
         "config": "B1 H32 S8192 D128 causal bf16 fwd+bwd",
         "ms": round(ms, 3),
         "tflops": round(useful / (ms * 1e-3) / 1e12, 1),
-        "tile_skip_efficiency_fwd": round(fwd_t["needed"] / fwd_t["executed"], 4),
-        "tile_skip_efficiency_bwd": round(bwd_t["needed"] / bwd_t["executed"], 4),
-        "useful_flop_fraction_fwd": round(fwd_t["useful_fraction"], 4),
-        "useful_flop_fraction_bwd": round(bwd_t["useful_fraction"], 4),
-        "tiles_fwd": {k_: fwd_t[k_] for k_ in ("executed", "needed", "total")},
-        "tiles_bwd": {k_: bwd_t[k_] for k_ in ("executed", "needed", "total")},
+        "tile_units": "32 x 32 (query, key) units whose products each kernel ran, counted by the kernels "
+                      "(libtheria_sdpa_tiles.so); needed = units holding an unmasked element",
+        "tiles_needed": needed,
+        "tiles_total": total,
     }
+    for name, ex in zip(("fwd", "dq", "dkdv"), counted):
+        out[f"tiles_executed_{name}"] = ex
+        out[f"tile_skip_efficiency_{name}"] = round(needed / ex, 4) if ex else None
+    # unmasked elements over the elements of the executed units
+    out["useful_flop_fraction_fwd"] = round(B * H * S * (S + 1) / 2 / (counted[0] * 32 * 32), 4) if counted[0] else None
+    return out
 
 
-def _causal_tiles(S: int, qt: int, kt: int) -> dict:
-    """Tile accounting of a causal S x S problem cut into qt-query x kt-key wave tiles.
+def _kernel_tile_counts(q, k, v, do, scale: float, causal: bool):
+    """[forward, dQ, dK/dV] executed 32 x 32 tile units of one fwd + bwd step, counted by the kernels themselves in
+    the counter-enabled build of the same sources (libtheria_sdpa_tiles.so: THERIA_TILE_COUNT), run through its C
+    ABI on the same inputs."""
+    import ctypes
 
-    executed: tiles whose products the kernels run, by their skip rule (a wave skips a key tile, or a dK/dV
-    wave a query subtile, when its first key lies after the tile's last query: k0 > q0 + qt - 1);
-    needed: tiles holding at least one unmasked (key <= query) element, found from the mask itself.
-    useful_fraction: unmasked elements over the elements of the executed tiles."""
-    import numpy as np
+    import torch
 
-    nq, nk = S // qt, S // kt
-    q0 = np.arange(nq)[:, None] * qt
-    k0 = np.arange(nk)[None, :] * kt
-    executed = k0 <= q0 + qt - 1
-    mask = np.tri(S, S, dtype=bool)  # mask[q, k] = k <= q
-    needed = mask.reshape(nq, qt, nk, kt).any(axis=(1, 3))
-    return {
-        "executed": int(executed.sum()),
-        "needed": int(needed.sum()),
-        "total": nq * nk,
-        "useful_fraction": float(mask.sum()) / float(executed.sum() * qt * kt),
-    }
+    from theria_amd import _lib, _ops
+
+    lib = _lib.load(_lib.TILES_LIB_PATH)
+    B, H, S, _ = q.shape
+    o, dq = torch.empty_like(q), torch.empty_like(q)
+    dk, dv = torch.empty_like(k), torch.empty_like(v)
+    lse = torch.empty((B, H, S), dtype=torch.float32, device=q.device)
+    delta = torch.empty_like(lse)
+    prob = _ops._problem(q, k, scale, causal)
+    counts = (ctypes.c_uint64 * 3)()
+
+    def ok(rc, what):
+        if rc != _lib.OK:
+            raise RuntimeError(f"{what}: {lib.theria_last_error().decode(errors='replace')}")
+
+    torch.cuda.synchronize()
+    ok(lib.theria_debug_tile_counts(counts, 1), "theria_debug_tile_counts")  # zero them
+    st = _ops._stream(q.device)
+    tv = _ops._tv
+    ok(lib.theria_sdpa_fwd(ctypes.byref(prob), tv(q), tv(k), tv(v), tv(o), 0, lse.data_ptr(), None, None, st),
+       "theria_sdpa_fwd (tile counting build)")
+    ok(lib.theria_sdpa_bwd_dq(ctypes.byref(prob), tv(q), tv(k), tv(v), tv(o), 0, tv(do), lse.data_ptr(),
+                              delta.data_ptr(), tv(dq), st), "theria_sdpa_bwd_dq (tile counting build)")
+    ok(lib.theria_sdpa_bwd_dkdv(ctypes.byref(prob), tv(q), tv(k), tv(v), tv(do), lse.data_ptr(), delta.data_ptr(),
+                                tv(dk), tv(dv), st), "theria_sdpa_bwd_dkdv (tile counting build)")
+    torch.cuda.synchronize()
+    ok(lib.theria_debug_tile_counts(counts, 1), "theria_debug_tile_counts")
+    return [int(c) for c in counts]
 
 
 def extras_scores():

@@ -184,7 +184,9 @@ int theria_sdpa_bwd_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q
  * that each GPU the library runs on holds until the process ends, so 5 * batch * heads * tq must not exceed
  * 5 * 2^20 (a larger problem is rejected with THERIA_ERR_CONTRACT). Every call on one GPU shares that GPU's
  * array: calls that overlap on one GPU (other streams, other threads) race and must be serialised by the
- * caller. Results equal theria_sdpa_bwd_bwd's bit for bit.
+ * caller. Results equal theria_sdpa_bwd_bwd's bit for bit. The first call on a device looks up that device's
+ * scratch address (hipGetSymbolAddress, which may load the library's code object): make one call outside any
+ * stream capture before capturing it in a HIP graph; captured calls then only launch kernels.
  */
 int theria_sdpa_bwd_bwd_noalloc(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k,
                                 const theria_tensor_t* v, const theria_tensor_t* o, const theria_tensor_t* dout,
@@ -206,6 +208,16 @@ int theria_qk_scores(const theria_sdpa_problem_t* p, const theria_tensor_t* q, c
                      int32_t out_f32, void* stream);
 int theria_qk_softmax(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k, float* probs,
                       void* stream);
+
+/*
+ * Measurement hook with no counterpart in the reference: the executed tile units of the pipelined 16-bit
+ * kernels, counted by the kernels themselves, for measuring causal tile skipping. counts[0..2] receive the
+ * 32 x 32 (query, key) units whose products the forward, dQ and dK/dV kernels ran since the last reset (on the
+ * current device, after the work is complete: the call synchronises with a device copy); reset = 1 zeroes
+ * them afterwards. Only the counter-enabled build (libtheria_sdpa_tiles.so, the same sources compiled with
+ * THERIA_TILE_COUNT) counts; libtheria_sdpa.so returns THERIA_ERR_CONTRACT and zeros.
+ */
+int theria_debug_tile_counts(uint64_t* counts, int32_t reset);
 
 #ifdef __cplusplus
 }

@@ -21,16 +21,19 @@ def _declared_functions():
     return sorted(set(re.findall(r"\b(theria_[a-z_]+)\s*\(", text)))
 
 
-def test_library_exports_every_declared_symbol():
+@pytest.mark.parametrize("which", ["production", "tile counting"])
+def test_library_exports_every_declared_symbol(which):
+    """Both builds (libtheria_sdpa.so and the counter-enabled libtheria_sdpa_tiles.so) export exactly the header."""
     from theria_amd import _lib
 
-    lib = _lib.load()
+    path = _lib.LIB_PATH if which == "production" else _lib.TILES_LIB_PATH
+    lib = _lib.load(path)
     declared = _declared_functions()
     assert declared, "no declarations parsed from the header"
     for name in declared:
         assert hasattr(lib, name), f"{name} declared in {HEADER.name} but not exported"
     assert set(declared) == set(_lib.SIGNATURES), "ctypes signature table out of sync with the header"
-    nm = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True, check=True)
+    nm = subprocess.run(["nm", "-D", "--defined-only", str(path)], capture_output=True, text=True, check=True)
     exported = sorted(set(re.findall(r"\sT\s(theria_\w+)", nm.stdout)))
     assert exported == declared, f"exported {exported} != declared {declared}"
     # Nothing else: exported kernel stubs (weak template symbols) would bind to another copy of the
@@ -123,3 +126,14 @@ def test_torch_binding_loads_and_matches_the_abi():
     assert host.abi_version() == _lib.ABI_VERSION
     for name in ("fwd", "bwd", "jvp", "bwd_bwd"):
         assert callable(getattr(host, name))
+
+
+def test_production_library_has_no_tile_counters():
+    """theria_debug_tile_counts answers only in the counter-enabled build; the production library refuses it before
+    any HIP call."""
+    from theria_amd import _lib
+
+    counts = (ctypes.c_uint64 * 3)(7, 7, 7)
+    assert _lib.load().theria_debug_tile_counts(counts, 0) == _lib.ERR_CONTRACT
+    assert list(counts) == [0, 0, 0]
+    assert b"without tile counters" in _lib.load().theria_last_error()

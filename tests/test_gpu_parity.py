@@ -495,3 +495,44 @@ def test_caller_given_outputs_are_checked(hip_device):
                          out=(torch.empty_like(q), bad, torch.empty_like(v)))
     with pytest.raises(AssertionError, match="dout"):
         _ops.bwd(q, k, v, o, lse, do[:, :, :-1], s, False)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_tile_counting_build(causal, hip_device):
+    """The counter-enabled build (libtheria_sdpa_tiles.so) gives the production library's results bit for bit and
+    counts the 32 x 32 units its pipelined kernels run: every unit without a mask; with the causal mask at least
+    every unit holding an unmasked element (key <= query) and fewer than all."""
+    import ctypes
+
+    from theria_amd import _lib
+
+    dt, B, H, T, D = torch.bfloat16, 1, 2, 512, 128
+    q, k, v, do = (make((B, H, T, D), dt, hip_device, 300 + i)[0] for i in range(4))
+    s = 1 / math.sqrt(D)
+    print(f"[tile counts] causal={causal}", flush=True)
+    o, lse, _, _ = _ops.fwd(q, k, v, s, causal)
+    dq, dk, dv, _ = _ops.bwd(q, k, v, o, lse, do, s, causal)
+    lib = _lib.load(_lib.TILES_LIB_PATH)
+    counts = (ctypes.c_uint64 * 3)()
+    torch.cuda.synchronize()
+    assert lib.theria_debug_tile_counts(counts, 1) == _lib.OK
+    o2, lse2 = torch.empty_like(o), torch.empty_like(lse)
+    dq2, dk2, dv2, delta2 = torch.empty_like(dq), torch.empty_like(dk), torch.empty_like(dv), torch.empty_like(lse)
+    prob = _ops._problem(q, k, s, causal)
+    st = _ops._stream(q.device)
+    tv = _ops._tv
+    assert lib.theria_sdpa_fwd(ctypes.byref(prob), tv(q), tv(k), tv(v), tv(o2), 0, lse2.data_ptr(), None, None,
+                               st) == _lib.OK
+    assert lib.theria_sdpa_bwd(ctypes.byref(prob), tv(q), tv(k), tv(v), tv(o2), 0, tv(do), lse2.data_ptr(),
+                               delta2.data_ptr(), tv(dq2), tv(dk2), tv(dv2), st) == _lib.OK
+    torch.cuda.synchronize()
+    assert lib.theria_debug_tile_counts(counts, 1) == _lib.OK
+    for name, a, b in (("O", o2, o), ("lse", lse2, lse), ("dQ", dq2, dq), ("dK", dk2, dk), ("dV", dv2, dv)):
+        assert torch.equal(a, b), f"{name} of the counting build differs"
+    n = T // 32
+    total, needed = B * H * n * n, B * H * n * (n + 1) // 2
+    for name, c in zip(("fwd", "dq", "dkdv"), counts):
+        if causal:
+            assert needed <= c < total, f"{name}: {c} units executed, {needed} needed, {total} in all"
+        else:
+            assert c == total, f"{name}: {c} units executed, {total} in the grid"

@@ -41,3 +41,35 @@ def test_noalloc_rejects_problems_beyond_the_static_scratch(hip_device):
     lse = torch.zeros(B, H, T, device=hip_device)
     with pytest.raises(AssertionError, match="static scratch"):
         _ops.bwd_bwd(q, k, k, q, q, lse, lse, None, k, None, 0.25, False, noalloc=True)
+
+
+def test_noalloc_double_backward_replays_in_a_graph(hip_device):
+    """Captured in a HIP graph (after one eager call, which looks up the device's scratch address), the
+    allocation-free double backward replays bit for bit equal to the eager result, also when an eager call on
+    other inputs has rewritten the shared scratch in between (the kernels rewrite every element they read)."""
+    dt, B, H, T, M, D = torch.bfloat16, 2, 2, 256, 192, 64
+    print("[noalloc graph] capture + replays", flush=True)
+    args = _problem(hip_device, dt, B, H, T, M, D, seed=7)
+    other = _problem(hip_device, dt, B, H, T, M, D, seed=8)
+    s = 1 / math.sqrt(D)
+
+    def call(q, k, v, do, gq, gk, gv):
+        o, lse, _, _ = _ops.fwd(q, k, v, s, False)
+        return _ops.bwd_bwd(q, k, v, o, do, lse, None, gq, gk, gv, s, False, noalloc=True)
+
+    ref = [t.clone() for t in call(*args)]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm-up on a side stream, as torch's graph capture recommends
+        call(*args)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = call(*args)
+    for i in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, a, b in zip(("G_Q", "G_K", "G_V", "G_dO"), out, ref):
+            assert torch.equal(a, b), f"replay {i}: {name} differs from the eager result"
+        call(*other)  # eager work on the same scratch between replays
+        torch.cuda.synchronize()

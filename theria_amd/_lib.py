@@ -14,8 +14,10 @@ from pathlib import Path
 
 import torch  # noqa: F401  (must be imported first: it loads the HIP runtime the library binds to)
 
-# THERIA_SDPA_LIB overrides the in-tree build (e.g. a library installed elsewhere).
-LIB_PATH = Path(os.environ.get("THERIA_SDPA_LIB") or Path(__file__).resolve().parent / "lib" / "libtheria_sdpa.so")
+# The in-tree build (the torch binding _theria_host is linked against this same file).
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libtheria_sdpa.so"
+# The counter-enabled build of the same sources (theria_debug_tile_counts counts there), for measurements only.
+TILES_LIB_PATH = LIB_PATH.with_name("libtheria_sdpa_tiles.so")
 ABI_VERSION = 8
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
@@ -80,6 +82,7 @@ SIGNATURES = {
     ),
     "theria_qk_scores": ([_PR, _TV, _TV, _P, ctypes.c_int32, _P], ctypes.c_int),
     "theria_qk_softmax": ([_PR, _TV, _TV, _P, _P], ctypes.c_int),
+    "theria_debug_tile_counts": ([ctypes.POINTER(ctypes.c_uint64), ctypes.c_int32], ctypes.c_int),
 }
 
 _lock = threading.Lock()

@@ -2,7 +2,8 @@
 
 Usage: ``python -m theria_amd.build`` (or ``theria_amd.build.build()``). Every ``csrc/*.hip`` file is
 compiled for gfx950 in parallel into ``_build/`` at the repository root and linked into
-``theria_amd/lib/libtheria_sdpa.so``. ``csrc/host/theria_host.cpp`` (host code only, g++) is compiled beside
+``theria_amd/lib/libtheria_sdpa.so``; a second time with ``THERIA_TILE_COUNT`` into ``libtheria_sdpa_tiles.so``
+(kernels that count the tiles they run, for measurements only). ``csrc/host/theria_host.cpp`` (host code only, g++) is compiled beside
 them and linked against that library into the Python module ``theria_amd/_theria_host*.so``, the tensor-level
 binding of the hot entry points that the autograd operator calls. The library links against the HIP runtime by its soname
 (libamdhip64.so.7), so inside a process that already imported torch it binds to the runtime torch
@@ -26,6 +27,8 @@ REPO_DIR = PKG_DIR.parent
 CSRC = PKG_DIR / "csrc"
 LIB_DIR = PKG_DIR / "lib"
 LIB_PATH = LIB_DIR / "libtheria_sdpa.so"
+# The same sources compiled with THERIA_TILE_COUNT: kernels that count the tiles they run (measurement only).
+TILES_LIB_PATH = LIB_DIR / "libtheria_sdpa_tiles.so"
 BUILD_DIR = REPO_DIR / "_build"
 
 ARCH = "gfx950"
@@ -56,9 +59,9 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found: the HIP toolchain is required to build libtheria_sdpa.so")
 
 
-def _compile(hipcc: str, src: Path) -> Path:
-    obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [hipcc, *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+def _compile(hipcc: str, src: Path, tiles: bool = False) -> Path:
+    obj = (BUILD_DIR / "tiles" if tiles else BUILD_DIR) / (src.stem + ".o")
+    cmd = [hipcc, *COMMON_FLAGS, *(["-DTHERIA_TILE_COUNT"] if tiles else []), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}")
@@ -123,11 +126,23 @@ def build(verbose: bool = True, jobs: int | None = None) -> Path:
     if verbose:
         print(f"[theria_amd.build] compiling {len(sources)} sources for {ARCH} and the torch binding with {jobs} jobs",
               flush=True)
+    (BUILD_DIR / "tiles").mkdir(exist_ok=True)
     with _cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         host_obj = ex.submit(_compile_host)
-        objs = list(ex.map(lambda s: _compile(hipcc, s), sources))
-        host_obj = host_obj.result()
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+        objs = ex.map(lambda s: _compile(hipcc, s), sources)
+        tile_objs = ex.map(lambda s: _compile(hipcc, s, tiles=True), sources)
+        objs, tile_objs, host_obj = list(objs), list(tile_objs), host_obj.result()
+    _link(hipcc, objs, LIB_PATH)
+    _link(hipcc, tile_objs, TILES_LIB_PATH)
+    host = _link_host(host_obj)
+    if verbose:
+        print(f"[theria_amd.build] built {LIB_PATH.name}, {TILES_LIB_PATH.name} and {host.name} in {LIB_DIR.parent}",
+              flush=True)
+    return LIB_PATH
+
+
+def _link(hipcc: str, objs, out: Path) -> None:
+    tmp = out.with_suffix(".so.tmp")
     vmap = BUILD_DIR / "exports.map"
     vmap.write_text(EXPORTS)
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", f"-Wl,--version-script={vmap}", "-o", str(tmp),
@@ -135,11 +150,7 @@ def build(verbose: bool = True, jobs: int | None = None) -> Path:
     res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{res.stdout}")
-    os.replace(tmp, LIB_PATH)
-    host = _link_host(host_obj)
-    if verbose:
-        print(f"[theria_amd.build] built {LIB_PATH} and {host.name}", flush=True)
-    return LIB_PATH
+    os.replace(tmp, out)
 
 
 if __name__ == "__main__":

@@ -510,6 +510,24 @@ THERIA_API int theria_sdpa_bwd_bwd_noalloc(const theria_sdpa_problem_t* p, const
                      stream);
 }
 
+THERIA_API int theria_debug_tile_counts(uint64_t* counts, int32_t reset) {
+  if (!counts) return fail(THERIA_ERR_CONTRACT, "theria_debug_tile_counts: counts is NULL");
+#ifdef THERIA_TILE_COUNT
+  unsigned long long f = 0, q = 0, kv = 0;
+  hipError_t e = theria::tile_counts_fwd(&f, reset != 0);
+  if (e == hipSuccess) e = theria::tile_counts_bwd(&q, &kv, reset != 0);
+  if (e != hipSuccess) return hip_status(e, "theria_debug_tile_counts");
+  counts[0] = f;
+  counts[1] = q;
+  counts[2] = kv;
+  return THERIA_OK;
+#else
+  counts[0] = counts[1] = counts[2] = 0;
+  return fail(THERIA_ERR_CONTRACT, "theria_debug_tile_counts: this library was built without tile counters "
+                                   "(libtheria_sdpa_tiles.so has them)");
+#endif
+}
+
 // Partial-fusion score kernels: the problem's v-related fields are unused; causal must be 0.
 static int run_scores(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k, void* out,
                       bool out_f32, bool softmax, void* stream, const char* what) {

@@ -28,6 +28,7 @@
 #include "sdpa_common.hpp"
 #include "sdpa_lds.hpp"
 #include "sdpa_params.hpp"
+#include "tile_count.hpp"
 
 // Waves per workgroup (compile-time knobs; the defaults are the measured best on MI355X).
 #ifndef DQ_PIPE_NW
@@ -66,6 +67,21 @@
 #endif
 
 namespace theria {
+
+#ifdef THERIA_TILE_COUNT
+// 32 x 32 (query, key) units whose products the dQ and dK/dV kernels ran (counter-enabled build only)
+static __device__ unsigned long long g_tiles_dq, g_tiles_dkdv;
+hipError_t tile_counts_bwd(unsigned long long* dq, unsigned long long* dkdv, bool reset) {
+  hipError_t e = hipMemcpyFromSymbol(dq, HIP_SYMBOL(g_tiles_dq), sizeof(*dq));
+  if (e == hipSuccess) e = hipMemcpyFromSymbol(dkdv, HIP_SYMBOL(g_tiles_dkdv), sizeof(*dkdv));
+  if (e == hipSuccess && reset) {
+    const unsigned long long zero = 0;
+    e = hipMemcpyToSymbol(HIP_SYMBOL(g_tiles_dq), &zero, sizeof(zero));
+    if (e == hipSuccess) e = hipMemcpyToSymbol(HIP_SYMBOL(g_tiles_dkdv), &zero, sizeof(zero));
+  }
+  return e;
+}
+#endif
 
 // FD: the head dim is DP itself (compile-time bounds); otherwise the runtime head dim s.D < DP bounds the
 // loads, stores and DMA chunks (both kernels).
@@ -112,6 +128,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
   const T* dO = (const T*)p.dout.p + b * p.dout.sb + h * p.dout.sh;
   const int64_t rowbase = (int64_t)bh * s.T;
   const float c2 = s.scale * kLog2e;
+  THERIA_TILES_DECL;
 
   for (int pass = 0; pass < (PAIR ? 2 : 1); ++pass) {
   const int kb = pass == 0 ? unit : nkb - 1 - unit;
@@ -237,6 +254,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
       constexpr bool FAST = decltype(fast_tag)::value;
       const int q0 = qbeg + it * BM;
       if constexpr (FAST && OVERLAP) {
+        THERIA_TILES_ADD(2 * HALVES);
 #pragma unroll
         for (int hf = 0; hf < HALVES; ++hf) {
           f32x16_t s0, p0, s1, p1;
@@ -257,6 +275,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
         for (int qs = 0; qs < 2 * HALVES; ++qs) {
           const int q0s = q0 + 32 * qs;
           if (!FAST && (q0s >= s.T || (CAUSAL && kw0 > q0s + 31))) continue;  // wave-uniform
+          THERIA_TILES_ADD(1);
           f32x16_t sc, dp;
           F pf[2], df[2];
           sdp(tq, to, tr, qs, sc, dp);
@@ -276,6 +295,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
       for (int qs = 0; qs < 2 * HALVES; ++qs) {
         const int q0s = q0 + 32 * qs;
         if (!FAST && (q0s >= s.T || (CAUSAL && kw0 > q0s + 31))) continue;  // wave-uniform
+        THERIA_TILES_ADD(1);
         f32x16_t se = zero16(), dp;
 #pragma unroll
         for (int qd = 0; qd < 4; ++qd) {
@@ -431,6 +451,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
       }
     }
   }  // pass
+  THERIA_TILES_FLUSH(g_tiles_dkdv);
 }
 
 // dQ pass with the contract of dq_kernel (sdpa_bwd.hip): dQ = scale dS K with dS = P o (dO V^T - delta)
@@ -476,6 +497,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
   const T* K = (const T*)p.k.p + b * p.k.sb + h * p.k.sh;
   const T* V = (const T*)p.v.p + b * p.v.sb + h * p.v.sh;
   const T* dO = (const T*)p.dout.p + b * p.dout.sb + h * p.dout.sh;
+  THERIA_TILES_DECL;
 
   for (int pass = 0; pass < (CAUSAL ? 2 : 1); ++pass) {
   const int qb = CAUSAL ? (pass == 0 ? nqb - 1 - unit : unit) : unit;
@@ -623,6 +645,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
         dma.template issue_clamped<NSLAB>(vrsrc, vrs, k0 + BN, s.M, nv);
       }
       if constexpr (FAST && OVERLAP && !SPLIT) {
+        THERIA_TILES_ADD(2 * HALVES);
 #pragma unroll
         for (int hf = 0; hf < HALVES; ++hf) {
           f32x16_t s0, p0, s1, p1;
@@ -643,6 +666,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
         for (int t = 0; t < 2 * HALVES; ++t) {
           const int k0t = k0 + 32 * t;
           if (!FAST && CAUSAL && k0t > q0w + 31) continue;  // every key after every query of the wave (uniform)
+          THERIA_TILES_ADD(1);
           f32x16_t sc, dp;
           F df[2];
           sdp(split_tag, tk, tv, t, sc, dp);
@@ -759,6 +783,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
         run(std::false_type{});
     }
   }  // pass
+  THERIA_TILES_FLUSH(g_tiles_dq);
 }
 
 // Launches with FD = (head dim == DP): one fused launch at head dim 64; at 128 the common launch (unless every

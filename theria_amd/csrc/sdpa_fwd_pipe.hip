@@ -27,6 +27,7 @@
 
 #include "sdpa_common.hpp"
 #include "sdpa_lds.hpp"
+#include "tile_count.hpp"
 #include "sdpa_params.hpp"
 
 namespace theria {
@@ -37,6 +38,19 @@ namespace theria {
 // block to fill the GPU.
 // FD: the head dim is DP itself (compile-time bounds); otherwise the runtime head dim s.D < DP bounds the
 // loads, stores and DMA chunks.
+#ifdef THERIA_TILE_COUNT
+// 32 x 32 (query, key) units whose products the forward kernel ran (counter-enabled build only)
+static __device__ unsigned long long g_tiles_fwd;
+hipError_t tile_counts_fwd(unsigned long long* fwd, bool reset) {
+  hipError_t e = hipMemcpyFromSymbol(fwd, HIP_SYMBOL(g_tiles_fwd), sizeof(*fwd));
+  if (e == hipSuccess && reset) {
+    const unsigned long long zero = 0;
+    e = hipMemcpyToSymbol(HIP_SYMBOL(g_tiles_fwd), &zero, sizeof(zero));
+  }
+  return e;
+}
+#endif
+
 template <typename T, bool CAUSAL, bool STATS, int NW, int DP, int QT, bool FD>
 __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p) {
   using MM = Mfma<T>;
@@ -68,6 +82,7 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
   const T* V = (const T*)p.v.p + b * p.v.sb + h * p.v.sh;
   const int64_t rowbase = (int64_t)bh * s.T;
   const float c2 = s.scale * kLog2e;
+  THERIA_TILES_DECL;
 
   for (int pass = 0; pass < (CAUSAL ? 2 : 1); ++pass) {
   const int qb = CAUSAL ? (pass == 0 ? nqb - 1 - unit : unit) : unit;
@@ -247,6 +262,8 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
         dma.template issue_clamped<NSLAB>(vrsrc, vrs, k0, s.M, vn);
       }
       F pn[QT][2][2];
+      // QT query tiles x two 32-key subtiles, unless every key of the tile follows every query of the wave
+      if (FAST || !(CAUSAL && k0 > q0w + 32 * QT - 1)) THERIA_TILES_ADD(2 * QT);
       if constexpr (FAST) {
         // Phase order (kept by scheduling barriers, which also bound the live registers):
         //   S(k) subtile 0 | S(k) subtile 1 with exp of subtile 0 | O += V(k-1)^T P(k-1)^T with exp of subtile 1.
@@ -423,6 +440,7 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
       }
     }
   }  // pass
+  THERIA_TILES_FLUSH(g_tiles_fwd);
 }
 
 template <typename T, bool CAUSAL, int NW, int DP, int QT>

@@ -120,4 +120,10 @@ hipError_t launch_bwdbwd_rows(const BwdBwdParams& p, hipStream_t st);
 hipError_t launch_bwdbwd_cols(const BwdBwdParams& p, hipStream_t st);
 hipError_t launch_scores(const ScoresParams& p, hipStream_t st);
 
+#ifdef THERIA_TILE_COUNT
+// Executed 32 x 32 tile units of the pipelined kernels (counter-enabled build only; reset: zero them after reading).
+hipError_t tile_counts_fwd(unsigned long long* fwd, bool reset);
+hipError_t tile_counts_bwd(unsigned long long* dq, unsigned long long* dkdv, bool reset);
+#endif
+
 }  // namespace theria
