@@ -451,7 +451,16 @@ static int run_bwd_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q,
     bp.lse = m2;
     bp.row_l2 = l2;
   }
-  if (s.dtype != THERIA_DTYPE_F32 && s.T > 0) {
+  const bool rows_make_terms = s.dtype != THERIA_DTYPE_F32 && s.T > 0 && theria::bwdbwd_rows_make_row_terms(bp);
+  if (rows_make_terms) {
+    // 16-bit inputs at head dim 64 (LDS-DMA tiles): the key-split row kernel forms the row term and the exact
+    // normaliser itself in its first pass (from the forward's lse) and writes them for the column kernel.
+    bp.lse_fwd = lse;
+    bp.z_out = row_ws + 2 * nrows;
+    bp.lse_out = row_ws + 3 * nrows;
+    bp.delta = bp.z_out;
+    bp.lse = bp.lse_out;
+  } else if (s.dtype != THERIA_DTYPE_F32 && s.T > 0) {
     // 16-bit inputs: a 16-bit forward's lse comes from rounded probabilities, so P rebuilt from it sums to one
     // only within ~2^-9, and on peaked rows the second-order terms (Gam - r, dP - z, E1 - t) are differences
     // that such a scale error does not cancel from. The row-term pass of the dQ kernel forms the exact

@@ -782,11 +782,296 @@ template <typename T, int DP>
 static bool cols_dma(const BwdBwdParams& p) {
   return dma_tiles_ok<T, DP>(p, p.s.T, {&p.q, &p.dout, &p.gq});
 }
+// The key-split row kernel takes 16-bit problems at head dim 64 whose K, V, gK, gV slabs allow LDS DMA.
+template <typename T, int DP>
+static bool rows_ks_ok(const BwdBwdParams& p) {
+  return DP == 64 && sizeof(T) == 2 && dma_tiles_ok<T, DP>(p, p.s.M, {&p.k, &p.v, &p.gk, &p.gv});
+}
+
 // 16-bit: the rows kernel's exact launch rides in the column grid when both take the same tile path.
 template <typename T, int DP>
 static bool exact_in_cols(const BwdBwdParams& p) {
-  return sizeof(T) == 2 && rows_dma<T, DP>(p) == cols_dma<T, DP>(p);
+  return sizeof(T) == 2 && !rows_ks_ok<T, DP>(p) && rows_dma<T, DP>(p) == cols_dma<T, DP>(p);
 }
+
+// The row pass for 16-bit inputs at head dim 64 with LDS-DMA tiles, as two key groups of four waves (eight-wave
+// workgroups, two waves per SIMD): the keys of each query block are split between the groups, whose partial
+// sums meet in LDS. Each group makes two passes over its key tiles:
+//   1. with P from the forward's lse: L = sum_j P, sum_j P dP, sum_j P Gam, sum_j P Gam dP, sum_j P W and the
+//      largest P, partial per group, then exchanged. They give the row's exact normaliser (P_c = P / L: a
+//      16-bit forward's lse comes from rounded probabilities, so P sums to one only within ~2^-9), the row
+//      term z = sum_j P dP / L and the second-order row terms r = sum_j P_c Gam and t = sum_j P_c E1 with
+//      E1 = Gam (dP - z) + W, i.e. t = (sum_j P Gam dP - z sum_j P Gam + sum_j P W) / L;
+//   2. G_Q = s sum_j (Gbar_S K + dS gK) with Gbar_S = P_c o ((Gam - r)(dP - z) + W - t), the exact form, in two
+//      D-wide accumulators; waves holding a row flagged peaked in the forward's lse enter Gbar_S and dS as two
+//      16-bit terms.
+// Every row takes the exact form (no centring, no second launch for flagged rows, no separate row-term pass),
+// and the two accumulators with the per-wave Q, dO, gQ fragments fit 256 registers, so no accumulator is
+// shuttled between register files. Writes G_Q, and r, t, z and lse + ln L (flagged peaked when the row's
+// largest P_c exceeds 1/4) for the column kernel.
+template <typename T, bool CAUSAL>
+__global__ __launch_bounds__(512, 2) void bwdbwd_rows_ks_kernel(const BwdBwdParams p) {
+  using MM = Mfma<T>;
+  using F = typename MM::frag_t;
+  static_assert(sizeof(T) == 2, "16-bit inputs only");
+  constexpr int DP = 64, NW = 4, BM = 32 * NW, BN = 64, NST = BN / 32;
+  constexpr int NDT = DP / 32, NKC = DP / MM::KC, NPC = 32 / MM::KC;
+  constexpr int TB = BN * DP * 2;  // bytes per tile
+  using Dma = SwzDma<NW, DP>;
+  constexpr int NSLAB = BN / Dma::SLAB_ROWS;
+  static_assert(NSLAB * Dma::SLAB_ROWS == BN, "key tiles must be whole DMA slabs");
+  // [group][set][K, V, gK, gV]; reused for the exchanges between the passes and after the second
+  __shared__ __attribute__((aligned(1024))) char smem[2 * 2 * 4 * TB];
+  static_assert(sizeof(smem) >= 4 * 2 * NDT * 16 * 256, "the accumulator exchange fits in the tile memory");
+
+  const Shape& s = p.s;
+  const int lane = threadIdx.x & 63, li = lane & 31, g = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave >> 2, wig = wave & 3;  // key group, wave in group
+  const int nqb = (s.T + BM - 1) / BM;
+  const int bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int bh = bid / nqb;
+  int qb = bid - bh * nqb;
+  if (CAUSAL) qb = nqb - 1 - qb;  // longest first
+  const int b = bh / s.H, h = bh - b * s.H;
+  const T* Q = (const T*)p.q.p + b * p.q.sb + h * p.q.sh;
+  const T* K = (const T*)p.k.p + b * p.k.sb + h * p.k.sh;
+  const T* V = (const T*)p.v.p + b * p.v.sb + h * p.v.sh;
+  const T* dO = (const T*)p.dout.p + b * p.dout.sb + h * p.dout.sh;
+  const bool has_gq = p.gq.p != nullptr, has_gk = p.gk.p != nullptr, has_gv = p.gv.p != nullptr;
+  const T* GQ = has_gq ? (const T*)p.gq.p + b * p.gq.sb + h * p.gq.sh : nullptr;
+  const T* GK = has_gk ? (const T*)p.gk.p + b * p.gk.sb + h * p.gk.sh : nullptr;
+  const T* GV = has_gv ? (const T*)p.gv.p + b * p.gv.sb + h * p.gv.sh : nullptr;
+  const int q0w = qb * BM + wig * 32;
+  const int myq = q0w + li;
+  const bool qvalid = myq < s.T;
+  const int64_t row_id = (int64_t)bh * s.T + myq;
+
+  F qf[NKC], dof[NKC], gqf[NKC];
+#pragma unroll
+  for (int c = 0; c < NKC; ++c) {
+    qf[c] = gload_frag<T>(Q, p.q.sr, myq, s.T, c, s.D, s.vec);
+    dof[c] = gload_frag<T>(dO, p.dout.sr, myq, s.T, c, s.D, s.vec);
+    gqf[c] = has_gq ? gload_frag<T>(GQ, p.gq.sr, myq, s.T, c, s.D, s.vec) : F{};
+  }
+  const float c2 = s.scale * kLog2e;
+  const float lse_raw = qvalid ? p.lse_fwd[row_id] : THERIA_INF;
+  const float lse2 = lse_raw * kLog2e;
+  float moff = lse2 == -THERIA_INF ? THERIA_INF : lse2;  // a row without visible keys has P = 0; pass 2: P_c
+  float z = 0.f;                                          // pass 2: the row term (pass 1 forms dP itself)
+  const bool split = __any(lse_peaked(lse_raw));  // uniform per wave (the forward's bound: a superset)
+
+  int kend = s.M;
+  if (CAUSAL) kend = min(s.M, qb * BM + BM);
+  const int nkt = (kend + BN - 1) / BN;
+  const int half = (nkt + 1) / 2;
+  const int kt0 = grp * half, kt1 = min(nkt, kt0 + half);  // this group's tiles [kt0, kt1)
+
+  // S^T, Gam^T / s, W^T and dP^T - z of 32-key subtile st of the tile in (tK, tV, tgK, tgV); P from S.
+  auto products = [&](int k0s, const char* tK, const char* tV, const char* tgK, const char* tgV, int st,
+                      f32x16_t& pv, f32x16_t& gm, f32x16_t& w, f32x16_t& dpz) __attribute__((always_inline)) {
+    f32x16_t sc = zero16();
+    gm = zero16();
+    w = zero16();
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dpz[r] = -z;
+#pragma unroll
+    for (int c = 0; c < NKC; ++c) {
+      const F kfr = swz_cols<T, DP>(tK, 32 * st + li, c);
+      sc = MM::mma(kfr, qf[c], sc);
+      dpz = MM::mma(swz_cols<T, DP>(tV, 32 * st + li, c), dof[c], dpz);
+      if (has_gq) gm = MM::mma(kfr, gqf[c], gm);
+      if (has_gk) gm = MM::mma(swz_cols<T, DP>(tgK, 32 * st + li, c), qf[c], gm);
+      if (has_gv) w = MM::mma(swz_cols<T, DP>(tgV, 32 * st + li, c), dof[c], w);
+    }
+    const bool need_mask = (k0s + 32 > s.M) || (CAUSAL && k0s + 31 > q0w);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float x = fast_exp2(fmaf(sc[r], c2, -moff));
+      if (need_mask) {
+        const int key = k0s + acc_row(r, g);
+        if (key >= s.M || (CAUSAL && key > myq)) x = 0.f;
+      }
+      pv[r] = x;
+    }
+  };
+
+  // pass 1: sum_j of P, P dP, P Gam, P Gam dP, P W, and max_j P (this lane's keys)
+  float l_part = 0.f, a_part = 0.f, r_part = 0.f, u_part = 0.f, w_part = 0.f, p_max = 0.f;
+  float rx = 0.f, tx = 0.f;  // r, t of the row after the exchange
+  f32x16_t acc[NDT], accy[NDT];      // pass 2: sum_j Gbar_S K and sum_j dS gK (transposed, lane per query)
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) acc[dt] = accy[dt] = zero16();
+
+  // PASS 1: the sums r and t over this group's keys.
+  auto compute_sums = [&](int kt, const char* tK, const char* tV, const char* tgK, const char* tgV)
+                          __attribute__((always_inline)) {
+#pragma unroll
+    for (int st = 0; st < NST; ++st) {
+      const int k0s = kt * BN + 32 * st;
+      if (CAUSAL && k0s > q0w + 31) continue;
+      f32x16_t pv, gm, w, dpz;
+      products(k0s, tK, tV, tgK, tgV, st, pv, gm, w, dpz);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float pg = pv[r] * (s.scale * gm[r]);
+        l_part += pv[r];
+        a_part = fmaf(pv[r], dpz[r], a_part);
+        r_part += pg;
+        u_part = fmaf(pg, dpz[r], u_part);
+        w_part = fmaf(pv[r], w[r], w_part);
+        p_max = fmaxf(p_max, pv[r]);
+      }
+    }
+  };
+  // PASS 2: Gbar_S and dS products (SPLIT: two 16-bit terms each).
+  auto compute_exact = [&](auto split_tag, int kt, const char* tK, const char* tV, const char* tgK, const char* tgV)
+                           __attribute__((always_inline)) {
+    constexpr bool SPLIT = decltype(split_tag)::value;
+#pragma unroll
+    for (int st = 0; st < NST; ++st) {
+      const int k0s = kt * BN + 32 * st;
+      if (CAUSAL && k0s > q0w + 31) continue;
+      f32x16_t pv, gm, w, dpz;
+      products(k0s, tK, tV, tgK, tgV, st, pv, gm, w, dpz);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float gam = s.scale * gm[r];
+        gm[r] = pv[r] * (fmaf(gam - rx, dpz[r], w[r]) - tx);  // Gbar_S
+        dpz[r] = pv[r] * dpz[r];                              // dS
+      }
+#pragma unroll
+      for (int cc = 0; cc < NPC; ++cc) {
+        if constexpr (SPLIT) {
+          F gh, gl, dh, dl;
+          split_frag<T>(gm, cc, gh, gl);
+          split_frag<T>(dpz, cc, dh, dl);
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) {
+            const F kr = swz_rows<T, DP>(tK, 32 * st, cc, dt * 32);
+            acc[dt] = MM::mma(kr, gh, acc[dt]);
+            acc[dt] = MM::mma(kr, gl, acc[dt]);
+            if (has_gk) {
+              const F gkr = swz_rows<T, DP>(tgK, 32 * st, cc, dt * 32);
+              accy[dt] = MM::mma(gkr, dh, accy[dt]);
+              accy[dt] = MM::mma(gkr, dl, accy[dt]);
+            }
+          }
+        } else {
+          const F gf = acc_frag<T>(gm, cc), df = acc_frag<T>(dpz, cc);
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) {
+            acc[dt] = MM::mma(swz_rows<T, DP>(tK, 32 * st, cc, dt * 32), gf, acc[dt]);
+            if (has_gk) accy[dt] = MM::mma(swz_rows<T, DP>(tgK, 32 * st, cc, dt * 32), df, accy[dt]);
+          }
+        }
+      }
+    }
+  };
+
+  const Dma dma(wig, lane);
+  // Byte offsets fit in 32 bits: the host only selects this kernel when each (batch, head) slab of K, V, gK and
+  // gV spans less than 2^31 bytes.
+  const uint32_t krs = (uint32_t)p.k.sr * 2, vrs = (uint32_t)p.v.sr * 2;
+  const uint32_t gkrs = has_gk ? (uint32_t)p.gk.sr * 2 : 0u, gvrs = has_gv ? (uint32_t)p.gv.sr * 2 : 0u;
+  const rsrc_t krsrc = make_rsrc(K, (uint32_t)slab_span(s.M, krs, 2 * DP)),
+               vrsrc = make_rsrc(V, (uint32_t)slab_span(s.M, vrs, 2 * DP));
+  const rsrc_t gkrsrc = make_rsrc(has_gk ? (const void*)GK : (const void*)K, (uint32_t)slab_span(s.M, gkrs, 2 * DP));
+  const rsrc_t gvrsrc = make_rsrc(has_gv ? (const void*)GV : (const void*)V, (uint32_t)slab_span(s.M, gvrs, 2 * DP));
+  auto tile = [&](int set, int a) { return smem + ((grp * 2 + set) * 4 + a) * TB; };  // a: K, V, gK, gV
+  auto issue = [&](int kt, int set) {
+    const int k0 = kt * BN;
+    dma.template issue_clamped<NSLAB>(krsrc, krs, k0, s.M, tile(set, 0));
+    dma.template issue_clamped<NSLAB>(vrsrc, vrs, k0, s.M, tile(set, 1));
+    if (has_gk) dma.template issue_clamped<NSLAB>(gkrsrc, gkrs, k0, s.M, tile(set, 2));
+    if (has_gv) dma.template issue_clamped<NSLAB>(gvrsrc, gvrs, k0, s.M, tile(set, 3));
+  };
+  // Step i: tile kt0 + i of this group (if it has one) from set i & 1; the next one's copies go to the other set,
+  // read in step i - 1, which every wave has finished at the barrier. Both groups run `half` steps (the same
+  // barriers); a group with fewer tiles idles through its last one.
+  auto sweep = [&](auto body) __attribute__((always_inline)) {
+    if (kt0 < kt1) issue(kt0, 0);
+    for (int i = 0; i < half; ++i) {
+      const int kt = kt0 + i;
+      wait_vm_all();
+      __syncthreads();
+      if (kt + 1 < kt1) issue(kt + 1, (i + 1) & 1);
+      if (kt < kt1) body(kt, tile(i & 1, 0), tile(i & 1, 1), tile(i & 1, 2), tile(i & 1, 3));
+    }
+    __syncthreads();  // every wave is done with the tiles
+  };
+  float* buf = reinterpret_cast<float*>(smem);
+
+  sweep([&](int kt, const char* a, const char* b_, const char* c, const char* d) __attribute__((always_inline)) {
+    compute_sums(kt, a, b_, c, d);
+  });
+  // the sums of the row: both lane halves of a query, then both key groups
+  float sums[6] = {pair_sum(l_part), pair_sum(a_part), pair_sum(r_part), pair_sum(u_part), pair_sum(w_part),
+                   pair_max(p_max)};
+#pragma unroll
+  for (int i = 0; i < 6; ++i) buf[(i * 8 + grp * 4 + wig) * 64 + lane] = sums[i];
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 5; ++i) sums[i] += buf[(i * 8 + (1 - grp) * 4 + wig) * 64 + lane];
+  sums[5] = fmaxf(sums[5], buf[(5 * 8 + (1 - grp) * 4 + wig) * 64 + lane]);
+  __syncthreads();  // the exchange is read before the tiles are refilled
+  const float L = sums[0];
+  float lse_c = lse_raw;
+  if (L > 0.f) {
+    const float inv = 1.f / L;
+    z = sums[1] * inv;
+    rx = sums[2] * inv;
+    tx = (sums[3] - z * sums[2] + sums[4]) * inv;
+    moff += __builtin_log2f(L);
+    lse_c = lse_with_flag(lse_raw + __builtin_log2f(L) * kLn2, sums[5] > kPeakedFrac * L);
+  }
+  if (grp == 0 && qvalid && g == 0) {
+    p.r_row[row_id] = rx;
+    p.t_row[row_id] = tx;
+    p.z_out[row_id] = z;
+    p.lse_out[row_id] = lse_c;
+  }
+  if (split)
+    sweep([&](int kt, const char* a, const char* b_, const char* c, const char* d) __attribute__((always_inline)) {
+      compute_exact(std::true_type{}, kt, a, b_, c, d);
+    });
+  else
+    sweep([&](int kt, const char* a, const char* b_, const char* c, const char* d) __attribute__((always_inline)) {
+      compute_exact(std::false_type{}, kt, a, b_, c, d);
+    });
+
+  // group 1's accumulators to group 0 (element e of lane l of wave w at e * 256 + w * 64 + l)
+  if (grp == 1) {
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        buf[(dt * 16 + r) * 256 + wig * 64 + lane] = acc[dt][r];
+        buf[((NDT + dt) * 16 + r) * 256 + wig * 64 + lane] = accy[dt][r];
+      }
+  }
+  __syncthreads();
+  if (grp == 1) return;
+  if (qvalid) {
+    T* OG = (T*)p.out_gq.p + b * p.out_gq.sb + h * p.out_gq.sh;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const int d0 = dt * 32 + 8 * qd + 4 * g;
+        float r4[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 4 * qd + e;
+          const float x = acc[dt][i] + buf[(dt * 16 + i) * 256 + wig * 64 + lane];
+          const float y = accy[dt][i] + buf[((NDT + dt) * 16 + i) * 256 + wig * 64 + lane];
+          r4[e] = s.scale * (x + y);
+        }
+        store4<T>(OG, p.out_gq.sr, myq, d0, s.D, r4[0], r4[1], r4[2], r4[3], s.vec);
+      }
+  }
+}
+
 
 struct RowsLauncher {
   template <typename T, int DP, bool CAUSAL>
@@ -794,6 +1079,12 @@ struct RowsLauncher {
     const int nqb = (p.s.T + 127) / 128;
     const int64_t nblk = (int64_t)nqb * p.s.B * p.s.H;
     if (nblk == 0) return hipSuccess;
+    if constexpr (sizeof(T) == 2 && DP == 64) {
+      if (rows_ks_ok<T, DP>(p)) {  // every row block exact in one launch (the column grid has no row blocks)
+        hipLaunchKernelGGL((bwdbwd_rows_ks_kernel<T, CAUSAL>), dim3((unsigned)nblk), dim3(512), 0, st, p);
+        return hipGetLastError();
+      }
+    }
     const bool with_cols = exact_in_cols<T, DP>(p);
     if constexpr (sizeof(T) == 2 && (DP == 64 || DP == 128)) {
       if (rows_dma<T, DP>(p)) {
@@ -843,6 +1134,13 @@ struct ColsLauncher {
 };
 
 hipError_t launch_bwdbwd_rows(const BwdBwdParams& p, hipStream_t st) { return dispatch_all<RowsLauncher>(p, st); }
+
+bool bwdbwd_rows_make_row_terms(const BwdBwdParams& p) {
+  if (p.s.dp != 64) return false;
+  if (p.s.dtype == 1) return rows_ks_ok<_Float16, 64>(p);
+  if (p.s.dtype == 2) return rows_ks_ok<__bf16, 64>(p);
+  return false;
+}
 hipError_t launch_bwdbwd_cols(const BwdBwdParams& p, hipStream_t st) { return dispatch_all<ColsLauncher>(p, st); }
 
 }  // namespace theria

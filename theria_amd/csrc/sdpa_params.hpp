@@ -97,7 +97,16 @@ struct BwdBwdParams {
   float* r_row;
   float* t_row;
   MutView out_gq, out_gk, out_gv;
+  // The key-split row kernel (16-bit, head dim 64) forms the row statistics itself from the forward's lse
+  // (lse_fwd) and writes the row term and the exact normaliser to z_out and lse_out, which the column kernel
+  // then reads as delta and lse.
+  const float* lse_fwd;
+  float* z_out;
+  float* lse_out;
 };
+
+// The row kernel of this problem forms the row term and the exact normaliser itself (no row-term pass needed).
+bool bwdbwd_rows_make_row_terms(const BwdBwdParams& p);
 
 // Materialised scores (partial-fusion backends): S = Q K^T or P = softmax(scale Q K^T), contiguous
 // (B, H, T, M) output.
