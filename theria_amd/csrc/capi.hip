@@ -454,8 +454,10 @@ static int run_bwd_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q,
   const bool rows_make_terms = s.dtype != THERIA_DTYPE_F32 && s.T > 0 && theria::bwdbwd_rows_make_row_terms(bp);
   if (rows_make_terms) {
     // 16-bit inputs at head dim 64 (LDS-DMA tiles): the key-split row kernel forms the row term and the exact
-    // normaliser itself in its first pass (from the forward's lse) and writes them for the column kernel.
+    // normaliser itself in its first pass (from the forward's lse) and writes them for the column kernel; that
+    // pass also forms G_dO, so no JVP launch follows.
     bp.lse_fwd = lse;
+    bp.out_gdo = mv(out_gdout);
     bp.z_out = row_ws + 2 * nrows;
     bp.lse_out = row_ws + 3 * nrows;
     bp.delta = bp.z_out;
@@ -482,7 +484,7 @@ static int run_bwd_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q,
     if (rc != THERIA_OK) return rc;
   }
   int rc = hip_status(theria::launch_bwdbwd_cols(bp, st), "theria_sdpa_bwd_bwd (cols)");
-  if (rc != THERIA_OK || s.T == 0) return rc;
+  if (rc != THERIA_OK || s.T == 0 || rows_make_terms) return rc;
   theria::JvpParams jp{};
   jp.s = s;
   jp.q = cv(q);

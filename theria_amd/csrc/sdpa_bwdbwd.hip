@@ -822,7 +822,10 @@ __global__ __launch_bounds__(512, 2) void bwdbwd_rows_ks_kernel(const BwdBwdPara
   static_assert(NSLAB * Dma::SLAB_ROWS == BN, "key tiles must be whole DMA slabs");
   // [group][set][K, V, gK, gV]; reused for the exchanges between the passes and after the second
   __shared__ __attribute__((aligned(1024))) char smem[2 * 2 * 4 * TB];
-  static_assert(sizeof(smem) >= 4 * 2 * NDT * 16 * 256, "the accumulator exchange fits in the tile memory");
+  static_assert(sizeof(smem) >= 4 * (4096 + 2 * NDT * 16 * 256), "the exchanges fit in the tile memory");
+  // the gQ fragments of the four query slices (both key groups read them; kept here rather than in registers,
+  // which the two passes' accumulators fill): fragment c of lane l of slice w at (w * NKC + c) * 64 + l
+  __shared__ __attribute__((aligned(16))) F sGQ[NW * NKC * 64];
 
   const Shape& s = p.s;
   const int lane = threadIdx.x & 63, li = lane & 31, g = lane >> 5;
@@ -847,12 +850,13 @@ __global__ __launch_bounds__(512, 2) void bwdbwd_rows_ks_kernel(const BwdBwdPara
   const bool qvalid = myq < s.T;
   const int64_t row_id = (int64_t)bh * s.T + myq;
 
-  F qf[NKC], dof[NKC], gqf[NKC];
+  F qf[NKC], dof[NKC];
 #pragma unroll
   for (int c = 0; c < NKC; ++c) {
     qf[c] = gload_frag<T>(Q, p.q.sr, myq, s.T, c, s.D, s.vec);
     dof[c] = gload_frag<T>(dO, p.dout.sr, myq, s.T, c, s.D, s.vec);
-    gqf[c] = has_gq ? gload_frag<T>(GQ, p.gq.sr, myq, s.T, c, s.D, s.vec) : F{};
+    // read after the first barrier of the first sweep
+    if (has_gq && grp == 0) sGQ[(wig * NKC + c) * 64 + lane] = gload_frag<T>(GQ, p.gq.sr, myq, s.T, c, s.D, s.vec);
   }
   const float c2 = s.scale * kLog2e;
   const float lse_raw = qvalid ? p.lse_fwd[row_id] : THERIA_INF;
@@ -867,22 +871,26 @@ __global__ __launch_bounds__(512, 2) void bwdbwd_rows_ks_kernel(const BwdBwdPara
   const int half = (nkt + 1) / 2;
   const int kt0 = grp * half, kt1 = min(nkt, kt0 + half);  // this group's tiles [kt0, kt1)
 
-  // S^T, Gam^T / s, W^T and dP^T - z of 32-key subtile st of the tile in (tK, tV, tgK, tgV); P from S.
-  auto products = [&](int k0s, const char* tK, const char* tV, const char* tgK, const char* tgV, int st,
-                      f32x16_t& pv, f32x16_t& gm, f32x16_t& w, f32x16_t& dpz) __attribute__((always_inline)) {
+  // S^T, Gam^T / s and (FULL) W^T and dP^T - z of 32-key subtile st of the tile in (tK, tV, tgK, tgV); P from S.
+  auto products = [&](auto full_tag, int k0s, const char* tK, const char* tV, const char* tgK, const char* tgV,
+                      int st, f32x16_t& pv, f32x16_t& gm, f32x16_t& w, f32x16_t& dpz) __attribute__((always_inline)) {
+    constexpr bool FULL = decltype(full_tag)::value;
     f32x16_t sc = zero16();
     gm = zero16();
-    w = zero16();
+    if constexpr (FULL) {
+      w = zero16();
 #pragma unroll
-    for (int r = 0; r < 16; ++r) dpz[r] = -z;
+      for (int r = 0; r < 16; ++r) dpz[r] = -z;
+    }
 #pragma unroll
     for (int c = 0; c < NKC; ++c) {
       const F kfr = swz_cols<T, DP>(tK, 32 * st + li, c);
       sc = MM::mma(kfr, qf[c], sc);
-      dpz = MM::mma(swz_cols<T, DP>(tV, 32 * st + li, c), dof[c], dpz);
-      if (has_gq) gm = MM::mma(kfr, gqf[c], gm);
+      if constexpr (FULL) dpz = MM::mma(swz_cols<T, DP>(tV, 32 * st + li, c), dof[c], dpz);
+      if (has_gq) gm = MM::mma(kfr, sGQ[(wig * NKC + c) * 64 + lane], gm);
       if (has_gk) gm = MM::mma(swz_cols<T, DP>(tgK, 32 * st + li, c), qf[c], gm);
-      if (has_gv) w = MM::mma(swz_cols<T, DP>(tgV, 32 * st + li, c), dof[c], w);
+      if constexpr (FULL)
+        if (has_gv) w = MM::mma(swz_cols<T, DP>(tgV, 32 * st + li, c), dof[c], w);
     }
     const bool need_mask = (k0s + 32 > s.M) || (CAUSAL && k0s + 31 > q0w);
 #pragma unroll
@@ -896,31 +904,66 @@ __global__ __launch_bounds__(512, 2) void bwdbwd_rows_ks_kernel(const BwdBwdPara
     }
   };
 
-  // pass 1: sum_j of P, P dP, P Gam, P Gam dP, P W, and max_j P (this lane's keys)
-  float l_part = 0.f, a_part = 0.f, r_part = 0.f, u_part = 0.f, w_part = 0.f, p_max = 0.f;
+  // pass 1: sum_j of P and P Gam, and max_j P (this lane's keys); sum_j P dP and sum_j P (Gam dP + W) follow from
+  // the G_dO products as dO . sum_j P V and dO . (sum_j (P o Gam) V + sum_j P gV)
+  float l_part = 0.f, r_part = 0.f, p_max = 0.f;
   float rx = 0.f, tx = 0.f;  // r, t of the row after the exchange
-  f32x16_t acc[NDT], accy[NDT];      // pass 2: sum_j Gbar_S K and sum_j dS gK (transposed, lane per query)
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) acc[dt] = accy[dt] = zero16();
+  f32x16_t acc[NDT], accy[NDT];  // pass 2: sum_j Gbar_S K and sum_j dS gK (transposed, lane per query)
 
-  // PASS 1: the sums r and t over this group's keys.
-  auto compute_sums = [&](int kt, const char* tK, const char* tV, const char* tgK, const char* tgV)
+  // G_dO (the JVP of O along (gQ, gK, gV)) from pass 1, as the JVP kernel forms it with normalised P:
+  // G_dO = (sum_j (P o Gam) V + sum_j P gV) / L - r (sum_j P V) / L (jvp_kernel's epilogue). The first two sums
+  // share one accumulator (their products chain into it).
+  f32x16_t acc_a[NDT], acc_o[NDT];  // sum_j (P o Gam) V + sum_j P gV, and sum_j P V (transposed)
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) acc_a[dt] = acc_o[dt] = zero16();
+
+  // PASS 1: the row sums and the G_dO products over this group's keys (SPLIT: P o Gam and P as two 16-bit terms).
+  auto compute_sums = [&](auto split_tag, int kt, const char* tK, const char* tV, const char* tgK, const char* tgV)
                           __attribute__((always_inline)) {
+    constexpr bool SPLIT = decltype(split_tag)::value;
 #pragma unroll
     for (int st = 0; st < NST; ++st) {
       const int k0s = kt * BN + 32 * st;
       if (CAUSAL && k0s > q0w + 31) continue;
       f32x16_t pv, gm, w, dpz;
-      products(k0s, tK, tV, tgK, tgV, st, pv, gm, w, dpz);
+      products(std::false_type{}, k0s, tK, tV, tgK, tgV, st, pv, gm, w, dpz);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float pg = pv[r] * (s.scale * gm[r]);
+        const float pg = pv[r] * (s.scale * gm[r]);  // P o Gam
         l_part += pv[r];
-        a_part = fmaf(pv[r], dpz[r], a_part);
         r_part += pg;
-        u_part = fmaf(pg, dpz[r], u_part);
-        w_part = fmaf(pv[r], w[r], w_part);
         p_max = fmaxf(p_max, pv[r]);
+        gm[r] = pg;
+      }
+#pragma unroll
+      for (int cc = 0; cc < NPC; ++cc) {
+        if constexpr (SPLIT) {
+          F ph, pl, gh, gl;
+          split_frag<T>(pv, cc, ph, pl);
+          split_frag<T>(gm, cc, gh, gl);
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) {
+            const F vr = swz_rows<T, DP>(tV, 32 * st, cc, dt * 32);
+            acc_a[dt] = MM::mma(vr, gh, acc_a[dt]);
+            acc_a[dt] = MM::mma(vr, gl, acc_a[dt]);
+            if (has_gv) {
+              const F gvr = swz_rows<T, DP>(tgV, 32 * st, cc, dt * 32);
+              acc_a[dt] = MM::mma(gvr, ph, acc_a[dt]);
+              acc_a[dt] = MM::mma(gvr, pl, acc_a[dt]);
+            }
+            acc_o[dt] = MM::mma(vr, ph, acc_o[dt]);
+            acc_o[dt] = MM::mma(vr, pl, acc_o[dt]);
+          }
+        } else {
+          const F pf = acc_frag<T>(pv, cc), gf = acc_frag<T>(gm, cc);
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) {
+            const F vr = swz_rows<T, DP>(tV, 32 * st, cc, dt * 32);
+            acc_a[dt] = MM::mma(vr, gf, acc_a[dt]);
+            if (has_gv) acc_a[dt] = MM::mma(swz_rows<T, DP>(tgV, 32 * st, cc, dt * 32), pf, acc_a[dt]);
+            acc_o[dt] = MM::mma(vr, pf, acc_o[dt]);
+          }
+        }
       }
     }
   };
@@ -933,7 +976,7 @@ __global__ __launch_bounds__(512, 2) void bwdbwd_rows_ks_kernel(const BwdBwdPara
       const int k0s = kt * BN + 32 * st;
       if (CAUSAL && k0s > q0w + 31) continue;
       f32x16_t pv, gm, w, dpz;
-      products(k0s, tK, tV, tgK, tgV, st, pv, gm, w, dpz);
+      products(std::true_type{}, k0s, tK, tV, tgK, tgV, st, pv, gm, w, dpz);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const float gam = s.scale * gm[r];
@@ -1002,28 +1045,79 @@ __global__ __launch_bounds__(512, 2) void bwdbwd_rows_ks_kernel(const BwdBwdPara
   };
   float* buf = reinterpret_cast<float*>(smem);
 
-  sweep([&](int kt, const char* a, const char* b_, const char* c, const char* d) __attribute__((always_inline)) {
-    compute_sums(kt, a, b_, c, d);
-  });
-  // the sums of the row: both lane halves of a query, then both key groups
-  float sums[6] = {pair_sum(l_part), pair_sum(a_part), pair_sum(r_part), pair_sum(u_part), pair_sum(w_part),
-                   pair_max(p_max)};
+  if (split)
+    sweep([&](int kt, const char* a, const char* b_, const char* c, const char* d) __attribute__((always_inline)) {
+      compute_sums(std::true_type{}, kt, a, b_, c, d);
+    });
+  else
+    sweep([&](int kt, const char* a, const char* b_, const char* c, const char* d) __attribute__((always_inline)) {
+      compute_sums(std::false_type{}, kt, a, b_, c, d);
+    });
+  // dO . sum_j P V and dO . (sum_j (P o Gam) V + sum_j P gV) over this lane's columns of the accumulators
+  float a_dot = 0.f, uw_dot = 0.f;
+  if (qvalid) {
 #pragma unroll
-  for (int i = 0; i < 6; ++i) buf[(i * 8 + grp * 4 + wig) * 64 + lane] = sums[i];
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const f32x4_t d4 = load4<T>(dO, p.dout.sr, myq, dt * 32 + 8 * qd + 4 * g, s.D, s.vec);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          a_dot = fmaf(d4[e], acc_o[dt][4 * qd + e], a_dot);
+          uw_dot = fmaf(d4[e], acc_a[dt][4 * qd + e], uw_dot);
+        }
+      }
+  }
+  // the sums of the row: both lane halves of a query, then both key groups; group 1's G_dO accumulators to group 0
+  // (sums at [0, 2560) floats, accumulator element e of lane l of wave w at 4096 + e * 256 + w * 64 + l):
+  // sum_j P, sum_j P dP, sum_j P Gam, sum_j P (Gam dP + W), max_j P
+  float sums[5] = {pair_sum(l_part), pair_sum(a_dot), pair_sum(r_part), pair_sum(uw_dot), pair_max(p_max)};
+#pragma unroll
+  for (int i = 0; i < 5; ++i) buf[(i * 8 + grp * 4 + wig) * 64 + lane] = sums[i];
+  if (grp == 1) {
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        buf[4096 + ((0 * NDT + dt) * 16 + r) * 256 + wig * 64 + lane] = acc_a[dt][r];
+        buf[4096 + ((1 * NDT + dt) * 16 + r) * 256 + wig * 64 + lane] = acc_o[dt][r];
+      }
+  }
   __syncthreads();
 #pragma unroll
-  for (int i = 0; i < 5; ++i) sums[i] += buf[(i * 8 + (1 - grp) * 4 + wig) * 64 + lane];
-  sums[5] = fmaxf(sums[5], buf[(5 * 8 + (1 - grp) * 4 + wig) * 64 + lane]);
-  __syncthreads();  // the exchange is read before the tiles are refilled
+  for (int i = 0; i < 4; ++i) sums[i] += buf[(i * 8 + (1 - grp) * 4 + wig) * 64 + lane];
+  sums[4] = fmaxf(sums[4], buf[(4 * 8 + (1 - grp) * 4 + wig) * 64 + lane]);
   const float L = sums[0];
+  if (grp == 0 && qvalid) {
+    // G_dO = inv (A + C) - (r inv) (O inv) with the normalised P (inv = 1 / L)
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    const float cval = sums[2] * inv;
+    T* OD = (T*)p.out_gdo.p + b * p.out_gdo.sb + h * p.out_gdo.sh;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int qd = 0; qd < 4; ++qd) {
+        const int d0 = dt * 32 + 8 * qd + 4 * g;
+        float r4[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 4 * qd + e;
+          const float a = acc_a[dt][i] + buf[4096 + ((0 * NDT + dt) * 16 + i) * 256 + wig * 64 + lane];
+          const float o = acc_o[dt][i] + buf[4096 + ((1 * NDT + dt) * 16 + i) * 256 + wig * 64 + lane];
+          r4[e] = inv * a - cval * (o * inv);
+        }
+        store4<T>(OD, p.out_gdo.sr, myq, d0, s.D, r4[0], r4[1], r4[2], r4[3], s.vec);
+      }
+  }
+  __syncthreads();  // the exchange is read before the tiles are refilled
   float lse_c = lse_raw;
   if (L > 0.f) {
     const float inv = 1.f / L;
     z = sums[1] * inv;
     rx = sums[2] * inv;
-    tx = (sums[3] - z * sums[2] + sums[4]) * inv;
+    tx = (sums[3] - z * sums[2]) * inv;
     moff += __builtin_log2f(L);
-    lse_c = lse_with_flag(lse_raw + __builtin_log2f(L) * kLn2, sums[5] > kPeakedFrac * L);
+    lse_c = lse_with_flag(lse_raw + __builtin_log2f(L) * kLn2, sums[4] > kPeakedFrac * L);
   }
   if (grp == 0 && qvalid && g == 0) {
     p.r_row[row_id] = rx;
@@ -1031,6 +1125,8 @@ __global__ __launch_bounds__(512, 2) void bwdbwd_rows_ks_kernel(const BwdBwdPara
     p.z_out[row_id] = z;
     p.lse_out[row_id] = lse_c;
   }
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) acc[dt] = accy[dt] = zero16();
   if (split)
     sweep([&](int kt, const char* a, const char* b_, const char* c, const char* d) __attribute__((always_inline)) {
       compute_exact(std::true_type{}, kt, a, b_, c, d);

@@ -360,8 +360,7 @@ __device__ __forceinline__ void store4(T* base, int64_t rs, int row, int col, in
   }
 }
 
-// Load 4 consecutive elements as float (zero beyond D).
-// The same for 16-bit T and a head dim D that is a multiple of 8, with 16-byte aligned rows: a lane's 8
+// gload_frag for 16-bit T and a head dim D that is a multiple of 8, with 16-byte aligned rows: a lane's 8
 // columns are all in range or all out of range, so one vector load (or zero) covers them.
 template <typename T>
 __device__ __forceinline__ typename Mfma<T>::frag_t gload_frag8(const T* base, int64_t rs, int row, int nrows, int c,
@@ -387,6 +386,7 @@ __device__ __forceinline__ void store4_8(T* base, int64_t rs, int row, int col, 
   }
 }
 
+// Load 4 consecutive elements (columns col..col+3 of row `row`) as float, zero beyond D.
 template <typename T>
 __device__ __forceinline__ f32x4_t load4(const T* base, int64_t rs, int row, int col, int D, bool vec) {
   const T* p = base + (int64_t)row * rs + col;

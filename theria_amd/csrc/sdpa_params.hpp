@@ -103,6 +103,7 @@ struct BwdBwdParams {
   const float* lse_fwd;
   float* z_out;
   float* lse_out;
+  MutView out_gdo;  // the key-split row kernel also writes G_dO (no separate JVP launch)
 };
 
 // The row kernel of this problem forms the row term and the exact normaliser itself (no row-term pass needed).
