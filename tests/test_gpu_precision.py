@@ -76,6 +76,9 @@ PEAKED = [
     (torch.float32, 1, 1, 150, 170, 32, True, 3.0),
     (torch.bfloat16, 1, 1, 150, 90, 32, False, 3.0),
     (torch.bfloat16, 1, 2, 200, 200, 32, True, 3.0),
+    # more than 64 query tiles of 32 per key block: the column pass scans its flagged tiles in two chunks
+    (torch.bfloat16, 1, 1, 2200, 160, 64, False, 3.0),
+    (torch.float16, 1, 1, 2200, 160, 64, True, 3.0),
 ]
 
 

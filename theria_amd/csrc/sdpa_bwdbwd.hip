@@ -797,19 +797,21 @@ static bool exact_in_cols(const BwdBwdParams& p) {
 // The row pass for 16-bit inputs at head dim 64 with LDS-DMA tiles, as two key groups of four waves (eight-wave
 // workgroups, two waves per SIMD): the keys of each query block are split between the groups, whose partial
 // sums meet in LDS. Each group makes two passes over its key tiles:
-//   1. with P from the forward's lse: L = sum_j P, sum_j P dP, sum_j P Gam, sum_j P Gam dP, sum_j P W and the
-//      largest P, partial per group, then exchanged. They give the row's exact normaliser (P_c = P / L: a
-//      16-bit forward's lse comes from rounded probabilities, so P sums to one only within ~2^-9), the row
+//   1. with P from the forward's lse: L = sum_j P, sum_j P Gam and the largest P, and the D-wide products
+//      A = sum_j (P o Gam) V + sum_j P gV and O = sum_j P V, partial per group, then exchanged. Then
+//      sum_j P dP = dO . O and sum_j P (Gam dP + W) = dO . A, which give the row's exact normaliser (P_c = P / L:
+//      a 16-bit forward's lse comes from rounded probabilities, so P sums to one only within ~2^-9), the row
 //      term z = sum_j P dP / L and the second-order row terms r = sum_j P_c Gam and t = sum_j P_c E1 with
-//      E1 = Gam (dP - z) + W, i.e. t = (sum_j P Gam dP - z sum_j P Gam + sum_j P W) / L;
+//      E1 = Gam (dP - z) + W, i.e. t = (dO . A - z sum_j P Gam) / L; and G_dO = (A - r O) / L, the JVP of O;
 //   2. G_Q = s sum_j (Gbar_S K + dS gK) with Gbar_S = P_c o ((Gam - r)(dP - z) + W - t), the exact form, in two
-//      D-wide accumulators; waves holding a row flagged peaked in the forward's lse enter Gbar_S and dS as two
-//      16-bit terms.
-// Every row takes the exact form (no centring, no second launch for flagged rows, no separate row-term pass),
-// and the two accumulators with the per-wave Q, dO, gQ fragments fit 256 registers, so no accumulator is
-// shuttled between register files. Writes G_Q, and r, t, z and lse + ln L (flagged peaked when the row's
-// largest P_c exceeds 1/4) for the column kernel.
-template <typename T, bool CAUSAL>
+//      D-wide accumulators.
+// Waves holding a row flagged peaked in the forward's lse enter P, P o Gam, Gbar_S and dS as two 16-bit terms.
+// Every row takes the exact form (no centring, no second launch for flagged rows, no separate row-term or JVP
+// pass); the gQ fragments sit in LDS, so that each pass's two accumulators, the per-wave Q and dO fragments and
+// the products fit 256 registers. Writes G_Q and G_dO, and r, t, z and lse + ln L (flagged peaked when the
+// row's largest P_c exceeds 1/4) for the column kernel. ALL: gQ, gK and gV are all given (the presence tests are
+// then constants, and the loop bodies have no branches between their products).
+template <typename T, bool CAUSAL, bool ALL>
 __global__ __launch_bounds__(512, 2) void bwdbwd_rows_ks_kernel(const BwdBwdParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
@@ -841,7 +843,7 @@ __global__ __launch_bounds__(512, 2) void bwdbwd_rows_ks_kernel(const BwdBwdPara
   const T* K = (const T*)p.k.p + b * p.k.sb + h * p.k.sh;
   const T* V = (const T*)p.v.p + b * p.v.sb + h * p.v.sh;
   const T* dO = (const T*)p.dout.p + b * p.dout.sb + h * p.dout.sh;
-  const bool has_gq = p.gq.p != nullptr, has_gk = p.gk.p != nullptr, has_gv = p.gv.p != nullptr;
+  const bool has_gq = ALL || p.gq.p != nullptr, has_gk = ALL || p.gk.p != nullptr, has_gv = ALL || p.gv.p != nullptr;
   const T* GQ = has_gq ? (const T*)p.gq.p + b * p.gq.sb + h * p.gq.sh : nullptr;
   const T* GK = has_gk ? (const T*)p.gk.p + b * p.gk.sb + h * p.gk.sh : nullptr;
   const T* GV = has_gv ? (const T*)p.gv.p + b * p.gv.sb + h * p.gv.sh : nullptr;
@@ -872,9 +874,12 @@ __global__ __launch_bounds__(512, 2) void bwdbwd_rows_ks_kernel(const BwdBwdPara
   const int kt0 = grp * half, kt1 = min(nkt, kt0 + half);  // this group's tiles [kt0, kt1)
 
   // S^T, Gam^T / s and (FULL) W^T and dP^T - z of 32-key subtile st of the tile in (tK, tV, tgK, tgV); P from S.
-  auto products = [&](auto full_tag, int k0s, const char* tK, const char* tV, const char* tgK, const char* tgV,
-                      int st, f32x16_t& pv, f32x16_t& gm, f32x16_t& w, f32x16_t& dpz) __attribute__((always_inline)) {
+  // MASK: the tile reaches past the last key or (causal) past this wave's first query.
+  auto products = [&](auto full_tag, auto mask_tag, int k0s, const char* tK, const char* tV, const char* tgK,
+                      const char* tgV, int st, f32x16_t& pv, f32x16_t& gm, f32x16_t& w,
+                      f32x16_t& dpz) __attribute__((always_inline)) {
     constexpr bool FULL = decltype(full_tag)::value;
+    constexpr bool MASK = decltype(mask_tag)::value;
     f32x16_t sc = zero16();
     gm = zero16();
     if constexpr (FULL) {
@@ -892,11 +897,10 @@ __global__ __launch_bounds__(512, 2) void bwdbwd_rows_ks_kernel(const BwdBwdPara
       if constexpr (FULL)
         if (has_gv) w = MM::mma(swz_cols<T, DP>(tgV, 32 * st + li, c), dof[c], w);
     }
-    const bool need_mask = (k0s + 32 > s.M) || (CAUSAL && k0s + 31 > q0w);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       float x = fast_exp2(fmaf(sc[r], c2, -moff));
-      if (need_mask) {
+      if constexpr (MASK) {
         const int key = k0s + acc_row(r, g);
         if (key >= s.M || (CAUSAL && key > myq)) x = 0.f;
       }
@@ -918,15 +922,15 @@ __global__ __launch_bounds__(512, 2) void bwdbwd_rows_ks_kernel(const BwdBwdPara
   for (int dt = 0; dt < NDT; ++dt) acc_a[dt] = acc_o[dt] = zero16();
 
   // PASS 1: the row sums and the G_dO products over this group's keys (SPLIT: P o Gam and P as two 16-bit terms).
-  auto compute_sums = [&](auto split_tag, int kt, const char* tK, const char* tV, const char* tgK, const char* tgV)
-                          __attribute__((always_inline)) {
+  auto compute_sums = [&](auto split_tag, auto mask_tag, int kt, const char* tK, const char* tV, const char* tgK,
+                          const char* tgV) __attribute__((always_inline)) {
     constexpr bool SPLIT = decltype(split_tag)::value;
 #pragma unroll
     for (int st = 0; st < NST; ++st) {
       const int k0s = kt * BN + 32 * st;
       if (CAUSAL && k0s > q0w + 31) continue;
       f32x16_t pv, gm, w, dpz;
-      products(std::false_type{}, k0s, tK, tV, tgK, tgV, st, pv, gm, w, dpz);
+      products(std::false_type{}, mask_tag, k0s, tK, tV, tgK, tgV, st, pv, gm, w, dpz);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const float pg = pv[r] * (s.scale * gm[r]);  // P o Gam
@@ -968,15 +972,15 @@ __global__ __launch_bounds__(512, 2) void bwdbwd_rows_ks_kernel(const BwdBwdPara
     }
   };
   // PASS 2: Gbar_S and dS products (SPLIT: two 16-bit terms each).
-  auto compute_exact = [&](auto split_tag, int kt, const char* tK, const char* tV, const char* tgK, const char* tgV)
-                           __attribute__((always_inline)) {
+  auto compute_exact = [&](auto split_tag, auto mask_tag, int kt, const char* tK, const char* tV, const char* tgK,
+                           const char* tgV) __attribute__((always_inline)) {
     constexpr bool SPLIT = decltype(split_tag)::value;
 #pragma unroll
     for (int st = 0; st < NST; ++st) {
       const int k0s = kt * BN + 32 * st;
       if (CAUSAL && k0s > q0w + 31) continue;
       f32x16_t pv, gm, w, dpz;
-      products(std::true_type{}, k0s, tK, tV, tgK, tgV, st, pv, gm, w, dpz);
+      products(std::true_type{}, mask_tag, k0s, tK, tV, tgK, tgV, st, pv, gm, w, dpz);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const float gam = s.scale * gm[r];
@@ -1031,28 +1035,33 @@ __global__ __launch_bounds__(512, 2) void bwdbwd_rows_ks_kernel(const BwdBwdPara
   };
   // Step i: tile kt0 + i of this group (if it has one) from set i & 1; the next one's copies go to the other set,
   // read in step i - 1, which every wave has finished at the barrier. Both groups run `half` steps (the same
-  // barriers); a group with fewer tiles idles through its last one.
+  // barriers); a group with fewer tiles idles through its last one. The tiles from mask_from on may reach past
+  // the last key or (causal) past the block's first query and take the masked copy of the loop; the groups may
+  // be in different copies at a step, but both meet the same barriers.
+  const int mask_from = min(kend % BN ? nkt - 1 : nkt, CAUSAL ? qb * BM / BN : nkt);
   auto sweep = [&](auto body) __attribute__((always_inline)) {
-    if (kt0 < kt1) issue(kt0, 0);
-    for (int i = 0; i < half; ++i) {
+    auto step = [&](auto mask_tag, int i) __attribute__((always_inline)) {
       const int kt = kt0 + i;
       wait_vm_all();
       __syncthreads();
       if (kt + 1 < kt1) issue(kt + 1, (i + 1) & 1);
-      if (kt < kt1) body(kt, tile(i & 1, 0), tile(i & 1, 1), tile(i & 1, 2), tile(i & 1, 3));
-    }
+      if (kt < kt1) body(mask_tag, kt, tile(i & 1, 0), tile(i & 1, 1), tile(i & 1, 2), tile(i & 1, 3));
+    };
+    if (kt0 < kt1) issue(kt0, 0);
+    const int isplit = min(half, max(0, mask_from - kt0));
+    int i = 0;
+    for (; i < isplit; ++i) step(std::false_type{}, i);
+    for (; i < half; ++i) step(std::true_type{}, i);
     __syncthreads();  // every wave is done with the tiles
   };
   float* buf = reinterpret_cast<float*>(smem);
 
   if (split)
-    sweep([&](int kt, const char* a, const char* b_, const char* c, const char* d) __attribute__((always_inline)) {
-      compute_sums(std::true_type{}, kt, a, b_, c, d);
-    });
+    sweep([&](auto mask_tag, int kt, const char* a, const char* b_, const char* c, const char* d)
+              __attribute__((always_inline)) { compute_sums(std::true_type{}, mask_tag, kt, a, b_, c, d); });
   else
-    sweep([&](int kt, const char* a, const char* b_, const char* c, const char* d) __attribute__((always_inline)) {
-      compute_sums(std::false_type{}, kt, a, b_, c, d);
-    });
+    sweep([&](auto mask_tag, int kt, const char* a, const char* b_, const char* c, const char* d)
+              __attribute__((always_inline)) { compute_sums(std::false_type{}, mask_tag, kt, a, b_, c, d); });
   // dO . sum_j P V and dO . (sum_j (P o Gam) V + sum_j P gV) over this lane's columns of the accumulators
   float a_dot = 0.f, uw_dot = 0.f;
   if (qvalid) {
@@ -1128,13 +1137,11 @@ __global__ __launch_bounds__(512, 2) void bwdbwd_rows_ks_kernel(const BwdBwdPara
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) acc[dt] = accy[dt] = zero16();
   if (split)
-    sweep([&](int kt, const char* a, const char* b_, const char* c, const char* d) __attribute__((always_inline)) {
-      compute_exact(std::true_type{}, kt, a, b_, c, d);
-    });
+    sweep([&](auto mask_tag, int kt, const char* a, const char* b_, const char* c, const char* d)
+              __attribute__((always_inline)) { compute_exact(std::true_type{}, mask_tag, kt, a, b_, c, d); });
   else
-    sweep([&](int kt, const char* a, const char* b_, const char* c, const char* d) __attribute__((always_inline)) {
-      compute_exact(std::false_type{}, kt, a, b_, c, d);
-    });
+    sweep([&](auto mask_tag, int kt, const char* a, const char* b_, const char* c, const char* d)
+              __attribute__((always_inline)) { compute_exact(std::false_type{}, mask_tag, kt, a, b_, c, d); });
 
   // group 1's accumulators to group 0 (element e of lane l of wave w at e * 256 + w * 64 + l)
   if (grp == 1) {
@@ -1169,6 +1176,311 @@ __global__ __launch_bounds__(512, 2) void bwdbwd_rows_ks_kernel(const BwdBwdPara
 }
 
 
+// The column pass for 16-bit inputs at head dim 64 with LDS-DMA tiles, as two query groups of four waves
+// (eight-wave workgroups, two waves per SIMD). A workgroup owns 128 keys (32 per wave, lane per key, as in
+// cols_block); the groups sweep the two halves of its 32-query tiles and sum G_V and G_K in registers, and
+// group 1's sums reach group 0 through LDS at the end. Query tiles holding a row flagged peaked in lse are
+// skipped by the sweep and run after it, shared out between the groups, with Gbar_dP, Gbar_S and dS entered as
+// two 16-bit terms. The gK and gV fragments sit in LDS, so that the K and V fragments, the two accumulators and
+// the products fit 256 registers. ALL as in the key-split row kernel.
+template <typename T, bool CAUSAL, bool ALL>
+__global__ __launch_bounds__(512, 2) void bwdbwd_cols_qs_kernel(const BwdBwdParams p) {
+  using MM = Mfma<T>;
+  using F = typename MM::frag_t;
+  static_assert(sizeof(T) == 2, "16-bit inputs only");
+  constexpr int DP = 64, NW = 4, BN = 32 * NW, BM = 32;
+  constexpr int NDT = DP / 32, NKC = DP / MM::KC, NPC = 32 / MM::KC;
+  constexpr int TB = BM * DP * 2;  // bytes per tile
+  using Dma = SwzDma<NW, DP>;
+  constexpr int NSLAB = BM / Dma::SLAB_ROWS;
+  static_assert(NSLAB * Dma::SLAB_ROWS == BM, "query tiles must be whole DMA slabs");
+  constexpr int FLAG = 4 * BM, RB = FLAG + 4;  // row terms [lse * log2(e) | z | r | t] of a tile, then its flag
+  constexpr int TILES = 2 * 2 * 3 * TB;        // [group][set][Q, dO, gQ]
+  constexpr int NFR = NW * NKC * 64;           // fragments per operand
+  // the tiles, then the gK and gV fragments (fragment c of lane l of key slice w at (w * NKC + c) * 64 + l);
+  // group 1's accumulators reach group 0 through the same memory at the end
+  __shared__ __attribute__((aligned(1024))) char smem[TILES + 2 * NFR * sizeof(F)];
+  static_assert(sizeof(smem) >= 2 * NDT * 16 * 256 * sizeof(float), "the exchange fits in the tile memory");
+  __shared__ __attribute__((aligned(16))) float sRow[2][2][RB];  // [group][set]
+  __shared__ int sPk[64];
+  __shared__ int sAny;
+
+  const Shape& s = p.s;
+  const int tid = threadIdx.x, lane = tid & 63, li = lane & 31, g = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2, wig = wave & 3;  // query group, wave in group
+  const int ltid = tid & 255;                 // thread in group
+  const int nkb = (s.M + BN - 1) / BN;
+  const int bid = xcd_remap(blockIdx.x, gridDim.x);
+  const int bh = bid / nkb;
+  const int kb = bid - bh * nkb;
+  const int b = bh / s.H, h = bh - b * s.H;
+  const T* Q = (const T*)p.q.p + b * p.q.sb + h * p.q.sh;
+  const T* K = (const T*)p.k.p + b * p.k.sb + h * p.k.sh;
+  const T* V = (const T*)p.v.p + b * p.v.sb + h * p.v.sh;
+  const T* dO = (const T*)p.dout.p + b * p.dout.sb + h * p.dout.sh;
+  const bool has_gq = ALL || p.gq.p != nullptr, has_gk = ALL || p.gk.p != nullptr, has_gv = ALL || p.gv.p != nullptr;
+  const T* GQ = has_gq ? (const T*)p.gq.p + b * p.gq.sb + h * p.gq.sh : nullptr;
+  const T* GK = has_gk ? (const T*)p.gk.p + b * p.gk.sb + h * p.gk.sh : nullptr;
+  const T* GV = has_gv ? (const T*)p.gv.p + b * p.gv.sb + h * p.gv.sh : nullptr;
+  const int key0 = kb * BN;
+  const int kw0 = key0 + wig * 32;
+  const int mykey = kw0 + li;
+  const bool kvalid = mykey < s.M;
+
+  F* sFr = reinterpret_cast<F*>(smem + TILES);
+  F kf[NKC], vf[NKC];
+#pragma unroll
+  for (int c = 0; c < NKC; ++c) {
+    kf[c] = gload_frag<T>(K, p.k.sr, mykey, s.M, c, s.D, s.vec);
+    vf[c] = gload_frag<T>(V, p.v.sr, mykey, s.M, c, s.D, s.vec);
+    // read after the sweep's first barrier
+    if (grp == 0) {
+      if (has_gk) sFr[(wig * NKC + c) * 64 + lane] = gload_frag<T>(GK, p.gk.sr, mykey, s.M, c, s.D, s.vec);
+      if (has_gv) sFr[NFR + (wig * NKC + c) * 64 + lane] = gload_frag<T>(GV, p.gv.sr, mykey, s.M, c, s.D, s.vec);
+    }
+  }
+  if (tid == 0) sAny = 0;
+  f32x16_t accV[NDT], accK[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) accV[dt] = accK[dt] = zero16();
+  const float c2 = s.scale * kLog2e;
+  const int qbeg = CAUSAL ? (key0 / BM) * BM : 0;
+  const int nqt = s.T > qbeg ? (s.T - qbeg + BM - 1) / BM : 0;
+  const int half = (nqt + 1) / 2;
+  const int it0 = grp * half, it1 = min(nqt, it0 + half);  // this group's tiles [it0, it1) of the sweep
+  const int64_t rowbase = (int64_t)bh * s.T;
+
+  // Row terms of a tile for group thread ltid < BM, held raw (rows past the end: lse = +inf) and converted when
+  // stored: lse * log2(e) (+inf for rows past the end or without visible keys, so P = 0), z, r, t.
+  float r_lse = THERIA_INF, r_z = 0.f, r_r = 0.f, r_t = 0.f;
+  auto load_rows = [&](int it, int lim) {
+    if (ltid < BM && it < lim) {
+      const int qq = qbeg + it * BM + ltid;
+      const bool ok = qq < s.T;
+      r_lse = ok ? p.lse[rowbase + qq] : THERIA_INF;
+      r_z = ok ? p.delta[rowbase + qq] : 0.f;
+      r_r = ok ? p.r_row[rowbase + qq] : 0.f;
+      r_t = ok ? p.t_row[rowbase + qq] : 0.f;
+    }
+  };
+  auto store_rows = [&](float* sr) {
+    if (ltid < BM) {
+      sr[ltid] = __builtin_isinf(r_lse) ? THERIA_INF : r_lse * kLog2e;
+      sr[BM + ltid] = r_z;
+      sr[2 * BM + ltid] = r_r;
+      sr[3 * BM + ltid] = r_t;
+      const bool pk = __any(lse_peaked(r_lse));  // the tile's rows are the lanes of the group's first wave
+      if (ltid == 0) sr[FLAG] = pk ? 1.f : 0.f;
+    }
+  };
+
+  // Query tile it held in (tQ, tO, tgQ) with its row terms in sr. SPLIT: Gbar_dP, Gbar_S and dS enter the
+  // products as two 16-bit terms each.
+  auto tile = [&](auto split_tag, int it, const char* tQ, const char* tO, const char* tgQ,
+                  const float* sr) __attribute__((always_inline)) {
+    constexpr bool SPLIT = decltype(split_tag)::value;
+    const int q0 = qbeg + it * BM;
+    if (CAUSAL && kw0 > q0 + BM - 1) return;
+    f32x16_t sc = zero16(), gm = zero16(), w = zero16(), dpz;
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      const f32x4_t z4 = *reinterpret_cast<const f32x4_t*>(sr + BM + 8 * qd + 4 * g);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dpz[4 * qd + e] = -z4[e];
+    }
+#pragma unroll
+    for (int c = 0; c < NKC; ++c) {
+      const F qfr = swz_cols<T, DP>(tQ, li, c);
+      const F ofr = swz_cols<T, DP>(tO, li, c);
+      sc = MM::mma(qfr, kf[c], sc);
+      dpz = MM::mma(ofr, vf[c], dpz);
+      if (has_gq) gm = MM::mma(swz_cols<T, DP>(tgQ, li, c), kf[c], gm);
+      if (has_gk) gm = MM::mma(qfr, sFr[(wig * NKC + c) * 64 + lane], gm);
+      if (has_gv) w = MM::mma(ofr, sFr[NFR + (wig * NKC + c) * 64 + lane], w);
+    }
+    const bool diag = CAUSAL && (kw0 + 31 > q0);
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      const int o = 8 * qd + 4 * g;
+      const f32x4_t l4 = *reinterpret_cast<const f32x4_t*>(sr + o);
+      const f32x4_t r4 = *reinterpret_cast<const f32x4_t*>(sr + 2 * BM + o);
+      const f32x4_t t4 = *reinterpret_cast<const f32x4_t*>(sr + 3 * BM + o);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = 4 * qd + e;
+        float pv = fast_exp2(fmaf(sc[r], c2, -l4[e]));
+        if (!kvalid) pv = 0.f;
+        if (diag && mykey > q0 + acc_row(r, g)) pv = 0.f;
+        const float gam = s.scale * gm[r];
+        const float ds = pv * dpz[r];
+        const float e1 = fmaf(gam, dpz[r], w[r]);
+        gm[r] = pv * (gam - r4[e]);                        // Gbar_dP
+        w[r] = pv * e1 - r4[e] * ds - t4[e] * pv;          // Gbar_S
+        dpz[r] = ds;                                       // dS
+      }
+    }
+#pragma unroll
+    for (int cc = 0; cc < NPC; ++cc) {
+      if constexpr (SPLIT) {
+        F gdph, gdpl, gsh, gsl, dsh, dsl;
+        split_frag<T>(gm, cc, gdph, gdpl);
+        split_frag<T>(w, cc, gsh, gsl);
+        split_frag<T>(dpz, cc, dsh, dsl);
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+          const F ro = swz_rows<T, DP>(tO, 0, cc, dt * 32);
+          accV[dt] = MM::mma(gdph, ro, accV[dt]);
+          accV[dt] = MM::mma(gdpl, ro, accV[dt]);
+          const F rq = swz_rows<T, DP>(tQ, 0, cc, dt * 32);
+          accK[dt] = MM::mma(gsh, rq, accK[dt]);
+          accK[dt] = MM::mma(gsl, rq, accK[dt]);
+          if (has_gq) {
+            const F rg = swz_rows<T, DP>(tgQ, 0, cc, dt * 32);
+            accK[dt] = MM::mma(dsh, rg, accK[dt]);
+            accK[dt] = MM::mma(dsl, rg, accK[dt]);
+          }
+        }
+      } else {
+        const F gdpf = acc_frag<T>(gm, cc), gsf = acc_frag<T>(w, cc), dsf = acc_frag<T>(dpz, cc);
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+          accV[dt] = MM::mma(gdpf, swz_rows<T, DP>(tO, 0, cc, dt * 32), accV[dt]);
+          accK[dt] = MM::mma(gsf, swz_rows<T, DP>(tQ, 0, cc, dt * 32), accK[dt]);
+          if (has_gq) accK[dt] = MM::mma(dsf, swz_rows<T, DP>(tgQ, 0, cc, dt * 32), accK[dt]);
+        }
+      }
+    }
+  };
+
+  const Dma dma(wig, lane);
+  // Byte offsets fit in 32 bits: the host only selects this kernel when each (batch, head) slab of Q, dO and gQ
+  // spans less than 2^31 bytes.
+  const uint32_t qrs = (uint32_t)p.q.sr * 2, ors = (uint32_t)p.dout.sr * 2;
+  const uint32_t gqrs = has_gq ? (uint32_t)p.gq.sr * 2 : 0u;
+  const rsrc_t qrsrc = make_rsrc(Q, (uint32_t)slab_span(s.T, qrs, 2 * DP)),
+               orsrc = make_rsrc(dO, (uint32_t)slab_span(s.T, ors, 2 * DP));
+  const rsrc_t gqrsrc = make_rsrc(has_gq ? (const void*)GQ : (const void*)Q, (uint32_t)slab_span(s.T, gqrs, 2 * DP));
+  auto tiles = [&](int set) { return smem + (grp * 2 + set) * 3 * TB; };  // Q, dO, gQ at 0, TB, 2 TB
+  auto issue = [&](int it, int set) {
+    const int q0 = qbeg + it * BM;
+    char* t = tiles(set);
+    dma.template issue_clamped<NSLAB>(qrsrc, qrs, q0, s.T, t);
+    dma.template issue_clamped<NSLAB>(orsrc, ors, q0, s.T, t + TB);
+    if (has_gq) dma.template issue_clamped<NSLAB>(gqrsrc, gqrs, q0, s.T, t + 2 * TB);
+  };
+
+  // The sweep. Step i: tile it0 + i of this group (if it has one) from set i & 1; the next one's copies and row
+  // terms go to the other set, read in step i - 1, which every wave has finished at the barrier. Both groups run
+  // `half` steps (the same barriers); a group with fewer tiles idles through its last one.
+  bool pk_any = false;  // a tile holding a peaked row was skipped
+  if (it0 < it1) {
+    issue(it0, 0);
+    load_rows(it0, it1);
+    store_rows(sRow[grp][0]);
+    load_rows(it0 + 1, it1);
+  }
+  for (int i = 0; i < half; ++i) {
+    const int it = it0 + i;
+    wait_vm_all();
+    __syncthreads();
+    if (it + 1 < it1) {
+      issue(it + 1, (i + 1) & 1);
+      store_rows(sRow[grp][(i + 1) & 1]);
+      load_rows(it + 2, it1);
+    }
+    if (it < it1) {
+      const float* sr = sRow[grp][i & 1];
+      const bool pk = __builtin_amdgcn_readfirstlane(__float_as_uint(sr[FLAG])) != 0u;  // uniform
+      pk_any |= pk;
+      const char* t = tiles(i & 1);
+      if (!pk) tile(std::false_type{}, it, t, t + TB, t + 2 * TB, sr);
+    }
+  }
+  if (pk_any && lane == 0) sAny = 1;
+  __syncthreads();  // every wave is done with the tiles; sAny is final
+
+  // The tiles holding a peaked row, found 64 at a time from the lse flags; the groups take alternate ones.
+  if (sAny) {
+    for (int t0 = 0; t0 < nqt; t0 += 64) {
+      const int nt = min(64, nqt - t0);
+      __syncthreads();  // every thread is done with the previous flags and tiles
+      if (tid < 64) sPk[tid] = 0;
+      __syncthreads();
+      constexpr int RPT = 64 * BM / 512;
+      const int r0 = qbeg + t0 * BM, r1 = min(s.T, qbeg + (t0 + nt) * BM);
+#pragma unroll
+      for (int j = 0; j < RPT; ++j) {
+        const int r = r0 + tid + 512 * j;
+        if (r < r1 && lse_peaked(p.lse[rowbase + r])) sPk[(tid + 512 * j) / BM] = 1;
+      }
+      __syncthreads();
+      const uint64_t mask = __ballot(sPk[lane] != 0);  // the same in every wave
+      const int npk = __builtin_popcountll(mask);
+      for (int j = 0; j < npk; j += 2) {
+        int ti = -1;  // this group's tile: the (j + grp)-th flagged one
+        if (j + grp < npk) {
+          uint64_t m = mask;
+          for (int x = 0; x < j + grp; ++x) m &= m - 1;
+          ti = t0 + __builtin_ctzll(m);
+        }
+        __syncthreads();  // the tile buffers are free
+        if (ti >= 0) {
+          issue(ti, 0);
+          load_rows(ti, nqt);
+          store_rows(sRow[grp][0]);
+        }
+        wait_vm_all();
+        __syncthreads();
+        if (ti >= 0) {
+          const char* t = tiles(0);
+          tile(std::true_type{}, ti, t, t + TB, t + 2 * TB, sRow[grp][0]);
+        }
+      }
+    }
+    __syncthreads();  // every wave is done with the tiles
+  }
+
+  // group 1's accumulators to group 0 (element e of lane l of wave w at e * 256 + w * 64 + l)
+  float* xb = reinterpret_cast<float*>(smem);
+  if (grp == 1) {
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        xb[(dt * 16 + r) * 256 + wig * 64 + lane] = accV[dt][r];
+        xb[((NDT + dt) * 16 + r) * 256 + wig * 64 + lane] = accK[dt][r];
+      }
+  }
+  __syncthreads();
+  if (grp == 1) return;
+  T* OV = (T*)p.out_gv.p + b * p.out_gv.sb + h * p.out_gv.sh;
+  T* OK = (T*)p.out_gk.p + b * p.out_gk.sb + h * p.out_gk.sh;
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) {
+    const int d = dt * 32 + li;
+    if (d < s.D) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kw0 + acc_row(r, g);
+        if (key < s.M) {
+          const float v = accV[dt][r] + xb[(dt * 16 + r) * 256 + wig * 64 + lane];
+          const float k = accK[dt][r] + xb[((NDT + dt) * 16 + r) * 256 + wig * 64 + lane];
+          OV[(int64_t)key * p.out_gv.sr + d] = (T)v;
+          OK[(int64_t)key * p.out_gk.sr + d] = (T)(k * s.scale);
+        }
+      }
+    }
+  }
+}
+
+// The query-split column kernel takes 16-bit problems at head dim 64 whose Q, dO, gQ slabs allow LDS DMA and
+// whose rows kernel runs its exact row blocks on its own (no row blocks in the column grid).
+template <typename T, int DP>
+static bool cols_qs_ok(const BwdBwdParams& p) {
+  return DP == 64 && sizeof(T) == 2 && cols_dma<T, DP>(p) && !exact_in_cols<T, DP>(p);
+}
+
 struct RowsLauncher {
   template <typename T, int DP, bool CAUSAL>
   static hipError_t run(const BwdBwdParams& p, hipStream_t st) {
@@ -1177,7 +1489,10 @@ struct RowsLauncher {
     if (nblk == 0) return hipSuccess;
     if constexpr (sizeof(T) == 2 && DP == 64) {
       if (rows_ks_ok<T, DP>(p)) {  // every row block exact in one launch (the column grid has no row blocks)
-        hipLaunchKernelGGL((bwdbwd_rows_ks_kernel<T, CAUSAL>), dim3((unsigned)nblk), dim3(512), 0, st, p);
+        if (p.gq.p && p.gk.p && p.gv.p)
+          hipLaunchKernelGGL((bwdbwd_rows_ks_kernel<T, CAUSAL, true>), dim3((unsigned)nblk), dim3(512), 0, st, p);
+        else
+          hipLaunchKernelGGL((bwdbwd_rows_ks_kernel<T, CAUSAL, false>), dim3((unsigned)nblk), dim3(512), 0, st, p);
         return hipGetLastError();
       }
     }
@@ -1205,6 +1520,16 @@ struct ColsLauncher {
     const int64_t nblk = (int64_t)((p.s.M + 127) / 128) * p.s.B * p.s.H;
     const int64_t nrow = (int64_t)((p.s.T + 127) / 128) * p.s.B * p.s.H;
     const bool dma = (sizeof(T) == 2 && (DP == 64 || DP == 128)) && cols_dma<T, DP>(p);
+    if constexpr (sizeof(T) == 2 && DP == 64) {
+      if (cols_qs_ok<T, DP>(p)) {
+        if (nblk == 0) return hipSuccess;
+        if (p.gq.p && p.gk.p && p.gv.p)
+          hipLaunchKernelGGL((bwdbwd_cols_qs_kernel<T, CAUSAL, true>), dim3((unsigned)nblk), dim3(512), 0, st, p);
+        else
+          hipLaunchKernelGGL((bwdbwd_cols_qs_kernel<T, CAUSAL, false>), dim3((unsigned)nblk), dim3(512), 0, st, p);
+        return hipGetLastError();
+      }
+    }
     if constexpr (sizeof(T) == 2) {
       if (exact_in_cols<T, DP>(p)) {
         if (nblk + nrow == 0) return hipSuccess;

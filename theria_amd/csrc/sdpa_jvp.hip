@@ -267,8 +267,9 @@ __global__ __launch_bounds__(256) void jvp_kernel(const JvpParams p) {
 // there, same box). Each group streams its own half of the key tiles (64 keys per tile, 128 KB of LDS in
 // all) through its own double-buffered tiles; both groups meet at the same barrier every step (a group
 // whose half is shorter idles through the last step). The float32 partial sums of group 1 (accumulators,
-// row sums) pass to group 0 through LDS at the end.
-template <typename T, bool CAUSAL, bool HAS_O>
+// row sums) pass to group 0 through LDS at the end. ALL: every tangent is given (the presence tests are then
+// constants, and the loop body has no branches between its products).
+template <typename T, bool CAUSAL, bool HAS_O, bool ALL>
 __global__ __launch_bounds__(512, 2) void jvp_ksplit_kernel(const JvpParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
@@ -296,7 +297,7 @@ __global__ __launch_bounds__(512, 2) void jvp_ksplit_kernel(const JvpParams p) {
   const T* Q = (const T*)p.q.p + b * p.q.sb + h * p.q.sh;
   const T* K = (const T*)p.k.p + b * p.k.sb + h * p.k.sh;
   const T* V = (const T*)p.v.p + b * p.v.sb + h * p.v.sh;
-  const bool has_tq = p.tq.p != nullptr, has_tk = p.tk.p != nullptr, has_tv = p.tv.p != nullptr;
+  const bool has_tq = ALL || p.tq.p != nullptr, has_tk = ALL || p.tk.p != nullptr, has_tv = ALL || p.tv.p != nullptr;
   const T* TQ = has_tq ? (const T*)p.tq.p + b * p.tq.sb + h * p.tq.sh : nullptr;
   const T* TK = has_tk ? (const T*)p.tk.p + b * p.tk.sb + h * p.tk.sh : nullptr;
   const T* TV = has_tv ? (const T*)p.tv.p + b * p.tv.sb + h * p.tv.sh : nullptr;
@@ -334,10 +335,12 @@ __global__ __launch_bounds__(512, 2) void jvp_ksplit_kernel(const JvpParams p) {
   const int half = (nkt + 1) / 2;
   const int kt0 = grp * half, kt1 = min(nkt, kt0 + half);  // this group's tiles [kt0, kt1)
 
-  // The key tile kt held in (tK, tV, ttK, ttV): as jvp_kernel, 32-key subtiles one after the other.
-  auto compute = [&](auto split_tag, int kt, const char* tK, const char* tV, const char* ttK,
+  // The key tile kt held in (tK, tV, ttK, ttV): as jvp_kernel, 32-key subtiles one after the other. MASK: the
+  // tile reaches past the last key or (causal) past this wave's first query.
+  auto compute = [&](auto split_tag, auto mask_tag, int kt, const char* tK, const char* tV, const char* ttK,
                      const char* ttV) __attribute__((always_inline)) {
     constexpr bool SPLIT = decltype(split_tag)::value;
+    constexpr bool MASK = decltype(mask_tag)::value;
 #pragma unroll
     for (int st = 0; st < NST; ++st) {
       const int k0 = kt * BN + 32 * st;
@@ -350,11 +353,10 @@ __global__ __launch_bounds__(512, 2) void jvp_ksplit_kernel(const JvpParams p) {
         if (has_tq) gm = MM::mma(kfr, tqf[c], gm);
         if (has_tk) gm = MM::mma(swz_cols<T, DP>(ttK, 32 * st + li, c), qf[c], gm);
       }
-      const bool need_mask = (k0 + 32 > s.M) || (CAUSAL && k0 + 31 > q0w);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         float pv = fast_exp2(fmaf(sc[r], c2, -moff));
-        if (need_mask) {
+        if constexpr (MASK) {
           const int key = k0 + acc_row(r, g);
           if (key >= s.M || (CAUSAL && key > myq)) pv = 0.f;
         }
@@ -414,15 +416,22 @@ __global__ __launch_bounds__(512, 2) void jvp_ksplit_kernel(const JvpParams p) {
     if (has_tv) dma.template issue_clamped<NSLAB>(tvrsrc, tvrs, k0, s.M, tile(set, 3));
   };
   // Step i: tile kt0 + i of this group (if it has one) from set i & 1; the next one's copies go to the other
-  // set, read in step i - 1, which every wave has finished at the barrier.
+  // set, read in step i - 1, which every wave has finished at the barrier. The tiles from mask_from on may
+  // reach past the last key or (causal) past the block's first query and take the masked copy of the loop;
+  // the groups may be in different copies at a step, but both meet the same barriers.
+  const int mask_from = min(kend % BN ? nkt - 1 : nkt, CAUSAL ? qb * BM / BN : nkt);
   auto sweep = [&](auto split_tag) __attribute__((always_inline)) {
-    for (int i = 0; i < half; ++i) {
+    auto step = [&](auto mask_tag, int i) __attribute__((always_inline)) {
       const int kt = kt0 + i;
       wait_vm_all();
       __syncthreads();
       if (kt + 1 < kt1) issue(kt + 1, (i + 1) & 1);
-      if (kt < kt1) compute(split_tag, kt, tile(i & 1, 0), tile(i & 1, 1), tile(i & 1, 2), tile(i & 1, 3));
-    }
+      if (kt < kt1) compute(split_tag, mask_tag, kt, tile(i & 1, 0), tile(i & 1, 1), tile(i & 1, 2), tile(i & 1, 3));
+    };
+    const int isplit = min(half, max(0, mask_from - kt0));
+    int i = 0;
+    for (; i < isplit; ++i) step(std::false_type{}, i);
+    for (; i < half; ++i) step(std::true_type{}, i);
   };
   if (kt0 < kt1) issue(kt0, 0);
   // The waves of a workgroup may take different copies of the loop: both meet the same barriers.
@@ -501,9 +510,12 @@ struct JvpLauncher {
       for (const View* v : {&p.k, &p.v, &p.tk, &p.tv})
         if (v->p && !slab_fits_dma(p.s.M, v->sr, p.s.D)) ok = false;
       if (ok) {
-        if constexpr (DP == 64)
-          hipLaunchKernelGGL((jvp_ksplit_kernel<T, CAUSAL, HAS_O>), dim3((unsigned)nblk), dim3(512), 0, st, p);
-        else
+        if constexpr (DP == 64) {
+          if (p.tq.p && p.tk.p && p.tv.p)
+            hipLaunchKernelGGL((jvp_ksplit_kernel<T, CAUSAL, HAS_O, true>), dim3((unsigned)nblk), dim3(512), 0, st, p);
+          else
+            hipLaunchKernelGGL((jvp_ksplit_kernel<T, CAUSAL, HAS_O, false>), dim3((unsigned)nblk), dim3(512), 0, st, p);
+        } else
           hipLaunchKernelGGL((jvp_kernel<T, DP, CAUSAL, HAS_O, true>), dim3((unsigned)nblk), dim3(256), 0, st, p);
         return hipGetLastError();
       }
