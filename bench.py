@@ -55,6 +55,8 @@ def _args():
                     help="comma-separated subset of the other configs to run (c2_fp16, c3, c4, c5, scores)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (for profiling runs)")
     ap.add_argument("--copy-calibration", action="store_true", help="run a plain copy of known size (PMC scaling)")
+    ap.add_argument("--atomic-probe", action="store_true",
+                    help="time float32 atomic adds into a config-2 dQ-sized buffer (the fused-backward bound)")
     return ap.parse_args()
 
 
@@ -441,6 +443,36 @@ def copy_calibration():
     print(json.dumps({"copy_bytes_each_way": src.numel() * 4, "launches": 5}), flush=True)
 
 
+def atomic_probe():
+    """Float32 atomic-add throughput in the pattern a backward forming dQ inside the dK/dV kernel needs: every
+    key block adds its partial dQ (config 2: B4 H16 S2048 D64, 33.5 MB in float32) once, so 2048 / 256 = 8 adds
+    per element with eight-wave key blocks (16 with four-wave blocks). Runs theria_debug_atomic_probe from the
+    counter-enabled build; the same pattern as plain stores for scale. One JSON line."""
+    import ctypes
+
+    import torch
+
+    from theria_amd import _lib
+
+    lib = _lib.load(_lib.TILES_LIB_PATH)
+    dev = torch.device("cuda:0")
+    n = 4 * 16 * 2048 * 64
+    buf = torch.zeros(n, dtype=torch.float32, device=dev)
+    st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    out = {"probe": "float32 atomic adds, config-2 dQ (B4 H16 S2048 D64)", "buffer_bytes": n * 4}
+    for reps in (8, 16):
+        for atomic in (1, 0):
+            def go():
+                rc = lib.theria_debug_atomic_probe(ctypes.c_void_p(buf.data_ptr()), n, reps, atomic, st)
+                if rc != _lib.OK:
+                    raise RuntimeError(lib.theria_last_error().decode(errors="replace"))
+            ms = _time(go, 20)
+            key = f"{'atomic' if atomic else 'store'}_x{reps}"
+            out[f"{key}_us"] = round(ms * 1e3, 1)
+            out[f"{key}_TBps"] = round(n * 4 * reps / (ms * 1e-3) / 1e12, 2)
+    print(json.dumps(out), flush=True)
+
+
 def main() -> int:
     args = _args()
     if args.gpus != 1:
@@ -460,6 +492,9 @@ def main() -> int:
     _lib.load()
     if args.copy_calibration:
         copy_calibration()
+        return 0
+    if args.atomic_probe:
+        atomic_probe()
         return 0
     r = bench_config2(args.steps, args.warmup, args.warmup_seconds)
     value = r["flop_step"] / (r["wall_ms"] * 1e-3) / 1e12

@@ -219,6 +219,15 @@ int theria_qk_softmax(const theria_sdpa_problem_t* p, const theria_tensor_t* q, 
  */
 int theria_debug_tile_counts(uint64_t* counts, int32_t reset);
 
+/*
+ * Measurement only (no counterpart in the reference): float32 atomic-add throughput in the pattern a backward that
+ * formed dQ inside the dK/dV kernel would need. Each 256-thread workgroup adds a constant to 128 x 64 consecutive
+ * floats of buf (relaxed, device scope; atomic = 0: plain stores of the same shape), reps workgroups per
+ * 8192-float block, consecutive workgroups on different blocks; n rounded down to whole blocks. Only the
+ * counter-enabled build (libtheria_sdpa_tiles.so) runs it; libtheria_sdpa.so returns THERIA_ERR_CONTRACT.
+ */
+int theria_debug_atomic_probe(float* buf, int64_t n, int32_t reps, int32_t atomic, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -137,3 +137,14 @@ def test_production_library_has_no_tile_counters():
     assert _lib.load().theria_debug_tile_counts(counts, 0) == _lib.ERR_CONTRACT
     assert list(counts) == [0, 0, 0]
     assert b"without tile counters" in _lib.load().theria_last_error()
+
+
+def test_production_library_has_no_atomic_probe():
+    """theria_debug_atomic_probe runs only in the counter-enabled build; the production library refuses it before any
+    HIP call (the buffer pointer is never dereferenced on the host)."""
+    from theria_amd import _lib
+
+    fake = ctypes.c_void_p(0x1000)
+    assert _lib.load().theria_debug_atomic_probe(fake, 8192, 1, 1, None) == _lib.ERR_CONTRACT
+    assert b"without the measurement kernels" in _lib.load().theria_last_error()
+    assert _lib.load().theria_debug_atomic_probe(None, 8192, 1, 1, None) == _lib.ERR_CONTRACT

@@ -83,6 +83,7 @@ SIGNATURES = {
     "theria_qk_scores": ([_PR, _TV, _TV, _P, ctypes.c_int32, _P], ctypes.c_int),
     "theria_qk_softmax": ([_PR, _TV, _TV, _P, _P], ctypes.c_int),
     "theria_debug_tile_counts": ([ctypes.POINTER(ctypes.c_uint64), ctypes.c_int32], ctypes.c_int),
+    "theria_debug_atomic_probe": ([_P, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, _P], ctypes.c_int),
 }
 
 _lock = threading.Lock()

@@ -539,6 +539,19 @@ THERIA_API int theria_debug_tile_counts(uint64_t* counts, int32_t reset) {
 #endif
 }
 
+THERIA_API int theria_debug_atomic_probe(float* buf, int64_t n, int32_t reps, int32_t atomic, void* stream) {
+  if (!buf || n < 128 * 64 || reps <= 0)
+    return fail(THERIA_ERR_CONTRACT, "theria_debug_atomic_probe: needs a buffer of at least 8192 floats and reps > 0");
+#ifdef THERIA_TILE_COUNT
+  return hip_status(theria::launch_atomic_probe(buf, n, reps, atomic != 0, (hipStream_t)stream),
+                    "theria_debug_atomic_probe");
+#else
+  (void)stream;
+  return fail(THERIA_ERR_CONTRACT, "theria_debug_atomic_probe: this library was built without the measurement "
+                                   "kernels (libtheria_sdpa_tiles.so has them)");
+#endif
+}
+
 // Partial-fusion score kernels: the problem's v-related fields are unused; causal must be 0.
 static int run_scores(const theria_sdpa_problem_t* p, const theria_tensor_t* q, const theria_tensor_t* k, void* out,
                       bool out_f32, bool softmax, void* stream, const char* what) {

@@ -134,6 +134,8 @@ hipError_t launch_scores(const ScoresParams& p, hipStream_t st);
 // Executed 32 x 32 tile units of the pipelined kernels (counter-enabled build only; reset: zero them after reading).
 hipError_t tile_counts_fwd(unsigned long long* fwd, bool reset);
 hipError_t tile_counts_bwd(unsigned long long* dq, unsigned long long* dkdv, bool reset);
+// Float32 atomic adds (or, atomic = false, plain stores) over n floats, reps times, in dQ-tile-shaped workgroups.
+hipError_t launch_atomic_probe(float* buf, int64_t n, int reps, bool atomic, hipStream_t st);
 #endif
 
 }  // namespace theria
