@@ -34,7 +34,7 @@ __global__ __launch_bounds__(256) void scores_kernel(const ScoresParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
   constexpr int NKC = DP / MM::KC;
-  constexpr int NW = 4, NT = 64 * NW, BN = 64;
+  constexpr int NW = 4, NT = 64 * NW, BN = 64, NU = BN / 32;
   constexpr int PITCH = DP + 16 / (int)sizeof(T);  // K tile rows (padded)
   constexpr int OP = 32 + 4;                        // output staging rows, in floats (padded against bank conflicts)
   __shared__ __attribute__((aligned(16))) T sK[BN * PITCH];
@@ -58,24 +58,25 @@ __global__ __launch_bounds__(256) void scores_kernel(const ScoresParams p) {
 
   const int nkt = (s.M + BN - 1) / BN;
   TileStage<T, BN, DP, NT> stK;
-  // S^T of key tile kt for this wave's 32 queries: st[u] holds keys kt*BN + 32u + acc_row(r, g) of query li;
-  // keys past the end are -inf. Stages the tile (two barriers) and prefetches the next one.
-  auto tile_scores = [&](int kt, f32x16_t (&st)[2]) {
+  // Stages key tile kt (two barriers) and prefetches the next one.
+  auto stage = [&](int kt) {
     __syncthreads();  // every wave is done with the previous tile
     stK.store(sK, PITCH);
     __syncthreads();
     if (kt + 1 < nkt) stK.load_any(K, p.k.sr, (kt + 1) * BN, s.M, s.D, s.vec);
+  };
+  // S^T of subtile u of the staged tile kt for this wave's 32 queries: keys kt*BN + 32u + acc_row(r, g) of
+  // query li; keys past the end are -inf.
+  auto sub_scores = [&](int kt, int u) {
+    f32x16_t st = zero16();
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      st[u] = zero16();
+    for (int c = 0; c < NKC; ++c) st = MM::mma(lds_cols<T, KLIN>(sK, PITCH, 32 * u + li, 0, c), qf[c], st);
+    if (kt * BN + 32 * u + 32 > s.M) {
 #pragma unroll
-      for (int c = 0; c < NKC; ++c) st[u] = MM::mma(lds_cols<T, KLIN>(sK, PITCH, 32 * u + li, 0, c), qf[c], st[u]);
-      if (kt * BN + 32 * u + 32 > s.M) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (kt * BN + 32 * u + acc_row(r, g) >= s.M) st[u][r] = -THERIA_INF;
-      }
+      for (int r = 0; r < 16; ++r)
+        if (kt * BN + 32 * u + acc_row(r, g) >= s.M) st[r] = -THERIA_INF;
     }
+    return st;
   };
 
   // softmax statistics of query li (log2 domain): max m and sum l of exp2(S c2 - m) over its keys
@@ -84,21 +85,20 @@ __global__ __launch_bounds__(256) void scores_kernel(const ScoresParams p) {
     float m = -THERIA_INF, l = 0.f;
     if (nkt > 0) stK.load_any(K, p.k.sr, 0, s.M, s.D, s.vec);
     for (int kt = 0; kt < nkt; ++kt) {
-      f32x16_t st[2];
-      tile_scores(kt, st);
-      float mx = m;
+      stage(kt);
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
+      for (int u = 0; u < NU; ++u) {
+        const f32x16_t st = sub_scores(kt, u);
+        float mx = m;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[u][r] * c2);
-      if (mx == -THERIA_INF) continue;  // no visible key yet (M = 0 never reaches here)
-      float part = 0.f;
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[r] * c2);
+        if (mx == -THERIA_INF) continue;  // no visible key yet (M = 0 never reaches here)
+        float part = 0.f;
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) part += fast_exp2(fmaf(st[u][r], c2, -mx));
-      l = l * fast_exp2(m - mx) + part;
-      m = mx;
+        for (int r = 0; r < 16; ++r) part += fast_exp2(fmaf(st[r], c2, -mx));
+        l = l * fast_exp2(m - mx) + part;
+        m = mx;
+      }
     }
     const float mt = pair_max(m);
     const float lt = pair_sum(m == -THERIA_INF ? 0.f : l * fast_exp2(m - mt));
@@ -113,17 +113,17 @@ __global__ __launch_bounds__(256) void scores_kernel(const ScoresParams p) {
   const bool vrows = (s.M % 4) == 0;
   if (nkt > 0) stK.load_any(K, p.k.sr, 0, s.M, s.D, s.vec);
   for (int kt = 0; kt < nkt; ++kt) {
-    f32x16_t st[2];
-    tile_scores(kt, st);
+    stage(kt);
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < NU; ++u) {
+      const f32x16_t st = sub_scores(kt, u);
       // this lane's values into the wave's buffer: row li (query), keys 8j + 4g .. + 3 of subtile u
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         f32x4_t v;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float x = st[u][4 * j + e];
+          const float x = st[4 * j + e];
           v[e] = MODE == kProbs ? (x == -THERIA_INF ? 0.f : fast_exp2(fmaf(x, c2, -mrow)) * inv_l) : x;
         }
         *reinterpret_cast<f32x4_t*>(so + li * OP + 8 * j + 4 * g) = v;
