@@ -73,6 +73,7 @@ class SDPABackwardOp(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, o, lse, dout, scale, causal):
         dq, dk, dv, _ = _ops.bwd(q, k, v, o, lse, dout, scale, causal, checked=False)
+        ctx.set_materialize_grads(False)  # an absent cotangent stays None (the kernels skip it), not a zero fill
         ctx.save_for_backward(q, k, v, o, lse, dout)
         ctx.scale = scale
         ctx.causal = causal
@@ -105,6 +106,7 @@ class SDPAOp(torch.autograd.Function):
         ctx.scale = scale
         ctx.causal = causal
         ctx.mark_non_differentiable(lse)
+        ctx.set_materialize_grads(False)  # lse's gradient stays None rather than a zero fill on every backward
         ctx.save_for_backward(q, k, v, o, lse)
         ctx.save_for_forward(q, k, v, o, lse)
 

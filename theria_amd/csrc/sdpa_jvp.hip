@@ -282,7 +282,7 @@ __global__ __launch_bounds__(512, 2) void jvp_ksplit_kernel(const JvpParams p) {
   static_assert(NSLAB * Dma::SLAB_ROWS == BN, "key tiles must be whole DMA slabs");
   // [group][set][K, V, tK, tV]; reused for the partial sums after the key loop
   __shared__ __attribute__((aligned(1024))) char smem[2 * 2 * 4 * TB];
-  static_assert(sizeof(smem) >= 4 * 64 * 34 * 4, "the combine rounds fit in the tile memory");
+  static_assert(sizeof(smem) >= (3 * NDT * 16 + 2) * 256 * 4, "the partial sums fit in the tile memory");
 
   const Shape& s = p.s;
   const int lane = threadIdx.x & 63, li = lane & 31, g = lane >> 5;
@@ -440,37 +440,35 @@ __global__ __launch_bounds__(512, 2) void jvp_ksplit_kernel(const JvpParams p) {
   else
     sweep(std::integral_constant<bool, false>{});
 
-  // Group 1's partial sums to group 0, 32 floats per lane per round (element e of lane l of wave w at
-  // e * 256 + w * 64 + l: consecutive lanes, consecutive words).
+  // Group 1's partial sums to group 0 in one round (element e of accumulator a of lane l of wave w at
+  // (a * NDT * 16 + e) * 256 + w * 64 + l: consecutive lanes, consecutive words; the row sums after them).
   float* buf = reinterpret_cast<float*>(smem);
-  auto pass_over = [&](f32x16_t (&acc)[NDT]) {
-    __syncthreads();  // the previous readers (or the last tile's) are done
-    if (grp == 1) {
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) buf[(dt * 16 + r) * 256 + wig * 64 + lane] = acc[dt][r];
-    }
-    __syncthreads();
-    if (grp == 0) {
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[dt][r] += buf[(dt * 16 + r) * 256 + wig * 64 + lane];
-    }
-  };
-  pass_over(accA);
-  pass_over(accO);
-  if (has_tv) pass_over(accC);
-  __syncthreads();
+  constexpr int RS = 3 * NDT * 16 * 256;  // the row sums
+  __syncthreads();  // every wave is done with the last tile
   if (grp == 1) {
-    buf[wig * 64 + lane] = lpart;
-    buf[256 + wig * 64 + lane] = cpart;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        buf[((0 * NDT + dt) * 16 + r) * 256 + wig * 64 + lane] = accA[dt][r];
+        buf[((1 * NDT + dt) * 16 + r) * 256 + wig * 64 + lane] = accO[dt][r];
+        if (has_tv) buf[((2 * NDT + dt) * 16 + r) * 256 + wig * 64 + lane] = accC[dt][r];
+      }
+    buf[RS + wig * 64 + lane] = lpart;
+    buf[RS + 256 + wig * 64 + lane] = cpart;
   }
   __syncthreads();
   if (grp == 1) return;
-  lpart += buf[wig * 64 + lane];
-  cpart += buf[256 + wig * 64 + lane];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      accA[dt][r] += buf[((0 * NDT + dt) * 16 + r) * 256 + wig * 64 + lane];
+      accO[dt][r] += buf[((1 * NDT + dt) * 16 + r) * 256 + wig * 64 + lane];
+      if (has_tv) accC[dt][r] += buf[((2 * NDT + dt) * 16 + r) * 256 + wig * 64 + lane];
+    }
+  lpart += buf[RS + wig * 64 + lane];
+  cpart += buf[RS + 256 + wig * 64 + lane];
 
   // Epilogue as jvp_kernel's (O rebuilt from the same P; normalize: P divided by its own row sum).
   float inv = 1.f;
