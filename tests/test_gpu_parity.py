@@ -278,6 +278,30 @@ def test_double_backward_ignores_delta(dt, hip_device):
             assert torch.equal(a, b), f"{name} depends on delta ({dt})"
 
 
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_double_backward_every_cotangent_subset(dt, causal, hip_device):
+    """Every non-empty subset of (gQ, gK, gV) against the oracle at 16-bit head dim 64 (the key-split row kernel
+    and the query-split column kernel with their presence tests at run time; all three given takes the
+    variant where they are constants). Ragged sizes: T and M are not multiples of the tiles."""
+    B, H, T, M, D = 2, 2, 301, 275, 64
+    q, qc = make((B, H, T, D), dt, hip_device, 61)
+    k, kc = make((B, H, M, D), dt, hip_device, 62)
+    v, vc = make((B, H, M, D), dt, hip_device, 63)
+    do, doc = make((B, H, T, D), dt, hip_device, 64)
+    gs = [make(t.shape, dt, hip_device, 65 + i, std=0.5) for i, t in enumerate((q, k, v))]
+    s = 1 / math.sqrt(D)
+    o, lse, _, _ = _ops.fwd(q, k, v, s, causal)
+    for mask in range(1, 8):
+        pick = [gs[i] if mask >> i & 1 else (None, None) for i in range(3)]
+        tag = "".join(n for i, n in enumerate(("q", "k", "v")) if mask >> i & 1)
+        print(f"[bwd_bwd cotangents g{tag}] {dt} causal={causal}", flush=True)
+        G = _ops.bwd_bwd(q, k, v, o, do, lse, None, *(p[0] for p in pick), s, causal)
+        Gr = O.double_backward(qc, kc, vc, doc, *(p[1] for p in pick), s, causal)
+        for name, a, b in zip(("G_Q", "G_K", "G_V", "G_dO"), G, Gr):
+            close(a, b, dt, f"{name}(g{tag})")
+
+
 # bfloat16 causal cases whose G_Q on the first rows (two to ten visible keys) missed the bar by up to 0.044
 # while the rows kernel formed G_Q from uncentred products; (case, seed) as a random sweep drew them.
 CENTRED_GQ_CASES = [
