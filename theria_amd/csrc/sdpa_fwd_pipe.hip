@@ -122,8 +122,11 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
       for (int c = 0; c < NKC; ++c) qf[j][c] = gload_frag8<T>(Q, p.q.sr, q0w + 32 * j + li, s.T, c, Dh);
 
     f32x16_t o[QT][NDT];
-    // pk_max: the largest lane partial row sum of any tile (32 keys, relative to the current offset), an upper
-    // bound of the row's largest P that costs one max per tile; it marks the peaked rows in lse.
+    // pk_max: an upper bound of the row's largest P (relative to the current offset) that marks the peaked rows
+    // in lse: the largest lane partial row sum of any tile (32 keys), one max per tile; causal (FINE), the largest
+    // 8-key partial sum, one max per 8 keys: rows that see few keys would otherwise be flagged by the 32-key
+    // sums of rows up to ~160 keys long, and every flagged row sends its block down the backward's exact path.
+    constexpr bool FINE = CAUSAL;
     float m_use[QT], l_part[QT], m_max[QT], pk_max[QT];
 #pragma unroll
     for (int j = 0; j < QT; ++j) {
@@ -185,11 +188,13 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
         }
       }
     };
-    // P = exp2(S c2 - off) as 16-bit fragments into pn, and this tile's lane partial row sums into ps.
-    auto exps = [&](const f32x16_t (&sc)[QT][2], const float (&off)[QT], F (&pn)[QT][2][2], float (&ps)[QT]) {
+    // P = exp2(S c2 - off) as 16-bit fragments into pn, this tile's lane partial row sums into ps and (FINE) the
+    // largest 8-key partial sum into pk.
+    auto exps = [&](const f32x16_t (&sc)[QT][2], const float (&off)[QT], F (&pn)[QT][2][2], float (&ps)[QT],
+                    float (&pk)[QT]) {
 #pragma unroll
       for (int j = 0; j < QT; ++j) {
-        float acc = 0.f;
+        float acc = 0.f, mx = 0.f;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -198,13 +203,20 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
 #pragma unroll
             for (int e = 0; e < 8; ++e) f[e] = (T)fast_exp2(fmaf(sc[j][t][8 * cc + e], c2, -off[j]));
             pn[j][t][cc] = f;
-            acc = frag_sum<T>(f, acc);
+            if constexpr (FINE) {
+              const float fs = frag_sum<T>(f, 0.f);
+              acc += fs;
+              mx = fmaxf(mx, fs);
+            } else {
+              acc = frag_sum<T>(f, acc);
+            }
           }
         ps[j] = acc;
+        pk[j] = mx;
       }
     };
-    // The same for key subtile t only, accumulating the lane partial row sums into ps.
-    auto exps_t = [&](const f32x16_t (&st)[QT], int t, F (&pn)[QT][2][2], float (&ps)[QT]) {
+    // The same for key subtile t only, accumulating into ps and pk.
+    auto exps_t = [&](const f32x16_t (&st)[QT], int t, F (&pn)[QT][2][2], float (&ps)[QT], float (&pk)[QT]) {
 #pragma unroll
       for (int j = 0; j < QT; ++j)
 #pragma unroll
@@ -213,7 +225,13 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
 #pragma unroll
           for (int e = 0; e < 8; ++e) f[e] = (T)fast_exp2(fmaf(st[j][8 * cc + e], c2, -m_use[j]));
           pn[j][t][cc] = f;
-          ps[j] = frag_sum<T>(f, ps[j]);
+          if constexpr (FINE) {
+            const float fs = frag_sum<T>(f, 0.f);
+            ps[j] += fs;
+            pk[j] = fmaxf(pk[j], fs);
+          } else {
+            ps[j] = frag_sum<T>(f, ps[j]);
+          }
         }
     };
     auto tile_max = [&](const f32x16_t (&sc)[QT][2], int j) {
@@ -225,7 +243,7 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
       return pair_max(mx) * c2;
     };
     // Exact path: the running max becomes the offset; O and the row sums are rescaled to it.
-    auto exact = [&](const f32x16_t (&sc)[QT][2], F (&pn)[QT][2][2], float (&ps)[QT]) {
+    auto exact = [&](const f32x16_t (&sc)[QT][2], F (&pn)[QT][2][2], float (&ps)[QT], float (&pk)[QT]) {
       float off[QT];
 #pragma unroll
       for (int j = 0; j < QT; ++j) {
@@ -242,7 +260,7 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
           for (int r = 0; r < 16; ++r) o[j][dt][r] *= alpha;
         off[j] = mnew == -THERIA_INF ? 0.f : mnew;  // all keys so far masked: P = exp2(-inf) = 0
       }
-      exps(sc, off, pn, ps);
+      exps(sc, off, pn, ps, pk);
     };
 
     // One key tile. On entry K(k) and V(k-1) have been requested (one iteration earlier); this step
@@ -268,9 +286,9 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
         // Phase order (kept by scheduling barriers, which also bound the live registers):
         //   S(k) subtile 0 | S(k) subtile 1 with exp of subtile 0 | O += V(k-1)^T P(k-1)^T with exp of subtile 1.
         f32x16_t s0[QT], s1[QT];
-        float ps[QT];
+        float ps[QT], pk[QT];
 #pragma unroll
-        for (int j = 0; j < QT; ++j) ps[j] = 0.f;
+        for (int j = 0; j < QT; ++j) ps[j] = pk[j] = 0.f;
         scores_t(kc, 0, s0);
         __builtin_amdgcn_sched_barrier(0);
         scores_t(kc, 1, s1);
@@ -283,7 +301,7 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
             m_max[j] = fmaxf(m_max[j], pair_max(mx) * c2);
           }
         }
-        exps_t(s0, 0, pn, ps);
+        exps_t(s0, 0, pn, ps, pk);
         if constexpr (DP == 64) {
           // Issue order inside the phase: the four K fragment reads first, then each of the 8 MFMAs
           // followed by 12 VALU instructions of the exponentials (measured ~5% faster than the
@@ -307,7 +325,7 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
             m_max[j] = fmaxf(m_max[j], pair_max(mx) * c2);
           }
         }
-        exps_t(s1, 1, pn, ps);
+        exps_t(s1, 1, pn, ps, pk);
         if constexpr (DP == 64) {
           // V fragment reads first, then each of the 16 PV MFMAs followed by 6 VALU instructions.
 #pragma unroll
@@ -324,12 +342,12 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
         if (__any(bad)) {
           f32x16_t sc2[QT][2];
           scores(kc, sc2);
-          exact(sc2, pn, ps);
+          exact(sc2, pn, ps, pk);
         }
 #pragma unroll
         for (int j = 0; j < QT; ++j) {
           l_part[j] += ps[j];
-          pk_max[j] = fmaxf(pk_max[j], ps[j]);
+          pk_max[j] = fmaxf(pk_max[j], FINE ? pk[j] : ps[j]);
         }
 #pragma unroll
         for (int j = 0; j < QT; ++j)
@@ -344,16 +362,16 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
         if (!skip) scores(kc, sc);
         if (k > 0 && !pf_skip) pv_mma(vp);
         if (!skip) {
-          float ps[QT];
+          float ps[QT], pk[QT];
           mask(sc, k0);
           if (k == 0) {
-            exact(sc, pn, ps);
+            exact(sc, pn, ps, pk);
           } else {
             if (STATS) {
 #pragma unroll
               for (int j = 0; j < QT; ++j) m_max[j] = fmaxf(m_max[j], tile_max(sc, j));
             }
-            exps(sc, m_use, pn, ps);
+            exps(sc, m_use, pn, ps, pk);
             bool bad = false;
 #pragma unroll
             for (int j = 0; j < QT; ++j) bad |= !(ps[j] <= 0x1p20f);
@@ -361,13 +379,13 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
               f32x16_t sc2[QT][2];
               scores(kc, sc2);
               mask(sc2, k0);
-              exact(sc2, pn, ps);
+              exact(sc2, pn, ps, pk);
             }
           }
 #pragma unroll
           for (int j = 0; j < QT; ++j) {
             l_part[j] += ps[j];
-            pk_max[j] = fmaxf(pk_max[j], ps[j]);
+            pk_max[j] = fmaxf(pk_max[j], FINE ? pk[j] : ps[j]);
           }
 #pragma unroll
           for (int j = 0; j < QT; ++j)
