@@ -81,6 +81,14 @@ CASES = [
     (torch.bfloat16, 1, 1, 333, 129, 120, False),
     (torch.float16, 1, 2, 150, 170, 40, False),
     (torch.bfloat16, 1, 2, 260, 260, 72, True),
+    # head dims 8..32 (multiples of 8) in the pipelined kernels at DP = 32: 64-byte tile rows, four- and two-wave
+    # workgroups, zero-filled columns past D
+    (torch.bfloat16, 2, 2, 300, 260, 32, False),
+    (torch.float16, 1, 3, 257, 190, 32, True),
+    (torch.bfloat16, 1, 2, 520, 520, 16, True),
+    (torch.bfloat16, 2, 2, 200, 333, 24, False),
+    (torch.float16, 1, 1, 700, 700, 8, False),
+    (torch.bfloat16, 4, 4, 1030, 1030, 16, True),
 ]
 
 

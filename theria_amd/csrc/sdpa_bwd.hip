@@ -560,14 +560,14 @@ __global__ __launch_bounds__(256, (DP <= 64 ? DKDV_MINW : 1)) void dkdv_kernel(c
     }
 }
 
-// Pipelined 16-bit head-dim-64 dQ (sdpa_bwd_pipe.hip); false when it does not cover the problem.
+// Pipelined 16-bit dQ (sdpa_bwd_pipe.hip); false when it does not cover the problem.
 template <typename T, bool CAUSAL>
 bool launch_dq_pipe(const DqParams& p, hipStream_t st, hipError_t* err);
 
 struct DqLauncher {
   template <typename T, int DP, bool CAUSAL>
   static hipError_t run(const DqParams& p, hipStream_t st) {
-    if constexpr (sizeof(T) == 2 && DP >= 64) {
+    if constexpr (sizeof(T) == 2) {
       hipError_t err;
       if (launch_dq_pipe<T, CAUSAL>(p, st, &err)) return err;
     }
@@ -587,7 +587,7 @@ struct DqLauncher {
   }
 };
 
-// Pipelined 16-bit head-dim-64 dK/dV (sdpa_bwd_pipe.hip); false when it does not cover the problem.
+// Pipelined 16-bit dK/dV (sdpa_bwd_pipe.hip); false when it does not cover the problem.
 template <typename T, bool CAUSAL>
 bool launch_dkdv_pipe(const DkdvParams& p, hipStream_t st, hipError_t* err);
 
@@ -601,7 +601,7 @@ struct DkdvLauncher {
   }
   template <typename T, int DP, bool CAUSAL>
   static hipError_t run(const DkdvParams& p, hipStream_t st) {
-    if constexpr (sizeof(T) == 2 && DP >= 64) {
+    if constexpr (sizeof(T) == 2) {
       hipError_t err;
       if (launch_dkdv_pipe<T, CAUSAL>(p, st, &err)) return err;
     }

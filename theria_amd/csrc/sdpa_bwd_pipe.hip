@@ -97,6 +97,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
   using Dma = SwzDma<NW, DP>;
   constexpr int NKC = DP / 16, NDT = DP / 32;
   constexpr int BN = 32 * NW, BM = 64 * HALVES, TILE = BM * 2 * DP, NSLAB = BM / Dma::SLAB_ROWS;
+  static_assert(NSLAB * Dma::SLAB_ROWS == BM, "query tiles must be whole DMA slabs");
   static_assert(64 * NW >= BM, "the row terms of a tile are loaded one per thread");
   // OVERLAP: the exp / dS work of one subtile overlaps the products of the next (more live registers);
   // otherwise subtiles run one after the other. WPS: waves per SIMD the register budget is sized for.
@@ -113,10 +114,10 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
   const int lane = tid & 63, li = lane & 31, g = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nkb = (s.M + BN - 1) / BN;
-  // Causal at head dim 64: workgroup `unit` runs key block `unit` (the longest query range) and then its
+  // Causal at head dim <= 64: workgroup `unit` runs key block `unit` (the longest query range) and then its
   // mirror block nkb - 1 - unit, so every workgroup gets the same number of query tiles; an odd middle
   // block runs once. At head dim 128 (one workgroup per CU) the plain longest-first order measured faster.
-  constexpr bool PAIR = CAUSAL && DP == 64;
+  constexpr bool PAIR = CAUSAL && DP <= 64;
   const int nunit = PAIR ? (nkb + 1) / 2 : nkb;
   const int bid = xcd_remap(blockIdx.x, gridDim.x);
   const int bh = bid / nunit;
@@ -477,6 +478,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
   using Dma = SwzDma<NW, DP>;
   constexpr int NKC = DP / 16, NDT = DP / 32;
   constexpr int BM = 32 * NW, BN = 64 * HALVES, TILE = BN * 2 * DP, NSLAB = BN / Dma::SLAB_ROWS;
+  static_assert(NSLAB * Dma::SLAB_ROWS == BN, "key tiles must be whole DMA slabs");
   __shared__ __attribute__((aligned(1024))) char sK0[TILE];
   __shared__ __attribute__((aligned(1024))) char sK1[TILE];
   __shared__ __attribute__((aligned(1024))) char sV0[TILE];
@@ -790,7 +792,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
 // block takes the row-term pass), then the peaked launch.
 template <typename T, bool CAUSAL, int NW, int DP, bool OVERLAP, int WPS, int HALVES, bool FD>
 static void dq_go_fd(const DqParams& p, int64_t nblk, hipStream_t st) {
-  if constexpr (DP == 64) {
+  if constexpr (DP <= 64) {
     hipLaunchKernelGGL((dq_pipe_kernel<T, CAUSAL, NW, DP, OVERLAP, WPS, HALVES, FD, 2>), dim3((unsigned)nblk),
                        dim3(64 * NW), 0, st, p);
   } else {
@@ -821,9 +823,9 @@ static void dkdv_go(const DkdvParams& p, int64_t nblk, hipStream_t st) {
     dkdv_go_fd<T, CAUSAL, NW, DP, OVERLAP, WPS, HALVES, false>(p, nblk, st);
 }
 
-// Head dims the pipelined kernels take: a multiple of 8 in 40..64 (run at DP = 64) or 72..128 (DP = 128);
-// columns past D are zero in every tile and are never stored.
-static bool pipe_head_dim(const Shape& s) { return s.vec && s.D % 8 == 0 && (s.dp == 64 || s.dp == 128) && s.D > 32; }
+// Head dims the pipelined kernels take: a multiple of 8 in 8..32 (run at DP = 32), 40..64 (DP = 64) or 72..128
+// (DP = 128); columns past D are zero in every tile and are never stored.
+static bool pipe_head_dim(const Shape& s) { return s.vec && s.D % 8 == 0 && s.D >= 8; }
 
 template <typename T, bool CAUSAL>
 bool launch_dq_pipe(const DqParams& p, hipStream_t st, hipError_t* err) {
@@ -837,7 +839,9 @@ bool launch_dq_pipe(const DqParams& p, hipStream_t st, hipError_t* err) {
     *err = hipSuccess;
     return true;
   }
-  if (p.s.dp == 64)
+  if (p.s.dp == 32)
+    dq_go<T, CAUSAL, NW, 32, true, 2, DQ64_HALVES>(p, nblk, st);
+  else if (p.s.dp == 64)
     dq_go<T, CAUSAL, NW, 64, true, 2, DQ64_HALVES>(p, nblk, st);
   else
     dq_go<T, CAUSAL, NW, 128, DQ128_OVERLAP, DQ128_WPS, DQ128_HALVES>(p, nblk, st);
@@ -862,13 +866,21 @@ bool launch_dkdv_pipe(const DkdvParams& p, hipStream_t st, hipError_t* err) {
   // workgroups of nw waves (32 keys each): key blocks, or (causal head dim 64) pairs of mirrored blocks
   auto blocks = [&](int nw) {
     const int64_t nkb = (p.s.M + 32 * nw - 1) / (32 * nw);
-    return ((CAUSAL && p.s.dp == 64) ? (nkb + 1) / 2 : nkb) * p.s.B * p.s.H;
+    return ((CAUSAL && p.s.dp <= 64) ? (nkb + 1) / 2 : nkb) * p.s.B * p.s.H;
   };
   if (blocks(4) == 0) {
     *err = hipSuccess;
     return true;
   }
-  if (p.s.dp == 64) {
+  if (p.s.dp == 32) {
+    // Four-wave workgroups (eight waves would copy 128-row DMA slabs into 64-row query tiles), two-wave ones
+    // where four-wave ones would leave CUs idle.
+    const int64_t cus = device_cu_count();
+    if (blocks(4) >= cus)
+      dkdv_go<T, CAUSAL, 4, 32, true, 2, DKDV64_HALVES>(p, blocks(4), st);
+    else
+      dkdv_go<T, CAUSAL, 2, 32, true, 2, DKDV64_HALVES>(p, blocks(2), st);
+  } else if (p.s.dp == 64) {
     // Eight-wave workgroups (both waves of a SIMD in one workgroup) whenever they still fill every CU:
     // two independent four-wave workgroups on a CU progress unevenly (the older one is issued first), and
     // with two rounds of them the CUs that finish early idle through a ~10% tail at config 2.

@@ -215,7 +215,7 @@ bool launch_fwd_pipe(const FwdParams& p, hipStream_t st, hipError_t* err);
 struct FwdLauncher {
   template <typename T, int DP, bool CAUSAL>
   static hipError_t run(const FwdParams& p, hipStream_t st) {
-    if constexpr (sizeof(T) == 2 && DP >= 64) {
+    if constexpr (sizeof(T) == 2) {
       hipError_t err;
       if (launch_fwd_pipe<T, CAUSAL>(p, st, &err)) return err;
     }

@@ -102,6 +102,7 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
     using Dma = SwzDma<NW, DP>;
     const Dma dma(wave, lane, Dh / 8);  // head dims below DP: zero-filled chunks past D
     constexpr int NSLAB = BN / Dma::SLAB_ROWS;
+    static_assert(NSLAB * Dma::SLAB_ROWS == BN, "key tiles must be whole DMA slabs");
     // Byte offsets fit in 32 bits: the host only selects this kernel when every (batch, head) slab of K
     // and V spans less than 2^31 bytes.
     const uint32_t krs = (uint32_t)p.k.sr * 2, vrs = (uint32_t)p.v.sr * 2;
@@ -480,15 +481,16 @@ static void fwd_pipe_go(const FwdParams& p, int64_t nblk, hipStream_t st) {
 
 template <typename T, bool CAUSAL, int DP>
 static void fwd_pipe_launch(const FwdParams& p, hipStream_t st) {
-  constexpr int QT = (DP == 64 && !CAUSAL) ? 2 : 1;
+  constexpr int QT = (DP <= 64 && !CAUSAL) ? 2 : 1;
   const int64_t bh = (int64_t)p.s.B * p.s.H;
   const int64_t cus = device_cu_count();
   // workgroups per (batch, head): query blocks, or (causal) pairs of mirrored query blocks
   auto units = [](int64_t nqb) { return CAUSAL ? (nqb + 1) / 2 : nqb; };
   const int64_t nblk8 = units((p.s.T + 256 * QT - 1) / (256 * QT)) * bh;
   const int64_t nblk4 = units((p.s.T + 128 * QT - 1) / (128 * QT)) * bh;
-  if (nblk8 >= cus) {
-    fwd_pipe_go<T, CAUSAL, 8, DP, QT>(p, nblk8, st);
+  // eight waves fill a 64-key DMA slab only at head dims 64 and 128 (at 32 one wave instruction copies 16 rows)
+  if (DP >= 64 && nblk8 >= cus) {
+    if constexpr (DP >= 64) fwd_pipe_go<T, CAUSAL, 8, DP, QT>(p, nblk8, st);
     return;
   }
   if constexpr (QT == 2) {
@@ -501,18 +503,21 @@ static void fwd_pipe_launch(const FwdParams& p, hipStream_t st) {
   fwd_pipe_go<T, CAUSAL, 4, DP, QT>(p, nblk4, st);
 }
 
-// Launch if the pipelined kernel covers this problem (16-bit, head dim a multiple of 8 in 40..64 (run at
-// DP = 64) or 72..128 (DP = 128), vector access, more than 128 queries); returns false otherwise.
+// Launch if the pipelined kernel covers this problem (16-bit, head dim a multiple of 8 in 8..32 (run at
+// DP = 32), 40..64 (DP = 64) or 72..128 (DP = 128), vector access, more than 128 queries); returns false
+// otherwise.
 template <typename T, bool CAUSAL>
 bool launch_fwd_pipe(const FwdParams& p, hipStream_t st, hipError_t* err) {
-  if (!(p.s.vec && p.s.D % 8 == 0 && p.s.D > 32 && (p.s.dp == 64 || p.s.dp == 128) && p.s.T > 128)) return false;
+  if (!(p.s.vec && p.s.D % 8 == 0 && p.s.D >= 8 && p.s.T > 128)) return false;
   // 32-bit byte offsets inside each (batch, head) slab of K and V
   if (!slab_fits_dma(p.s.M, p.k.sr, p.s.D) || !slab_fits_dma(p.s.M, p.v.sr, p.s.D)) return false;
   if ((int64_t)p.s.B * p.s.H == 0) {
     *err = hipSuccess;
     return true;
   }
-  if (p.s.dp == 64)
+  if (p.s.dp == 32)
+    fwd_pipe_launch<T, CAUSAL, 32>(p, st);
+  else if (p.s.dp == 64)
     fwd_pipe_launch<T, CAUSAL, 64>(p, st);
   else
     fwd_pipe_launch<T, CAUSAL, 128>(p, st);

@@ -1,6 +1,6 @@
-// LDS tiles filled by DMA for 16-bit inputs with a head dimension DP of 64 or 128 (gfx950).
+// LDS tiles filled by DMA for 16-bit inputs with a head dimension DP of 32, 64 or 128 (gfx950).
 //
-// A tile holds R rows x DP columns of a 16-bit type, RB = 2 DP bytes per row (128 or 256), with no
+// A tile holds R rows x DP columns of a 16-bit type, RB = 2 DP bytes per row (64, 128 or 256), with no
 // padding. Its global rows are copied by LDS DMA (buffer_load_dwordx4 ... lds), which writes the 16
 // bytes of lane l of a wave to LDS address M0 + 16 * l (checked on the device), so one wave instruction
 // fills 1024 / RB consecutive rows and the data never passes through VGPRs.
@@ -9,11 +9,14 @@
 // c ^ swz<DP>(r), and the DMA lane that fills slot s of row r fetches logical chunk s ^ swz<DP>(r). The
 // swizzle makes both read patterns bank-conflict free:
 //  * "cols" fragments (ds_read_b128, one lane-fixed row, k along the row): 16 lanes read the same logical
-//    chunk of 16 consecutive rows (16-aligned). DP = 64: rows of one parity share a 32-bank half and
+//    chunk of 16 consecutive rows (16-aligned). DP = 32: four rows span the 64 banks, so rows r and r + 4
+//    share banks and swz = (r >> 2) & 3 sends the four rows of each residue r & 3 to distinct slots. DP = 64:
+//    rows of one parity share a 32-bank half and
 //    swz = bits 1..3 of r (bit-reversed) gives them distinct slots. DP = 128: every row spans all 64
 //    banks and swz = ((r & 3) << 2) | ((r >> 2) & 3) is a bijection of r & 15.
 //  * "rows" (transpose) fragments (ds_read_b64_tr_b16, k down a column): 32 lanes read 4 consecutive rows
-//    (4-aligned) x 4 consecutive chunks (4-aligned). DP = 64: the two rows of one parity differ in bit 1,
+//    (4-aligned) x 4 consecutive chunks (4-aligned). DP = 32: the 4 rows are the 64 banks, whatever the slots.
+//    DP = 64: the two rows of one parity differ in bit 1,
 //    which flips slot bit 2. DP = 128: the 4 rows XOR by 0, 4, 8, 12, i.e. land in 4 different chunk quads.
 #pragma once
 
@@ -23,7 +26,10 @@ namespace theria {
 
 template <int DP>
 __device__ __forceinline__ int swz(int r) {
-  if constexpr (DP == 64)
+  static_assert(DP == 32 || DP == 64 || DP == 128, "tile rows of 64, 128 or 256 bytes");
+  if constexpr (DP == 32)
+    return (r >> 2) & 3;
+  else if constexpr (DP == 64)
     return (((r >> 1) & 1) << 2) | (((r >> 2) & 1) << 1) | ((r >> 3) & 1);
   else
     return ((r & 3) << 2) | ((r >> 2) & 3);
