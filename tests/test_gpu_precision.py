@@ -113,8 +113,10 @@ def test_peaked_rows_double_backward(case, hip_device):
 
 PLANTED = [
     # dtype, B, H, T, M, D, causal, planted key, gap (nats)
-    # pipelined forward (16-bit, head dim 40..128, more than 128 queries): 64-key tiles
+    # pipelined forward (16-bit, head dim 8..128 a multiple of 8, more than 128 queries): 64-key tiles
     (torch.bfloat16, 1, 2, 300, 300, 64, False, 290, 24.0),
+    (torch.bfloat16, 1, 2, 300, 300, 32, False, 290, 24.0),
+    (torch.float16, 1, 1, 260, 260, 16, True, 200, 24.0),
     (torch.bfloat16, 1, 2, 300, 330, 64, False, 140, 30.0),
     (torch.float16, 1, 1, 260, 260, 128, False, 250, 24.0),
     (torch.bfloat16, 1, 2, 300, 300, 64, True, 100, 24.0),
@@ -284,12 +286,13 @@ def test_broadcast_row_operands(D, hip_device):
         close(a, b, dt, f"{name} (dO, gK row stride 0)")
 
 
-@pytest.mark.parametrize("D", [32, 64])
+@pytest.mark.parametrize("D", [20, 32, 64])
 @pytest.mark.parametrize("causal", [False, True])
 def test_backward_without_dq_keeps_the_exact_row_term(D, causal, hip_device):
     """theria_sdpa_bwd with dq absent forms the same row term as with dq on query blocks holding a peaked row
-    (D = 32 takes the general dQ kernel, D = 64 the pipelined one): delta, dK and dV are bit for bit those of the
-    call that also writes dQ, and the row term is the exact one (the oracle's dO . O)."""
+    (D = 20, not a multiple of 8, takes the general dQ kernel; D = 32 and 64 the pipelined one): delta, dK and dV
+    are bit for bit those of the call that also writes dQ, and the row term is the exact one (the oracle's
+    dO . O)."""
     dev = hip_device
     dt = torch.bfloat16
     B, H, T, M = 1, 2, 300, 260
