@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define THERIA_SDPA_ABI_VERSION 8
+#define THERIA_SDPA_ABI_VERSION 9
 
 enum theria_dtype { THERIA_DTYPE_F32 = 0, THERIA_DTYPE_F16 = 1, THERIA_DTYPE_BF16 = 2 };
 enum theria_status { THERIA_OK = 0, THERIA_ERR_CONTRACT = 1, THERIA_ERR_HIP = 2 };

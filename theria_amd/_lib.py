@@ -18,7 +18,7 @@ import torch  # noqa: F401  (must be imported first: it loads the HIP runtime th
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libtheria_sdpa.so"
 # The counter-enabled build of the same sources (theria_debug_tile_counts counts there), for measurements only.
 TILES_LIB_PATH = LIB_PATH.with_name("libtheria_sdpa_tiles.so")
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 OK, ERR_CONTRACT, ERR_HIP = 0, 1, 2
