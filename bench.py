@@ -339,6 +339,7 @@ def extras_c4():
     import torch
 
     from theria_amd import _ops
+    from theria_amd.autograd import GraphedSDPAHVP
     from theria_amd.autograd.hip_sdpa import hip_sdpa, hip_sdpa_hvp
 
     dev = torch.device("cuda:0")
@@ -363,6 +364,10 @@ def extras_c4():
             return torch.autograd.grad(g, (qg, kg, vg), grad_outputs=(vq, vk, vv))
 
         out[f"hvp_ms_{name}"] = round(_time(hvp, 50), 4)
+        # the same autograd HVP captured once in a HIP graph and replayed (no autograd engine on the host)
+        graphed = GraphedSDPAHVP(q, k, v, vq, vk, vv, target=T_, scale=1 / 8.0)
+        out[f"hvp_graph_ms_{name}"] = round(_time(lambda: graphed(q=q), 200), 4)
+        del graphed
         # the same HVP from the kernels directly (forward, double backward, backward of J v; no autograd graph)
         hv = lambda: hip_sdpa_hvp(q, k, v, vq, vk, vv, target=T_, scale=1 / 8.0)  # noqa: E731
         out[f"hvp_kernels_only_ms_{name}"] = round(_time(hv, 100), 4)
@@ -372,7 +377,8 @@ def extras_c4():
     unit = B * H * S * S * D
     out["jvp_tflops_bf16"] = round(10 * unit / (out["jvp_ms_bf16"] * 1e-3) / 1e12, 1)
     out["config"] = ("B8 H8 S512 D64; JVP with saved stats; HVP of 0.5||O-T||^2 via autograd double backward "
-                     "(hvp_ms) and from the kernels directly (hvp_kernels_only_ms)")
+                     "(hvp_ms), the same captured in a HIP graph (hvp_graph_ms) and from the kernels directly "
+                     "(hvp_kernels_only_ms)")
     return out
 
 

@@ -128,3 +128,43 @@ def test_gradient_of_dout_path_is_not_double_counted(kernels):
         return torch.autograd.grad(sum(x.pow(2).sum() for x in g), qkv, create_graph=True)
 
     _close(second(_hip(False), a), second(_ref(False), b))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("loss", ["sum", "weight", "target"])
+def test_graphed_hvp_body_is_the_autograd_hvp(kernels, loss, causal):
+    """The body GraphedSDPAHVP captures (run here eagerly, without a graph) is the HVP of its loss: sum(O),
+    <W, O> or 0.5 ||O - T||^2, against autograd's double backward through textbook attention. The second
+    gradient runs the double-backward kernel (grad mode is off there)."""
+    from theria_amd.autograd.graphed_hvp import GraphedSDPAHVP
+
+    q, k, v = _inputs(3)
+    u = _inputs(4)
+    extra = _inputs(5)[0]  # shaped like O
+    G = object.__new__(GraphedSDPAHVP)
+    G.causal, G.scale = causal, _ops.default_scale(q.shape[-1])
+    G.q, G.k, G.v = (t.clone().requires_grad_(True) for t in (q, k, v))
+    G.vq, G.vk, G.vv = u
+    G.target = extra if loss == "target" else None
+    G.weight = extra if loss == "weight" else None
+    got = G._body()
+    assert kernels["bwd_bwd"] == 1
+
+    qr, kr, vr = (t.clone().requires_grad_(True) for t in (q, k, v))
+    o = O.autograd_attention(qr, kr, vr, causal=causal)
+    losses = {"sum": lambda: o.sum(), "weight": lambda: (o * extra).sum(),
+              "target": lambda: 0.5 * ((o - extra) ** 2).sum()}
+    L = losses[loss]()
+    g = torch.autograd.grad(L, (qr, kr, vr), create_graph=True)
+    want = torch.autograd.grad(g, (qr, kr, vr), grad_outputs=tuple(u))
+    _close(got, want)
+
+
+def test_graphed_hvp_refuses_cpu_inputs_and_two_losses():
+    from theria_amd.autograd import GraphedSDPAHVP
+
+    q, k, v = _inputs(1)
+    with pytest.raises(ValueError, match="weight or target"):
+        GraphedSDPAHVP(q, k, v, q, k, v, target=q, weight=q)
+    with pytest.raises(ValueError, match="GPU"):
+        GraphedSDPAHVP(q, k, v, q, k, v)

@@ -58,3 +58,53 @@ def test_graph_replay_matches_eager(case, hip_device):
         # eager work between replays (allocations and launches outside the graph)
         step()
         torch.cuda.synchronize()
+
+
+HVP_CASES = [
+    # dtype, B, H, T, M, D, causal, loss
+    (torch.bfloat16, 2, 2, 256, 256, 64, False, "target"),
+    (torch.float16, 1, 2, 200, 200, 128, True, "weight"),
+    (torch.float32, 1, 2, 96, 80, 40, False, "sum"),
+]
+
+
+@pytest.mark.parametrize("case", HVP_CASES, ids=[f"{c[0]}-T{c[3]}-D{c[5]}-{c[7]}{'-causal' if c[6] else ''}"
+                                                 for c in HVP_CASES])
+def test_graphed_hvp_matches_eager_autograd(case, hip_device):
+    """GraphedSDPAHVP replays return the eager autograd HVP (gradient with create_graph, then its VJP with v) bit for
+    bit, for new inputs on every replay, with eager work between the replays."""
+    from theria_amd.autograd import GraphedSDPAHVP, hip_sdpa
+
+    dt, B, H, T, M, D, causal, loss = case
+    dev = hip_device
+    print(f"[graphed hvp] {case}", flush=True)
+
+    def inputs(seed):
+        x = {"q": _make((B, H, T, D), dt, dev, seed), "k": _make((B, H, M, D), dt, dev, seed + 1),
+             "v": _make((B, H, M, D), dt, dev, seed + 2), "vq": _make((B, H, T, D), dt, dev, seed + 3),
+             "vk": _make((B, H, M, D), dt, dev, seed + 4), "vv": _make((B, H, M, D), dt, dev, seed + 5)}
+        if loss != "sum":
+            x[loss] = _make((B, H, T, D), dt, dev, seed + 6)
+        return x
+
+    def eager(x):
+        q, k, v = (x[n].clone().requires_grad_(True) for n in ("q", "k", "v"))
+        o = hip_sdpa(q, k, v, causal=causal)
+        dout = {"target": lambda: o - x.get("target"), "weight": lambda: x.get("weight"),
+                "sum": lambda: torch.ones_like(o)}[loss]()
+        g = torch.autograd.grad(o, (q, k, v), grad_outputs=dout, create_graph=True)
+        return torch.autograd.grad(g, (q, k, v), grad_outputs=(x["vq"], x["vk"], x["vv"]))
+
+    x0 = inputs(10)
+    graphed = GraphedSDPAHVP(causal=causal, **x0)
+    for rep in range(3):
+        x = inputs(20 + 10 * rep)
+        out = graphed(**x)
+        torch.cuda.synchronize()
+        ref = eager(x)
+        torch.cuda.synchronize()
+        for name, a, b in zip(("hq", "hk", "hv"), out, ref):
+            assert torch.isfinite(b).all(), f"{name}: eager HVP not finite"
+            assert torch.equal(a, b), f"replay {rep}: {name} differs from the eager autograd HVP"
+    with pytest.raises(ValueError):
+        graphed(q=torch.zeros(1, device=dev, dtype=dt))
