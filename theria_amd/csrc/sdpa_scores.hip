@@ -18,8 +18,11 @@
 //    each in float32) with non-temporal stores (the output is not read again by this kernel; K stays in L2).
 //    The buffer holds one subtile (4.5 KiB per wave), so five workgroups fit a CU's LDS and config 2's 4096
 //    waves are all resident at once;
-//  * P: a first pass over the key tiles keeps an online row max and sum per lane (the two lane halves of a
-//    query combined at the end), the second forms exp2(S scale log2 e - m) / l and stores it.
+//  * P: a first pass over the key tiles keeps a running offset and row sum per lane (the offset only moves when
+//    a subtile's partial sum leaves (0, 2^20], so the pass has no per-score max; the two lane halves of a query
+//    are combined at the end), the second forms exp2(S scale log2 e - m) / l and stores it;
+//  * at most 128 registers at head dim <= 64 (four waves per SIMD): the accumulators then stay in VGPRs instead
+//    of AGPRs, which the statistics pass would read back one v_accvgpr_read per score.
 #include <type_traits>
 
 #include "dispatch.hpp"
@@ -30,7 +33,7 @@ namespace theria {
 enum ScoreMode { kScoresF32 = 0, kScoresT = 1, kProbs = 2 };
 
 template <typename T, int DP, int MODE>
-__global__ __launch_bounds__(256) void scores_kernel(const ScoresParams p) {
+__global__ __launch_bounds__(256, DP <= 64 ? 4 : 2) void scores_kernel(const ScoresParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
   constexpr int NKC = DP / MM::KC;
@@ -79,30 +82,40 @@ __global__ __launch_bounds__(256) void scores_kernel(const ScoresParams p) {
     return st;
   };
 
-  // softmax statistics of query li (log2 domain): max m and sum l of exp2(S c2 - m) over its keys
+  // softmax statistics of query li (log2 domain): a running offset `off` and the sum l of exp2(S c2 - off) over
+  // its keys. The offset only moves when a subtile's lane partial sum leaves (0, 2^20] (always on the lane's
+  // first visible subtile): then it becomes the running max and l is rescaled. Below 2^20 every term is finite
+  // and far from float32 overflow, and P = exp2(S c2 - off) / l does not depend on which offset was used.
   float mrow = 0.f, inv_l = 0.f;
   if constexpr (MODE == kProbs) {
-    float m = -THERIA_INF, l = 0.f;
+    float off = -THERIA_INF, l = 0.f;
     if (nkt > 0) stK.load_any(K, p.k.sr, 0, s.M, s.D, s.vec);
     for (int kt = 0; kt < nkt; ++kt) {
       stage(kt);
 #pragma unroll
       for (int u = 0; u < NU; ++u) {
         const f32x16_t st = sub_scores(kt, u);
-        float mx = m;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[r] * c2);
-        if (mx == -THERIA_INF) continue;  // no visible key yet (M = 0 never reaches here)
         float part = 0.f;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) part += fast_exp2(fmaf(st[r], c2, -mx));
-        l = l * fast_exp2(m - mx) + part;
-        m = mx;
+        for (int r = 0; r < 16; ++r) part += fast_exp2(fmaf(st[r], c2, -off));
+        if (!(part <= 0x1p20f)) {  // first visible subtile of the lane, or scores far above the offset
+          float mx = st[0];
+#pragma unroll
+          for (int r = 1; r < 16; ++r) mx = fmaxf(mx, st[r]);
+          mx = fmaxf(off, mx * c2);
+          if (mx == -THERIA_INF) continue;  // no visible key yet
+          part = 0.f;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) part += fast_exp2(fmaf(st[r], c2, -mx));
+          l = l * fast_exp2(off - mx);
+          off = mx;
+        }
+        l += part;
       }
     }
-    const float mt = pair_max(m);
-    const float lt = pair_sum(m == -THERIA_INF ? 0.f : l * fast_exp2(m - mt));
-    mrow = mt;
+    const float mt = pair_max(off);
+    const float lt = pair_sum(off == -THERIA_INF ? 0.f : l * fast_exp2(off - mt));
+    mrow = mt == -THERIA_INF ? 0.f : mt;  // finite, so exp2(-inf * c2 - mrow) = 0 for masked keys
     inv_l = lt > 0.f ? 1.f / lt : 0.f;
   }
 
@@ -124,7 +137,7 @@ __global__ __launch_bounds__(256) void scores_kernel(const ScoresParams p) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const float x = st[4 * j + e];
-          v[e] = MODE == kProbs ? (x == -THERIA_INF ? 0.f : fast_exp2(fmaf(x, c2, -mrow)) * inv_l) : x;
+          v[e] = MODE == kProbs ? fast_exp2(fmaf(x, c2, -mrow)) * inv_l : x;
         }
         *reinterpret_cast<f32x4_t*>(so + li * OP + 8 * j + 4 * g) = v;
       }
