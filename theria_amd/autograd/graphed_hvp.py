@@ -78,9 +78,9 @@ class GraphedSDPAHVP:
                 dst = getattr(self, name)
                 if dst is None:
                     raise ValueError(f"GraphedSDPAHVP: {name} was not part of the captured loss")
-                if src.shape != dst.shape or src.dtype != dst.dtype:
-                    raise ValueError(f"GraphedSDPAHVP: {name} is {tuple(src.shape)} {src.dtype}, the capture "
-                                     f"used {tuple(dst.shape)} {dst.dtype}")
+                if src.shape != dst.shape or src.dtype != dst.dtype or src.device != dst.device:
+                    raise ValueError(f"GraphedSDPAHVP: {name} is {tuple(src.shape)} {src.dtype} on {src.device}, "
+                                     f"the capture used {tuple(dst.shape)} {dst.dtype} on {dst.device}")
                 dst.copy_(src)
         self.graph.replay()
         return self.out
