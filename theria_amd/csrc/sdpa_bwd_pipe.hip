@@ -1,5 +1,5 @@
 // Pipelined dQ and dK/dV passes of the SDPA backward for 16-bit inputs on gfx950 (head dim a multiple of 8
-// in 40..128, computed at DP = 64 or 128 with the columns past D zero).
+// in 8..128, computed at DP = 32, 64 or 128 with the columns past D zero).
 //
 // dkdv_pipe_kernel has the contract of dkdv_kernel (sdpa_bwd.hip): dV = P^T dO and dK = scale dS^T Q with
 // P = exp(scale Q K^T - lse) rebuilt from the saved row statistic and dS = P o (dO V^T - delta)

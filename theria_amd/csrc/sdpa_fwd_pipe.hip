@@ -2,11 +2,11 @@
 //
 // Same contract as fwd_kernel (sdpa_fwd.hip): O = softmax(scale Q K^T) V with lse and the optional
 // reference statistics (m, l) (reference theria/attention/triton_qk.py:242-304). It is used when
-// the head dim is a multiple of 8 in 40..128 (computed at DP = 64 or 128, the columns past D zero),
+// the head dim is a multiple of 8 in 8..128 (computed at DP = 32, 64 or 128, the columns past D zero),
 // every view allows 16-byte access and there are more than 128 queries.
 //
-// Work decomposition: one workgroup = NW waves x QT tiles of 32 queries (QT = 2 at head dim 64, 1 at
-// 128); keys in tiles of 64. Scores are
+// Work decomposition: one workgroup = NW waves x QT tiles of 32 queries (QT = 2 at DP = 32 and 64 without the
+// causal mask, else 1); keys in tiles of 64. Scores are
 // transposed (S^T = K Q^T), so each lane owns one query and the row sums are per-lane. Every SIMD runs two
 // waves. With NW = 8 both are waves of one workgroup, kept in step by the per-tile barrier; two
 // independent 4-wave workgroups on one CU do not share the SIMDs evenly (the older one is issued
