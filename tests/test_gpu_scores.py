@@ -37,6 +37,9 @@ SHAPES = [
     (2, 1, 65, 1, 16),
     (1, 2, 130, 257, 128),
     (2, 4, 256, 384, 64),
+    # 16-bit head dims <= 64 store 128 keys per round: a partial last round (six subtiles) and nine tiles
+    (1, 2, 100, 190, 64),
+    (1, 1, 300, 520, 32),
 ]
 
 
