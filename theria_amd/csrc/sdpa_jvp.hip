@@ -440,19 +440,25 @@ __global__ __launch_bounds__(512, 2) void jvp_ksplit_kernel(const JvpParams p) {
   else
     sweep(std::integral_constant<bool, false>{});
 
-  // Group 1's partial sums to group 0 in one round (element e of accumulator a of lane l of wave w at
-  // (a * NDT * 16 + e) * 256 + w * 64 + l: consecutive lanes, consecutive words; the row sums after them).
+  // Group 1's partial sums to group 0 in one round, 16 bytes per lane per store: elements 4c .. 4c + 3 of
+  // accumulator a, column tile dt, of lane l of wave w at words ((a * NDT * 4 + dt * 4 + c) * 256 + w * 64 + l) * 4,
+  // so one store instruction covers 1 KiB of consecutive words; the row sums after them.
   float* buf = reinterpret_cast<float*>(smem);
+  f32x4_t* buf4 = reinterpret_cast<f32x4_t*>(smem);
   constexpr int RS = 3 * NDT * 16 * 256;  // the row sums
   __syncthreads();  // every wave is done with the last tile
   if (grp == 1) {
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        buf[((0 * NDT + dt) * 16 + r) * 256 + wig * 64 + lane] = accA[dt][r];
-        buf[((1 * NDT + dt) * 16 + r) * 256 + wig * 64 + lane] = accO[dt][r];
-        if (has_tv) buf[((2 * NDT + dt) * 16 + r) * 256 + wig * 64 + lane] = accC[dt][r];
+      for (int c = 0; c < 4; ++c) {
+        const int i = (dt * 4 + c) * 256 + wig * 64 + lane;
+        buf4[i] = f32x4_t{accA[dt][4 * c], accA[dt][4 * c + 1], accA[dt][4 * c + 2], accA[dt][4 * c + 3]};
+        buf4[i + NDT * 4 * 256] =
+            f32x4_t{accO[dt][4 * c], accO[dt][4 * c + 1], accO[dt][4 * c + 2], accO[dt][4 * c + 3]};
+        if (has_tv)
+          buf4[i + 2 * NDT * 4 * 256] =
+              f32x4_t{accC[dt][4 * c], accC[dt][4 * c + 1], accC[dt][4 * c + 2], accC[dt][4 * c + 3]};
       }
     buf[RS + wig * 64 + lane] = lpart;
     buf[RS + 256 + wig * 64 + lane] = cpart;
@@ -462,10 +468,19 @@ __global__ __launch_bounds__(512, 2) void jvp_ksplit_kernel(const JvpParams p) {
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      accA[dt][r] += buf[((0 * NDT + dt) * 16 + r) * 256 + wig * 64 + lane];
-      accO[dt][r] += buf[((1 * NDT + dt) * 16 + r) * 256 + wig * 64 + lane];
-      if (has_tv) accC[dt][r] += buf[((2 * NDT + dt) * 16 + r) * 256 + wig * 64 + lane];
+    for (int c = 0; c < 4; ++c) {
+      const int i = (dt * 4 + c) * 256 + wig * 64 + lane;
+      const f32x4_t a = buf4[i], o4 = buf4[i + NDT * 4 * 256];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        accA[dt][4 * c + e] += a[e];
+        accO[dt][4 * c + e] += o4[e];
+      }
+      if (has_tv) {
+        const f32x4_t c4 = buf4[i + 2 * NDT * 4 * 256];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) accC[dt][4 * c + e] += c4[e];
+      }
     }
   lpart += buf[RS + wig * 64 + lane];
   cpart += buf[RS + 256 + wig * 64 + lane];
