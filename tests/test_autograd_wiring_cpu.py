@@ -118,6 +118,33 @@ def test_functional_hvp_and_jvp(kernels):
         _close((j1,), (j2,))
 
 
+def test_forward_mode_in_both_function_forms(kernels, monkeypatch):
+    """Outside torch.func transforms hip_sdpa takes the ctx-first Function (no per-call signature binding),
+    inside them the setup_context one: both give the JVP kernel's tangent, and reverse mode through the
+    ctx-first form gives the oracle's gradient."""
+    q, k, v = _inputs(10)
+    tq, tk, tv = _inputs(11)
+    used = []
+
+    def spy(name, apply):  # records which Function's apply ran, then runs it
+        return classmethod(lambda cls, *args: (used.append(name), apply(*args))[1])
+
+    for cls in (H.SDPAOp, H._SDPAOpEager):
+        monkeypatch.setattr(cls, "apply", spy(cls.__name__, cls.apply))
+    with torch.autograd.forward_ad.dual_level():
+        duals = [torch.autograd.forward_ad.make_dual(x, t) for x, t in ((q, tq), (k, tk), (v, tv))]
+        t_eager = torch.autograd.forward_ad.unpack_dual(H.hip_sdpa(*duals)).tangent
+    assert used == ["_SDPAOpEager"]
+    _, t_func = torch.func.jvp(lambda a, b, c: H.hip_sdpa(a, b, c), (q, k, v), (tq, tk, tv))
+    assert used[0] == "_SDPAOpEager" and set(used[1:]) == {"SDPAOp"}  # torch.func re-enters apply per level
+    expect = O.jvp(q, k, v, tq, tk, tv, q.shape[-1] ** -0.5, False)
+    _close((t_eager, t_func), (expect, expect))
+    a, b = _pair(12)
+    g1 = torch.autograd.grad(H.hip_sdpa(*a).pow(2).sum(), a)
+    g2 = torch.autograd.grad(_ref(False)(*b).pow(2).sum(), b)
+    _close(g1, g2)
+
+
 def test_gradient_of_dout_path_is_not_double_counted(kernels):
     """dO = 2 O depends on q, k, v: differentiating the create_graph'ed double backward must take
     partial derivatives of the backward map and leave the dO path to G_dO."""

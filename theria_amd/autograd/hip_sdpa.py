@@ -92,8 +92,34 @@ class SDPABackwardOp(torch.autograd.Function):
         return g_q, g_k, g_v, None, None, g_do.to(dout.dtype), None, None
 
 
+def _save_forward(ctx, q, k, v, scale, causal, o, lse) -> None:
+    ctx.scale = scale
+    ctx.causal = causal
+    ctx.mark_non_differentiable(lse)
+    ctx.set_materialize_grads(False)  # lse's gradient stays None rather than a zero fill on every backward
+    ctx.save_for_backward(q, k, v, o, lse)
+    ctx.save_for_forward(q, k, v, o, lse)
+
+
+def _sdpa_backward(ctx, do, _dlse):
+    if do is None:
+        return None, None, None, None, None, None
+    q, k, v, o, lse = ctx.saved_tensors
+    dq, dk, dv = SDPABackwardOp.apply(q, k, v, o.detach(), lse, do, ctx.scale, ctx.causal)
+    return dq, dk, dv, None, None, None
+
+
+def _sdpa_jvp(ctx, tq, tk, tv, _ts, _tc, _tf):
+    q, k, v, o, lse = ctx.saved_tensors
+    to = _ops.jvp(q, k, v, o, lse, tq, tk, tv, ctx.scale, ctx.causal, normalize=True, checked=False)
+    if to.dtype != o.dtype:
+        to = to.to(o.dtype)
+    return to, None
+
+
 class SDPAOp(torch.autograd.Function):
-    """(q, k, v, scale, causal, out_fp32) -> (o, lse)."""
+    """(q, k, v, scale, causal, out_fp32) -> (o, lse). The setup_context form, which torch.func transforms
+    (vmap, jvp, grad) require; hip_sdpa takes _SDPAOpEager outside them."""
 
     @staticmethod
     def forward(q, k, v, scale, causal, out_fp32):
@@ -101,30 +127,36 @@ class SDPAOp(torch.autograd.Function):
 
     @staticmethod
     def setup_context(ctx, inputs, output):
-        q, k, v, scale, causal, out_fp32 = inputs
-        o, lse = output
-        ctx.scale = scale
-        ctx.causal = causal
-        ctx.mark_non_differentiable(lse)
-        ctx.set_materialize_grads(False)  # lse's gradient stays None rather than a zero fill on every backward
-        ctx.save_for_backward(q, k, v, o, lse)
-        ctx.save_for_forward(q, k, v, o, lse)
+        q, k, v, scale, causal, _ = inputs
+        _save_forward(ctx, q, k, v, scale, causal, *output)
+
+    backward = staticmethod(_sdpa_backward)
+    jvp = staticmethod(_sdpa_jvp)
+
+
+class _SDPAOpEager(torch.autograd.Function):
+    """SDPAOp in the ctx-first form, for calls outside torch.func transforms (which refuse this form).
+    torch.autograd.Function.apply binds the arguments of a setup_context-form forward through
+    inspect.signature on every call, ~30 us of host time, as much as the forward kernel's own launch path;
+    this form skips it. Same kernels, saved tensors, backward and JVP as SDPAOp."""
 
     @staticmethod
-    def backward(ctx, do, _dlse):
-        if do is None:
-            return None, None, None, None, None, None
-        q, k, v, o, lse = ctx.saved_tensors
-        dq, dk, dv = SDPABackwardOp.apply(q, k, v, o.detach(), lse, do, ctx.scale, ctx.causal)
-        return dq, dk, dv, None, None, None
+    def forward(ctx, q, k, v, scale, causal, out_fp32):
+        o, lse = _ops.fwd(q, k, v, scale, causal, out_fp32=out_fp32)[:2]
+        _save_forward(ctx, q, k, v, scale, causal, o, lse)
+        return o, lse
 
-    @staticmethod
-    def jvp(ctx, tq, tk, tv, _ts, _tc, _tf):
-        q, k, v, o, lse = ctx.saved_tensors
-        to = _ops.jvp(q, k, v, o, lse, tq, tk, tv, ctx.scale, ctx.causal, normalize=True, checked=False)
-        if to.dtype != o.dtype:
-            to = to.to(o.dtype)
-        return to, None
+    backward = staticmethod(_sdpa_backward)
+    jvp = staticmethod(_sdpa_jvp)
+
+
+# torch's own test for an active torch.func transform (what Function.apply checks); without it, always SDPAOp
+_transforms_active = getattr(torch._C, "_are_functorch_transforms_active", lambda: True)
+
+
+def _sdpa_op(q, k, v, scale: float, causal: bool, out_fp32: bool):
+    op = SDPAOp if _transforms_active() else _SDPAOpEager
+    return op.apply(q, k, v, scale, causal, out_fp32)
 
 
 def _common_head_dim(q, k, v):
@@ -154,7 +186,7 @@ def hip_sdpa(q, k, v, *, causal: bool = False, scale: float | None = None, out_f
     if scale is None:
         scale = _ops.default_scale(q.shape[-1])
     q, k, v, dv = _common_head_dim(q, k, v)
-    o = SDPAOp.apply(q, k, v, float(scale), bool(causal), bool(out_fp32))[0]
+    o = _sdpa_op(q, k, v, float(scale), bool(causal), bool(out_fp32))[0]
     return o if o.shape[-1] == dv else o[..., :dv]
 
 
@@ -163,7 +195,7 @@ def hip_sdpa_with_lse(q, k, v, *, causal: bool = False, scale: float | None = No
     if scale is None:
         scale = _ops.default_scale(q.shape[-1])
     q, k, v, dv = _common_head_dim(q, k, v)
-    o, lse = SDPAOp.apply(q, k, v, float(scale), bool(causal), False)[:2]
+    o, lse = _sdpa_op(q, k, v, float(scale), bool(causal), False)[:2]
     return (o if o.shape[-1] == dv else o[..., :dv]), lse
 
 
