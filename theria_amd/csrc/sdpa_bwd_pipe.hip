@@ -9,7 +9,7 @@
 // Work decomposition: one workgroup = NW waves, each owning 32 keys (K and V fragments in registers,
 // dK and dV accumulated in registers); the workgroup streams the query tiles (64 or 128 rows) of its head.
 //  * Q and dO tiles reach LDS by DMA (sdpa_lds.hpp) into double buffers with one barrier per tile;
-//    the row terms -lse / scale and -delta of the next tile are loaded by the first 64 threads during
+//    the row terms -lse * log2(e) and -delta of the next tile are loaded by the first 64 threads during
 //    the current tile and written beside them, with a flag for a tile holding a peaked row (largest
 //    probability above 1/4, flagged in lse): the tile loop skips such tiles, and a workgroup that skipped
 //    any runs them after the loop (found from the lse flags) from exact float32 scores, with P and dS as
@@ -19,10 +19,11 @@
 //  * Phase order per 64-row half of a tile, i.e. two 32-query subtiles (scheduling barriers keep it):
 //      S, dP of subtile 0 | S, dP of subtile 1 with exp / dS of subtile 0
 //      | dV, dK of subtile 0 with exp / dS of subtile 1 | dV, dK of subtile 1.
-//  * dP starts from -delta as the MFMA accumulator input, so dS = P o dP is one multiply; S starts from
-//    -lse / scale, so P = exp2(S * scale * log2(e)) takes one multiply per score. (Holding K pre-multiplied
-//    by scale * log2(e) would save it, but rounds every score's factors once more to 16 bits: P off by up
-//    to ~10% on rows whose scores are large.)
+//  * dP starts from -delta as the MFMA accumulator input, so dS = P o dP is one multiply; K is held
+//    pre-multiplied by scale * log2(e) (rounded once to 16 bits) and S starts from -lse * log2(e), so
+//    P = exp2(S) takes no multiply per score. That rounding moves each score by ~2^-9 of its terms, below the
+//    16-bit rounding of P on rows without a peaked flag; the peaked tiles (above) form exact scores from the
+//    unscaled K instead.
 #include <type_traits>
 
 #include "sdpa_common.hpp"
