@@ -16,7 +16,8 @@
 // single pass over the keys suffices for G_Q.)
 //
 // rows kernel: lane per query (transposed score tiles, as in the forward). One pass over key tiles (64
-//   keys as two 32-key subtiles for 16-bit inputs at head dim <= 64, else 32) accumulates the four D-wide products of the G_Q expression plus r and t, writes G_Q, r, t.
+//   keys as two 32-key subtiles for 16-bit inputs at head dim <= 64, else 32) accumulates the four D-wide
+//   products of the G_Q expression plus r and t, writes G_Q, r, t.
 //   16-bit workgroups holding a row flagged peaked in lse are redone after it (as extra workgroups of the
 //   cols kernel's grid): with the exact r and t the first launch wrote, Gbar_S = P o ((Gam - r)(dP - z) + W - t)
 //   is formed in float32 and, with dS, entered as two 16-bit terms (hi + lo), so that
@@ -26,6 +27,11 @@
 //   accumulates G_V and G_K in registers. 16-bit query tiles holding a row flagged peaked are skipped by
 //   that pass and run after it with Gbar_dP, Gbar_S and dS entered as two 16-bit terms each (their sums over
 //   many queries are small there).
+// 16-bit inputs at head dim 64 with LDS-DMA tiles take two split kernels instead, eight-wave workgroups of two
+// four-wave groups (two waves per SIMD at 256 registers): the key-split row kernel (bwdbwd_rows_ks_kernel) forms
+// the exact row terms, G_Q and G_dO in one launch (the groups split each query block's key tiles and combine
+// through LDS), and the query-split column kernel (bwdbwd_cols_qs_kernel) G_K and G_V (the groups split each
+// key block's query tiles).
 #include <initializer_list>
 #include <type_traits>
 

@@ -32,7 +32,7 @@
 
 namespace theria {
 
-// QT query tiles of 32 per wave: two at DP = 64 without the causal mask, where each K / V^T fragment then
+// QT query tiles of 32 per wave: two at DP = 32 and 64 without the causal mask, where each K / V^T fragment then
 // feeds two MFMAs, unless the grid would then leave CUs without two waves per SIMD; one at DP = 128, where
 // the registers would not allow two, and one with the causal mask, whose paired blocks need the smaller
 // block to fill the GPU.

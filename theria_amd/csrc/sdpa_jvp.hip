@@ -11,7 +11,9 @@
 // 16-bit inputs: the two large terms (P o G) V and c o O of tO cancel, so operand rounding in them is
 // amplified (a bfloat16-rounded P o G gave 0.03 absolute error on a row with four visible keys). Both
 // products are therefore formed from two-term 16-bit splits (hi + lo) of P o G and of P, and O is always
-// rebuilt in the pass from the same P (the saved O, rounded to 16 bits, is not used).
+// rebuilt in the pass from the same P (the saved O, rounded to 16 bits, is not used). The key-split kernel
+// (jvp_ksplit_kernel, below) takes the split only in waves holding a row flagged peaked in lse: elsewhere the
+// rounding of P o G and P spreads over many keys and one 16-bit term each suffices.
 // p.normalize divides P by its own row sum (every dtype): the JVP of the exact softmax for an lse this
 // library's forward wrote (a 16-bit forward's lse comes from rounded probabilities, so P rebuilt from it
 // sums to 1 only within ~2^-9). Without it P = exp(S - lse) is held exactly as given, which is the
