@@ -269,28 +269,31 @@ def test_hvp_fd_vjp_agrees_with_exact_hvp(hip_device):
     assert float(cos) > 0.99
 
 
-@pytest.mark.parametrize("D,Dv,causal", [(32, 64, False), (64, 24, True), (16, 128, False)])
-def test_value_head_dim_differs(D, Dv, causal, hip_device):
-    """Dv != D through hip_sdpa: O, first order, HVP by double backward and forward-mode JVP."""
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("T,M,D,Dv,causal", [(37, 45, 32, 64, False), (37, 45, 64, 24, True), (37, 45, 16, 128, False),
+                                            (200, 260, 64, 40, False)])
+def test_value_head_dim_differs(T, M, D, Dv, causal, dt, hip_device):
+    """Dv != D through hip_sdpa: O, first order, HVP by double backward and forward-mode JVP. The last shape
+    takes the pipelined 16-bit kernels (more than 128 queries, head dim 64 after padding)."""
     dev = hip_device
-    print(f"Dv != D: D={D} Dv={Dv} causal={causal}", flush=True)
-    q, qc = make((2, 2, 37, D), torch.float32, dev, 91, grad=True)
-    k, kc = make((2, 2, 45, D), torch.float32, dev, 92, grad=True)
-    v, vc = make((2, 2, 45, Dv), torch.float32, dev, 93, grad=True)
-    w, wc = make((2, 2, 37, Dv), torch.float32, dev, 94)
-    u = [make(t.shape, torch.float32, dev, 95 + i) for i, t in enumerate((q, k, v))]
+    print(f"Dv != D: {dt} T={T} M={M} D={D} Dv={Dv} causal={causal}", flush=True)
+    q, qc = make((2, 2, T, D), dt, dev, 91, grad=True)
+    k, kc = make((2, 2, M, D), dt, dev, 92, grad=True)
+    v, vc = make((2, 2, M, Dv), dt, dev, 93, grad=True)
+    w, wc = make((2, 2, T, Dv), dt, dev, 94)
+    u = [make(t.shape, dt, dev, 95 + i) for i, t in enumerate((q, k, v))]
     o = hip_sdpa(q, k, v, causal=causal)
-    assert o.shape == (2, 2, 37, Dv)
-    close(o, O.forward(qc, kc, vc, causal=causal)[0], torch.float32, "O")
+    assert o.shape == (2, 2, T, Dv)
+    close(o, O.forward(qc, kc, vc, causal=causal)[0], dt, "O")
     g = torch.autograd.grad((o * w).sum(), (q, k, v), create_graph=True)
     for name, a, b in zip(("dQ", "dK", "dV"), g, O.backward(qc, kc, vc, wc, causal=causal)):
-        close(a, b, torch.float32, name)
+        close(a, b, dt, name)
     h = torch.autograd.grad(sum((a * b[0]).sum() for a, b in zip(g, u)), (q, k, v))
     for name, a, b in zip(("q", "k", "v"), h, O.hvp_weighted_sum(qc, kc, vc, wc, *(x[1] for x in u), causal=causal)):
-        close(a, b, torch.float32, f"hvp {name}")
+        close(a, b, dt, f"hvp {name}")
     _, jv = torch.func.jvp(lambda a, b, c: hip_sdpa(a, b, c, causal=causal), (q.detach(), k.detach(), v.detach()),
                            tuple(x[0] for x in u))
-    close(jv, O.jvp(qc, kc, vc, *(x[1] for x in u), causal=causal), torch.float32, "jvp")
+    close(jv, O.jvp(qc, kc, vc, *(x[1] for x in u), causal=causal), dt, "jvp")
     assert sdpa_custom(q, k, v, backend="hip", causal=causal).shape[-1] == Dv
     with pytest.raises(AssertionError):
         sdpa_custom(q, k, v, backend="triton_full_fused")
