@@ -103,7 +103,7 @@ def test_kernels_match_oracle(case, hip_device):
     _check_all_entry_points(case, hip_device, seed=1)
 
 
-def _random_cases(n: int = 24, seed: int = 2024):
+def _random_cases(n: int = 120, seed: int = 2024):
     """Seeded random configurations: dtype, head dim 8-128, 1-700 query / key rows, T != M, causal."""
     rng = random.Random(seed)
     cases = []
