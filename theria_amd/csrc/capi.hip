@@ -81,6 +81,7 @@ bool shape_from(const theria_sdpa_problem_t* p, theria::Shape& s, std::string& e
   s.dtype = p->dtype;
   s.dp = p->head_dim <= 32 ? 32 : (p->head_dim <= 64 ? 64 : 128);
   s.vec = true;
+  s.unpaired = false;
   return true;
 }
 

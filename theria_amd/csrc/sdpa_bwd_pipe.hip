@@ -118,8 +118,9 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
   // Causal at head dim <= 64: workgroup `unit` runs key block `unit` (the longest query range) and then its
   // mirror block nkb - 1 - unit, so every workgroup gets the same number of query tiles; an odd middle
   // block runs once. At head dim 128 (one workgroup per CU) the plain longest-first order measured faster.
-  constexpr bool PAIR = CAUSAL && DP <= 64;
-  const int nunit = PAIR ? (nkb + 1) / 2 : nkb;
+  // Unpaired (grids too small to fill the CUs in pairs): one block per workgroup, the longest first.
+  const bool pair = CAUSAL && DP <= 64 && !s.unpaired;
+  const int nunit = pair ? (nkb + 1) / 2 : nkb;
   const int bid = xcd_remap(blockIdx.x, gridDim.x);
   const int bh = bid / nunit;
   const int unit = bid - bh * nunit;
@@ -132,7 +133,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dkdv_pipe_kernel(const DkdvParam
   const float c2 = s.scale * kLog2e;
   THERIA_TILES_DECL;
 
-  for (int pass = 0; pass < (PAIR ? 2 : 1); ++pass) {
+  for (int pass = 0; pass < (pair ? 2 : 1); ++pass) {
   const int kb = pass == 0 ? unit : nkb - 1 - unit;
   if (pass == 1) {
     if (kb == unit) break;  // odd number of blocks: the middle one ran in pass 0
@@ -491,7 +492,9 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
   const int nqb = (s.T + BM - 1) / BM;
   // Causal: workgroup `unit` runs query block nqb - 1 - unit (the longest rows) and then its mirror
   // block `unit`, so every workgroup gets the same number of key tiles; an odd middle block runs once.
-  const int nunit = CAUSAL ? (nqb + 1) / 2 : nqb;
+  // Unpaired (grids too small to fill the CUs in pairs): one block per workgroup, the longest first.
+  const bool pair = CAUSAL && !s.unpaired;
+  const int nunit = pair ? (nqb + 1) / 2 : nqb;
   const int bid = xcd_remap(blockIdx.x, gridDim.x);
   const int bh = bid / nunit;
   const int unit = bid - bh * nunit;
@@ -502,7 +505,7 @@ __global__ __launch_bounds__(64 * NW, WPS) void dq_pipe_kernel(const DqParams p)
   const T* dO = (const T*)p.dout.p + b * p.dout.sb + h * p.dout.sh;
   THERIA_TILES_DECL;
 
-  for (int pass = 0; pass < (CAUSAL ? 2 : 1); ++pass) {
+  for (int pass = 0; pass < (pair ? 2 : 1); ++pass) {
   const int qb = CAUSAL ? (pass == 0 ? nqb - 1 - unit : unit) : unit;
   if (pass == 1) {
     if (qb == nqb - 1 - unit) break;  // odd number of blocks: the middle one ran in pass 0
@@ -829,13 +832,19 @@ static void dkdv_go(const DkdvParams& p, int64_t nblk, hipStream_t st) {
 static bool pipe_head_dim(const Shape& s) { return s.vec && s.D % 8 == 0 && s.D >= 8; }
 
 template <typename T, bool CAUSAL>
-bool launch_dq_pipe(const DqParams& p, hipStream_t st, hipError_t* err) {
-  if (!pipe_head_dim(p.s)) return false;
+bool launch_dq_pipe(const DqParams& p0, hipStream_t st, hipError_t* err) {
+  if (!pipe_head_dim(p0.s)) return false;
   // 32-bit byte offsets inside each (batch, head) slab of K and V
-  if (!slab_fits_dma(p.s.M, p.k.sr, p.s.D) || !slab_fits_dma(p.s.M, p.v.sr, p.s.D)) return false;
+  if (!slab_fits_dma(p0.s.M, p0.k.sr, p0.s.D) || !slab_fits_dma(p0.s.M, p0.v.sr, p0.s.D)) return false;
   constexpr int NW = DQ_PIPE_NW;
+  DqParams p = p0;
   const int64_t nqb = (p.s.T + 32 * NW - 1) / (32 * NW);
-  const int64_t nblk = (CAUSAL ? (nqb + 1) / 2 : nqb) * p.s.B * p.s.H;  // causal: mirrored pairs
+  int64_t nblk = (CAUSAL ? (nqb + 1) / 2 : nqb) * p.s.B * p.s.H;  // causal: mirrored pairs
+  if (CAUSAL && nblk > 0 && nblk < device_cu_count()) {
+    // the pairs would leave CUs without a workgroup: one block each, the longest first
+    p.s.unpaired = true;
+    nblk = nqb * p.s.B * p.s.H;
+  }
   if (nblk == 0) {
     *err = hipSuccess;
     return true;
@@ -858,17 +867,22 @@ template bool launch_dq_pipe<_Float16, true>(const DqParams&, hipStream_t, hipEr
 // Launch if the pipelined kernel covers this problem (16-bit, a head dim pipe_head_dim takes, vector
 // access, dK and dV both wanted); returns false otherwise.
 template <typename T, bool CAUSAL>
-bool launch_dkdv_pipe(const DkdvParams& p, hipStream_t st, hipError_t* err) {
-  if (!(pipe_head_dim(p.s) && !p.dv_only)) return false;
+bool launch_dkdv_pipe(const DkdvParams& p0, hipStream_t st, hipError_t* err) {
+  if (!(pipe_head_dim(p0.s) && !p0.dv_only)) return false;
   // 32-bit byte offsets inside each (batch, head) slab of Q, dO and K
-  if (!slab_fits_dma(p.s.T, p.q.sr, p.s.D) || !slab_fits_dma(p.s.T, p.dout.sr, p.s.D) ||
-      !slab_fits_dma(p.s.M, p.k.sr, p.s.D))
+  if (!slab_fits_dma(p0.s.T, p0.q.sr, p0.s.D) || !slab_fits_dma(p0.s.T, p0.dout.sr, p0.s.D) ||
+      !slab_fits_dma(p0.s.M, p0.k.sr, p0.s.D))
     return false;
-  // workgroups of nw waves (32 keys each): key blocks, or (causal head dim 64) pairs of mirrored blocks
+  DkdvParams p = p0;
+  const int64_t cus = device_cu_count();
+  // workgroups of nw waves (32 keys each): key blocks, or (causal head dim <= 64) pairs of mirrored blocks
   auto blocks = [&](int nw) {
     const int64_t nkb = (p.s.M + 32 * nw - 1) / (32 * nw);
-    return ((CAUSAL && p.s.dp <= 64) ? (nkb + 1) / 2 : nkb) * p.s.B * p.s.H;
+    return ((CAUSAL && p.s.dp <= 64 && !p.s.unpaired) ? (nkb + 1) / 2 : nkb) * p.s.B * p.s.H;
   };
+  // Causal grids whose pairs of four-wave workgroups would leave CUs without one (two-wave workgroups, half the
+  // waves per SIMD): one block per workgroup, the longest first.
+  if (CAUSAL && p.s.dp <= 64 && blocks(4) < cus) p.s.unpaired = true;
   if (blocks(4) == 0) {
     *err = hipSuccess;
     return true;
@@ -876,7 +890,6 @@ bool launch_dkdv_pipe(const DkdvParams& p, hipStream_t st, hipError_t* err) {
   if (p.s.dp == 32) {
     // Four-wave workgroups (eight waves would copy 128-row DMA slabs into 64-row query tiles), two-wave ones
     // where four-wave ones would leave CUs idle.
-    const int64_t cus = device_cu_count();
     if (blocks(4) >= cus)
       dkdv_go<T, CAUSAL, 4, 32, true, 2, DKDV64_HALVES>(p, blocks(4), st);
     else
@@ -887,7 +900,7 @@ bool launch_dkdv_pipe(const DkdvParams& p, hipStream_t st, hipError_t* err) {
     // with two rounds of them the CUs that finish early idle through a ~10% tail at config 2.
     // Grids that would leave CUs without a four-wave workgroup use two-wave ones (twice as many; per
     // workgroup they are slower, so only then).
-    const int64_t nblk8 = blocks(8), cus = device_cu_count();
+    const int64_t nblk8 = blocks(8);
     if (nblk8 >= cus)
       dkdv_go<T, CAUSAL, 8, 64, true, 2, DKDV64_HALVES>(p, nblk8, st);
     else if (blocks(4) >= cus)

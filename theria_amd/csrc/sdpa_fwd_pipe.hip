@@ -72,7 +72,9 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
   const int nqb = (s.T + BM - 1) / BM;
   // Causal: workgroup `unit` runs query block nqb - 1 - unit (the longest rows) and then its mirror
   // block `unit`, so every workgroup gets the same number of key tiles; an odd middle block runs once.
-  const int nunit = CAUSAL ? (nqb + 1) / 2 : nqb;
+  // Unpaired (grids too small to fill the CUs in pairs): one block per workgroup, the longest first.
+  const bool pair = CAUSAL && !s.unpaired;
+  const int nunit = pair ? (nqb + 1) / 2 : nqb;
   const int bid = xcd_remap(blockIdx.x, gridDim.x);
   const int bh = bid / nunit;
   const int unit = bid - bh * nunit;
@@ -84,7 +86,7 @@ __global__ __launch_bounds__(64 * NW, 2) void fwd_pipe_kernel(const FwdParams p)
   const float c2 = s.scale * kLog2e;
   THERIA_TILES_DECL;
 
-  for (int pass = 0; pass < (CAUSAL ? 2 : 1); ++pass) {
+  for (int pass = 0; pass < (pair ? 2 : 1); ++pass) {
   const int qb = CAUSAL ? (pass == 0 ? nqb - 1 - unit : unit) : unit;
   if (pass == 1) {
     if (qb == nqb - 1 - unit) break;  // odd number of blocks: the middle one ran in pass 0
@@ -480,8 +482,9 @@ static void fwd_pipe_go(const FwdParams& p, int64_t nblk, hipStream_t st) {
 }
 
 template <typename T, bool CAUSAL, int DP>
-static void fwd_pipe_launch(const FwdParams& p, hipStream_t st) {
+static void fwd_pipe_launch(const FwdParams& p0, hipStream_t st) {
   constexpr int QT = (DP <= 64 && !CAUSAL) ? 2 : 1;
+  FwdParams p = p0;
   const int64_t bh = (int64_t)p.s.B * p.s.H;
   const int64_t cus = device_cu_count();
   // workgroups per (batch, head): query blocks, or (causal) pairs of mirrored query blocks
@@ -499,6 +502,12 @@ static void fwd_pipe_launch(const FwdParams& p, hipStream_t st) {
       fwd_pipe_go<T, CAUSAL, 4, DP, 1>(p, units((p.s.T + 127) / 128) * bh, st);
       return;
     }
+  }
+  if (CAUSAL && nblk4 < cus) {
+    // mirrored pairs would leave CUs without a workgroup: one block each, the longest first
+    p.s.unpaired = true;
+    fwd_pipe_go<T, CAUSAL, 4, DP, QT>(p, (p.s.T + 128 * QT - 1) / (128 * QT) * bh, st);
+    return;
   }
   fwd_pipe_go<T, CAUSAL, 4, DP, QT>(p, nblk4, st);
 }

@@ -23,6 +23,9 @@ struct Shape {
   int dtype;  // theria_dtype
   int dp;     // padded head dim: 32, 64 or 128
   bool vec;   // every view allows 16-byte vector access
+  // causal pipelined kernels: one block per workgroup, longest first, instead of a block and its mirror (set by
+  // the launchers when the mirrored pairs would leave CUs without a workgroup)
+  bool unpaired;
 };
 
 // Forward: O, lse and the optional reference statistics m (row_max) and l (row_sum).
