@@ -263,8 +263,9 @@ __global__ __launch_bounds__(256) void jvp_kernel(const JvpParams p) {
   }
 }
 
-// 16-bit inputs at head dim 64 with LDS-DMA tiles: the same JVP with the keys of a query block split between
-// two groups of four waves (eight-wave workgroups), so that a SIMD holds two waves at 256 registers each
+// 16-bit inputs at head dims up to 64 (a multiple of 8, computed at 64 with the tile columns past D zero) with
+// LDS-DMA tiles: the same JVP with the keys of a query block split between two groups of four waves
+// (eight-wave workgroups), so that a SIMD holds two waves at 256 registers each
 // where jvp_kernel holds one at ~380 (config 4: B H T / 32 = 1024 query waves for 1024 SIMDs; 27.1 -> 23.0 us
 // there, same box). Each group streams its own half of the key tiles (64 keys per tile, 128 KB of LDS in
 // all) through its own double-buffered tiles; both groups meet at the same barrier every step (a group
@@ -400,15 +401,16 @@ __global__ __launch_bounds__(512, 2) void jvp_ksplit_kernel(const JvpParams p) {
     }
   };
 
-  const Dma dma(wig, lane);
+  // Head dims below 64 (a multiple of 8): the tiles' columns D .. 63 are filled with zeros by the DMA.
+  const Dma dma(wig, lane, s.D / 8);
   // Byte offsets fit in 32 bits: the host only selects this path when each (batch, head) slab of K, V, tK
   // and tV spans less than 2^31 bytes.
   const uint32_t krs = (uint32_t)p.k.sr * 2, vrs = (uint32_t)p.v.sr * 2;
   const uint32_t tkrs = has_tk ? (uint32_t)p.tk.sr * 2 : 0u, tvrs = has_tv ? (uint32_t)p.tv.sr * 2 : 0u;
-  const rsrc_t krsrc = make_rsrc(K, (uint32_t)slab_span(s.M, krs, 2 * DP)),
-               vrsrc = make_rsrc(V, (uint32_t)slab_span(s.M, vrs, 2 * DP));
-  const rsrc_t tkrsrc = make_rsrc(has_tk ? (const void*)TK : (const void*)K, (uint32_t)slab_span(s.M, tkrs, 2 * DP));
-  const rsrc_t tvrsrc = make_rsrc(has_tv ? (const void*)TV : (const void*)V, (uint32_t)slab_span(s.M, tvrs, 2 * DP));
+  const rsrc_t krsrc = make_rsrc(K, (uint32_t)slab_span(s.M, krs, 2 * s.D)),
+               vrsrc = make_rsrc(V, (uint32_t)slab_span(s.M, vrs, 2 * s.D));
+  const rsrc_t tkrsrc = make_rsrc(has_tk ? (const void*)TK : (const void*)K, (uint32_t)slab_span(s.M, tkrs, 2 * s.D));
+  const rsrc_t tvrsrc = make_rsrc(has_tv ? (const void*)TV : (const void*)V, (uint32_t)slab_span(s.M, tvrs, 2 * s.D));
   auto tile = [&](int set, int a) { return smem + ((grp * 2 + set) * 4 + a) * TB; };  // a: K, V, tK, tV
   auto issue = [&](int kt, int set) {
     const int k0 = kt * BN;
@@ -519,13 +521,14 @@ struct JvpLauncher {
     const int nqb = (p.s.T + 127) / 128;
     const int64_t nblk = (int64_t)nqb * p.s.B * p.s.H;
     if (nblk == 0) return hipSuccess;
-    if constexpr (sizeof(T) == 2 && (DP == 64 || DP == 128)) {
-      // LDS-DMA tiles: head dim exactly DP, 16-byte-aligned views, each streamed (batch, head) slab < 2^31 bytes
-      bool ok = p.s.D == DP && p.s.vec;
+    if constexpr (sizeof(T) == 2) {
+      // LDS-DMA tiles: 16-byte-aligned views, each streamed (batch, head) slab < 2^31 bytes, and a head dim that
+      // is a multiple of 8 up to 64 (the key-split kernel, columns past D zero-filled) or exactly 128
+      bool ok = p.s.vec && (DP <= 64 ? p.s.D % 8 == 0 : p.s.D == DP);
       for (const View* v : {&p.k, &p.v, &p.tk, &p.tv})
         if (v->p && !slab_fits_dma(p.s.M, v->sr, p.s.D)) ok = false;
       if (ok) {
-        if constexpr (DP == 64) {
+        if constexpr (DP <= 64) {
           if (p.tq.p && p.tk.p && p.tv.p)
             hipLaunchKernelGGL((jvp_ksplit_kernel<T, CAUSAL, HAS_O, true>), dim3((unsigned)nblk), dim3(512), 0, st, p);
           else
