@@ -454,7 +454,7 @@ static int run_bwd_bwd(const theria_sdpa_problem_t* p, const theria_tensor_t* q,
   }
   const bool rows_make_terms = s.dtype != THERIA_DTYPE_F32 && s.T > 0 && theria::bwdbwd_rows_make_row_terms(bp);
   if (rows_make_terms) {
-    // 16-bit inputs at head dim 64 (LDS-DMA tiles): the key-split row kernel forms the row term and the exact
+    // 16-bit inputs at head dims up to 64 (LDS-DMA tiles): the key-split row kernel forms the row term and the exact
     // normaliser itself in its first pass (from the forward's lse) and writes them for the column kernel; that
     // pass also forms G_dO, so no JVP launch follows.
     bp.lse_fwd = lse;

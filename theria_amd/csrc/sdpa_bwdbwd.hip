@@ -27,7 +27,8 @@
 //   accumulates G_V and G_K in registers. 16-bit query tiles holding a row flagged peaked are skipped by
 //   that pass and run after it with Gbar_dP, Gbar_S and dS entered as two 16-bit terms each (their sums over
 //   many queries are small there).
-// 16-bit inputs at head dim 64 with LDS-DMA tiles take two split kernels instead, eight-wave workgroups of two
+// 16-bit inputs at head dims up to 64 (a multiple of 8, computed at 64 with the tile columns past D zero-filled by
+// the DMA) take two split kernels instead, eight-wave workgroups of two
 // four-wave groups (two waves per SIMD at 256 registers): the key-split row kernel (bwdbwd_rows_ks_kernel) forms
 // the exact row terms, G_Q and G_dO in one launch (the groups split each query block's key tiles and combine
 // through LDS), and the query-split column kernel (bwdbwd_cols_qs_kernel) G_K and G_V (the groups split each
@@ -788,10 +789,21 @@ template <typename T, int DP>
 static bool cols_dma(const BwdBwdParams& p) {
   return dma_tiles_ok<T, DP>(p, p.s.T, {&p.q, &p.dout, &p.gq});
 }
-// The key-split row kernel takes 16-bit problems at head dim 64 whose K, V, gK, gV slabs allow LDS DMA.
+// The split kernels' LDS-DMA tiles: 16-bit inputs, a head dim that is a multiple of 8 up to 64 (computed at 64,
+// the tile columns past D zero-filled by the DMA), 16-byte-aligned views, and every (batch, head) slab of the
+// streamed tensors below 2^31 bytes.
+template <typename T>
+static bool split_tiles_ok(const BwdBwdParams& p, int64_t rows, std::initializer_list<const View*> streamed) {
+  if (!(sizeof(T) == 2 && p.s.dp <= 64 && p.s.D % 8 == 0 && p.s.vec)) return false;
+  for (const View* v : streamed)
+    if (v->p && !slab_fits_dma(rows, v->sr, p.s.D)) return false;
+  return true;
+}
+
+// The key-split row kernel takes 16-bit problems at head dims up to 64 whose K, V, gK, gV slabs allow LDS DMA.
 template <typename T, int DP>
 static bool rows_ks_ok(const BwdBwdParams& p) {
-  return DP == 64 && sizeof(T) == 2 && dma_tiles_ok<T, DP>(p, p.s.M, {&p.k, &p.v, &p.gk, &p.gv});
+  return (DP == 32 || DP == 64) && split_tiles_ok<T>(p, p.s.M, {&p.k, &p.v, &p.gk, &p.gv});
 }
 
 // 16-bit: the rows kernel's exact launch rides in the column grid when both take the same tile path.
@@ -800,9 +812,9 @@ static bool exact_in_cols(const BwdBwdParams& p) {
   return sizeof(T) == 2 && !rows_ks_ok<T, DP>(p) && rows_dma<T, DP>(p) == cols_dma<T, DP>(p);
 }
 
-// The row pass for 16-bit inputs at head dim 64 with LDS-DMA tiles, as two key groups of four waves (eight-wave
-// workgroups, two waves per SIMD): the keys of each query block are split between the groups, whose partial
-// sums meet in LDS. Each group makes two passes over its key tiles:
+// The row pass for 16-bit inputs at head dims up to 64 with LDS-DMA tiles (FD: exactly 64; otherwise a multiple of
+// 8, the tile columns past D zero-filled), as two key groups of four waves (eight-wave workgroups, two waves per
+// SIMD): the keys of each query block are split between the groups, whose partial sums meet in LDS. Each group makes two passes over its key tiles:
 //   1. with P from the forward's lse: L = sum_j P, sum_j P Gam and the largest P, and the D-wide products
 //      A = sum_j (P o Gam) V + sum_j P gV and O = sum_j P V, partial per group, then exchanged. Then
 //      sum_j P dP = dO . O and sum_j P (Gam dP + W) = dO . A, which give the row's exact normaliser (P_c = P / L:
@@ -817,7 +829,7 @@ static bool exact_in_cols(const BwdBwdParams& p) {
 // the products fit 256 registers. Writes G_Q and G_dO, and r, t, z and lse + ln L (flagged peaked when the
 // row's largest P_c exceeds 1/4) for the column kernel. ALL: gQ, gK and gV are all given (the presence tests are
 // then constants, and the loop bodies have no branches between their products).
-template <typename T, bool CAUSAL, bool ALL>
+template <typename T, bool CAUSAL, bool ALL, bool FD>
 __global__ __launch_bounds__(512, 2) void bwdbwd_rows_ks_kernel(const BwdBwdParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
@@ -1022,15 +1034,16 @@ __global__ __launch_bounds__(512, 2) void bwdbwd_rows_ks_kernel(const BwdBwdPara
     }
   };
 
-  const Dma dma(wig, lane);
+  const Dma dma(wig, lane, FD ? 8 : s.D / 8);  // FD: head dim 64; else tile columns D .. 63 zero-filled
   // Byte offsets fit in 32 bits: the host only selects this kernel when each (batch, head) slab of K, V, gK and
   // gV spans less than 2^31 bytes.
   const uint32_t krs = (uint32_t)p.k.sr * 2, vrs = (uint32_t)p.v.sr * 2;
   const uint32_t gkrs = has_gk ? (uint32_t)p.gk.sr * 2 : 0u, gvrs = has_gv ? (uint32_t)p.gv.sr * 2 : 0u;
-  const rsrc_t krsrc = make_rsrc(K, (uint32_t)slab_span(s.M, krs, 2 * DP)),
-               vrsrc = make_rsrc(V, (uint32_t)slab_span(s.M, vrs, 2 * DP));
-  const rsrc_t gkrsrc = make_rsrc(has_gk ? (const void*)GK : (const void*)K, (uint32_t)slab_span(s.M, gkrs, 2 * DP));
-  const rsrc_t gvrsrc = make_rsrc(has_gv ? (const void*)GV : (const void*)V, (uint32_t)slab_span(s.M, gvrs, 2 * DP));
+  const int64_t rb = 2 * (FD ? 64 : s.D);  // bytes of a row the DMA reads
+  const rsrc_t krsrc = make_rsrc(K, (uint32_t)slab_span(s.M, krs, rb)),
+               vrsrc = make_rsrc(V, (uint32_t)slab_span(s.M, vrs, rb));
+  const rsrc_t gkrsrc = make_rsrc(has_gk ? (const void*)GK : (const void*)K, (uint32_t)slab_span(s.M, gkrs, rb));
+  const rsrc_t gvrsrc = make_rsrc(has_gv ? (const void*)GV : (const void*)V, (uint32_t)slab_span(s.M, gvrs, rb));
   auto tile = [&](int set, int a) { return smem + ((grp * 2 + set) * 4 + a) * TB; };  // a: K, V, gK, gV
   auto issue = [&](int kt, int set) {
     const int k0 = kt * BN;
@@ -1182,14 +1195,14 @@ __global__ __launch_bounds__(512, 2) void bwdbwd_rows_ks_kernel(const BwdBwdPara
 }
 
 
-// The column pass for 16-bit inputs at head dim 64 with LDS-DMA tiles, as two query groups of four waves
-// (eight-wave workgroups, two waves per SIMD). A workgroup owns 128 keys (32 per wave, lane per key, as in
-// cols_block); the groups sweep the two halves of its 32-query tiles and sum G_V and G_K in registers, and
-// group 1's sums reach group 0 through LDS at the end. Query tiles holding a row flagged peaked in lse are
+// The column pass for 16-bit inputs at head dims up to 64 with LDS-DMA tiles (FD as in the row pass), as two
+// query groups of four waves (eight-wave workgroups, two waves per SIMD). A workgroup owns 128 keys (32 per wave,
+// lane per key, as in cols_block); the groups sweep the two halves of its 32-query tiles and sum G_V and G_K in
+// registers, and group 1's sums reach group 0 through LDS at the end. Query tiles holding a row flagged peaked in lse are
 // skipped by the sweep and run after it, shared out between the groups, with Gbar_dP, Gbar_S and dS entered as
 // two 16-bit terms. The gK and gV fragments sit in LDS, so that the K and V fragments, the two accumulators and
 // the products fit 256 registers. ALL as in the key-split row kernel.
-template <typename T, bool CAUSAL, bool ALL>
+template <typename T, bool CAUSAL, bool ALL, bool FD>
 __global__ __launch_bounds__(512, 2) void bwdbwd_cols_qs_kernel(const BwdBwdParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
@@ -1359,14 +1372,15 @@ __global__ __launch_bounds__(512, 2) void bwdbwd_cols_qs_kernel(const BwdBwdPara
     }
   };
 
-  const Dma dma(wig, lane);
+  const Dma dma(wig, lane, FD ? 8 : s.D / 8);  // FD: head dim 64; else tile columns D .. 63 zero-filled
   // Byte offsets fit in 32 bits: the host only selects this kernel when each (batch, head) slab of Q, dO and gQ
   // spans less than 2^31 bytes.
   const uint32_t qrs = (uint32_t)p.q.sr * 2, ors = (uint32_t)p.dout.sr * 2;
   const uint32_t gqrs = has_gq ? (uint32_t)p.gq.sr * 2 : 0u;
-  const rsrc_t qrsrc = make_rsrc(Q, (uint32_t)slab_span(s.T, qrs, 2 * DP)),
-               orsrc = make_rsrc(dO, (uint32_t)slab_span(s.T, ors, 2 * DP));
-  const rsrc_t gqrsrc = make_rsrc(has_gq ? (const void*)GQ : (const void*)Q, (uint32_t)slab_span(s.T, gqrs, 2 * DP));
+  const int64_t rb = 2 * (FD ? 64 : s.D);  // bytes of a row the DMA reads
+  const rsrc_t qrsrc = make_rsrc(Q, (uint32_t)slab_span(s.T, qrs, rb)),
+               orsrc = make_rsrc(dO, (uint32_t)slab_span(s.T, ors, rb));
+  const rsrc_t gqrsrc = make_rsrc(has_gq ? (const void*)GQ : (const void*)Q, (uint32_t)slab_span(s.T, gqrs, rb));
   auto tiles = [&](int set) { return smem + (grp * 2 + set) * 3 * TB; };  // Q, dO, gQ at 0, TB, 2 TB
   auto issue = [&](int it, int set) {
     const int q0 = qbeg + it * BM;
@@ -1484,7 +1498,7 @@ __global__ __launch_bounds__(512, 2) void bwdbwd_cols_qs_kernel(const BwdBwdPara
 // whose rows kernel runs its exact row blocks on its own (no row blocks in the column grid).
 template <typename T, int DP>
 static bool cols_qs_ok(const BwdBwdParams& p) {
-  return DP == 64 && sizeof(T) == 2 && cols_dma<T, DP>(p) && !exact_in_cols<T, DP>(p);
+  return (DP == 32 || DP == 64) && split_tiles_ok<T>(p, p.s.T, {&p.q, &p.dout, &p.gq}) && !exact_in_cols<T, DP>(p);
 }
 
 struct RowsLauncher {
@@ -1493,12 +1507,18 @@ struct RowsLauncher {
     const int nqb = (p.s.T + 127) / 128;
     const int64_t nblk = (int64_t)nqb * p.s.B * p.s.H;
     if (nblk == 0) return hipSuccess;
-    if constexpr (sizeof(T) == 2 && DP == 64) {
+    if constexpr (sizeof(T) == 2 && (DP == 32 || DP == 64)) {
       if (rows_ks_ok<T, DP>(p)) {  // every row block exact in one launch (the column grid has no row blocks)
-        if (p.gq.p && p.gk.p && p.gv.p)
-          hipLaunchKernelGGL((bwdbwd_rows_ks_kernel<T, CAUSAL, true>), dim3((unsigned)nblk), dim3(512), 0, st, p);
+        const bool all = p.gq.p && p.gk.p && p.gv.p, fd = p.s.D == 64;
+        const dim3 grid((unsigned)nblk), block(512);
+        if (all && fd)
+          hipLaunchKernelGGL((bwdbwd_rows_ks_kernel<T, CAUSAL, true, true>), grid, block, 0, st, p);
+        else if (all)
+          hipLaunchKernelGGL((bwdbwd_rows_ks_kernel<T, CAUSAL, true, false>), grid, block, 0, st, p);
+        else if (fd)
+          hipLaunchKernelGGL((bwdbwd_rows_ks_kernel<T, CAUSAL, false, true>), grid, block, 0, st, p);
         else
-          hipLaunchKernelGGL((bwdbwd_rows_ks_kernel<T, CAUSAL, false>), dim3((unsigned)nblk), dim3(512), 0, st, p);
+          hipLaunchKernelGGL((bwdbwd_rows_ks_kernel<T, CAUSAL, false, false>), grid, block, 0, st, p);
         return hipGetLastError();
       }
     }
@@ -1526,13 +1546,19 @@ struct ColsLauncher {
     const int64_t nblk = (int64_t)((p.s.M + 127) / 128) * p.s.B * p.s.H;
     const int64_t nrow = (int64_t)((p.s.T + 127) / 128) * p.s.B * p.s.H;
     const bool dma = (sizeof(T) == 2 && (DP == 64 || DP == 128)) && cols_dma<T, DP>(p);
-    if constexpr (sizeof(T) == 2 && DP == 64) {
+    if constexpr (sizeof(T) == 2 && (DP == 32 || DP == 64)) {
       if (cols_qs_ok<T, DP>(p)) {
         if (nblk == 0) return hipSuccess;
-        if (p.gq.p && p.gk.p && p.gv.p)
-          hipLaunchKernelGGL((bwdbwd_cols_qs_kernel<T, CAUSAL, true>), dim3((unsigned)nblk), dim3(512), 0, st, p);
+        const bool all = p.gq.p && p.gk.p && p.gv.p, fd = p.s.D == 64;
+        const dim3 grid((unsigned)nblk), block(512);
+        if (all && fd)
+          hipLaunchKernelGGL((bwdbwd_cols_qs_kernel<T, CAUSAL, true, true>), grid, block, 0, st, p);
+        else if (all)
+          hipLaunchKernelGGL((bwdbwd_cols_qs_kernel<T, CAUSAL, true, false>), grid, block, 0, st, p);
+        else if (fd)
+          hipLaunchKernelGGL((bwdbwd_cols_qs_kernel<T, CAUSAL, false, true>), grid, block, 0, st, p);
         else
-          hipLaunchKernelGGL((bwdbwd_cols_qs_kernel<T, CAUSAL, false>), dim3((unsigned)nblk), dim3(512), 0, st, p);
+          hipLaunchKernelGGL((bwdbwd_cols_qs_kernel<T, CAUSAL, false, false>), grid, block, 0, st, p);
         return hipGetLastError();
       }
     }
@@ -1563,7 +1589,7 @@ struct ColsLauncher {
 hipError_t launch_bwdbwd_rows(const BwdBwdParams& p, hipStream_t st) { return dispatch_all<RowsLauncher>(p, st); }
 
 bool bwdbwd_rows_make_row_terms(const BwdBwdParams& p) {
-  if (p.s.dp != 64) return false;
+  if (p.s.dp > 64) return false;
   if (p.s.dtype == 1) return rows_ks_ok<_Float16, 64>(p);
   if (p.s.dtype == 2) return rows_ks_ok<__bf16, 64>(p);
   return false;

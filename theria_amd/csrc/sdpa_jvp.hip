@@ -272,7 +272,7 @@ __global__ __launch_bounds__(256) void jvp_kernel(const JvpParams p) {
 // whose half is shorter idles through the last step). The float32 partial sums of group 1 (accumulators,
 // row sums) pass to group 0 through LDS at the end. ALL: every tangent is given (the presence tests are then
 // constants, and the loop body has no branches between its products).
-template <typename T, bool CAUSAL, bool HAS_O, bool ALL>
+template <typename T, bool CAUSAL, bool HAS_O, bool ALL, bool FD>
 __global__ __launch_bounds__(512, 2) void jvp_ksplit_kernel(const JvpParams p) {
   using MM = Mfma<T>;
   using F = typename MM::frag_t;
@@ -402,15 +402,16 @@ __global__ __launch_bounds__(512, 2) void jvp_ksplit_kernel(const JvpParams p) {
   };
 
   // Head dims below 64 (a multiple of 8): the tiles' columns D .. 63 are filled with zeros by the DMA.
-  const Dma dma(wig, lane, s.D / 8);
+  const Dma dma(wig, lane, FD ? 8 : s.D / 8);  // FD: head dim 64
   // Byte offsets fit in 32 bits: the host only selects this path when each (batch, head) slab of K, V, tK
   // and tV spans less than 2^31 bytes.
   const uint32_t krs = (uint32_t)p.k.sr * 2, vrs = (uint32_t)p.v.sr * 2;
   const uint32_t tkrs = has_tk ? (uint32_t)p.tk.sr * 2 : 0u, tvrs = has_tv ? (uint32_t)p.tv.sr * 2 : 0u;
-  const rsrc_t krsrc = make_rsrc(K, (uint32_t)slab_span(s.M, krs, 2 * s.D)),
-               vrsrc = make_rsrc(V, (uint32_t)slab_span(s.M, vrs, 2 * s.D));
-  const rsrc_t tkrsrc = make_rsrc(has_tk ? (const void*)TK : (const void*)K, (uint32_t)slab_span(s.M, tkrs, 2 * s.D));
-  const rsrc_t tvrsrc = make_rsrc(has_tv ? (const void*)TV : (const void*)V, (uint32_t)slab_span(s.M, tvrs, 2 * s.D));
+  const int64_t rb = 2 * (FD ? 64 : s.D);  // bytes of a row the DMA reads
+  const rsrc_t krsrc = make_rsrc(K, (uint32_t)slab_span(s.M, krs, rb)),
+               vrsrc = make_rsrc(V, (uint32_t)slab_span(s.M, vrs, rb));
+  const rsrc_t tkrsrc = make_rsrc(has_tk ? (const void*)TK : (const void*)K, (uint32_t)slab_span(s.M, tkrs, rb));
+  const rsrc_t tvrsrc = make_rsrc(has_tv ? (const void*)TV : (const void*)V, (uint32_t)slab_span(s.M, tvrs, rb));
   auto tile = [&](int set, int a) { return smem + ((grp * 2 + set) * 4 + a) * TB; };  // a: K, V, tK, tV
   auto issue = [&](int kt, int set) {
     const int k0 = kt * BN;
@@ -529,10 +530,16 @@ struct JvpLauncher {
         if (v->p && !slab_fits_dma(p.s.M, v->sr, p.s.D)) ok = false;
       if (ok) {
         if constexpr (DP <= 64) {
-          if (p.tq.p && p.tk.p && p.tv.p)
-            hipLaunchKernelGGL((jvp_ksplit_kernel<T, CAUSAL, HAS_O, true>), dim3((unsigned)nblk), dim3(512), 0, st, p);
+          const bool all = p.tq.p && p.tk.p && p.tv.p, fd = p.s.D == 64;
+          const dim3 grid((unsigned)nblk), block(512);
+          if (all && fd)
+            hipLaunchKernelGGL((jvp_ksplit_kernel<T, CAUSAL, HAS_O, true, true>), grid, block, 0, st, p);
+          else if (all)
+            hipLaunchKernelGGL((jvp_ksplit_kernel<T, CAUSAL, HAS_O, true, false>), grid, block, 0, st, p);
+          else if (fd)
+            hipLaunchKernelGGL((jvp_ksplit_kernel<T, CAUSAL, HAS_O, false, true>), grid, block, 0, st, p);
           else
-            hipLaunchKernelGGL((jvp_ksplit_kernel<T, CAUSAL, HAS_O, false>), dim3((unsigned)nblk), dim3(512), 0, st, p);
+            hipLaunchKernelGGL((jvp_ksplit_kernel<T, CAUSAL, HAS_O, false, false>), grid, block, 0, st, p);
         } else
           hipLaunchKernelGGL((jvp_kernel<T, DP, CAUSAL, HAS_O, true>), dim3((unsigned)nblk), dim3(256), 0, st, p);
         return hipGetLastError();
