@@ -126,6 +126,13 @@ def test_random_configurations_match_oracle(case, hip_device):
     _check_all_entry_points(case, hip_device, seed=100)
 
 
+def test_row_term_of_a_long_head(hip_device):
+    """bf16 at head dim 128: the row term dO . O over 128 columns of the 16-bit O is off by its rounding (here
+    0.022 on |delta| = 7.2, over the 2e-2 absolute bar alone), so the 16-bit row term is held to the 16-bit bar.
+    Found by a random sweep (the generator of _random_cases, seed 21, case 721)."""
+    _check_all_entry_points((torch.bfloat16, 2, 2, 82, 82, 128, False), hip_device, seed=1021)
+
+
 def _check_all_entry_points(case, dev, seed: int):
     """Forward (O, lse, m, l), backward (with O, from stats, dV only), JVP (saved / rebuilt O, one tangent)
     and the double backward (all cotangents, one) against the float64 oracle on the same inputs."""
@@ -208,11 +215,13 @@ def check_entry_points_on(dev, dt, causal, q, k, v, do, tq, tk, tv, scale=None, 
     for name, a, b in zip(("dQ", "dK", "dV"), (dq, dk, dv), ref):
         close(a, b, dt, name)
     # the row term: dO . O, or its exact form sum_j P_ij dP_ij / sum_j P_ij on query blocks holding a peaked
-    # row; both equal the oracle's dO . O_exact within the float32-output bar
-    torch.testing.assert_close(delta.double().cpu(), (doc * Or).sum(-1), **f32_out, msg=lambda m_: f"delta: {m_}")
+    # row; both equal the oracle's dO . O_exact within the 16-bit bar (dO . O reads the forward's 16-bit O, whose
+    # rounding, 2^-9 relative per element, carries into the sum: one rounding unit of |delta| on top of 2e-2)
+    delta_tol = f32_out if dt == torch.float32 else bars.tol(dt)
+    torch.testing.assert_close(delta.double().cpu(), (doc * Or).sum(-1), **delta_tol, msg=lambda m_: f"delta: {m_}")
     # every 16-bit row flagged peaked: two-term operands and the exact row term everywhere
     aq, ak, av, adelta = _ops.bwd(q, k, v, o, flag_all(lse) if dt != torch.float32 else lse, do, s, causal)
-    torch.testing.assert_close(adelta.double().cpu(), (doc * Or).sum(-1), **f32_out,
+    torch.testing.assert_close(adelta.double().cpu(), (doc * Or).sum(-1), **delta_tol,
                                msg=lambda m_: f"delta(all peaked): {m_}")
     for name, a, b in zip(("dQ(all split)", "dK(all split)", "dV(all split)"), (aq, ak, av), ref):
         close(a, b, dt, name)
