@@ -285,7 +285,7 @@ __global__ __launch_bounds__(512, 2) void jvp_ksplit_kernel(const JvpParams p) {
   static_assert(NSLAB * Dma::SLAB_ROWS == BN, "key tiles must be whole DMA slabs");
   // [group][set][K, V, tK, tV]; reused for the partial sums after the key loop
   __shared__ __attribute__((aligned(1024))) char smem[2 * 2 * 4 * TB];
-  static_assert(sizeof(smem) >= (3 * NDT * 16 + 2) * 256 * 4, "the partial sums fit in the tile memory");
+  static_assert(sizeof(smem) >= (2 * 3 * 16 + 4) * 256 * 4, "the partial sums fit in the tile memory");
 
   const Shape& s = p.s;
   const int lane = threadIdx.x & 63, li = lane & 31, g = lane >> 5;
@@ -445,74 +445,77 @@ __global__ __launch_bounds__(512, 2) void jvp_ksplit_kernel(const JvpParams p) {
   else
     sweep(std::integral_constant<bool, false>{});
 
-  // Group 1's partial sums to group 0 in one round, 16 bytes per lane per store: elements 4c .. 4c + 3 of
-  // accumulator a, column tile dt, of lane l of wave w at words ((a * NDT * 4 + dt * 4 + c) * 256 + w * 64 + l) * 4,
-  // so one store instruction covers 1 KiB of consecutive words; the row sums after them.
+  // The groups finish one column tile each (group g the tile dt = g): each hands the other tile's partial sums
+  // and its row sums to the other group in one round, 16 bytes per lane per store (elements 4c .. 4c + 3 of
+  // accumulator a of lane l of wave w of group g at words (((g * 3 + a) * 4 + c) * 256 + w * 64 + l) * 4, so one
+  // store instruction covers 1 KiB of consecutive words), then stores its half of the output.
+  static_assert(NDT == 2, "one column tile per group");
   float* buf = reinterpret_cast<float*>(smem);
   f32x4_t* buf4 = reinterpret_cast<f32x4_t*>(smem);
-  constexpr int RS = 3 * NDT * 16 * 256;  // the row sums
+  constexpr int RS = 2 * 3 * 4 * 256 * 4;  // the row sums, [group][l, c]
   __syncthreads();  // every wave is done with the last tile
-  if (grp == 1) {
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int i = (dt * 4 + c) * 256 + wig * 64 + lane;
-        buf4[i] = f32x4_t{accA[dt][4 * c], accA[dt][4 * c + 1], accA[dt][4 * c + 2], accA[dt][4 * c + 3]};
-        buf4[i + NDT * 4 * 256] =
-            f32x4_t{accO[dt][4 * c], accO[dt][4 * c + 1], accO[dt][4 * c + 2], accO[dt][4 * c + 3]};
-        if (has_tv)
-          buf4[i + 2 * NDT * 4 * 256] =
-              f32x4_t{accC[dt][4 * c], accC[dt][4 * c + 1], accC[dt][4 * c + 2], accC[dt][4 * c + 3]};
-      }
-    buf[RS + wig * 64 + lane] = lpart;
-    buf[RS + 256 + wig * 64 + lane] = cpart;
-  }
-  __syncthreads();
-  if (grp == 1) return;
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
+  auto finish = [&](auto keep_tag) __attribute__((always_inline)) {
+    constexpr int KEEP = decltype(keep_tag)::value, GIVE = 1 - KEEP;
+    const int mine = KEEP * 3 * 4 * 256, theirs = GIVE * 3 * 4 * 256;  // group KEEP writes at `mine`
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const int i = (dt * 4 + c) * 256 + wig * 64 + lane;
-      const f32x4_t a = buf4[i], o4 = buf4[i + NDT * 4 * 256];
+      const int i = c * 256 + wig * 64 + lane;
+      buf4[mine + i] = f32x4_t{accA[GIVE][4 * c], accA[GIVE][4 * c + 1], accA[GIVE][4 * c + 2], accA[GIVE][4 * c + 3]};
+      buf4[mine + 4 * 256 + i] =
+          f32x4_t{accO[GIVE][4 * c], accO[GIVE][4 * c + 1], accO[GIVE][4 * c + 2], accO[GIVE][4 * c + 3]};
+      if (has_tv)
+        buf4[mine + 8 * 256 + i] =
+            f32x4_t{accC[GIVE][4 * c], accC[GIVE][4 * c + 1], accC[GIVE][4 * c + 2], accC[GIVE][4 * c + 3]};
+    }
+    buf[RS + KEEP * 512 + wig * 64 + lane] = lpart;
+    buf[RS + KEEP * 512 + 256 + wig * 64 + lane] = cpart;
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int i = c * 256 + wig * 64 + lane;
+      const f32x4_t a = buf4[theirs + i], o4 = buf4[theirs + 4 * 256 + i];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        accA[dt][4 * c + e] += a[e];
-        accO[dt][4 * c + e] += o4[e];
+        accA[KEEP][4 * c + e] += a[e];
+        accO[KEEP][4 * c + e] += o4[e];
       }
       if (has_tv) {
-        const f32x4_t c4 = buf4[i + 2 * NDT * 4 * 256];
+        const f32x4_t c4 = buf4[theirs + 8 * 256 + i];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) accC[dt][4 * c + e] += c4[e];
+        for (int e = 0; e < 4; ++e) accC[KEEP][4 * c + e] += c4[e];
       }
     }
-  lpart += buf[RS + wig * 64 + lane];
-  cpart += buf[RS + 256 + wig * 64 + lane];
+    lpart += buf[RS + GIVE * 512 + wig * 64 + lane];
+    cpart += buf[RS + GIVE * 512 + 256 + wig * 64 + lane];
 
-  // Epilogue as jvp_kernel's (O rebuilt from the same P; normalize: P divided by its own row sum).
-  float inv = 1.f;
-  if (p.normalize) {
-    const float L = pair_sum(lpart);
-    inv = L > 0.f ? 1.f / L : 0.f;
-  }
-  const float cval = pair_sum(cpart) * s.scale * inv;
-  if (qvalid) {
-    T* TO = (T*)p.tout.p + b * p.tout.sb + h * p.tout.sh;
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
+    // Epilogue as jvp_kernel's (O rebuilt from the same P; normalize: P divided by its own row sum), for the
+    // columns of tile KEEP.
+    float inv = 1.f;
+    if (p.normalize) {
+      const float L = pair_sum(lpart);
+      inv = L > 0.f ? 1.f / L : 0.f;
+    }
+    const float cval = pair_sum(cpart) * s.scale * inv;
+    if (qvalid) {
+      T* TO = (T*)p.tout.p + b * p.tout.sb + h * p.tout.sh;
 #pragma unroll
       for (int qd = 0; qd < 4; ++qd) {
-        const int d0 = dt * 32 + 8 * qd + 4 * g;
+        const int d0 = KEEP * 32 + 8 * qd + 4 * g;
         float r4[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float ov = accO[dt][4 * qd + e] * inv;
-          r4[e] = inv * (s.scale * accA[dt][4 * qd + e] + accC[dt][4 * qd + e]) - cval * ov;
+          const float ov = accO[KEEP][4 * qd + e] * inv;
+          r4[e] = inv * (s.scale * accA[KEEP][4 * qd + e] + accC[KEEP][4 * qd + e]) - cval * ov;
         }
         store4<T>(TO, p.tout.sr, myq, d0, s.D, r4[0], r4[1], r4[2], r4[3], s.vec);
       }
-  }
+    }
+  };
+  // both branches meet the one barrier inside finish
+  if (grp == 0)
+    finish(std::integral_constant<int, 0>{});
+  else
+    finish(std::integral_constant<int, 1>{});
 }
 
 template <bool HAS_O>
