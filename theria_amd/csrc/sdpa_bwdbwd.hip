@@ -1461,37 +1461,40 @@ __global__ __launch_bounds__(512, 2) void bwdbwd_cols_qs_kernel(const BwdBwdPara
     __syncthreads();  // every wave is done with the tiles
   }
 
-  // group 1's accumulators to group 0 (element e of lane l of wave w at e * 256 + w * 64 + l)
+  // The groups finish one column tile each (group g the tile dt = g): each hands the other tile's G_V and G_K
+  // partial sums to the other group (element e of accumulator a (V, K) of lane l of wave w of group g at
+  // ((g * 2 + a) * 16 + e) * 256 + w * 64 + l), then stores its half of the columns.
+  static_assert(NDT == 2, "one column tile per group");
   float* xb = reinterpret_cast<float*>(smem);
-  if (grp == 1) {
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        xb[(dt * 16 + r) * 256 + wig * 64 + lane] = accV[dt][r];
-        xb[((NDT + dt) * 16 + r) * 256 + wig * 64 + lane] = accK[dt][r];
-      }
-  }
-  __syncthreads();
-  if (grp == 1) return;
   T* OV = (T*)p.out_gv.p + b * p.out_gv.sb + h * p.out_gv.sh;
   T* OK = (T*)p.out_gk.p + b * p.out_gk.sb + h * p.out_gk.sh;
+  auto finish = [&](auto keep_tag) __attribute__((always_inline)) {
+    constexpr int KEEP = decltype(keep_tag)::value, GIVE = 1 - KEEP;
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) {
-    const int d = dt * 32 + li;
+    for (int r = 0; r < 16; ++r) {
+      xb[((KEEP * 2 + 0) * 16 + r) * 256 + wig * 64 + lane] = accV[GIVE][r];
+      xb[((KEEP * 2 + 1) * 16 + r) * 256 + wig * 64 + lane] = accK[GIVE][r];
+    }
+    __syncthreads();
+    const int d = KEEP * 32 + li;
     if (d < s.D) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int key = kw0 + acc_row(r, g);
         if (key < s.M) {
-          const float v = accV[dt][r] + xb[(dt * 16 + r) * 256 + wig * 64 + lane];
-          const float k = accK[dt][r] + xb[((NDT + dt) * 16 + r) * 256 + wig * 64 + lane];
+          const float v = accV[KEEP][r] + xb[((GIVE * 2 + 0) * 16 + r) * 256 + wig * 64 + lane];
+          const float k = accK[KEEP][r] + xb[((GIVE * 2 + 1) * 16 + r) * 256 + wig * 64 + lane];
           OV[(int64_t)key * p.out_gv.sr + d] = (T)v;
           OK[(int64_t)key * p.out_gk.sr + d] = (T)(k * s.scale);
         }
       }
     }
-  }
+  };
+  // both branches meet the one barrier inside finish
+  if (grp == 0)
+    finish(std::integral_constant<int, 0>{});
+  else
+    finish(std::integral_constant<int, 1>{});
 }
 
 // The query-split column kernel takes 16-bit problems at head dim 64 whose Q, dO, gQ slabs allow LDS DMA and
